@@ -1,0 +1,123 @@
+/* wptv.h — the C ABI of the MI355X (gfx950) speculative-decoding verify step.
+ *
+ * One shared library, libwptv.so, built with hipcc for gfx950 only.  Every
+ * entry point is stream-ordered and asynchronous: it validates its arguments
+ * on the host, enqueues kernels on `stream` and returns.  Device pointers are
+ * on the current HIP device; the caller owns every buffer, the workspaces
+ * included, and the library allocates nothing.  The library keeps no state
+ * between calls apart from a per-device cache of the compute-unit count, so
+ * it is re-entrant across host threads (calls that share a workspace on one
+ * stream are ordered by that stream).
+ *
+ * Status codes: WPTV_OK, or a negative WPTV_E_* value; wptv_last_error()
+ * then holds a thread-local message naming the argument or the HIP error.
+ *
+ * Tensor layouts are row-major.  A "row" of the key/value table is the c
+ * contiguous elements of one token; tables are addressed by a batch stride
+ * and a row stride in elements, so the keys and values may be the two halves
+ * of one (B, N, 2c) entries table, as the reference's exact layer keeps them
+ * (packages/wpt-model/src/wpt_model/attention.py:184-186).
+ */
+#ifndef WPTV_H
+#define WPTV_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WPTV_ABI_VERSION 1
+
+enum {
+  WPTV_OK = 0,
+  WPTV_E_INVALID = -1,     /* a bad argument or shape */
+  WPTV_E_HIP = -2,         /* a HIP runtime error (launch, device query) */
+  WPTV_E_UNSUPPORTED = -3  /* a dtype, head width or feature this build has no kernel for */
+};
+
+enum { WPTV_F32 = 0, WPTV_BF16 = 1 };
+
+/* wptv_verify_attention flags */
+enum {
+  WPTV_ATTN_FORCE_GENERIC = 1 /* run the wave-per-query VALU kernel even where the MFMA kernel applies */
+};
+
+int wptv_abi_version(void);
+const char* wptv_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * Verify attention: MQA (one key/value head shared by H query heads) of the
+ * k+1 (= T) query positions of each batch row against its key/value table.
+ *
+ * Replaces the reference's exact_attention with top_k = 0
+ * (packages/wpt-model/src/wpt_model/pytorch_kernels.py:98-121,142-146, the
+ * contract at :18-26, dispatched by kernels.py:160-171), its window-only
+ * sparse_attention (pytorch_kernels.py:149-153,171-187,213-217 with no
+ * chosen rows) and its tree-mask primitive dense_attention
+ * (attention.py:74-82) with the mask "prefix plus ancestors-or-self".
+ *
+ *   q          [B, T, H, c] contiguous, dtype
+ *   k, v       row n of batch b at k + b*k_stride_b + n*k_stride_n (elements)
+ *   positions  [B, T] int64: query t of row b sees table rows
+ *              max(0, p - window + 1) .. min(p, N - 1), p = positions[b, t]
+ *              (window <= 0: from row 0).  A padding query past the table
+ *              reads up to its last row.
+ *   tree_base, tree_ancestors  NULL, or [B] int64 and [T] uint64: rows
+ *              r >= tree_base[b] are draft-tree nodes, and query t sees node
+ *              r - tree_base[b] only where that bit of tree_ancestors[t] is
+ *              set (node indices < 64)
+ *   sink       NULL, or [H] fp32: a per-head logit added to the softmax
+ *              denominator (log-sum-exp with the scores)
+ *   scale      the factor on q.k (c^-0.5 in the reference)
+ *   splits     in: the number of parts each batch row's key range is cut
+ *              into (0 = chosen from B, T, N and the GPU); the workspace must
+ *              hold wptv_attention_workspace() bytes for the same arguments
+ *   out        [B, T, H, c] contiguous, dtype
+ *   lse        NULL, or [B, T, H] fp32: each query head's natural-log
+ *              log-sum-exp, the sink included
+ * ------------------------------------------------------------------------- */
+int wptv_attention_workspace(int B, int T, int H, int c, int N, int window, int dtype, int flags,
+                             int* splits, size_t* bytes);
+
+int wptv_verify_attention(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
+                          const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
+                          const int64_t* positions, int window, const int64_t* tree_base,
+                          const uint64_t* tree_ancestors, const float* sink, int B, int T, int H, int c,
+                          int N, float scale, int splits, int flags, void* out, float* lse,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Sparse attention over chosen rows plus the last `window` rows, with a sink:
+ * the reference's sparse_attention with chosen rows
+ * (pytorch_kernels.py:171-187,213-217).  idx [B, T, K] int64, -1 = none;
+ * a row named both in idx and in the window is counted twice, as the
+ * reference's concatenation of the two lists counts it. */
+int wptv_sparse_attention(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
+                          const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
+                          const int64_t* idx, int K, const int64_t* positions, int window,
+                          const float* sink, int B, int T, int H, int c, int N, float scale,
+                          void* out, float* lse, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * KV append: table[b, start[b] + j, :] = rows[b, j, :] for j < counts[b].
+ * Replaces the scatter of the reference's Reading.everything
+ * (packages/wpt-model/src/wpt_model/cache.py:110-128; the index_put at :126).
+ * Rows with start[b] + j >= capacity are not written and make the call
+ * fail after the fact only through the host's own check (the host keeps the
+ * table large enough; the kernel never writes past capacity).
+ *   table  row n of batch b at table + b*table_stride_b + n*table_stride_n
+ *   rows   row j of batch b at rows + b*rows_stride_b + j*rows_stride_n
+ *   width  elements per row (2c for an entries table), contiguous
+ * ------------------------------------------------------------------------- */
+int wptv_kv_append(void* table, int64_t table_stride_b, int64_t table_stride_n, int64_t capacity,
+                   const void* rows, int64_t rows_stride_b, int64_t rows_stride_n,
+                   const int64_t* start, const int64_t* counts, int B, int n, int width, int dtype,
+                   hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WPTV_H */

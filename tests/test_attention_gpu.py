@@ -1,0 +1,162 @@
+"""The HIP verify attention against the oracle, on the GPU, through the C ABI
+(wpt_amd.kernels calls libwptv.so): bf16 within 1e-2 of the largest expected
+value (the reference's own kernel tolerance, test_kernels.py:173, tighter than
+the 2e-2 the verify step allows), fp32 within 1e-5."""
+
+import pytest
+import torch
+
+from oracle import attention as oracle
+from tests.formulas import relative_error
+from wpt_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def draw(*shape, seed, dtype=torch.bfloat16):
+    generator = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=generator).to(dtype)
+
+
+def entries_table(B, N, c, seed, dtype=torch.bfloat16):
+    """k and v as the strided halves of one (B, N, 2c) entries table."""
+    table = draw(B, N, 2 * c, seed=seed, dtype=dtype)
+    return table, table[..., :c], table[..., c:]
+
+
+def on(device, *tensors):
+    return [t.to(device) for t in tensors]
+
+
+@pytest.mark.parametrize("B, T, H, c, N, splits", [
+    (32, 5, 16, 128, 4096, 0),   # the verify-attention workload: 16 query heads, 1 KV head, k+1 = 5
+    (32, 5, 16, 128, 4096, 1),   # one part per batch row: no combine
+    (4, 5, 16, 128, 1000, 3),    # a key range that does not split evenly
+    (3, 4, 4, 128, 400, 0),      # the reference's generation-pass shape (test_triton_kernels.py:58)
+    (2, 7, 12, 128, 300, 0),     # 84 query rows: five 16-row blocks, the last partly padding
+    (2, 5, 16, 64, 777, 0),      # head width 64
+    (1, 1, 4, 64, 1, 0),         # a single row
+])
+def test_exact_attention_matches_the_oracle(device, B, T, H, c, N, splits):
+    q = draw(B, T, H, c, seed=1)
+    _, k, v = entries_table(B, N, c, seed=2)
+    positions = (N - T + torch.arange(T)).clamp(min=0).expand(B, T).contiguous()
+    expected, _ = oracle.exact_attention(q, k, v, positions, c ** -0.5, 0, 128)
+    qd, kd, vd, pd = on(device, q, k, v, positions)
+    # the strided halves of the device table, as the model's cache gives them
+    table = torch.cat([kd, vd], -1)
+    got = kernels.verify_attention(qd, table[..., :c], table[..., c:], pd, c ** -0.5, splits=splits)
+    assert got.dtype == torch.bfloat16 and got.shape == (B, T, H, c)
+    assert relative_error(got.cpu(), expected) < 1e-2
+
+
+def test_padding_queries_past_the_table(device):
+    # the reference's generation pass: rows at different places, the last
+    # row's later queries past the table read up to its last row
+    B, T, H, c, N = 3, 4, 4, 128, 400
+    q = draw(B, T, H, c, seed=0)
+    table, k, v = entries_table(B, N, c, seed=1)
+    positions = torch.tensor([[396, 397, 398, 399], [100, 101, 102, 103], [398, 399, 400, 401]])
+    expected, _ = oracle.exact_attention(q, k, v, positions, c ** -0.5, 0, 16)
+    qd, td, pd = on(device, q, table, positions)
+    out, chosen = kernels.exact_attention(qd, td[..., :c], td[..., c:], pd, c ** -0.5, 0, 16)
+    assert chosen.shape == (B, T, 0)
+    assert relative_error(out.cpu(), expected) < 1e-2
+
+
+def test_fp32_attention_is_within_1e_5(device):
+    # the fp32 form (the CPU-runnable plumbing decoder's head layout)
+    B, T, H, c, N = 1, 5, 4, 64, 69
+    q = draw(B, T, H, c, seed=3, dtype=torch.float32)
+    _, k, v = entries_table(B, N, c, seed=4, dtype=torch.float32)
+    positions = (N - T + torch.arange(T)).expand(B, T).contiguous()
+    expected, _ = oracle.exact_attention(q, k, v, positions, c ** -0.5, 0, 128)
+    got = kernels.verify_attention(*on(device, q, k, v, positions), c ** -0.5)
+    assert (got.cpu() - expected).abs().max() < 1e-5
+
+
+def test_the_generic_and_mfma_kernels_agree(device):
+    B, T, H, c, N = 2, 5, 16, 128, 1500
+    q, (_, k, v) = draw(B, T, H, c, seed=5), entries_table(B, N, c, seed=6)
+    positions = (N - T + torch.arange(T)).expand(B, T).contiguous()
+    args = on(device, q, k, v, positions)
+    mfma = kernels.verify_attention(*args, c ** -0.5)
+    generic = kernels.verify_attention(*args, c ** -0.5, generic=True)
+    assert relative_error(mfma.cpu(), generic.cpu().float()) < 1e-2
+
+
+@pytest.mark.parametrize("with_sink", [False, True])
+def test_sliding_window_verify_matches_the_oracle(device, with_sink):
+    # the sliding-window workload: per-row lengths uniform in [N/2, N], window
+    # 1024, k+1 = 5 queries at each row's end
+    B, T, H, c, N, W = 8, 5, 16, 128, 32768, 1024
+    generator = torch.Generator().manual_seed(7)
+    lengths = torch.randint(N // 2, N + 1, (B,), generator=generator)
+    positions = lengths[:, None] - T + torch.arange(T)
+    q = draw(B, T, H, c, seed=8)
+    _, k, v = entries_table(B, N, c, seed=9)
+    sink = draw(H, seed=10, dtype=torch.float32) if with_sink else torch.full((H,), float("-inf"))
+    idx = torch.empty(B, T, 0, dtype=torch.long)
+    expected = oracle.sparse_attention(q, k, v, sink, idx, positions, c ** -0.5, W)
+    qd, kd, vd, pd, sd, id_ = on(device, q, k, v, positions, sink, idx)
+    got = kernels.sparse_attention(qd, kd, vd, sd, id_, pd, c ** -0.5, W)
+    assert relative_error(got.cpu(), expected) < 1e-2
+
+
+def test_chosen_rows_with_a_window_and_sink_match_the_oracle(device):
+    # the sparse form with chosen rows (the generic kernel's gather)
+    B, T, H, c, N, W, K = 2, 6, 4, 128, 300, 32, 16
+    q = draw(B, T, H, c, seed=11)
+    _, k, v = entries_table(B, N, c, seed=12)
+    sink = draw(H, seed=13, dtype=torch.float32)
+    positions = (N - T + torch.arange(T)).expand(B, T).contiguous()
+    generator = torch.Generator().manual_seed(14)
+    idx = torch.stack([torch.stack([torch.randperm(int(p) - W + 1, generator=generator)[:K] for p in row])
+                       for row in positions])
+    idx[:, ::2, -3:] = -1
+    expected = oracle.sparse_attention(q, k, v, sink, idx, positions, c ** -0.5, W)
+    got = kernels.sparse_attention(*on(device, q, k, v, sink, idx, positions), c ** -0.5, W)
+    assert relative_error(got.cpu(), expected) < 1e-2
+
+
+def test_tree_attention_matches_the_oracle(device):
+    # the tree workload's shape at a smaller prefix: a binary draft tree of 31
+    # nodes (depth 5) after the prefix, ancestor-only mask
+    B, M, H, c, prefix = 4, 31, 16, 128, 1000
+    parents = oracle.binary_tree_parents(M)
+    q = draw(B, M, H, c, seed=15)
+    _, k, v = entries_table(B, prefix + M, c, seed=16)
+    prefixes = torch.full((B,), prefix)
+    expected = oracle.tree_attention(q, k, v, prefixes, parents, c ** -0.5)
+    qd, kd, vd, bd = on(device, q, k, v, prefixes)
+    got = kernels.tree_attention(qd, kd, vd, bd, parents, c ** -0.5)
+    assert relative_error(got.cpu(), expected) < 1e-2
+
+
+def test_lse_is_the_log_sum_exp(device):
+    B, T, H, c, N = 2, 5, 16, 128, 513
+    q, (_, k, v) = draw(B, T, H, c, seed=17), entries_table(B, N, c, seed=18)
+    positions = (N - T + torch.arange(T)).expand(B, T).contiguous()
+    z = torch.einsum("bthc,bnc->bthn", q.float(), k.float()) * c ** -0.5
+    z = z.masked_fill(torch.arange(N) > positions[..., None, None], float("-inf"))
+    for splits in (1, 4):
+        _, lse = kernels.verify_attention(*on(device, q, k, v, positions), c ** -0.5, lse=True, splits=splits)
+        assert (lse.cpu() - z.logsumexp(-1)).abs().max() < 2e-2
+
+
+def test_bad_shapes_raise_value_error(device):
+    q = torch.zeros(2, 5, 16, 128, dtype=torch.bfloat16, device=device)
+    k = torch.zeros(2, 64, 128, dtype=torch.bfloat16, device=device)
+    positions = torch.zeros(2, 4, dtype=torch.long, device=device)
+    with pytest.raises(ValueError):
+        kernels.verify_attention(q, k, k, positions, 0.1)
+    with pytest.raises(ValueError):
+        kernels.verify_attention(q, k.float(), k.float(), positions[:, :1].expand(2, 5), 0.1)
+
+
+def test_the_choice_is_not_built_yet(device):
+    q = torch.zeros(1, 2, 4, 128, dtype=torch.bfloat16, device=device)
+    k = torch.zeros(1, 300, 128, dtype=torch.bfloat16, device=device)
+    positions = torch.tensor([[298, 299]], device=device)
+    with pytest.raises(NotImplementedError):
+        kernels.exact_attention(q, k, k, positions, 0.1, 16, 128)

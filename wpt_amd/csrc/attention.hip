@@ -1,0 +1,762 @@
+// Verify attention for gfx950: MQA of the k+1 (or tree) query positions of a
+// speculative-decoding step against each batch row's key/value table.
+//
+// Semantics follow the reference's PyTorch form (pytorch_kernels.py:98-121
+// exact attention; :149-153,171-187 window and sink; attention.py:74-82 the
+// masked dense form): FP32 scores q.k*scale, FP32 softmax, output in the
+// input dtype.
+//
+// MFMA kernel (bf16, head width 64 or 128).  The H query heads of the T
+// positions of one batch row are stacked as R = T*H rows (row r = t*H + h),
+// so the single shared K/V head is read once per query group and feeds
+// 16-row MFMA blocks.  Each workgroup (4 wavefronts) owns one part ("split")
+// of a batch row's visible key range; each wavefront streams its own 16-row
+// key/value blocks straight from HBM with 16-byte loads, one block ahead:
+//
+//   S^T[kv, q] = K[kv, :] . Q[q, :]     v_mfma_f32_16x16x32_bf16, K as the A
+//                                      operand (one key row per lane), Q^T
+//                                      held in registers as the B operand
+//   online softmax per query row        each lane holds 4 keys x 1 query row;
+//                                      max/sum across the 4 lane groups
+//   O^T[c, q] += V^T[c, kv] . P^T[kv,q] v_mfma_f32_16x16x16_bf16: the S^T
+//                                      accumulator is already P^T's operand
+//                                      layout; V^T comes from a per-wavefront
+//                                      LDS staging buffer read transposed
+//
+// The four wavefronts of a workgroup are merged through LDS at the end; the
+// splits of one batch row are merged by a second kernel (log-sum-exp
+// combine, fixed order, so results do not depend on scheduling).
+//
+// Generic kernel (fp32 or bf16, any head width <= 256, chosen rows): one
+// wavefront per (batch row, query position, head), one key row per lane,
+// the reference algorithm in FP32 with an online softmax.  It is the fp32
+// path and the chosen-row (sparse) path.
+#include "wptv_common.h"
+
+#include <climits>
+
+namespace wptv {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr float kNegInf = -__builtin_inff();
+
+struct Bounds {
+  int lo, hi;  // inclusive key-row range a query sees (hi < lo: none)
+};
+
+// The key rows query position t of batch row b sees, before the tree mask.
+__device__ __forceinline__ Bounds query_bounds(const int64_t* __restrict__ pos_b, int t, int window, int N) {
+  const int64_t p = pos_b[t];
+  int64_t hi = p < (int64_t)N - 1 ? p : (int64_t)N - 1;
+  int64_t lo = window > 0 ? p - window + 1 : 0;
+  if (lo < 0) lo = 0;
+  Bounds r;
+  r.lo = (int)lo;
+  r.hi = hi < lo ? (int)lo - 1 : (int)hi;
+  return r;
+}
+
+__device__ __forceinline__ bool tree_visible(int n, int64_t tbase, uint64_t anc) {
+  if ((int64_t)n < tbase) return true;
+  const int64_t node = (int64_t)n - tbase;
+  return node < 64 && ((anc >> node) & 1ull);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA kernel
+// ---------------------------------------------------------------------------
+
+template <int C, int MBW, int NS>
+struct MfmaShape {
+  static constexpr int kRows = 16 * MBW;         // query rows per workgroup
+  static constexpr int kSteps = C / 32;          // k-steps of the QK^T product
+  static constexpr int kCBlocks = C / 16;        // 16-wide column blocks of O
+  static constexpr int kChunks = C / 8;          // 16-byte chunks per key/value row
+  static constexpr int kBlock = 16 * C;          // one 16-row block of K or V (bf16 elements)
+  static constexpr int kLoads = kBlock * 2 / 1024;  // 1 KiB LDS-DMA loads per block
+  static constexpr int kStage = 2 * kBlock;      // K block then V block
+  static constexpr int kStages = NS;             // blocks in flight per wavefront
+  static constexpr int kLdsElems = kWaves * NS * kStage;
+};
+
+// Softmax rescaling is deferred until a row's maximum grows by more than this
+// many powers of two (the stale maximum stays the reference for p and l, so
+// the result is exact; p stays below 2^8).
+constexpr float kRescale = 8.f;
+
+// s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+  asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// A raw buffer resource over `bytes` bytes from `base` (gfx9 dword3 format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+template <int C, int MBW, int NS, bool TREE>
+__global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
+    const unsigned short* __restrict__ q, const unsigned short* __restrict__ k, int64_t ksb, int64_t ksn,
+    const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn, const int64_t* __restrict__ positions,
+    int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
+    const float* __restrict__ sink, int T, int H, int N, float scale_log2, int splits, int range_from_positions,
+    unsigned short* __restrict__ out, float* __restrict__ lse_out, float* __restrict__ part_o,
+    float* __restrict__ part_lse) {
+  using S = MfmaShape<C, MBW, NS>;
+  static_assert(S::kRows * C * 4 <= S::kLdsElems * 2, "the merge buffer reuses the stages");
+  static_assert(S::kLoads * 64 % S::kChunks == 0 && 64 % S::kChunks == 0, "rows per DMA load");
+  __shared__ __attribute__((aligned(16))) unsigned short lds[S::kLdsElems];
+  __shared__ float sm_m[kWaves][S::kRows];
+  __shared__ float sm_l[kWaves][S::kRows];
+  __shared__ float fin_scale[S::kRows];
+  __shared__ float fin_lse[S::kRows];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int j = lane & 15;  // this lane's column: query row (S^T, O^T) or key row (K operand)
+  const int g = lane >> 4;  // lane group 0..3
+  const int split = blockIdx.x;
+  const int grp = blockIdx.y;
+  const int b = blockIdx.z;
+  const int R = T * H;
+  const int r_base = grp * S::kRows;
+  const int64_t* pos_b = positions + (int64_t)b * T;
+
+  // The key rows this workgroup's queries can see.  Full causal attention of
+  // one query group reads the whole table, whatever the positions say, so the
+  // first loads need no position (rows past a query are masked below).
+  int u_lo = 0, u_hi = N - 1;
+  if (range_from_positions) {
+    u_lo = INT_MAX;
+    u_hi = -1;
+    const int t_first = r_base / H;
+    const int t_last = ((r_base + S::kRows < R ? r_base + S::kRows : R) - 1) / H;
+    for (int t = t_first; t <= t_last; ++t) {
+      const Bounds bt = query_bounds(pos_b, t, window, N);
+      if (bt.hi >= bt.lo) {
+        u_lo = min(u_lo, bt.lo);
+        u_hi = max(u_hi, bt.hi);
+      }
+    }
+  }
+  int s_lo = 0, s_hi = -1;
+  if (u_hi >= u_lo) {
+    const int U = u_hi - u_lo + 1;
+    int per = (U + splits - 1) / splits;
+    per = (per + 16 * kWaves - 1) / (16 * kWaves) * (16 * kWaves);
+    s_lo = u_lo + split * per;
+    s_hi = min(s_lo + per - 1, u_hi);
+  }
+  const int nblocks = s_hi >= s_lo ? (s_hi - s_lo + 1 + 15) / 16 : 0;
+  const int mine = nblocks > wave ? (nblocks - wave + kWaves - 1) / kWaves : 0;  // blocks of this wavefront
+
+  unsigned short* ring = lds + wave * NS * S::kStage;
+  // Byte offsets within one batch row's keys and values fit 32 bits: the
+  // host checks that N rows of the table do.
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(k + (int64_t)b * ksb, 0xFFFFFFFFu);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(v + (int64_t)b * vsb, 0xFFFFFFFFu);
+  const uint32_t krow_bytes = (uint32_t)ksn * 2u, vrow_bytes = (uint32_t)vsn * 2u;
+  // LDS layout of a 16-row block, chunk-major: the 16-byte chunk x (columns
+  // 8x..8x+7) of row r sits at unit 16x + r.  Lane l of DMA load i fills
+  // unit 64i + l, i.e. chunk 4i + (l >> 4) of row l & 15, so each load reads
+  // 64 contiguous bytes of 16 rows and every MFMA operand read below is a
+  // per-lane base plus a constant offset.
+  auto issue = [&](int it) {
+    const int blk = wave + it * kWaves;
+    unsigned short* st = ring + (it % NS) * S::kStage;
+    int n = s_lo + blk * 16 + j;
+    n = n < s_hi ? n : s_hi;  // rows past the split are masked; read a valid one
+    const uint32_t koff = (uint32_t)n * krow_bytes + 16u * g;
+    const uint32_t voff = (uint32_t)n * vrow_bytes + 16u * g;
+#pragma unroll
+    for (int i = 0; i < S::kLoads; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(st + 512 * i), 16, koff + 64u * i, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(st + S::kBlock + 512 * i), 16, voff + 64u * i, 0, 0,
+                                               0);
+    }
+  };
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int it = 0; it < NS - 1; ++it)
+    if (it < mine) issue(it);
+
+  // Workgroup-uniform bounds: the rows every query of the group sees.
+  int f_lo = 0, f_hi = INT_MAX;
+  {
+    const int t_first = r_base / H;
+    const int t_last = ((r_base + S::kRows < R ? r_base + S::kRows : R) - 1) / H;
+    for (int t = t_first; t <= t_last; ++t) {
+      const Bounds bt = query_bounds(pos_b, t, window, N);
+      f_lo = max(f_lo, bt.lo);
+      f_hi = min(f_hi, bt.hi);
+    }
+  }
+  const int64_t tbase = TREE ? tree_base[b] : (int64_t)INT_MAX;
+  if (TREE && tbase <= (int64_t)f_hi) f_hi = (int)tbase - 1;
+
+  // Per-lane query rows (one per m-block): bounds and the Q^T operand.
+  int lo[MBW], hi[MBW];
+  uint64_t anc[TREE ? MBW : 1];
+  bf16x8 qf[MBW][S::kSteps];
+#pragma unroll
+  for (int mb = 0; mb < MBW; ++mb) {
+    const int r = r_base + 16 * mb + j;
+    if (r < R) {
+      const int t = r / H;
+      const Bounds bt = query_bounds(pos_b, t, window, N);
+      lo[mb] = bt.lo;
+      hi[mb] = bt.hi;
+      if constexpr (TREE) anc[mb] = ancestors[t];
+      const unsigned short* qrow = q + ((int64_t)b * R + r) * C;
+#pragma unroll
+      for (int s = 0; s < S::kSteps; ++s) qf[mb][s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g);
+    } else {
+      lo[mb] = 0;
+      hi[mb] = -1;
+      if constexpr (TREE) anc[mb] = 0;
+#pragma unroll
+      for (int s = 0; s < S::kSteps; ++s) {
+        const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+        qf[mb][s] = __builtin_bit_cast(bf16x8, z);
+      }
+    }
+  }
+
+  f32x4 o[MBW][S::kCBlocks];
+  float m_run[MBW], l_run[MBW];
+#pragma unroll
+  for (int mb = 0; mb < MBW; ++mb) {
+    m_run[mb] = kNegInf;
+    l_run[mb] = 0.f;
+#pragma unroll
+    for (int cb = 0; cb < S::kCBlocks; ++cb) o[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+#pragma unroll 1
+  for (int it = 0; it < mine; ++it) {
+    // Refill the stage freed by the previous block, then wait for this one.
+    asm volatile("" ::: "memory");
+    if (it + NS - 1 < mine) {
+      issue(it + NS - 1);
+      wait_vmcnt<2 * S::kLoads * (NS - 1)>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    const unsigned short* st = ring + (it % NS) * S::kStage;
+    const int n0 = s_lo + (wave + it * kWaves) * 16;
+
+    // S^T = K . Q^T: lane (j, g) reads key row j, chunk 4s + g (unit 64s + lane).
+    f32x4 sacc[MBW];
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb) sacc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < S::kSteps; ++s) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(st + 512 * s + 8 * lane);
+#pragma unroll
+      for (int mb = 0; mb < MBW; ++mb)
+        sacc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[mb][s], sacc[mb], 0, 0, 0);
+    }
+
+    // Mask, online softmax (deferred rescaling), P^T operand.
+    const bool full = n0 >= f_lo && n0 + 15 <= f_hi && n0 + 15 <= s_hi;
+    float x[MBW][4];
+    float bm[MBW];
+    bool grow = false;
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[mb][i] = sacc[mb][i] * scale_log2;
+      if (!full) {
+        const int top = min(hi[mb], s_hi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = n0 + 4 * g + i;
+          bool vis = n >= lo[mb] && n <= top;
+          if constexpr (TREE) vis = vis && tree_visible(n, tbase, anc[mb]);
+          x[mb][i] = vis ? x[mb][i] : kNegInf;
+        }
+      }
+      float t = fmaxf(fmaxf(x[mb][0], x[mb][1]), fmaxf(x[mb][2], x[mb][3]));
+      t = fmaxf(t, __shfl_xor(t, 16, 64));
+      t = fmaxf(t, __shfl_xor(t, 32, 64));
+      bm[mb] = t;
+      grow = grow || (t > m_run[mb] + kRescale);
+    }
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+      for (int mb = 0; mb < MBW; ++mb) {
+        const float m_new = fmaxf(m_run[mb], bm[mb]);
+        const float alpha = (m_new == kNegInf) ? 1.f : exp2f(m_run[mb] - m_new);
+        m_run[mb] = m_new;
+        l_run[mb] *= alpha;
+#pragma unroll
+        for (int cb = 0; cb < S::kCBlocks; ++cb) {
+          o[mb][cb] *= alpha;
+          __builtin_amdgcn_sched_barrier(0);  // one accumulator at a time through the VALU
+        }
+      }
+    }
+    s16x4 pt[MBW];
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb) {
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = (m_run[mb] == kNegInf) ? 0.f : exp2f(x[mb][i] - m_run[mb]);
+      l_run[mb] += (p[0] + p[1]) + (p[2] + p[3]);
+      pt[mb] = s16x4{(short)f32_to_bf16(p[0]), (short)f32_to_bf16(p[1]), (short)f32_to_bf16(p[2]),
+                     (short)f32_to_bf16(p[3])};
+    }
+
+    // O^T += V^T . P^T: lane (j, g) gathers column cb*16 + j of value rows
+    // 4g..4g+3: chunk 2cb + (j >> 3), units 16 (2cb + (j >> 3)) + 4g + i.
+    const unsigned short* vs = st + S::kBlock + 128 * (j >> 3) + 32 * g + (j & 7);
+#pragma unroll
+    for (int cb = 0; cb < S::kCBlocks; ++cb) {
+      const s16x4 vt = s16x4{(short)vs[256 * cb], (short)vs[256 * cb + 8], (short)vs[256 * cb + 16],
+                             (short)vs[256 * cb + 24]};
+#pragma unroll
+      for (int mb = 0; mb < MBW; ++mb)
+        o[mb][cb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, pt[mb], o[mb][cb], 0, 0, 0);
+    }
+  }
+  wait_vmcnt<0>();
+
+  // ---- merge the four wavefronts (the merge buffer reuses the stages) ----
+#pragma unroll
+  for (int mb = 0; mb < MBW; ++mb) {
+    l_run[mb] += __shfl_xor(l_run[mb], 16, 64);
+    l_run[mb] += __shfl_xor(l_run[mb], 32, 64);
+    if (g == 0) {
+      sm_m[wave][mb * 16 + j] = m_run[mb];
+      sm_l[wave][mb * 16 + j] = l_run[mb];
+    }
+  }
+  __syncthreads();
+  float* obuf = reinterpret_cast<float*>(lds);
+  float wscale[MBW];
+#pragma unroll
+  for (int mb = 0; mb < MBW; ++mb) {
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][mb * 16 + j]);
+    wscale[mb] = (m_run[mb] == kNegInf) ? 0.f : exp2f(m_run[mb] - M);
+  }
+  for (int w = 0; w < kWaves; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int mb = 0; mb < MBW; ++mb) {
+#pragma unroll
+        for (int cb = 0; cb < S::kCBlocks; ++cb) {
+          f32x4* dst = reinterpret_cast<f32x4*>(obuf + (mb * 16 + j) * C + cb * 16 + 4 * g);
+          const f32x4 val = o[mb][cb] * wscale[mb];
+          if (w == 0)
+            *dst = val;
+          else
+            *dst += val;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // Final statistics per query row (the sink joins the denominator when the
+  // split is the whole range), then the output or this split's part.
+  if (threadIdx.x < S::kRows) {
+    const int rr = threadIdx.x;
+    float M = kNegInf;
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][rr]);
+    float L = 0.f;
+    if (M != kNegInf)
+      for (int w = 0; w < kWaves; ++w)
+        if (sm_m[w][rr] != kNegInf) L += sm_l[w][rr] * exp2f(sm_m[w][rr] - M);
+    float f = 1.f;
+    if (splits == 1 && sink && r_base + rr < R) {
+      const float sl = sink[(r_base + rr) % H] * kLog2e;
+      const float M2 = fmaxf(M, sl);
+      f = (M == kNegInf) ? 0.f : exp2f(M - M2);
+      L = L * f + exp2f(sl - M2);
+      M = M2;
+    }
+    fin_scale[rr] = L > 0.f ? f / L : 0.f;
+    fin_lse[rr] = L > 0.f ? M + log2f(L) : kNegInf;
+  }
+  __syncthreads();
+
+  const int rows_here = min(S::kRows, R - r_base);
+  constexpr int kVec = 4;
+  for (int idx = threadIdx.x; idx < rows_here * (C / kVec); idx += kThreads) {
+    const int rr = idx / (C / kVec);
+    const int c4 = (idx % (C / kVec)) * kVec;
+    const int r = r_base + rr;
+    const f32x4 val = *reinterpret_cast<const f32x4*>(obuf + rr * C + c4) * fin_scale[rr];
+    if (splits == 1) {
+      typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<u16x4*>(out + ((int64_t)b * R + r) * C + c4) =
+          u16x4{f32_to_bf16(val[0]), f32_to_bf16(val[1]), f32_to_bf16(val[2]), f32_to_bf16(val[3])};
+      if (lse_out && c4 == 0) lse_out[(int64_t)b * R + r] = fin_lse[rr] * kLn2;
+    } else {
+      const int64_t prow = (((int64_t)b * gridDim.y + grp) * splits + split) * S::kRows + rr;
+      *reinterpret_cast<f32x4*>(part_o + prow * C + c4) = val;
+      if (c4 == 0) part_lse[prow] = fin_lse[rr];
+    }
+  }
+}
+
+// Merges the splits of each query row: fixed order, log-sum-exp weights,
+// the sink joining the denominator.
+template <typename OutT>
+__global__ __launch_bounds__(256) void combine_splits(const float* __restrict__ part_o,
+                                                       const float* __restrict__ part_lse,
+                                                       const float* __restrict__ sink, int R, int H, int C,
+                                                       int rows_per_group, int groups, int splits,
+                                                       OutT* __restrict__ out, float* __restrict__ lse_out) {
+  const int b = blockIdx.y;
+  const int per_row = C / 4;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= R * per_row) return;
+  const int r = idx / per_row;
+  const int c4 = (idx % per_row) * 4;
+  const int grp = r / rows_per_group, rr = r % rows_per_group;
+  const int64_t base = ((int64_t)b * groups + grp) * splits;
+  float M = kNegInf;
+  for (int s = 0; s < splits; ++s) M = fmaxf(M, part_lse[(base + s) * rows_per_group + rr]);
+  const float sl = sink ? sink[r % H] * kLog2e : kNegInf;
+  const float M2 = fmaxf(M, sl);
+  float L = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (M2 != kNegInf) {
+    for (int s = 0; s < splits; ++s) {
+      const int64_t prow = (base + s) * rows_per_group + rr;
+      const float ls = part_lse[prow];
+      if (ls == kNegInf) continue;
+      const float w = exp2f(ls - M2);
+      L += w;
+      acc += w * *reinterpret_cast<const f32x4*>(part_o + prow * C + c4);
+    }
+    if (sink) L += exp2f(sl - M2);
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  OutT* dst = out + ((int64_t)b * R + r) * C + c4;
+  for (int e = 0; e < 4; ++e) dst[e] = from_f32<OutT>(acc[e] * inv);
+  if (lse_out && c4 == 0) lse_out[(int64_t)b * R + r] = L > 0.f ? (M2 + log2f(L)) * kLn2 : kNegInf;
+}
+
+// ---------------------------------------------------------------------------
+// Generic kernel: one wavefront per (b, t, h)
+// ---------------------------------------------------------------------------
+
+constexpr int kMaxC = 256;
+
+template <typename T>
+__global__ __launch_bounds__(64) void attention_generic(
+    const T* __restrict__ q, const T* __restrict__ k, int64_t ksb, int64_t ksn, const T* __restrict__ v,
+    int64_t vsb, int64_t vsn, const int64_t* __restrict__ idx, int K, const int64_t* __restrict__ positions,
+    int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
+    const float* __restrict__ sink, int T_, int H, int C, int N, float scale_log2, T* __restrict__ out,
+    float* __restrict__ lse_out) {
+  const int lane = threadIdx.x;
+  const int h = blockIdx.x % H;
+  const int t = blockIdx.x / H;
+  const int b = blockIdx.y;
+  const int64_t row = ((int64_t)b * T_ + t) * H + h;
+  const T* qrow = q + row * C;
+  const int64_t* pos_b = positions + (int64_t)b * T_;
+
+  // Rows visited: the chosen rows idx[b, t, :] (K of them, -1 = none), then
+  // the rows max(0, p - window + 1) .. min(p, N - 1) (the sparse form's
+  // window drops rows outside [0, N) the same way).
+  const Bounds bt = query_bounds(pos_b, t, window, N);
+  const int lo = bt.lo, hi = bt.hi;
+  const int64_t tbase = tree_base ? tree_base[b] : (int64_t)INT_MAX;
+  const uint64_t anc = tree_base ? ancestors[t] : 0ull;
+  const int n_window = hi >= lo ? hi - lo + 1 : 0;
+  const int total = K + n_window;
+  const int64_t* idx_row = idx ? idx + ((int64_t)b * T_ + t) * K : nullptr;
+
+  float m_run = kNegInf, l_run = 0.f;
+  float acc[kMaxC / 64];
+  for (int u = 0; u < kMaxC / 64; ++u) acc[u] = 0.f;
+  const int per_lane = (C + 63) / 64;
+
+  for (int base = 0; base < total; base += 64) {
+    const int e = base + lane;
+    int n = -1;
+    if (e < total) {
+      if (e < K) {
+        const int64_t chosen = idx_row[e];
+        n = (chosen >= 0 && chosen < N) ? (int)chosen : -1;
+      } else {
+        n = lo + (e - K);
+        if (tree_base && !tree_visible(n, tbase, anc)) n = -1;
+      }
+    }
+    float z = kNegInf;
+    if (n >= 0) {
+      const T* krow = k + (int64_t)b * ksb + (int64_t)n * ksn;
+      float dot = 0.f;
+      for (int c = 0; c < C; ++c) dot += load_f32(qrow + c) * load_f32(krow + c);
+      z = dot * scale_log2;
+    }
+    const float bm = wave_max(z);
+    const float m_new = fmaxf(m_run, bm);
+    if (m_new == kNegInf) continue;
+    const float alpha = exp2f(m_run - m_new);
+    const float pz = (z == kNegInf) ? 0.f : exp2f(z - m_new);
+    l_run = l_run * alpha + wave_sum(pz);
+    for (int u = 0; u < per_lane; ++u) acc[u] *= alpha;
+    m_run = m_new;
+    const int count = min(64, total - base);
+    for (int i = 0; i < count; ++i) {
+      const float pi = __shfl(pz, i, 64);
+      const int ni = __shfl(n, i, 64);
+      if (ni < 0) continue;
+      const T* vrow = v + (int64_t)b * vsb + (int64_t)ni * vsn;
+      for (int u = 0; u < per_lane; ++u) {
+        const int c = lane + 64 * u;
+        if (c < C) acc[u] += pi * load_f32(vrow + c);
+      }
+    }
+  }
+  float M = m_run, L = l_run, f = 1.f;
+  if (sink) {
+    const float sl = sink[h] * kLog2e;
+    const float M2 = fmaxf(M, sl);
+    f = (M == kNegInf) ? 0.f : exp2f(M - M2);
+    L = L * f + exp2f(sl - M2);
+    M = M2;
+  }
+  const float inv = L > 0.f ? f / L : 0.f;
+  T* orow = out + row * C;
+  for (int u = 0; u < per_lane; ++u) {
+    const int c = lane + 64 * u;
+    if (c < C) orow[c] = from_f32<T>(acc[u] * inv);
+  }
+  if (lse_out && lane == 0) lse_out[row] = L > 0.f ? (M + log2f(L)) * kLn2 : kNegInf;
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+struct Plan {
+  bool mfma;
+  int mbw;      // m-blocks per workgroup
+  int groups;   // query-row groups per batch row
+  int splits;   // key-range parts per batch row
+  size_t bytes; // workspace
+};
+
+int pick_mbw(int R) {
+  // Query rows per workgroup: every row of a decode step in one group when
+  // it fits five 16-row blocks (k+1 = 5 positions of 16 heads), else groups
+  // of four blocks.
+  const int blocks = (R + 15) / 16;
+  if (blocks <= 1) return 1;
+  if (blocks <= 2) return 2;
+  if (blocks <= 3) return 3;
+  if (blocks <= 5) return 5;
+  return 4;
+}
+
+int plan(int B, int T, int H, int c, int N, int window, int dtype, int flags, int requested, Plan* out) {
+  if (B <= 0 || T <= 0 || H <= 0 || c <= 0 || N <= 0)
+    return fail(WPTV_E_INVALID, "verify_attention: B, T, H, c and N must be positive (got %d, %d, %d, %d, %d)", B,
+                T, H, c, N);
+  if ((long long)T * H > INT_MAX / 2) return fail(WPTV_E_INVALID, "verify_attention: T*H too large");
+  if (dtype != WPTV_F32 && dtype != WPTV_BF16)
+    return fail(WPTV_E_UNSUPPORTED, "verify_attention: dtype %d is neither fp32 nor bf16", dtype);
+  if (c > kMaxC) return fail(WPTV_E_UNSUPPORTED, "verify_attention: head width %d above %d", c, kMaxC);
+  Plan p{};
+  p.mfma = dtype == WPTV_BF16 && (c == 64 || c == 128) && !(flags & WPTV_ATTN_FORCE_GENERIC);
+  if (!p.mfma) {
+    p.mbw = 0;
+    p.groups = 1;
+    p.splits = 1;
+    p.bytes = 0;
+    *out = p;
+    return WPTV_OK;
+  }
+  const int R = T * H;
+  p.mbw = pick_mbw(R);
+  p.groups = (R + 16 * p.mbw - 1) / (16 * p.mbw);
+  // Key rows a group reads: the whole table, or the window plus the span of
+  // the query positions (T - 1 for consecutive positions).
+  long long span = N;
+  if (window > 0 && (long long)window + T - 1 < span) span = (long long)window + T - 1;
+  int splits = requested;
+  if (splits <= 0) {
+    const long long cus = compute_units();
+    const long long wgs = (long long)B * p.groups;
+    // Enough workgroups to fill the GPU, each at least 64 key rows.
+    long long s = (cus + wgs - 1) / wgs;
+    const long long max_s = (span + 63) / 64;
+    if (s > max_s) s = max_s;
+    if (s < 1) s = 1;
+    splits = (int)s;
+  }
+  if (splits > 4096) return fail(WPTV_E_INVALID, "verify_attention: splits %d above 4096", splits);
+  p.splits = splits;
+  if (splits > 1) {
+    const size_t rows = (size_t)B * p.groups * splits * 16 * p.mbw;
+    p.bytes = align_up(rows * c * sizeof(float), 256) + align_up(rows * sizeof(float), 256);
+  } else {
+    p.bytes = 0;
+  }
+  *out = p;
+  return WPTV_OK;
+}
+
+// Blocks in flight per wavefront: 4 x 8 KiB for head width 128, 6 x 4 KiB for 64.
+template <int C>
+constexpr int stages() { return C == 128 ? 4 : 6; }
+
+template <int C, int MBW, bool TREE>
+void launch_mfma(dim3 grid, hipStream_t stream, const unsigned short* q, const unsigned short* k, int64_t ksb,
+                 int64_t ksn, const unsigned short* v, int64_t vsb, int64_t vsn, const int64_t* positions,
+                 int window, const int64_t* tree_base, const uint64_t* ancestors, const float* sink, int T, int H,
+                 int N, float scale_log2, int splits, int range_from_positions, unsigned short* out, float* lse,
+                 float* part_o, float* part_lse) {
+  hipLaunchKernelGGL((verify_attention_mfma<C, MBW, stages<C>(), TREE>), grid, dim3(kThreads), 0, stream, q, k, ksb, ksn,
+                     v, vsb, vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, splits,
+                     range_from_positions, out, lse, part_o, part_lse);
+}
+
+}  // namespace
+}  // namespace wptv
+
+using namespace wptv;
+
+extern "C" int wptv_attention_workspace(int B, int T, int H, int c, int N, int window, int dtype, int flags,
+                                        int* splits, size_t* bytes) {
+  if (!splits || !bytes) return fail(WPTV_E_INVALID, "attention_workspace: null output pointer");
+  Plan p;
+  int st = plan(B, T, H, c, N, window, dtype, flags, *splits, &p);
+  if (st != WPTV_OK) return st;
+  *splits = p.splits;
+  *bytes = p.bytes;
+  return WPTV_OK;
+}
+
+extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
+                                     const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
+                                     const int64_t* positions, int window, const int64_t* tree_base,
+                                     const uint64_t* tree_ancestors, const float* sink, int B, int T, int H, int c,
+                                     int N, float scale, int splits, int flags, void* out, float* lse,
+                                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!q || !k || !v || !positions || !out)
+    return fail(WPTV_E_INVALID, "verify_attention: q, k, v, positions and out must be given");
+  if ((tree_base == nullptr) != (tree_ancestors == nullptr))
+    return fail(WPTV_E_INVALID, "verify_attention: tree_base and tree_ancestors go together");
+  if (k_stride_n < c || v_stride_n < c)
+    return fail(WPTV_E_INVALID, "verify_attention: a row stride below the head width");
+  Plan p;
+  int st = plan(B, T, H, c, N, window, dtype, flags, splits, &p);
+  if (st != WPTV_OK) return st;
+  const float scale_log2 = scale * kLog2e;
+  if (p.mfma) {
+    // 32-bit byte offsets within one batch row's table (buffer loads).
+    const bool ok_range = (double)N * (double)(k_stride_n > v_stride_n ? k_stride_n : v_stride_n) * 2.0 < 4.0e9;
+    const bool ok_align = ok_range && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && (k_stride_b % 8 == 0) &&
+                          (k_stride_n % 8 == 0) && (v_stride_b % 8 == 0) && (v_stride_n % 8 == 0);
+    if (!ok_align) p.mfma = false, p.splits = 1, p.bytes = 0;
+  }
+  if (!p.mfma) {
+    dim3 grid(T * H, B);
+    if (dtype == WPTV_F32)
+      hipLaunchKernelGGL(attention_generic<float>, grid, dim3(64), 0, stream, (const float*)q, (const float*)k,
+                         k_stride_b, k_stride_n, (const float*)v, v_stride_b, v_stride_n, nullptr, 0, positions,
+                         window, tree_base, tree_ancestors, sink, T, H, c, N, scale_log2, (float*)out, lse);
+    else
+      hipLaunchKernelGGL(attention_generic<unsigned short>, grid, dim3(64), 0, stream, (const unsigned short*)q,
+                         (const unsigned short*)k, k_stride_b, k_stride_n, (const unsigned short*)v, v_stride_b,
+                         v_stride_n, nullptr, 0, positions, window, tree_base, tree_ancestors, sink, T, H, c, N,
+                         scale_log2, (unsigned short*)out, lse);
+    return launched("attention_generic");
+  }
+  if (p.bytes > 0 && (!workspace || workspace_bytes < p.bytes))
+    return fail(WPTV_E_INVALID, "verify_attention: workspace of %zu bytes, %zu needed for %d splits",
+                workspace_bytes, p.bytes, p.splits);
+  const int R = T * H;
+  const int rows_per_group = 16 * p.mbw;
+  float* part_o = nullptr;
+  float* part_lse = nullptr;
+  if (p.splits > 1) {
+    const size_t rows = (size_t)B * p.groups * p.splits * rows_per_group;
+    part_o = static_cast<float*>(workspace);
+    part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(rows * c * sizeof(float), 256));
+  }
+  dim3 grid(p.splits, p.groups, B);
+  // Full causal attention of a single query group reads the whole table; any
+  // other case takes its key range from the positions.
+  const int from_positions = (window > 0 || p.groups > 1) ? 1 : 0;
+  const auto* qb = static_cast<const unsigned short*>(q);
+  const auto* kb = static_cast<const unsigned short*>(k);
+  const auto* vb = static_cast<const unsigned short*>(v);
+  auto* ob = static_cast<unsigned short*>(out);
+#define WPTV_LAUNCH(CC, MM)                                                                                    \
+  (tree_base ? launch_mfma<CC, MM, true> : launch_mfma<CC, MM, false>)(grid, stream, qb, kb, k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, positions,     \
+                      window, tree_base, tree_ancestors, sink, T, H, N, scale_log2, p.splits, from_positions, ob, \
+                      lse, part_o, part_lse)
+  if (c == 128) {
+    switch (p.mbw) {
+      case 1: WPTV_LAUNCH(128, 1); break;
+      case 2: WPTV_LAUNCH(128, 2); break;
+      case 3: WPTV_LAUNCH(128, 3); break;
+      case 4: WPTV_LAUNCH(128, 4); break;
+      default: WPTV_LAUNCH(128, 5); break;
+    }
+  } else {
+    switch (p.mbw) {
+      case 1: WPTV_LAUNCH(64, 1); break;
+      case 2: WPTV_LAUNCH(64, 2); break;
+      case 3: WPTV_LAUNCH(64, 3); break;
+      case 4: WPTV_LAUNCH(64, 4); break;
+      default: WPTV_LAUNCH(64, 5); break;
+    }
+  }
+#undef WPTV_LAUNCH
+  st = launched("verify_attention_mfma");
+  if (st != WPTV_OK || p.splits == 1) return st;
+  const int threads = 256;
+  dim3 cgrid((R * (c / 4) + threads - 1) / threads, B);
+  hipLaunchKernelGGL(combine_splits<unsigned short>, cgrid, dim3(threads), 0, stream, part_o, part_lse, sink, R, H, c,
+                     rows_per_group, p.groups, p.splits, ob, lse);
+  return launched("combine_splits");
+}
+
+extern "C" int wptv_sparse_attention(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
+                                     const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
+                                     const int64_t* idx, int K, const int64_t* positions, int window,
+                                     const float* sink, int B, int T, int H, int c, int N, float scale, void* out,
+                                     float* lse, hipStream_t stream) {
+  if (!q || !k || !v || !positions || !out || (K > 0 && !idx))
+    return fail(WPTV_E_INVALID, "sparse_attention: q, k, v, positions, out (and idx when K > 0) must be given");
+  if (B <= 0 || T <= 0 || H <= 0 || c <= 0 || N <= 0 || K < 0 || window < 0)
+    return fail(WPTV_E_INVALID, "sparse_attention: bad shape B=%d T=%d H=%d c=%d N=%d K=%d window=%d", B, T, H, c,
+                N, K, window);
+  if (c > kMaxC) return fail(WPTV_E_UNSUPPORTED, "sparse_attention: head width %d above %d", c, kMaxC);
+  if (k_stride_n < c || v_stride_n < c)
+    return fail(WPTV_E_INVALID, "sparse_attention: a row stride below the head width");
+  const float scale_log2 = scale * kLog2e;
+  const int64_t* rows = K > 0 ? idx : nullptr;
+  dim3 grid(T * H, B);
+  if (dtype == WPTV_F32)
+    hipLaunchKernelGGL(attention_generic<float>, grid, dim3(64), 0, stream, (const float*)q, (const float*)k, k_stride_b,
+                       k_stride_n, (const float*)v, v_stride_b, v_stride_n, rows, K, positions, window, nullptr,
+                       nullptr, sink, T, H, c, N, scale_log2, (float*)out, lse);
+  else if (dtype == WPTV_BF16)
+    hipLaunchKernelGGL(attention_generic<unsigned short>, grid, dim3(64), 0, stream, (const unsigned short*)q,
+                       (const unsigned short*)k, k_stride_b, k_stride_n, (const unsigned short*)v, v_stride_b,
+                       v_stride_n, rows, K, positions, window, nullptr, nullptr, sink, T, H, c, N, scale_log2,
+                       (unsigned short*)out, lse);
+  else
+    return fail(WPTV_E_UNSUPPORTED, "sparse_attention: dtype %d is neither fp32 nor bf16", dtype);
+  return launched("attention_generic");
+}

@@ -1,0 +1,87 @@
+// The in-place KV append of the generation cache: each row's new entries are
+// written after its earlier ones (the scatter of the reference's
+// Reading.everything, packages/wpt-model/src/wpt_model/cache.py:110-128,
+// held[row, first[row] + j] = new[row, j] for j < counts[row]).
+//
+// One thread moves 16 bytes; rows are contiguous, so a wavefront moves
+// 1 KiB of consecutive row bytes.  HBM-bound: B * n * width * elem bytes
+// read and written.
+#include "wptv_common.h"
+
+namespace wptv {
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void kv_append_16(unsigned char* __restrict__ table, int64_t tsb, int64_t tsn,
+                                                    int64_t capacity, const unsigned char* __restrict__ rows,
+                                                    int64_t rsb, int64_t rsn, const int64_t* __restrict__ start,
+                                                    const int64_t* __restrict__ counts, int n, int row_chunks) {
+  const int b = blockIdx.y;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)n * row_chunks) return;
+  const int j = (int)(idx / row_chunks);
+  const int chunk = (int)(idx % row_chunks);
+  if (j >= counts[b]) return;
+  const int64_t dst_row = start[b] + j;
+  if (dst_row < 0 || dst_row >= capacity) return;  // never past the table
+  const u32x4* src = reinterpret_cast<const u32x4*>(rows + b * rsb + j * rsn) + chunk;
+  u32x4* dst = reinterpret_cast<u32x4*>(table + b * tsb + dst_row * tsn) + chunk;
+  *dst = *src;
+}
+
+// Byte-wise form for rows whose size or strides are not multiples of 16 bytes.
+__global__ __launch_bounds__(256) void kv_append_bytes(unsigned char* __restrict__ table, int64_t tsb, int64_t tsn,
+                                                       int64_t capacity, const unsigned char* __restrict__ rows,
+                                                       int64_t rsb, int64_t rsn, const int64_t* __restrict__ start,
+                                                       const int64_t* __restrict__ counts, int n, int row_bytes) {
+  const int b = blockIdx.y;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)n * row_bytes) return;
+  const int j = (int)(idx / row_bytes);
+  const int byte = (int)(idx % row_bytes);
+  if (j >= counts[b]) return;
+  const int64_t dst_row = start[b] + j;
+  if (dst_row < 0 || dst_row >= capacity) return;
+  table[b * tsb + dst_row * tsn + byte] = rows[b * rsb + j * rsn + byte];
+}
+
+}  // namespace
+}  // namespace wptv
+
+using namespace wptv;
+
+extern "C" int wptv_kv_append(void* table, int64_t table_stride_b, int64_t table_stride_n, int64_t capacity,
+                              const void* rows, int64_t rows_stride_b, int64_t rows_stride_n, const int64_t* start,
+                              const int64_t* counts, int B, int n, int width, int dtype, hipStream_t stream) {
+  if (!table || !rows || !start || !counts)
+    return fail(WPTV_E_INVALID, "kv_append: table, rows, start and counts must be given");
+  if (B < 0 || n < 0 || width <= 0 || capacity < 0)
+    return fail(WPTV_E_INVALID, "kv_append: bad shape B=%d n=%d width=%d capacity=%lld", B, n, width,
+                (long long)capacity);
+  if (dtype != WPTV_F32 && dtype != WPTV_BF16)
+    return fail(WPTV_E_UNSUPPORTED, "kv_append: dtype %d is neither fp32 nor bf16", dtype);
+  if (table_stride_n < width || rows_stride_n < width)
+    return fail(WPTV_E_INVALID, "kv_append: a row stride below the row width");
+  if (B == 0 || n == 0) return WPTV_OK;
+  const int64_t elem = dtype == WPTV_F32 ? 4 : 2;
+  const int64_t row_bytes = width * elem;
+  const int64_t tsb = table_stride_b * elem, tsn = table_stride_n * elem;
+  const int64_t rsb = rows_stride_b * elem, rsn = rows_stride_n * elem;
+  const bool wide = row_bytes % 16 == 0 && tsb % 16 == 0 && tsn % 16 == 0 && rsb % 16 == 0 && rsn % 16 == 0 &&
+                    aligned(table, 16) && aligned(rows, 16);
+  const int threads = 256;
+  if (wide) {
+    const int row_chunks = (int)(row_bytes / 16);
+    const int64_t total = (int64_t)n * row_chunks;
+    dim3 grid((unsigned)((total + threads - 1) / threads), B);
+    hipLaunchKernelGGL(kv_append_16, grid, dim3(threads), 0, stream, static_cast<unsigned char*>(table), tsb, tsn,
+                       capacity, static_cast<const unsigned char*>(rows), rsb, rsn, start, counts, n, row_chunks);
+    return launched("kv_append_16");
+  }
+  const int64_t total = (int64_t)n * row_bytes;
+  dim3 grid((unsigned)((total + threads - 1) / threads), B);
+  hipLaunchKernelGGL(kv_append_bytes, grid, dim3(threads), 0, stream, static_cast<unsigned char*>(table), tsb, tsn,
+                     capacity, static_cast<const unsigned char*>(rows), rsb, rsn, start, counts, n, (int)row_bytes);
+  return launched("kv_append_bytes");
+}

@@ -1,0 +1,187 @@
+"""The HIP form of the attention operations of the verify step, with the
+reference's kernel-module contract (NAME, exact_attention, sparse_attention:
+packages/wpt-model/src/wpt_model/pytorch_kernels.py:18-26, dispatched by
+kernels.py:160-184), plus the tree-masked and general forms the contract has
+no name for (verify_attention, tree_attention).
+
+Contract, as the reference states it: q (B, T, H, c) and the table's k and v
+(B, N, c) in one dtype, token p at row p, k and v possibly the strided
+halves of one (B, N, 2c) entries table; positions (B, T) int64, each query's
+position, a padding query past the table reading up to its last row; sink
+(H,) FP32; indices (B, T, K) int64, -1 for none.  Outputs are in q's dtype,
+scores and softmax in FP32.
+
+These forms are forward-only: the verify step runs under torch.no_grad
+(wpt_model.WPT.extend, model.py:456).  Their backward raises
+NotImplementedError, which the reference's kernel tests read as "not
+written yet" (test_kernels.py:149-154); so does the exact layer's top-k
+choice (top_k > 0 with rows outside the window) until it is built.
+A bad shape or dtype is ValueError; a device without the library is
+KernelUnavailable, never a fall back to another form.
+"""
+
+import torch
+
+from . import _lib
+from ._lib import KernelUnavailable, check, ptr
+
+NAME = "HIP (gfx950)"
+
+__all__ = ["NAME", "KernelUnavailable", "chosen_columns", "exact_attention", "sparse_attention", "verify_attention",
+           "tree_attention", "tree_ancestors"]
+
+
+def chosen_columns(top_k, window, N):
+    """The columns of the chosen rows for a table of N rows: top_k, or the
+    rows at least window tokens before the table's last when fewer
+    (pytorch_kernels.py:73-77)."""
+    return max(0, min(top_k, N - window))
+
+
+class _ForwardOnly(torch.autograd.Function):
+    """Carries a forward result; its backward is not written."""
+
+    @staticmethod
+    def forward(ctx, out, *inputs):
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        raise NotImplementedError("the HIP attention forms are forward-only (the verify step runs under no_grad)")
+
+
+def _forward_only(out, *inputs):
+    if torch.is_grad_enabled() and any(x is not None and x.requires_grad for x in inputs):
+        return _ForwardOnly.apply(out, *[x for x in inputs if x is not None])
+    return out
+
+
+def _check_inputs(q, k, v, positions):
+    if q.dim() != 4 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError(f"q must be (B, T, H, c) and k, v (B, N, c); got {tuple(q.shape)}, {tuple(k.shape)}, "
+                         f"{tuple(v.shape)}")
+    B, T, H, c = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[2] != c:
+        raise ValueError(f"k and v must be (B={B}, N, c={c}); got {tuple(k.shape)}, {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"q, k and v must share one dtype; got {q.dtype}, {k.dtype}, {v.dtype}")
+    if not (q.device == k.device == v.device) or q.device.type != "cuda":
+        raise KernelUnavailable(f"the HIP attention runs on a GPU; q is on {q.device}")
+    if k.stride(2) != 1 or v.stride(2) != 1:
+        raise ValueError("each row of k and v must be contiguous")
+    if tuple(positions.shape) != (B, T):
+        raise ValueError(f"positions must be (B={B}, T={T}); got {tuple(positions.shape)}")
+    if k.shape[1] == 0:
+        raise ValueError("the table is empty")
+    return B, T, H, c, k.shape[1]
+
+
+def _long(x, device):
+    return x.to(device=device, dtype=torch.long).contiguous()
+
+
+def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=None, lse=False, splits=0,
+                     generic=False):
+    """MQA attention of q (B, T, H, c) over k, v (B, N, c): query t of row b
+    sees rows max(0, p - window + 1) .. min(p, N - 1), p = positions[b, t]
+    (window 0: from row 0), and with tree = (tree_base (B,), ancestors (T,)
+    int64 bit masks) a row r >= tree_base[b] only where bit r - tree_base[b]
+    of ancestors[t] is set; sink (H,) joins each head's softmax denominator.
+    Returns the output (B, T, H, c) in q's dtype, and with lse=True also the
+    (B, T, H) FP32 log-sum-exp.  splits: key-range parts per batch row (0:
+    the library chooses); generic: the wave-per-query kernel."""
+    B, T, H, c, N = _check_inputs(q, k, v, positions)
+    device = q.device
+    library = _lib.lib()
+    dtype = _lib.dtype_code(q.dtype)
+    q_ = q.contiguous()
+    positions_ = _long(positions, device)
+    sink_ = None if sink is None else sink.to(device=device, dtype=torch.float32).contiguous()
+    if sink_ is not None and sink_.shape != (H,):
+        raise ValueError(f"sink must be (H={H},); got {tuple(sink_.shape)}")
+    tree_base = ancestors = None
+    if tree is not None:
+        tree_base, ancestors = (_long(x, device) for x in tree)
+        if tree_base.shape != (B,) or ancestors.shape != (T,):
+            raise ValueError(f"tree must be (tree_base (B={B},), ancestors (T={T},))")
+    flags = _lib.FORCE_GENERIC if generic else 0
+    parts = _lib.ctypes.c_int(int(splits))
+    size = _lib.ctypes.c_size_t(0)
+    check(library.wptv_attention_workspace(B, T, H, c, N, int(window), dtype, flags, _lib.ctypes.byref(parts),
+                                           _lib.ctypes.byref(size)), "verify_attention")
+    workspace = torch.empty(max(1, size.value), dtype=torch.uint8, device=device) if size.value else None
+    out = torch.empty_like(q_)
+    lse_out = torch.empty(B, T, H, dtype=torch.float32, device=device) if lse else None
+    check(library.wptv_verify_attention(ptr(q_), ptr(k), k.stride(0), k.stride(1), ptr(v), v.stride(0), v.stride(1),
+                                        dtype, ptr(positions_), int(window), ptr(tree_base), ptr(ancestors),
+                                        ptr(sink_), B, T, H, c, N, float(scale), parts.value, flags, ptr(out),
+                                        ptr(lse_out), ptr(workspace), size.value, _lib.stream(device)),
+          "verify_attention")
+    out = _forward_only(out, q, k, v, sink)
+    return (out, lse_out) if lse else out
+
+
+def exact_attention(q, k, v, positions, scale, top_k, window):
+    """(output (B, T, H, c), the chosen rows (B, T, K)): every query attends
+    to every row up to its position (pytorch_kernels.py:98-121,142-146).
+    K = chosen_columns(top_k, window, N); a choice (K > 0) is not built yet
+    and raises NotImplementedError."""
+    B, T, H, c, N = _check_inputs(q, k, v, positions)
+    K = chosen_columns(top_k, window, N)
+    if K:
+        raise NotImplementedError("the exact layer's top-k choice of rows is not built in the HIP form yet")
+    out = verify_attention(q, k, v, positions, scale)
+    return out, torch.full((B, T, 0), -1, dtype=torch.long, device=q.device)
+
+
+def sparse_attention(q, k, v, sink, idx, positions, scale, window):
+    """The output (B, T, H, c) of attention over each query's rows idx
+    (B, T, K) and its last window tokens, with sink (H,) added to each
+    head's denominator (pytorch_kernels.py:149-153,171-187,213-217).  A row
+    in both lists counts twice, as the reference's concatenation counts it."""
+    B, T, H, c, N = _check_inputs(q, k, v, positions)
+    if idx.dim() != 3 or tuple(idx.shape[:2]) != (B, T):
+        raise ValueError(f"idx must be (B={B}, T={T}, K); got {tuple(idx.shape)}")
+    if window <= 0:
+        raise ValueError(f"the sparse form reads a window of at least one row; got {window}")
+    if idx.shape[2] == 0:
+        return verify_attention(q, k, v, positions, scale, window=window, sink=sink)
+    device = q.device
+    library = _lib.lib()
+    dtype = _lib.dtype_code(q.dtype)
+    q_ = q.contiguous()
+    idx_ = _long(idx, device)
+    positions_ = _long(positions, device)
+    sink_ = sink.to(device=device, dtype=torch.float32).contiguous()
+    out = torch.empty_like(q_)
+    check(library.wptv_sparse_attention(ptr(q_), ptr(k), k.stride(0), k.stride(1), ptr(v), v.stride(0), v.stride(1),
+                                        dtype, ptr(idx_), idx_.shape[2], ptr(positions_), int(window), ptr(sink_), B, T,
+                                        H, c, N, float(scale), ptr(out), None, _lib.stream(device)),
+          "sparse_attention")
+    return _forward_only(out, q, k, v, sink)
+
+
+def tree_ancestors(parents):
+    """The ancestors-or-self bit masks (M,) int64 of a draft tree given each
+    node's parent (parents[0] = -1, parents[i] < i), node i's bit i."""
+    masks = []
+    for i, parent in enumerate(parents):
+        if i >= 64:
+            raise ValueError("a draft tree holds at most 64 nodes")
+        if i == 0 and parent != -1 or i > 0 and not 0 <= parent < i:
+            raise ValueError(f"node {i} has parent {parent}: parents must come before their children")
+        masks.append((masks[parent] if parent >= 0 else 0) | (1 << i))
+    # two's complement: bit 63 is the sign bit of an int64
+    return torch.tensor([m - (1 << 64) if m >= 1 << 63 else m for m in masks], dtype=torch.long)
+
+
+def tree_attention(q, k, v, tree_base, parents, scale, sink=None):
+    """Attention of the M draft-tree nodes (q (B, M, H, c), node i at table
+    row tree_base[b] + i) over the prefix rows before tree_base[b] and over
+    the node's ancestors and itself: the reference's dense_attention
+    (attention.py:74-82) with the mask "prefix plus ancestors-or-self"."""
+    B, M = q.shape[:2]
+    base = tree_base.to(device=q.device, dtype=torch.long)
+    positions = base[:, None] + torch.arange(M, device=q.device)
+    masks = tree_ancestors(parents).to(q.device)
+    return verify_attention(q, k, v, positions, scale, sink=sink, tree=(base, masks))
