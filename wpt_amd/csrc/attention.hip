@@ -68,17 +68,16 @@ __device__ __forceinline__ bool tree_visible(int n, int64_t tbase, uint64_t anc)
 // MFMA kernel
 // ---------------------------------------------------------------------------
 
-template <int C, int MBW, int NS>
-struct MfmaShape {
-  static constexpr int kRows = 16 * MBW;         // query rows per workgroup
-  static constexpr int kSteps = C / 32;          // k-steps of the QK^T product
-  static constexpr int kCBlocks = C / 16;        // 16-wide column blocks of O
-  static constexpr int kChunks = C / 8;          // 16-byte chunks per key/value row
-  static constexpr int kBlock = 16 * C;          // one 16-row block of K or V (bf16 elements)
-  static constexpr int kLoads = kBlock * 2 / 1024;  // 1 KiB LDS-DMA loads per block
-  static constexpr int kStage = 2 * kBlock;      // K block then V block
-  static constexpr int kStages = NS;             // blocks in flight per wavefront
-  static constexpr int kLdsElems = kWaves * NS * kStage;
+template <int C>
+struct Geo {
+  static constexpr int kSteps = C / 32;             // k-steps of the QK^T product (16x16x32)
+  static constexpr int kCBlocks = C / 16;           // 16-wide column blocks of O
+  static constexpr int kBlock = 16 * C;             // one 16-row block of K or V (bf16 elements)
+  static constexpr int kLoads = kBlock * 2 / 1024;  // 1 KiB DMA instructions per block
+  static constexpr int kStage = 2 * kBlock;         // K block then V block
+  static constexpr int kSlots = C == 128 ? 4 : 8;   // 16-row stages per wavefront (32 KiB)
+  static constexpr int kAhead = kSlots / 2 - 1;     // 32-row pairs in flight while one is computed
+  static constexpr int kLdsElems = kWaves * kSlots * kStage;
 };
 
 // Softmax rescaling is deferred until a row's maximum grows by more than this
@@ -94,40 +93,91 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("" ::: "memory");
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-// A raw buffer resource over `bytes` bytes from `base` (gfx9 dword3 format).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+// A raw buffer resource over 4 GiB from `base` (gfx9 dword3 format).
+__device__ __forceinline__ i32x4 buffer_resource(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = static_cast<int>(static_cast<uint32_t>(a));
+  r[1] = static_cast<int>(static_cast<uint32_t>(a >> 32));  // stride 0
+  r[2] = -1;
+  r[3] = 0x00020000;
+  return r;
 }
 
-template <int C, int MBW, int NS, bool TREE>
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
+// Global -> LDS copy of 16 bytes per lane: lane l's bytes land at LDS byte
+// address `lds` + 16 l.  Written as inline assembly so that the compiler's
+// conservative wait (all loads, before any LDS read of the kernel) is not
+// inserted: the kernel waits for each stage itself with wait_vmcnt.  The
+// s_nop covers the M0-write -> LDS-DMA hazard.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_16B(i32x4 rsrc, uint32_t voffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ bf16x8 pack_bf16x8(const float (&p)[8]) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = static_cast<__bf16>(p[e]);
+  return r;
+}
+
+template <int C, int MBW, bool TREE>
 __global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
     const unsigned short* __restrict__ q, const unsigned short* __restrict__ k, int64_t ksb, int64_t ksn,
     const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn, const int64_t* __restrict__ positions,
     int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
-    const float* __restrict__ sink, int T, int H, int N, float scale_log2, int splits, int range_from_positions,
-    unsigned short* __restrict__ out, float* __restrict__ lse_out, float* __restrict__ part_o,
-    float* __restrict__ part_lse) {
-  using S = MfmaShape<C, MBW, NS>;
-  static_assert(S::kRows * C * 4 <= S::kLdsElems * 2, "the merge buffer reuses the stages");
-  static_assert(S::kLoads * 64 % S::kChunks == 0 && 64 % S::kChunks == 0, "rows per DMA load");
-  __shared__ __attribute__((aligned(16))) unsigned short lds[S::kLdsElems];
-  __shared__ float sm_m[kWaves][S::kRows];
-  __shared__ float sm_l[kWaves][S::kRows];
-  __shared__ float fin_scale[S::kRows];
-  __shared__ float fin_lse[S::kRows];
+    const float* __restrict__ sink, int T, int H, int N, float scale_log2, int groups, int splits,
+    int range_from_positions, int xcd_map, unsigned short* __restrict__ out, float* __restrict__ lse_out,
+    float* __restrict__ part_o, float* __restrict__ part_lse) {
+  using G = Geo<C>;
+  constexpr int kRows = 16 * MBW;  // query rows per workgroup
+  static_assert(kRows * C * 4 <= G::kLdsElems * 2, "the merge buffer reuses the stages");
+  static_assert(64 % (C / 8) == 0, "rows per DMA instruction");
+  __shared__ __attribute__((aligned(16))) unsigned short lds[G::kLdsElems];
+  __shared__ __attribute__((aligned(16))) unsigned short qlds[kRows * C];
+  __shared__ float sm_m[kWaves][kRows];
+  __shared__ float sm_l[kWaves][kRows];
+  __shared__ float fin_scale[kRows];
+  __shared__ float fin_lse[kRows];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15;  // this lane's column: query row (S^T, O^T) or key row (K operand)
   const int g = lane >> 4;  // lane group 0..3
-  const int split = blockIdx.x;
-  const int grp = blockIdx.y;
-  const int b = blockIdx.z;
+
+  // Workgroup -> (batch row, row group, split).  With xcd_map the splits of
+  // one (batch row, row group) unit share an XCD (workgroups are dispatched
+  // round-robin over the 8 XCDs), so its queries and parts stay in one L2.
+  int unit, split;
+  {
+    const int L = blockIdx.x;
+    if (xcd_map) {
+      const int kk = L >> 3;
+      unit = (L & 7) + 8 * (kk / splits);
+      split = kk % splits;
+    } else {
+      unit = L / splits;
+      split = L % splits;
+    }
+  }
+  const int b = unit / groups;
+  const int grp = unit % groups;
   const int R = T * H;
-  const int r_base = grp * S::kRows;
+  const int r_base = grp * kRows;
   const int64_t* pos_b = positions + (int64_t)b * T;
+  const int t_first = r_base / H;
+  const int t_last = ((r_base + kRows < R ? r_base + kRows : R) - 1) / H;
 
   // The key rows this workgroup's queries can see.  Full causal attention of
   // one query group reads the whole table, whatever the positions say, so the
@@ -136,8 +186,6 @@ __global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
   if (range_from_positions) {
     u_lo = INT_MAX;
     u_hi = -1;
-    const int t_first = r_base / H;
-    const int t_last = ((r_base + S::kRows < R ? r_base + S::kRows : R) - 1) / H;
     for (int t = t_first; t <= t_last; ++t) {
       const Bounds bt = query_bounds(pos_b, t, window, N);
       if (bt.hi >= bt.lo) {
@@ -150,61 +198,61 @@ __global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
   if (u_hi >= u_lo) {
     const int U = u_hi - u_lo + 1;
     int per = (U + splits - 1) / splits;
-    per = (per + 16 * kWaves - 1) / (16 * kWaves) * (16 * kWaves);
+    per = (per + 32 * kWaves - 1) / (32 * kWaves) * (32 * kWaves);
     s_lo = u_lo + split * per;
     s_hi = min(s_lo + per - 1, u_hi);
   }
   const int nblocks = s_hi >= s_lo ? (s_hi - s_lo + 1 + 15) / 16 : 0;
-  const int mine = nblocks > wave ? (nblocks - wave + kWaves - 1) / kWaves : 0;  // blocks of this wavefront
+  const int npairs = (nblocks + 1) / 2;
+  const int mine = npairs > wave ? (npairs - wave + kWaves - 1) / kWaves : 0;  // pairs of this wavefront
 
-  unsigned short* ring = lds + wave * NS * S::kStage;
   // Byte offsets within one batch row's keys and values fit 32 bits: the
   // host checks that N rows of the table do.
-  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(k + (int64_t)b * ksb, 0xFFFFFFFFu);
-  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(v + (int64_t)b * vsb, 0xFFFFFFFFu);
+  const i32x4 krs = buffer_resource(k + (int64_t)b * ksb);
+  const i32x4 vrs = buffer_resource(v + (int64_t)b * vsb);
   const uint32_t krow_bytes = (uint32_t)ksn * 2u, vrow_bytes = (uint32_t)vsn * 2u;
+  unsigned short* const ring = lds + wave * G::kSlots * G::kStage;
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_address(ring));
+
   // LDS layout of a 16-row block, chunk-major: the 16-byte chunk x (columns
-  // 8x..8x+7) of row r sits at unit 16x + r.  Lane l of DMA load i fills
-  // unit 64i + l, i.e. chunk 4i + (l >> 4) of row l & 15, so each load reads
-  // 64 contiguous bytes of 16 rows and every MFMA operand read below is a
-  // per-lane base plus a constant offset.
+  // 8x..8x+7) of row r sits at unit 16x + r.  Lane l of DMA instruction i
+  // fills unit 64i + l, i.e. chunk 4i + (l >> 4) of row l & 15, so every MFMA
+  // operand read below is a per-lane base plus a constant offset.  Pair p of
+  // this wavefront (32 rows) fills slots 2p, 2p + 1 (mod kSlots).
   auto issue = [&](int it) {
-    const int blk = wave + it * kWaves;
-    unsigned short* st = ring + (it % NS) * S::kStage;
-    int n = s_lo + blk * 16 + j;
-    n = n < s_hi ? n : s_hi;  // rows past the split are masked; read a valid one
-    const uint32_t koff = (uint32_t)n * krow_bytes + 16u * g;
-    const uint32_t voff = (uint32_t)n * vrow_bytes + 16u * g;
+    const int pair = wave + it * kWaves;
+    const uint32_t slot0 = ring_lds + (uint32_t)((2 * it) % G::kSlots) * (G::kStage * 2);
 #pragma unroll
-    for (int i = 0; i < S::kLoads; ++i) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(st + 512 * i), 16, koff + 64u * i, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(st + S::kBlock + 512 * i), 16, voff + 64u * i, 0, 0,
-                                               0);
+    for (int h = 0; h < 2; ++h) {
+      int n = s_lo + (2 * pair + h) * 16 + j;
+      n = n < s_hi ? n : s_hi;  // rows past the split are masked; read a valid one
+      const uint32_t koff = (uint32_t)n * krow_bytes + 16u * g;
+      const uint32_t voff = (uint32_t)n * vrow_bytes + 16u * g;
+      const uint32_t st = slot0 + h * (G::kStage * 2);
+#pragma unroll
+      for (int i = 0; i < G::kLoads; ++i) {
+        dma_16B(krs, koff + 64u * i, st + 1024u * i);
+        dma_16B(vrs, voff + 64u * i, st + G::kBlock * 2 + 1024u * i);
+      }
     }
   };
-  asm volatile("" ::: "memory");
 #pragma unroll
-  for (int it = 0; it < NS - 1; ++it)
+  for (int it = 0; it < G::kAhead; ++it)
     if (it < mine) issue(it);
 
   // Workgroup-uniform bounds: the rows every query of the group sees.
   int f_lo = 0, f_hi = INT_MAX;
-  {
-    const int t_first = r_base / H;
-    const int t_last = ((r_base + S::kRows < R ? r_base + S::kRows : R) - 1) / H;
-    for (int t = t_first; t <= t_last; ++t) {
-      const Bounds bt = query_bounds(pos_b, t, window, N);
-      f_lo = max(f_lo, bt.lo);
-      f_hi = min(f_hi, bt.hi);
-    }
+  for (int t = t_first; t <= t_last; ++t) {
+    const Bounds bt = query_bounds(pos_b, t, window, N);
+    f_lo = max(f_lo, bt.lo);
+    f_hi = min(f_hi, bt.hi);
   }
   const int64_t tbase = TREE ? tree_base[b] : (int64_t)INT_MAX;
   if (TREE && tbase <= (int64_t)f_hi) f_hi = (int)tbase - 1;
 
-  // Per-lane query rows (one per m-block): bounds and the Q^T operand.
+  // Per-lane query rows (one per m-block) and their bounds.
   int lo[MBW], hi[MBW];
   uint64_t anc[TREE ? MBW : 1];
-  bf16x8 qf[MBW][S::kSteps];
 #pragma unroll
   for (int mb = 0; mb < MBW; ++mb) {
     const int r = r_base + 16 * mb + j;
@@ -212,123 +260,154 @@ __global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
       const int t = r / H;
       const Bounds bt = query_bounds(pos_b, t, window, N);
       lo[mb] = bt.lo;
-      hi[mb] = bt.hi;
+      hi[mb] = min(bt.hi, s_hi);
       if constexpr (TREE) anc[mb] = ancestors[t];
-      const unsigned short* qrow = q + ((int64_t)b * R + r) * C;
-#pragma unroll
-      for (int s = 0; s < S::kSteps; ++s) qf[mb][s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g);
     } else {
       lo[mb] = 0;
       hi[mb] = -1;
       if constexpr (TREE) anc[mb] = 0;
-#pragma unroll
-      for (int s = 0; s < S::kSteps; ++s) {
-        const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-        qf[mb][s] = __builtin_bit_cast(bf16x8, z);
-      }
     }
   }
+  // The group's queries in LDS, each 16-row m-block laid out like a key
+  // block (chunk-major), zeros past the last row: the Q^T operand of m-block
+  // mb at k-step s is then one conflict-free 16-byte read per lane.
+  for (int u = threadIdx.x; u < kRows * (C / 8); u += kThreads) {
+    const int mb = u / (16 * (C / 8));
+    const int rest = u % (16 * (C / 8));
+    const int x = rest / 16, rr = rest % 16;  // chunk, row within the m-block
+    const int r = r_base + 16 * mb + rr;
+    u16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (r < R) val = *reinterpret_cast<const u16x8*>(q + ((int64_t)b * R + r) * C + 8 * x);
+    *reinterpret_cast<u16x8*>(qlds + u * 8) = val;
+  }
+  __syncthreads();
 
-  f32x4 o[MBW][S::kCBlocks];
+  f32x4 o[MBW][G::kCBlocks];
   float m_run[MBW], l_run[MBW];
 #pragma unroll
   for (int mb = 0; mb < MBW; ++mb) {
     m_run[mb] = kNegInf;
     l_run[mb] = 0.f;
 #pragma unroll
-    for (int cb = 0; cb < S::kCBlocks; ++cb) o[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int cb = 0; cb < G::kCBlocks; ++cb) o[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-#pragma unroll 1
-  for (int it = 0; it < mine; ++it) {
-    // Refill the stage freed by the previous block, then wait for this one.
-    asm volatile("" ::: "memory");
-    if (it + NS - 1 < mine) {
-      issue(it + NS - 1);
-      wait_vmcnt<2 * S::kLoads * (NS - 1)>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    const unsigned short* st = ring + (it % NS) * S::kStage;
-    const int n0 = s_lo + (wave + it * kWaves) * 16;
-
+  // One pair: scores of 32 key rows for every query row of the group.
+  float x[MBW][8];
+  float bm[MBW];
+  auto scores = [&](int it) {
+    const unsigned short* st0 = ring + ((2 * it) % G::kSlots) * G::kStage;
+    const unsigned short* st1 = st0 + G::kStage;
+    const int n0 = s_lo + (wave + it * kWaves) * 32;
     // S^T = K . Q^T: lane (j, g) reads key row j, chunk 4s + g (unit 64s + lane).
-    f32x4 sacc[MBW];
+    f32x4 sacc[2][MBW];
 #pragma unroll
-    for (int mb = 0; mb < MBW; ++mb) sacc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < MBW; ++mb) sacc[0][mb] = sacc[1][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < S::kSteps; ++s) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(st + 512 * s + 8 * lane);
+    for (int s = 0; s < G::kSteps; ++s) {
+      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(st0 + 512 * s + 8 * lane);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(st1 + 512 * s + 8 * lane);
 #pragma unroll
-      for (int mb = 0; mb < MBW; ++mb)
-        sacc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[mb][s], sacc[mb], 0, 0, 0);
+      for (int mb = 0; mb < MBW; ++mb) {
+        const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qlds + mb * 16 * C + 512 * s + 8 * lane);
+        sacc[0][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qv, sacc[0][mb], 0, 0, 0);
+        sacc[1][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qv, sacc[1][mb], 0, 0, 0);
+      }
     }
-
-    // Mask, online softmax (deferred rescaling), P^T operand.
-    const bool full = n0 >= f_lo && n0 + 15 <= f_hi && n0 + 15 <= s_hi;
-    float x[MBW][4];
-    float bm[MBW];
-    bool grow = false;
+    const bool full = n0 >= f_lo && n0 + 31 <= f_hi && n0 + 31 <= s_hi;
 #pragma unroll
     for (int mb = 0; mb < MBW; ++mb) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[mb][i] = sacc[mb][i] * scale_log2;
-      if (!full) {
-        const int top = min(hi[mb], s_hi);
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int n = n0 + 4 * g + i;
-          bool vis = n >= lo[mb] && n <= top;
-          if constexpr (TREE) vis = vis && tree_visible(n, tbase, anc[mb]);
-          x[mb][i] = vis ? x[mb][i] : kNegInf;
-        }
+        for (int i = 0; i < 4; ++i) x[mb][4 * h + i] = sacc[h][mb][i] * scale_log2;
+      if (!full) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int n = n0 + 16 * h + 4 * g + i;
+            bool vis = n >= lo[mb] && n <= hi[mb];
+            if constexpr (TREE) vis = vis && tree_visible(n, tbase, anc[mb]);
+            x[mb][4 * h + i] = vis ? x[mb][4 * h + i] : kNegInf;
+          }
       }
-      float t = fmaxf(fmaxf(x[mb][0], x[mb][1]), fmaxf(x[mb][2], x[mb][3]));
+      float t = fmaxf(fmaxf(fmaxf(x[mb][0], x[mb][1]), fmaxf(x[mb][2], x[mb][3])),
+                      fmaxf(fmaxf(x[mb][4], x[mb][5]), fmaxf(x[mb][6], x[mb][7])));
       t = fmaxf(t, __shfl_xor(t, 16, 64));
       t = fmaxf(t, __shfl_xor(t, 32, 64));
       bm[mb] = t;
-      grow = grow || (t > m_run[mb] + kRescale);
     }
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-#pragma unroll
-      for (int mb = 0; mb < MBW; ++mb) {
-        const float m_new = fmaxf(m_run[mb], bm[mb]);
-        const float alpha = (m_new == kNegInf) ? 1.f : exp2f(m_run[mb] - m_new);
-        m_run[mb] = m_new;
-        l_run[mb] *= alpha;
-#pragma unroll
-        for (int cb = 0; cb < S::kCBlocks; ++cb) {
-          o[mb][cb] *= alpha;
-          __builtin_amdgcn_sched_barrier(0);  // one accumulator at a time through the VALU
-        }
-      }
-    }
-    s16x4 pt[MBW];
+  };
+  // The probabilities of the pair against the running maxima, and O^T += V^T . P^T.
+  auto accumulate = [&](int it) {
+    const unsigned short* st0 = ring + ((2 * it) % G::kSlots) * G::kStage;
+    bf16x8 pt[MBW];
 #pragma unroll
     for (int mb = 0; mb < MBW; ++mb) {
-      float p[4];
+      float p[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = (m_run[mb] == kNegInf) ? 0.f : exp2f(x[mb][i] - m_run[mb]);
-      l_run[mb] += (p[0] + p[1]) + (p[2] + p[3]);
-      pt[mb] = s16x4{(short)f32_to_bf16(p[0]), (short)f32_to_bf16(p[1]), (short)f32_to_bf16(p[2]),
-                     (short)f32_to_bf16(p[3])};
+      for (int e = 0; e < 8; ++e) p[e] = (m_run[mb] == kNegInf) ? 0.f : exp2f(x[mb][e] - m_run[mb]);
+      l_run[mb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+      pt[mb] = pack_bf16x8(p);
     }
+    // P^T operand: lane (j, g) holds k-index 8g + e = key 4g + e (e < 4) of
+    // the first 16 rows, key 16 + 4g + e - 4 of the second.  V^T operand:
+    // the same keys at column cb*16 + j: chunk 2cb + (j >> 3), units
+    // 16 (2cb + (j >> 3)) + 4g + i of each stage.
+    const unsigned short* vs = st0 + G::kBlock + 128 * (j >> 3) + 32 * g + (j & 7);
+#pragma unroll
+    for (int cb = 0; cb < G::kCBlocks; ++cb) {
+      const unsigned short* w = vs + 256 * cb;
+      const u16x8 vt = u16x8{w[0], w[8], w[16], w[24], w[G::kStage], w[G::kStage + 8], w[G::kStage + 16],
+                             w[G::kStage + 24]};
+      const bf16x8 vb = __builtin_bit_cast(bf16x8, vt);
+#pragma unroll
+      for (int mb = 0; mb < MBW; ++mb) o[mb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vb, pt[mb], o[mb][cb], 0, 0, 0);
+    }
+  };
 
-    // O^T += V^T . P^T: lane (j, g) gathers column cb*16 + j of value rows
-    // 4g..4g+3: chunk 2cb + (j >> 3), units 16 (2cb + (j >> 3)) + 4g + i.
-    const unsigned short* vs = st + S::kBlock + 128 * (j >> 3) + 32 * g + (j & 7);
+  int it = 0;
+  while (it < mine) {
+    // Fast loop: the accumulators are touched by MFMAs only.
+    bool grown = false;
+#pragma unroll 1
+    for (; it < mine; ++it) {
+      asm volatile("" ::: "memory");
+      if (it + G::kAhead < mine) {
+        issue(it + G::kAhead);
+        wait_vmcnt<4 * G::kLoads * G::kAhead>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      scores(it);
+      bool grow = false;
 #pragma unroll
-    for (int cb = 0; cb < S::kCBlocks; ++cb) {
-      const s16x4 vt = s16x4{(short)vs[256 * cb], (short)vs[256 * cb + 8], (short)vs[256 * cb + 16],
-                             (short)vs[256 * cb + 24]};
-#pragma unroll
-      for (int mb = 0; mb < MBW; ++mb)
-        o[mb][cb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, pt[mb], o[mb][cb], 0, 0, 0);
+      for (int mb = 0; mb < MBW; ++mb) grow = grow || (bm[mb] > m_run[mb] + kRescale);
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        grown = true;
+        break;
+      }
+      accumulate(it);
     }
+    if (!grown) break;
+    // A row's maximum grew: rescale its sums to the new maximum, then finish the pair.
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb) {
+      const float m_new = fmaxf(m_run[mb], bm[mb]);
+      const float alpha = (m_new == kNegInf || m_run[mb] == kNegInf) ? 0.f : exp2f(m_run[mb] - m_new);
+      m_run[mb] = m_new;
+      l_run[mb] *= alpha;
+#pragma unroll
+      for (int cb = 0; cb < G::kCBlocks; ++cb) o[mb][cb] *= alpha;
+    }
+    accumulate(it);
+    ++it;
   }
   wait_vmcnt<0>();
 
   // ---- merge the four wavefronts (the merge buffer reuses the stages) ----
+  __syncthreads();
 #pragma unroll
   for (int mb = 0; mb < MBW; ++mb) {
     l_run[mb] += __shfl_xor(l_run[mb], 16, 64);
@@ -353,7 +432,7 @@ __global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
 #pragma unroll
       for (int mb = 0; mb < MBW; ++mb) {
 #pragma unroll
-        for (int cb = 0; cb < S::kCBlocks; ++cb) {
+        for (int cb = 0; cb < G::kCBlocks; ++cb) {
           f32x4* dst = reinterpret_cast<f32x4*>(obuf + (mb * 16 + j) * C + cb * 16 + 4 * g);
           const f32x4 val = o[mb][cb] * wscale[mb];
           if (w == 0)
@@ -368,7 +447,7 @@ __global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
 
   // Final statistics per query row (the sink joins the denominator when the
   // split is the whole range), then the output or this split's part.
-  if (threadIdx.x < S::kRows) {
+  if (threadIdx.x < kRows) {
     const int rr = threadIdx.x;
     float M = kNegInf;
     for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][rr]);
@@ -389,7 +468,7 @@ __global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
   }
   __syncthreads();
 
-  const int rows_here = min(S::kRows, R - r_base);
+  const int rows_here = min(kRows, R - r_base);
   constexpr int kVec = 4;
   for (int idx = threadIdx.x; idx < rows_here * (C / kVec); idx += kThreads) {
     const int rr = idx / (C / kVec);
@@ -402,7 +481,7 @@ __global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
           u16x4{f32_to_bf16(val[0]), f32_to_bf16(val[1]), f32_to_bf16(val[2]), f32_to_bf16(val[3])};
       if (lse_out && c4 == 0) lse_out[(int64_t)b * R + r] = fin_lse[rr] * kLn2;
     } else {
-      const int64_t prow = (((int64_t)b * gridDim.y + grp) * splits + split) * S::kRows + rr;
+      const int64_t prow = ((int64_t)unit * splits + split) * kRows + rr;
       *reinterpret_cast<f32x4*>(part_o + prow * C + c4) = val;
       if (c4 == 0) part_lse[prow] = fin_lse[rr];
     }
@@ -410,35 +489,54 @@ __global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
 }
 
 // Merges the splits of each query row: fixed order, log-sum-exp weights,
-// the sink joining the denominator.
+// the sink joining the denominator.  One thread per (batch row, query row,
+// 4 columns); the parts of one row are read with independent loads.
 template <typename OutT>
 __global__ __launch_bounds__(256) void combine_splits(const float* __restrict__ part_o,
                                                        const float* __restrict__ part_lse,
-                                                       const float* __restrict__ sink, int R, int H, int C,
+                                                       const float* __restrict__ sink, int B, int R, int H, int C,
                                                        int rows_per_group, int groups, int splits,
                                                        OutT* __restrict__ out, float* __restrict__ lse_out) {
-  const int b = blockIdx.y;
   const int per_row = C / 4;
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= R * per_row) return;
-  const int r = idx / per_row;
-  const int c4 = (idx % per_row) * 4;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)B * R * per_row) return;
+  const int b = (int)(idx / ((int64_t)R * per_row));
+  const int rem = (int)(idx % ((int64_t)R * per_row));
+  const int r = rem / per_row;
+  const int c4 = (rem % per_row) * 4;
   const int grp = r / rows_per_group, rr = r % rows_per_group;
-  const int64_t base = ((int64_t)b * groups + grp) * splits;
+  const int64_t row0 = ((int64_t)(b * groups + grp) * splits) * rows_per_group + rr;  // split 0's part
+  constexpr int kUnroll = 8;
   float M = kNegInf;
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, part_lse[(base + s) * rows_per_group + rr]);
+  for (int s0 = 0; s0 < splits; s0 += kUnroll) {
+    float ls[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) ls[u] = s0 + u < splits ? part_lse[row0 + (int64_t)(s0 + u) * rows_per_group] : kNegInf;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) M = fmaxf(M, ls[u]);
+  }
   const float sl = sink ? sink[r % H] * kLog2e : kNegInf;
   const float M2 = fmaxf(M, sl);
   float L = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   if (M2 != kNegInf) {
-    for (int s = 0; s < splits; ++s) {
-      const int64_t prow = (base + s) * rows_per_group + rr;
-      const float ls = part_lse[prow];
-      if (ls == kNegInf) continue;
-      const float w = exp2f(ls - M2);
-      L += w;
-      acc += w * *reinterpret_cast<const f32x4*>(part_o + prow * C + c4);
+    for (int s0 = 0; s0 < splits; s0 += kUnroll) {
+      float ls[kUnroll];
+      f32x4 po[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t prow = row0 + (int64_t)(s0 + u) * rows_per_group;
+        const bool in = s0 + u < splits;
+        ls[u] = in ? part_lse[prow] : kNegInf;
+        po[u] = in ? *reinterpret_cast<const f32x4*>(part_o + prow * C + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (ls[u] == kNegInf) continue;
+        const float w = exp2f(ls[u] - M2);
+        L += w;
+        acc += w * po[u];
+      }
     }
     if (sink) L += exp2f(sl - M2);
   }
@@ -594,9 +692,9 @@ int plan(int B, int T, int H, int c, int N, int window, int dtype, int flags, in
   if (splits <= 0) {
     const long long cus = compute_units();
     const long long wgs = (long long)B * p.groups;
-    // Enough workgroups to fill the GPU, each at least 64 key rows.
+    // Enough workgroups to fill the GPU, each at least 32 key rows per wavefront.
     long long s = (cus + wgs - 1) / wgs;
-    const long long max_s = (span + 63) / 64;
+    const long long max_s = (span + 32 * kWaves - 1) / (32 * kWaves);
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
     splits = (int)s;
@@ -613,19 +711,15 @@ int plan(int B, int T, int H, int c, int N, int window, int dtype, int flags, in
   return WPTV_OK;
 }
 
-// Blocks in flight per wavefront: 4 x 8 KiB for head width 128, 6 x 4 KiB for 64.
-template <int C>
-constexpr int stages() { return C == 128 ? 4 : 6; }
-
 template <int C, int MBW, bool TREE>
 void launch_mfma(dim3 grid, hipStream_t stream, const unsigned short* q, const unsigned short* k, int64_t ksb,
                  int64_t ksn, const unsigned short* v, int64_t vsb, int64_t vsn, const int64_t* positions,
                  int window, const int64_t* tree_base, const uint64_t* ancestors, const float* sink, int T, int H,
-                 int N, float scale_log2, int splits, int range_from_positions, unsigned short* out, float* lse,
-                 float* part_o, float* part_lse) {
-  hipLaunchKernelGGL((verify_attention_mfma<C, MBW, stages<C>(), TREE>), grid, dim3(kThreads), 0, stream, q, k, ksb, ksn,
-                     v, vsb, vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, splits,
-                     range_from_positions, out, lse, part_o, part_lse);
+                 int N, float scale_log2, int groups, int splits, int range_from_positions, int xcd_map,
+                 unsigned short* out, float* lse, float* part_o, float* part_lse) {
+  hipLaunchKernelGGL((verify_attention_mfma<C, MBW, TREE>), grid, dim3(kThreads), 0, stream, q, k, ksb, ksn, v, vsb,
+                     vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, groups, splits,
+                     range_from_positions, xcd_map, out, lse, part_o, part_lse);
 }
 
 }  // namespace
@@ -692,7 +786,9 @@ extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_str
     part_o = static_cast<float*>(workspace);
     part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(rows * c * sizeof(float), 256));
   }
-  dim3 grid(p.splits, p.groups, B);
+  const int units = B * p.groups;
+  dim3 grid(units * p.splits);
+  const int xcd_map = units % 8 == 0 ? 1 : 0;
   // Full causal attention of a single query group reads the whole table; any
   // other case takes its key range from the positions.
   const int from_positions = (window > 0 || p.groups > 1) ? 1 : 0;
@@ -700,10 +796,11 @@ extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_str
   const auto* kb = static_cast<const unsigned short*>(k);
   const auto* vb = static_cast<const unsigned short*>(v);
   auto* ob = static_cast<unsigned short*>(out);
-#define WPTV_LAUNCH(CC, MM)                                                                                    \
-  (tree_base ? launch_mfma<CC, MM, true> : launch_mfma<CC, MM, false>)(grid, stream, qb, kb, k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, positions,     \
-                      window, tree_base, tree_ancestors, sink, T, H, N, scale_log2, p.splits, from_positions, ob, \
-                      lse, part_o, part_lse)
+#define WPTV_LAUNCH(CC, MM)                                                                                     \
+  (tree_base ? launch_mfma<CC, MM, true> : launch_mfma<CC, MM, false>)(                                         \
+      grid, stream, qb, kb, k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, positions, window, tree_base,   \
+      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_map, ob, lse, part_o, \
+      part_lse)
   if (c == 128) {
     switch (p.mbw) {
       case 1: WPTV_LAUNCH(128, 1); break;
@@ -725,8 +822,9 @@ extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_str
   st = launched("verify_attention_mfma");
   if (st != WPTV_OK || p.splits == 1) return st;
   const int threads = 256;
-  dim3 cgrid((R * (c / 4) + threads - 1) / threads, B);
-  hipLaunchKernelGGL(combine_splits<unsigned short>, cgrid, dim3(threads), 0, stream, part_o, part_lse, sink, R, H, c,
+  const long long items = (long long)B * R * (c / 4);
+  dim3 cgrid((unsigned)((items + threads - 1) / threads));
+  hipLaunchKernelGGL(combine_splits<unsigned short>, cgrid, dim3(threads), 0, stream, part_o, part_lse, sink, B, R, H, c,
                      rows_per_group, p.groups, p.splits, ob, lse);
   return launched("combine_splits");
 }
