@@ -116,6 +116,64 @@ int wptv_kv_append(void* table, int64_t table_stride_b, int64_t table_stride_n, 
                    const int64_t* start, const int64_t* counts, int B, int n, int width, int dtype,
                    hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Acceptance: the reference's per-row verification loop of
+ * Writer._speculate (packages/wpt-inference/src/wpt_inference/__init__.py:
+ * 210-229) with its sampling distribution Writer._probabilities (:173-179),
+ * fused over the vocabulary for every row at once.
+ *
+ *   scores   position j (0..L) of row b at scores + b*scores_stride_b +
+ *            (firsts[b] + j)*scores_stride_t, V contiguous fp32: the model's
+ *            scores at the pending token and at each draft (the reference's
+ *            scores[i, firsts:firsts + L + 1], :210-212)
+ *   firsts   NULL (0 for every row) or [B] int32
+ *   q        draft distributions, position j (0..L-1) of row b at
+ *            q + b*q_stride_b + j*q_stride_t, V contiguous fp32
+ *   drafts   [B, L] int64 (row stride drafts_stride_b)
+ *   lengths  NULL (every row verifies L drafts) or [B] int32 <= L
+ *   u        [B, L] fp32 uniforms in [0, 1): draft j of row b is kept iff
+ *            u[b, j] * q[b, j, draft] < p[j, draft]
+ *   e        [B, V] fp32 Exp(1) draws: the replacement or bonus token is
+ *            argmax_v w_v / e[b, v], w the distribution it is drawn from
+ *            (the reference's multinomial draw of one token)
+ *   temperature, top_k  the reference's (top_k <= 0 or >= V: no cut)
+ *   greedy   1: greedy verification instead (q, u, e unused and may be
+ *            NULL): a draft is kept iff it is the first maximal index of its
+ *            position's scores, and the replacement or bonus is that index
+ *   tokens   [B, L + 1] int64 out: the kept drafts, then the drawn token;
+ *            entries past n_tokens[b] are -1
+ *   n_tokens [B] int32 out: kept drafts + 1; -1 for a row whose residual
+ *            distribution max(0, p - q) has no mass (the reference raises)
+ *   workspace  wptv_accept_workspace(B, L) bytes
+ * Rows and positions are independent; the vocabulary may hold up to 65536
+ * entries.
+ * ------------------------------------------------------------------------- */
+int wptv_accept_workspace(int B, int L, size_t* bytes);
+
+int wptv_accept(const float* scores, int64_t scores_stride_b, int64_t scores_stride_t, const int32_t* firsts,
+                const float* q, int64_t q_stride_b, int64_t q_stride_t, const int64_t* drafts,
+                int64_t drafts_stride_b, const int32_t* lengths, const float* u, const float* e, float temperature,
+                int top_k, int greedy, int B, int L, int V, int64_t* tokens, int32_t* n_tokens, void* workspace,
+                size_t workspace_bytes, hipStream_t stream);
+
+/* Greedy verification of a draft tree of M nodes per row (node 0 the root,
+ * the token already written; parents[i] < i, parents[0] = -1): from the root,
+ * move to the child whose token equals the argmax (first maximal index) of
+ * the current node's scores, the lowest node index among equal children,
+ * until none does; then the argmax.  Scores position i = node i (row stride
+ * scores_stride_b, node stride scores_stride_t, V contiguous fp32);
+ * node_tokens [B, M] int64; parents [M] int32.
+ *   path     [B, M + 1] int64 out: the accepted node indices from the root
+ *            (the root included), -1 after
+ *   tokens   [B, M + 1] int64 out: the accepted nodes' tokens after the
+ *            root, then the argmax; -1 after
+ *   n_tokens [B] int32 out: accepted nodes after the root + 1
+ *   workspace  wptv_accept_workspace(B, M - 1) bytes */
+int wptv_greedy_tree(const float* scores, int64_t scores_stride_b, int64_t scores_stride_t,
+                     const int64_t* node_tokens, const int32_t* parents, int B, int M, int V, int64_t* path,
+                     int64_t* tokens, int32_t* n_tokens, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

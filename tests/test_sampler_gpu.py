@@ -1,0 +1,172 @@
+"""The HIP acceptance step against the oracle, on the GPU, through the C ABI
+(wpt_amd.sampling calls libwptv.so).  Decisions are compared bit-exactly on
+identical scores and tapes; a decision whose two sides u*q and p lie within
+1e-5 (relative) of each other may differ by the last bits of the softmax, so
+such rows are counted and left out (none occur at these seeds)."""
+
+import pytest
+import torch
+
+from oracle import sampling as oracle
+from wpt_amd import sampling
+
+pytestmark = pytest.mark.gpu
+
+NEAR = 1e-5
+
+
+def step_inputs(B, L, V, seed, spread=4.0):
+    """Peaked scores correlated with the drafts' distributions, so that rows
+    keep, reject and resample at every position (also under a top-k cut)."""
+    generator = torch.Generator().manual_seed(seed)
+    logits = spread * torch.randn(B, L + 1, V, generator=generator)
+    q = torch.softmax(logits[:, :L] + torch.randn(B, L, V, generator=generator), -1)
+    drafts = torch.multinomial(q.reshape(-1, V), 1, generator=generator).reshape(B, L)
+    scores = logits
+    u = torch.rand(B, L, generator=generator)
+    e = torch.empty(B, V).exponential_(generator=generator)
+    return scores, q, drafts, u, e
+
+
+def compare(got, expected, gaps):
+    near = [b for b, gap in enumerate(gaps) if gap < NEAR]
+    for b, (g, x) in enumerate(zip(got, expected)):
+        if b not in near:
+            assert g == x, f"row {b}: {g} != {x}"
+    return near
+
+
+@pytest.mark.parametrize("V, top_k, temperature", [(32768, None, 0.8), (32768, 40, 0.8), (8192, 40, 1.0),
+                                                   (1000, 1, 0.8), (50, None, 1.3)])
+def test_accept_matches_the_oracle_on_one_tape(device, V, top_k, temperature):
+    B, L = 64, 4
+    scores, q, drafts, u, e = step_inputs(B, L, V, seed=V + (top_k or 0))
+    lengths = [L] * B
+    expected = oracle.accept(scores, q, drafts, lengths, temperature, top_k,
+                             [oracle.TapeDraws(u[b], e[b]) for b in range(B)])
+    tokens, counts = sampling.accept(*(x.to(device) for x in (scores, q, drafts, u, e)), temperature, top_k)
+    got = sampling.written(tokens, counts)
+    near = compare(got, expected, oracle.margins(scores, q, drafts, lengths, temperature, top_k, u))
+    assert not near
+    kept = [len(t) - 1 for t in expected]
+    assert min(kept) < L and (max(kept) > 0 or top_k == 1)  # rows keep and reject
+
+
+def test_per_row_lengths_and_first_positions(device):
+    B, L, V = 16, 4, 4096
+    scores, q, drafts, u, e = step_inputs(B, L, V, seed=3)
+    generator = torch.Generator().manual_seed(4)
+    lengths = torch.randint(0, L + 1, (B,), generator=generator)
+    firsts = torch.randint(0, 3, (B,), generator=generator)
+    # scores with firsts[b] pending positions before the verified ones
+    padded = torch.randn(B, L + 3, V, generator=generator)
+    for b in range(B):
+        padded[b, firsts[b]:firsts[b] + L + 1] = scores[b]
+    expected = oracle.accept(scores, q, drafts, lengths.tolist(), 0.8, 40,
+                             [oracle.TapeDraws(u[b], e[b]) for b in range(B)])
+    tokens, counts = sampling.accept(*(x.to(device) for x in (padded, q, drafts, u, e)), 0.8, 40,
+                                     lengths=lengths, firsts=firsts)
+    assert sampling.written(tokens, counts) == expected
+
+
+def test_a_lazy_run_is_replayed_through_its_tape(device):
+    # the reference's lazily drawn stream (torch.rand per draft, multinomial
+    # per row) recorded on the CPU and handed to the GPU as a tape
+    B, L, V = 32, 4, 2048
+    scores, q, drafts, _, _ = step_inputs(B, L, V, seed=6)
+    generator = torch.Generator().manual_seed(7)
+    lazy = [oracle.LazyDraws(generator) for _ in range(B)]
+    expected = [oracle.accept(scores[b:b + 1], q[b:b + 1], drafts[b:b + 1], [L], 0.8, 40, [lazy[b]])[0]
+                for b in range(B)]
+    u = torch.zeros(B, L)
+    for b in range(B):
+        u[b, :len(lazy[b].uniforms)] = torch.tensor(lazy[b].uniforms)
+    e = torch.stack([draws.exponentials[0] for draws in lazy])
+    tokens, counts = sampling.accept(*(x.to(device) for x in (scores, q, drafts, u, e)), 0.8, 40)
+    assert sampling.written(tokens, counts) == expected
+
+
+def test_greedy_chain_matches_the_oracle_and_top_k_one(device):
+    B, L, V = 64, 4, 32768
+    scores, q, drafts, u, e = step_inputs(B, L, V, seed=8)
+    best = scores.argmax(-1)
+    keep = torch.randint(0, L + 1, (B,), generator=torch.Generator().manual_seed(9))
+    for b in range(B):
+        drafts[b, :keep[b]] = best[b, :keep[b]]
+    expected = oracle.greedy_chain(scores, drafts, [L] * B)
+    args = [x.to(device) for x in (scores, q, drafts, u, e)]
+    assert sampling.written(*sampling.greedy_chain(args[0], args[2])) == expected
+    assert sampling.written(*sampling.accept(*args, 0.8, 1)) == expected
+
+
+def test_uniform_drafts_keep_the_model_s_distribution(device):
+    # the reference's statistical test (test_sampling.py:98-121) at 4000 rows
+    # of one model distribution: the first written token follows p
+    rows, L, V = 4000, 4, 20
+    generator = torch.Generator().manual_seed(10)
+    row_scores = torch.randn(1, L + 1, V, generator=generator)
+    scores = row_scores.expand(rows, -1, -1).contiguous()
+    q = torch.full((rows, L, V), 1.0 / V)
+    drafts = torch.randint(V, (rows, L), generator=generator)
+    u, e = torch.rand(rows, L, generator=generator), torch.empty(rows, V).exponential_(generator=generator)
+    tokens, counts = sampling.accept(*(x.to(device) for x in (scores, q, drafts, u, e)), 1.0, None)
+    first = tokens[:, 0].cpu()
+    p = oracle.probabilities(row_scores[0, 0], 1.0, None)
+    assert (torch.bincount(first, minlength=V) / rows - p).abs().sum() / 2 < 0.05
+
+
+def test_drafts_from_the_model_itself_are_all_kept(device):
+    B, L, V = 64, 4, 4096
+    generator = torch.Generator().manual_seed(11)
+    scores = torch.randn(B, L + 1, V, generator=generator)
+    p = oracle.probabilities(scores, 0.8, 40)
+    drafts = torch.multinomial(p[:, :L].reshape(-1, V), 1, generator=generator).reshape(B, L)
+    u, e = torch.rand(B, L, generator=generator), torch.empty(B, V).exponential_(generator=generator)
+    tokens, counts = sampling.accept(*(x.to(device) for x in (scores, p[:, :L].contiguous(), drafts, u, e)), 0.8, 40)
+    assert (counts == L + 1).all()
+    assert torch.equal(tokens[:, :L].cpu(), drafts)
+
+
+def test_greedy_tree_matches_the_oracle(device):
+    # the tree workload's acceptance: a binary draft tree of 31 nodes, with
+    # node tokens planted on the argmax path to random depths
+    B, V = 16, 32768
+    parents = [-1] + [(i - 1) // 2 for i in range(1, 31)]
+    generator = torch.Generator().manual_seed(12)
+    scores = torch.randn(B, 31, V, generator=generator)
+    best = scores.argmax(-1)
+    tokens = torch.randint(V, (B, 31), generator=generator)
+    for b in range(B):
+        node = 0
+        for _ in range(int(torch.randint(0, 5, (), generator=generator))):
+            child = 2 * node + 1 + int(torch.randint(0, 2, (), generator=generator))
+            tokens[b, child] = best[b, node]
+            node = child
+    expected = oracle.greedy_tree(scores, tokens, parents)
+    path, written, counts = sampling.greedy_tree(scores.to(device), tokens.to(device), parents)
+    for b, (p, w) in enumerate(expected):
+        assert int(counts[b]) == len(w)
+        assert path[b, :len(p)].tolist() == p and written[b, :len(w)].tolist() == w
+
+
+def test_a_residual_with_no_mass_raises(device):
+    V = 16
+    scores = torch.zeros(1, 2, V)
+    q = torch.softmax(scores[:, :1], -1)  # q equals p: the residual is zero everywhere
+    drafts = torch.tensor([[3]])
+    u = torch.tensor([[1.0]])  # u*q < p fails: the draft is rejected
+    e = torch.ones(1, V)
+    tokens, counts = sampling.accept(*(x.to(device) for x in (scores, q, drafts, u, e)), 1.0, None)
+    with pytest.raises(RuntimeError, match="no mass"):
+        sampling.written(tokens, counts)
+
+
+def test_bad_shapes_raise_value_error(device):
+    scores = torch.zeros(2, 5, 100, device=device)
+    q = torch.zeros(2, 4, 100, device=device)
+    with pytest.raises(ValueError):
+        sampling.accept(scores, q, torch.zeros(2, 5, dtype=torch.long, device=device), torch.zeros(2, 5, device=device),
+                        torch.ones(2, 100, device=device))
+    with pytest.raises(ValueError):
+        sampling.accept(scores, q, torch.zeros(2, 4, dtype=torch.long, device=device), torch.zeros(2, 4, device=device),
+                        torch.ones(2, 100, device=device), temperature=0.0)

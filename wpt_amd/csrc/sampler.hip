@@ -1,0 +1,425 @@
+// The acceptance step of speculative decoding for gfx950: the reference's
+// sampling distribution (Writer._probabilities,
+// packages/wpt-inference/src/wpt_inference/__init__.py:173-179) and its
+// per-row keep / reject / resample loop (Writer._speculate, :210-229), fused
+// over the vocabulary for every row at once, with the draws read from a tape.
+//
+//   accept_stats   one workgroup per (batch row, position): the row of scores
+//                  divided by the temperature, the top-k threshold (radix
+//                  select of the k-th largest, ties kept), the maximum and the
+//                  softmax denominator, and for a draft position the decision
+//                  u * q[draft] < p[draft]; in greedy mode the first maximal
+//                  index instead, the draft kept iff it is that index
+//   accept_finish  one workgroup per batch row: the first rejected draft, then
+//                  the replacement argmax_v (max(0, p_v - q_v) / S) / e_v, or
+//                  after every draft kept the bonus argmax_v p_v / e_v (one
+//                  draw from a distribution by the exponential race torch's
+//                  multinomial uses)
+//   tree_walk      greedy verification of a draft tree from the per-node argmax
+//
+// Each vocabulary row is read once per pass from HBM with coalesced loads and
+// kept in registers (ITEMS values per thread); reductions are wavefront
+// shuffles, then one LDS step across the 16 wavefronts.
+#include "wptv_common.h"
+
+#include <climits>
+
+namespace wptv {
+namespace {
+
+constexpr int kT = 1024;       // threads per workgroup
+constexpr int kW = kT / 64;    // wavefronts per workgroup
+constexpr float kNegInfS = -__builtin_inff();
+
+struct Stats {  // per (batch row, position); arrays of B * P in the workspace
+  float* m;     // maximum of scores / temperature over the kept entries
+  float* z;     // softmax denominator: sum of exp(s - m) over the kept entries
+  float* thr;   // top-k threshold (entries below it have p = 0), -inf without a cut
+  int* best;    // first maximal index of the scores
+  int* keep;    // 1 if the draft at this position is kept
+};
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ __forceinline__ float block_max(float x, float* red) {
+  x = wave_max(x);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[wave] = x;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < kW; ++w) r = fmaxf(r, red[w]);
+  return r;
+}
+
+// Sum in a fixed order (wave tree, then wavefronts in index order).
+__device__ __forceinline__ float block_sum(float x, float* red) {
+  x = wave_sum(x);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[wave] = x;
+  __syncthreads();
+  float r = 0.f;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) r += red[w];
+  return r;
+}
+
+// The larger value, the lower index on a tie (torch.argmax's first maximum).
+__device__ __forceinline__ void arg_better(float& v, int& i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i) || (v != v && v2 == v2)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+__device__ __forceinline__ int block_argmax(float v, int i, float* redv, int* redi) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(v, o, 64);
+    const int i2 = __shfl_xor(i, o, 64);
+    arg_better(v, i, v2, i2);
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) {
+    redv[wave] = v;
+    redi[wave] = i;
+  }
+  __syncthreads();
+  float bv = redv[0];
+  int bi = redi[0];
+  for (int w = 1; w < kW; ++w) arg_better(bv, bi, redv[w], redi[w]);
+  return bi;
+}
+
+// The k-th largest of the valid values (radix select over order-preserving
+// keys, most significant byte first).
+template <int ITEMS>
+__device__ float kth_largest(const float (&s)[ITEMS], int V, int k, int* hist, int* sel) {
+  uint32_t prefix = 0, mask = 0;
+  int remaining = k;
+  const int tid = threadIdx.x, lane = tid & 63;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    __syncthreads();
+    if (tid < 256) hist[tid] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int v = tid + i * kT;
+      if (v < V) {
+        const uint32_t key = order_key(s[i]);
+        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
+      }
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // lane l holds bins 4l .. 4l + 3; above[l] = entries in bins >= 4l + 4
+      int c[4], total = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) total += (c[e] = hist[4 * lane + e]);
+      int suffix = total;  // inclusive suffix sum over lanes >= l
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int other = __shfl_down(suffix, o, 64);
+        if (lane + o < 64) suffix += other;
+      }
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(suffix >= remaining);
+      const int top = 63 - __builtin_clzll(hit);  // the highest lane still reaching the k-th entry
+      if (lane == top) {
+        int above = suffix - total;
+        int digit = 4 * lane;
+        for (int e = 3; e >= 0; --e) {
+          if (above + c[e] >= remaining) {
+            digit = 4 * lane + e;
+            break;
+          }
+          above += c[e];
+        }
+        sel[0] = digit;
+        sel[1] = remaining - above;
+      }
+    }
+    __syncthreads();
+    prefix |= (uint32_t)sel[0] << shift;
+    mask |= 255u << shift;
+    remaining = sel[1];
+  }
+  return key_value(prefix);
+}
+
+template <int ITEMS>
+__global__ __launch_bounds__(kT) void accept_stats(const float* __restrict__ scores, int64_t sb, int64_t st,
+                                                   const int32_t* __restrict__ firsts, const float* __restrict__ q,
+                                                   int64_t qb, int64_t qt, const int64_t* __restrict__ drafts,
+                                                   int64_t db, const int32_t* __restrict__ lengths,
+                                                   const float* __restrict__ u, float temperature, int top_k,
+                                                   int greedy, int L, int V, Stats stats) {
+  __shared__ float redv[kW];
+  __shared__ int redi[kW];
+  __shared__ int hist[256];
+  __shared__ int sel[2];
+  const int j = blockIdx.x, b = blockIdx.y, P = L + 1;
+  const int n = lengths ? lengths[b] : L;
+  if (j > n) return;
+  const int64_t first = firsts ? firsts[b] : 0;
+  const float* row = scores + b * sb + (first + j) * st;
+  const int tid = threadIdx.x;
+  float x[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int v = tid + i * kT;
+    x[i] = v < V ? row[v] : kNegInfS;
+  }
+  // first maximal index of the raw scores
+  float bv = kNegInfS;
+  int bi = INT_MAX;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (tid + i * kT < V) arg_better(bv, bi, x[i], tid + i * kT);
+  const int best = block_argmax(bv, bi, redv, redi);
+  const int idx = b * P + j;
+  if (greedy) {
+    if (tid == 0) {
+      stats.best[idx] = best;
+      stats.keep[idx] = (j < n && drafts) ? (drafts[b * db + j] == best) : 0;
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) x[i] = x[i] / temperature;
+  float thr = kNegInfS;
+  if (top_k > 0 && top_k < V) thr = kth_largest<ITEMS>(x, V, top_k, hist, sel);
+  float mx = kNegInfS;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) mx = fmaxf(mx, x[i]);
+  const float m = block_max(mx, redv);
+  float part = 0.f;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (tid + i * kT < V && x[i] >= thr) part += expf(x[i] - m);
+  const float z = block_sum(part, redv);
+  if (tid == 0) {
+    stats.m[idx] = m;
+    stats.z[idx] = z;
+    stats.thr[idx] = thr;
+    stats.best[idx] = best;
+    int keep = 0;
+    if (j < n) {
+      const int64_t d = drafts[b * db + j];
+      if (d >= 0 && d < V) {
+        const float sd = row[d] / temperature;
+        const float pd = sd >= thr ? expf(sd - m) * (1.f / z) : 0.f;
+        keep = u[(int64_t)b * L + j] * q[b * qb + j * qt + d] < pd;
+      }
+    }
+    stats.keep[idx] = keep;
+  }
+}
+
+template <int ITEMS>
+__global__ __launch_bounds__(kT) void accept_finish(const float* __restrict__ scores, int64_t sb, int64_t st,
+                                                    const int32_t* __restrict__ firsts, const float* __restrict__ q,
+                                                    int64_t qb, int64_t qt, const int64_t* __restrict__ drafts,
+                                                    int64_t db, const int32_t* __restrict__ lengths,
+                                                    const float* __restrict__ e, float temperature, int greedy, int L,
+                                                    int V, Stats stats, int64_t* __restrict__ tokens,
+                                                    int32_t* __restrict__ n_tokens) {
+  __shared__ float redv[kW];
+  __shared__ int redi[kW];
+  const int b = blockIdx.x, P = L + 1, tid = threadIdx.x;
+  const int n = lengths ? lengths[b] : L;
+  int js = 0;  // the first rejected draft, n when every draft is kept
+  while (js < n && stats.keep[b * P + js]) ++js;
+  for (int t = tid; t < P; t += kT)
+    if (t != js) tokens[(int64_t)b * P + t] = t < js ? drafts[b * db + t] : -1;  // slot js: thread 0, below
+  const int idx = b * P + js;
+  if (greedy) {
+    if (tid == 0) {
+      tokens[(int64_t)b * P + js] = stats.best[idx];
+      n_tokens[b] = js + 1;
+    }
+    return;
+  }
+  const int64_t first = firsts ? firsts[b] : 0;
+  const float* row = scores + b * sb + (first + js) * st;
+  const float m = stats.m[idx], zinv = 1.f / stats.z[idx], thr = stats.thr[idx];
+  const bool rejected = js < n;
+  const float* qrow = rejected ? q + b * qb + js * qt : nullptr;
+  const float* erow = e + (int64_t)b * V;
+  float w[ITEMS];
+  float part = 0.f;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int v = tid + i * kT;
+    float p = 0.f;
+    if (v < V) {
+      const float s = row[v] / temperature;
+      p = s >= thr ? expf(s - m) * zinv : 0.f;
+      if (rejected) p = fmaxf(p - qrow[v], 0.f);
+    }
+    w[i] = p;
+    part += p;
+  }
+  float S = 1.f;
+  if (rejected) S = block_sum(part, redv);
+  float bv = kNegInfS;
+  int bi = INT_MAX;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int v = tid + i * kT;
+    if (v < V) arg_better(bv, bi, (rejected ? w[i] / S : w[i]) / erow[v], v);
+  }
+  const int token = block_argmax(bv, bi, redv, redi);
+  if (tid == 0) {
+    // a residual with no mass has no draw (the reference's multinomial raises)
+    const bool ok = !(rejected && !(S > 0.f)) && token >= 0 && token < V;
+    tokens[(int64_t)b * P + js] = ok ? token : -1;
+    n_tokens[b] = ok ? js + 1 : -1;
+  }
+}
+
+// Greedy walk down a draft tree: node i's parent parents[i] < i, the root 0.
+__global__ void tree_walk(const int64_t* __restrict__ node_tokens, const int32_t* __restrict__ parents, int B, int M,
+                          Stats stats, int64_t* __restrict__ path, int64_t* __restrict__ tokens,
+                          int32_t* __restrict__ n_tokens) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const int64_t* nt = node_tokens + (int64_t)b * M;
+  int64_t* pa = path + (int64_t)b * (M + 1);
+  int64_t* tk = tokens + (int64_t)b * (M + 1);
+  for (int i = 0; i <= M; ++i) pa[i] = tk[i] = -1;
+  int node = 0, depth = 0;
+  pa[0] = 0;
+  while (true) {
+    const int target = stats.best[b * M + node];
+    int next = -1;
+    for (int c = node + 1; c < M; ++c)
+      if (parents[c] == node && nt[c] == target) {
+        next = c;
+        break;
+      }
+    if (next < 0) {
+      tk[depth] = target;
+      break;
+    }
+    node = next;
+    tk[depth] = nt[node];
+    ++depth;
+    pa[depth] = node;
+  }
+  n_tokens[b] = depth + 1;
+}
+
+Stats carve(void* workspace, int B, int P) {
+  char* p = static_cast<char*>(workspace);
+  const size_t n = align_up((size_t)B * P * 4, 256);
+  Stats s;
+  s.m = reinterpret_cast<float*>(p);
+  s.z = reinterpret_cast<float*>(p + n);
+  s.thr = reinterpret_cast<float*>(p + 2 * n);
+  s.best = reinterpret_cast<int*>(p + 3 * n);
+  s.keep = reinterpret_cast<int*>(p + 4 * n);
+  return s;
+}
+
+size_t stats_bytes(int B, int P) { return 5 * align_up((size_t)B * P * 4, 256); }
+
+int items_for(int V) {
+  const int per = (V + kT - 1) / kT;
+  if (per <= 4) return 4;
+  if (per <= 8) return 8;
+  if (per <= 16) return 16;
+  if (per <= 32) return 32;
+  if (per <= 64) return 64;
+  return 0;
+}
+
+#define WPTV_ITEMS(V, CALL)                     \
+  switch (items_for(V)) {                       \
+    case 4: CALL(4); break;                     \
+    case 8: CALL(8); break;                     \
+    case 16: CALL(16); break;                   \
+    case 32: CALL(32); break;                   \
+    default: CALL(64); break;                   \
+  }
+
+}  // namespace
+}  // namespace wptv
+
+using namespace wptv;
+
+extern "C" int wptv_accept_workspace(int B, int L, size_t* bytes) {
+  if (!bytes) return fail(WPTV_E_INVALID, "accept_workspace: null output pointer");
+  if (B <= 0 || L < 0) return fail(WPTV_E_INVALID, "accept_workspace: B must be positive and L >= 0 (got %d, %d)", B, L);
+  *bytes = stats_bytes(B, L + 1);
+  return WPTV_OK;
+}
+
+extern "C" int wptv_accept(const float* scores, int64_t scores_stride_b, int64_t scores_stride_t,
+                           const int32_t* firsts, const float* q, int64_t q_stride_b, int64_t q_stride_t,
+                           const int64_t* drafts, int64_t drafts_stride_b, const int32_t* lengths, const float* u,
+                           const float* e, float temperature, int top_k, int greedy, int B, int L, int V,
+                           int64_t* tokens, int32_t* n_tokens, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream) {
+  if (!scores || !tokens || !n_tokens || (L > 0 && !drafts))
+    return fail(WPTV_E_INVALID, "accept: scores, tokens, n_tokens (and drafts when L > 0) must be given");
+  if (!greedy && (!e || (L > 0 && (!q || !u))))
+    return fail(WPTV_E_INVALID, "accept: sampling needs q, u and e");
+  if (B <= 0 || L < 0 || V <= 0)
+    return fail(WPTV_E_INVALID, "accept: bad shape B=%d L=%d V=%d", B, L, V);
+  if (!greedy && !(temperature > 0.f))
+    return fail(WPTV_E_INVALID, "accept: temperature must be positive (got %g)", (double)temperature);
+  if (items_for(V) == 0) return fail(WPTV_E_UNSUPPORTED, "accept: a vocabulary of %d is above %d", V, 64 * kT);
+  if (!workspace || workspace_bytes < stats_bytes(B, L + 1))
+    return fail(WPTV_E_INVALID, "accept: workspace of %zu bytes, %zu needed", workspace_bytes, stats_bytes(B, L + 1));
+  const Stats s = carve(workspace, B, L + 1);
+#define WPTV_STATS(I)                                                                                           \
+  hipLaunchKernelGGL(accept_stats<I>, dim3(L + 1, B), dim3(kT), 0, stream, scores, scores_stride_b,             \
+                     scores_stride_t, firsts, q, q_stride_b, q_stride_t, drafts, drafts_stride_b, lengths, u,   \
+                     temperature, top_k, greedy, L, V, s)
+  WPTV_ITEMS(V, WPTV_STATS)
+#undef WPTV_STATS
+  int st = launched("accept_stats");
+  if (st != WPTV_OK) return st;
+#define WPTV_FINISH(I)                                                                                          \
+  hipLaunchKernelGGL(accept_finish<I>, dim3(B), dim3(kT), 0, stream, scores, scores_stride_b, scores_stride_t, \
+                     firsts, q, q_stride_b, q_stride_t, drafts, drafts_stride_b, lengths, e, temperature, greedy, \
+                     L, V, s, tokens, n_tokens)
+  WPTV_ITEMS(V, WPTV_FINISH)
+#undef WPTV_FINISH
+  return launched("accept_finish");
+}
+
+extern "C" int wptv_greedy_tree(const float* scores, int64_t scores_stride_b, int64_t scores_stride_t,
+                                const int64_t* node_tokens, const int32_t* parents, int B, int M, int V,
+                                int64_t* path, int64_t* tokens, int32_t* n_tokens, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream) {
+  if (!scores || !node_tokens || !parents || !path || !tokens || !n_tokens)
+    return fail(WPTV_E_INVALID, "greedy_tree: every pointer must be given");
+  if (B <= 0 || M <= 0 || V <= 0) return fail(WPTV_E_INVALID, "greedy_tree: bad shape B=%d M=%d V=%d", B, M, V);
+  if (items_for(V) == 0) return fail(WPTV_E_UNSUPPORTED, "greedy_tree: a vocabulary of %d is above %d", V, 64 * kT);
+  if (!workspace || workspace_bytes < stats_bytes(B, M))
+    return fail(WPTV_E_INVALID, "greedy_tree: workspace of %zu bytes, %zu needed", workspace_bytes,
+                stats_bytes(B, M));
+  const Stats s = carve(workspace, B, M);
+  // per-node argmax: the stats pass in greedy mode over M positions with no drafts to judge
+#define WPTV_STATS(I)                                                                                             \
+  hipLaunchKernelGGL(accept_stats<I>, dim3(M, B), dim3(kT), 0, stream, scores, scores_stride_b, scores_stride_t, \
+                     nullptr, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, 1.f, 0, 1, M - 1, V, s)
+  WPTV_ITEMS(V, WPTV_STATS)
+#undef WPTV_STATS
+  int st = launched("accept_stats");
+  if (st != WPTV_OK) return st;
+  hipLaunchKernelGGL(tree_walk, dim3((B + 63) / 64), dim3(64), 0, stream, node_tokens, parents, B, M, s, path, tokens,
+                     n_tokens);
+  return launched("tree_walk");
+}

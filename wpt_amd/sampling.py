@@ -1,0 +1,139 @@
+"""The acceptance step of speculative decoding on the GPU (libwptv's
+wptv_accept / wptv_greedy_tree): the reference's sampling distribution
+(Writer._probabilities, packages/wpt-inference/src/wpt_inference/__init__.py:
+173-179) and keep / reject / resample loop (Writer._speculate, :210-229) for
+every row in two kernel launches and no host synchronization.
+
+The reference draws lazily from a torch generator, one uniform per draft it
+looks at and one multinomial per row.  Here the draws come from a tape drawn
+up front, `draws(B, L, V)`: u (B, L) uniforms, the one for draft j of row b,
+and e (B, V) Exp(1) values, the multinomial draw of row b being
+argmax_v w_v / e_v (the exponential race torch's multinomial runs for one
+sample).  A tape built from what a lazy run drew replays it exactly.
+"""
+
+import torch
+
+from . import _lib
+from ._lib import KernelUnavailable, check, ptr
+
+__all__ = ["accept", "greedy_chain", "greedy_tree", "draws", "written"]
+
+
+def _on_gpu(*tensors):
+    for x in tensors:
+        if x is not None and x.device.type != "cuda":
+            raise KernelUnavailable(f"the HIP sampler runs on a GPU; a tensor is on {x.device}")
+
+
+def _rows_last_contiguous(x, name, dims):
+    if x.dim() != dims:
+        raise ValueError(f"{name} must have {dims} dimensions; got {tuple(x.shape)}")
+    if x.dtype != torch.float32:
+        raise ValueError(f"{name} must be float32; got {x.dtype}")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    return x
+
+
+def _workspace(device, B, L):
+    size = _lib.ctypes.c_size_t(0)
+    check(_lib.lib().wptv_accept_workspace(B, L, _lib.ctypes.byref(size)), "accept")
+    return torch.empty(size.value, dtype=torch.uint8, device=device), size.value
+
+
+def draws(B, L, V, generator=None, device="cuda"):
+    """A tape for one step: (u (B, L) uniforms in [0, 1), e (B, V) Exp(1))."""
+    u = torch.rand(B, L, generator=generator, device=device)
+    e = torch.empty(B, V, device=device).exponential_(generator=generator)
+    return u, e
+
+
+def accept(scores, q, drafts, u, e, temperature=0.8, top_k=40, lengths=None, firsts=None, greedy=False):
+    """Each row's written tokens: (tokens (B, L + 1) int64, -1 past a row's
+    count; counts (B,) int32 = kept drafts + 1).
+
+    scores (B, >= L + 1, V) FP32: row b's position j is scores[b, firsts[b] + j]
+    (firsts None: 0); q (B, L, V) FP32 the drafts' distributions; drafts (B, L)
+    int64; u, e the tape (draws); lengths (B,) the drafts each row verifies
+    (None: L).  greedy: keep the drafts equal to the argmax (q, u, e unused)."""
+    scores = _rows_last_contiguous(scores, "scores", 3)
+    B, _, V = scores.shape
+    if drafts.dim() != 2 or drafts.shape[0] != B:
+        raise ValueError(f"drafts must be (B={B}, L); got {tuple(drafts.shape)}")
+    L = drafts.shape[1]
+    device = scores.device
+    drafts = drafts.to(device=device, dtype=torch.long).contiguous()
+    if not greedy:
+        q = _rows_last_contiguous(q, "q", 3)
+        if q.shape != (B, L, V):
+            raise ValueError(f"q must be (B={B}, L={L}, V={V}); got {tuple(q.shape)}")
+        u = u.to(device=device, dtype=torch.float32).contiguous()
+        e = e.to(device=device, dtype=torch.float32).contiguous()
+        if u.shape != (B, L) or e.shape != (B, V):
+            raise ValueError(f"the tape must be u (B={B}, L={L}) and e (B={B}, V={V}); got {tuple(u.shape)}, "
+                             f"{tuple(e.shape)}")
+        if not temperature > 0:
+            raise ValueError(f"the temperature must be positive; got {temperature}")
+    else:
+        q = u = e = None
+    lengths_ = None if lengths is None else torch.as_tensor(lengths, dtype=torch.int32, device=device).contiguous()
+    firsts_ = None if firsts is None else torch.as_tensor(firsts, dtype=torch.int32, device=device).contiguous()
+    need = L + 1 + (0 if firsts is None else int(torch.as_tensor(firsts).max()))
+    if scores.shape[1] < need:
+        raise ValueError(f"scores hold {scores.shape[1]} positions per row; {need} are read")
+    _on_gpu(scores, q, drafts, u, e)
+    tokens = torch.empty(B, L + 1, dtype=torch.long, device=device)
+    counts = torch.empty(B, dtype=torch.int32, device=device)
+    workspace, size = _workspace(device, B, L)
+    check(_lib.lib().wptv_accept(ptr(scores), scores.stride(0), scores.stride(1), ptr(firsts_), ptr(q),
+                                 q.stride(0) if q is not None else 0, q.stride(1) if q is not None else 0,
+                                 ptr(drafts), drafts.stride(0), ptr(lengths_), ptr(u), ptr(e), float(temperature),
+                                 0 if top_k is None else int(top_k), 1 if greedy else 0, B, L, V, ptr(tokens),
+                                 ptr(counts), ptr(workspace), size, _lib.stream(device)), "accept")
+    return tokens, counts
+
+
+def greedy_chain(scores, drafts, lengths=None, firsts=None):
+    """Greedy verification: (tokens, counts) as accept, each row keeping the
+    longest prefix of drafts equal to the argmax, then the argmax."""
+    return accept(scores, None, drafts, None, None, lengths=lengths, firsts=firsts, greedy=True)
+
+
+def greedy_tree(scores, node_tokens, parents):
+    """Greedy verification of a draft tree: scores (B, M, V) FP32 at the M
+    nodes, node_tokens (B, M), parents (M,) (parents[0] = -1, parents[i] < i).
+    Returns (path (B, M + 1) node indices from the root, tokens (B, M + 1)
+    written, counts (B,)); -1 past each row's count."""
+    scores = _rows_last_contiguous(scores, "scores", 3)
+    B, M, V = scores.shape
+    device = scores.device
+    parents_ = torch.as_tensor(parents, dtype=torch.int32).to(device)
+    if parents_.shape != (M,) or int(parents_[0]) != -1 or any(not 0 <= int(p) < i for i, p in
+                                                              enumerate(parents_.tolist()) if i > 0):
+        raise ValueError("parents must be (M,) with parents[0] = -1 and 0 <= parents[i] < i")
+    node_tokens = node_tokens.to(device=device, dtype=torch.long).contiguous()
+    if node_tokens.shape != (B, M):
+        raise ValueError(f"node_tokens must be (B={B}, M={M}); got {tuple(node_tokens.shape)}")
+    _on_gpu(scores, node_tokens)
+    path = torch.empty(B, M + 1, dtype=torch.long, device=device)
+    tokens = torch.empty(B, M + 1, dtype=torch.long, device=device)
+    counts = torch.empty(B, dtype=torch.int32, device=device)
+    workspace, size = _workspace(device, B, M - 1)
+    check(_lib.lib().wptv_greedy_tree(ptr(scores), scores.stride(0), scores.stride(1), ptr(node_tokens),
+                                      ptr(parents_), B, M, V, ptr(path), ptr(tokens), ptr(counts), ptr(workspace),
+                                      size, _lib.stream(device)), "greedy_tree")
+    return path, tokens, counts
+
+
+def written(tokens, counts):
+    """The host lists of each row's written tokens (one synchronization);
+    a row with no residual mass raises as the reference's multinomial does."""
+    counts = counts.tolist()
+    rows = tokens.tolist()
+    out = []
+    for b, n in enumerate(counts):
+        if n < 0:
+            raise RuntimeError(f"row {b}: the residual distribution max(0, p - q) has no mass to draw from")
+        out.append(rows[b][:n])
+    return out
