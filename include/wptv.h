@@ -42,7 +42,10 @@ enum { WPTV_F32 = 0, WPTV_BF16 = 1 };
 
 /* wptv_verify_attention flags */
 enum {
-  WPTV_ATTN_FORCE_GENERIC = 1 /* run the wave-per-query VALU kernel even where the MFMA kernel applies */
+  WPTV_ATTN_FORCE_GENERIC = 1,        /* run the wave-per-query VALU kernel even where the MFMA kernel applies */
+  WPTV_ATTN_RANGE_FROM_POSITIONS = 2  /* read only the rows the positions reach (a table with spare capacity
+                                         past its rows); by default a single full-causal query group reads
+                                         rows 0..N-1 and masks the ones past each query */
 };
 
 int wptv_abi_version(void);

@@ -1,0 +1,77 @@
+"""Oracle MQA decoder: the verify step's model, restated on the CPU in FP32
+(test infrastructure; see oracle/__init__.py).
+
+The decoder is built from the reference's exact layer (ExactAttention,
+packages/wpt-model/src/wpt_model/attention.py:157-188: q = q_norm(q(x)) per
+head, entries = [k_norm(k(x)), v(x)] appended to the cache, exact attention
+over every row so far, the output projection) with pre-norm residual blocks,
+a SwiGLU feed-forward block and a final norm before the head, as the model's
+extend reads it (model.py:456-473: scores = head(final_norm(hidden)), FP32).
+RMSNorm's eps is the reference's (layers.py:9).  extend / undo / new_cache
+follow the reference's generation protocol through oracle.cache.
+
+Weights are a dict of tensors (any dtype; used in FP32):
+    embedding (V, D); head (V, D); final_norm (D,)
+    layers.{i}.attn_norm (D,)   layers.{i}.qkv (H*c + 2c, D): q rows, k, v
+    layers.{i}.q_norm (c,)      layers.{i}.k_norm (c,)
+    layers.{i}.out (D, H*c)     layers.{i}.ffn_norm (D,)
+    layers.{i}.gate_up (2F, D): gate rows, then up rows
+    layers.{i}.down (D, F)
+"""
+
+import torch
+import torch.nn.functional as F
+
+from . import attention, cache
+
+EPS = 1e-6
+
+
+def rms_norm(x, weight):
+    return F.rms_norm(x.float(), (x.shape[-1],), weight.float(), EPS)
+
+
+class Decoder:
+    def __init__(self, weights, layers, heads, head_dim):
+        self.w = {name: value.float() for name, value in weights.items()}
+        self.layers, self.heads, self.head_dim = layers, heads, head_dim
+
+    def new_cache(self, rows):
+        return cache.Rows(rows)
+
+    def _layer(self, i, h, reading):
+        w = lambda name: self.w[f"layers.{i}.{name}"]  # noqa: E731
+        B, T, _ = h.shape
+        H, c = self.heads, self.head_dim
+        x = rms_norm(h, w("attn_norm"))
+        qkv = x @ w("qkv").T
+        q = rms_norm(qkv[..., :H * c].reshape(B, T, H, c), w("q_norm"))
+        k = rms_norm(qkv[..., H * c:H * c + c], w("k_norm"))
+        v = qkv[..., H * c + c:]
+        table = reading.everything(("entries", i), torch.cat([k, v], -1))
+        o, _ = attention.exact_attention(q, table[..., :c], table[..., c:], reading.positions(T), c ** -0.5, 0, 128)
+        h = h + o.reshape(B, T, H * c) @ w("out").T
+        x = rms_norm(h, w("ffn_norm"))
+        gate, up = (x @ w("gate_up").T).chunk(2, -1)
+        return h + (F.silu(gate) * up) @ w("down").T
+
+    def extend(self, ids, rows, counts=None, undoable=False):
+        """(scores (B, n, V) FP32, hidden (B, n, D)) of ids (B, n), row b's
+        first counts[b] tokens after its earlier ones, the rest padding."""
+        ids = torch.as_tensor(ids, dtype=torch.long)
+        counts = torch.full((ids.shape[0],), ids.shape[1]) if counts is None else torch.as_tensor(counts)
+        reading = rows.reading(counts, undoable)
+        h = self.w["embedding"][ids]
+        for i in range(self.layers):
+            h = self._layer(i, h, reading)
+        scores = rms_norm(h, self.w["final_norm"]) @ self.w["head"].T
+        reading.finish()
+        return scores, h
+
+    def undo(self, rows, kept):
+        rows.undo(kept)
+
+    def forward(self, ids):
+        """The scores of each row's whole text (B, T, V), read in one pass."""
+        ids = torch.as_tensor(ids, dtype=torch.long)
+        return self.extend(ids, self.new_cache(ids.shape[0]))[0]

@@ -1,0 +1,225 @@
+"""The MQA decoder's generation protocol on the GPU (KV append, verify
+attention, undo) against the oracle decoder on the CPU, the plumbing
+workload's greedy verify step bit-exact, the Writer, and the verify step
+replayed from a HIP graph.  Scores: FP32 within 1e-5 of the largest expected
+magnitude, bf16 within 2e-2; token decisions exact."""
+
+import pytest
+import torch
+
+from oracle import decoder as oracle_decoder
+from oracle import sampling as oracle_sampling
+from wpt_amd.decoder import PLUMBING, DecoderConfig, MQADecoder, random_weights
+from wpt_amd import sampling
+from wpt_amd.step import VerifyStep, prefill
+from wpt_amd.writer import Writer
+
+pytestmark = pytest.mark.gpu
+
+SMALL_BF16 = DecoderConfig(layers=2, d_model=256, heads=16, head_dim=128, ffn=512, vocab=1024)
+
+
+def models(config, dtype, seed=0, std=0.02):
+    w = random_weights(config, seed=seed, std=std)
+    return MQADecoder(config, w, dtype=dtype), oracle_decoder.Decoder(w, config.layers, config.heads, config.head_dim)
+
+
+def close(got, expected, share):
+    return float((got.double() - expected.double()).abs().max()) <= share * float(expected.double().abs().max())
+
+
+def test_plumbing_scores_read_in_pieces_match_the_oracle_whole_text(device):
+    gpu, ora = models(PLUMBING, torch.float32)
+    ids = torch.randint(PLUMBING.vocab, (2, 69), generator=torch.Generator().manual_seed(1))
+    cache = gpu.new_cache(2, capacity=16)  # grows while reading
+    got = [gpu.extend(ids[:, a:b].to(device), cache)[0].cpu() for a, b in ((0, 37), (37, 38), (38, 64), (64, 69))]
+    assert cache.lengths.tolist() == [69, 69] and cache.capacity >= 69
+    assert close(torch.cat(got, 1), ora.forward(ids), 1e-5)
+
+
+def greedy_text(ora, prompt, n):
+    """The oracle's greedy continuation of prompt, n tokens."""
+    text = list(prompt)
+    for _ in range(n):
+        text.append(int(ora.forward(torch.tensor([text]))[0, -1].argmax()))
+    return text[len(prompt):]
+
+
+@pytest.mark.parametrize("planted", [0, 2, 4])
+def test_plumbing_greedy_verify_step_is_bit_exact(device, planted):
+    # the CPU-runnable plumbing workload: 4 layers, d_model 256, 4 query
+    # heads, 1 KV head, head width 64, vocab 8192, FP32; a prompt of 64
+    # tokens; a chain of 4 uniform drafts, the first `planted` of them the
+    # model's own greedy choices, verified greedily
+    gpu, ora = models(PLUMBING, torch.float32)
+    generator = torch.Generator().manual_seed(0)
+    prompt = torch.randint(PLUMBING.vocab, (64,), generator=generator).tolist()
+    drafts = torch.randint(PLUMBING.vocab, (4,), generator=generator)
+    drafts[:planted] = torch.tensor(greedy_text(ora, prompt, 4)[:planted], dtype=torch.long)
+    feeds = torch.tensor([[prompt[-1]] + drafts.tolist()])
+    # the oracle: read the prompt but its last token, then the step
+    rows = ora.new_cache(1)
+    ora.extend(torch.tensor([prompt[:-1]]), rows)
+    expected_scores, _ = ora.extend(feeds, rows, undoable=True)
+    expected = oracle_sampling.greedy_chain(expected_scores, drafts[None], [4])[0]
+    ora.undo(rows, [len(expected)])
+    # the GPU
+    cache = gpu.new_cache(1, capacity=128)
+    gpu.extend(torch.tensor([prompt[:-1]], device=device), cache)
+    scores, _ = gpu.extend(feeds.to(device), cache, undoable=True)
+    tokens, counts = sampling.greedy_chain(scores, drafts[None].to(device))
+    got = sampling.written(tokens, counts)[0]
+    gpu.undo(cache, counts.long())
+    top2 = expected_scores[0].topk(2, -1).values
+    assert float((top2[:, 0] - top2[:, 1]).min()) > 1e-4 * float(expected_scores.abs().max())  # no near ties
+    assert got == expected and len(got) == planted + 1
+    assert cache.lengths.tolist() == rows.lengths.tolist() == [63 + len(expected)]
+    assert close(scores.cpu(), expected_scores, 1e-5)
+
+
+@pytest.mark.parametrize("config, dtype, share", [(PLUMBING, torch.float32, 1e-5), (SMALL_BF16, torch.bfloat16, 2e-2)])
+def test_undoing_rejected_drafts_leaves_only_the_kept_tokens(device, config, dtype, share):
+    # the reference's undo contract (test_cache.py:206-238): every round
+    # reads 4 drafts per row and keeps a pattern of them
+    gpu, ora = models(config, dtype)
+    generator = torch.Generator().manual_seed(3)
+    texts = [torch.randint(config.vocab, (200,), generator=generator).tolist() for _ in range(2)]
+    cache = gpu.new_cache(2, capacity=64)
+    gpu.extend(torch.tensor([t[:60] for t in texts], device=device), cache)
+    place, got = [60, 60], [[], []]
+    for kept in ([4, 0], [1, 4], [0, 2], [3, 3], [2, 1], [4, 4], [0, 0], [1, 3]) * 3:
+        ids = torch.tensor([texts[row][place[row]:place[row] + 4] for row in range(2)])
+        drafts = ids.clone()
+        for row in range(2):
+            drafts[row, kept[row]:] = (ids[row, kept[row]:] + 1 + row) % config.vocab
+        scores, _ = gpu.extend(drafts.to(device), cache, undoable=True)
+        gpu.undo(cache, kept)
+        for row in range(2):
+            got[row].append(scores[row, :kept[row]].cpu())
+            place[row] += kept[row]
+    assert cache.lengths.tolist() == place
+    for row in range(2):
+        whole = ora.forward(torch.tensor([texts[row][:place[row]]]))[0]
+        assert close(torch.cat(got[row]), whole[60:], share)
+
+
+def test_bf16_rows_at_different_places_match_the_oracle(device):
+    gpu, ora = models(SMALL_BF16, torch.bfloat16)
+    generator = torch.Generator().manual_seed(5)
+    prompt = torch.randint(SMALL_BF16.vocab, (70,), generator=generator).tolist()
+    texts = [prompt + torch.randint(SMALL_BF16.vocab, (n,), generator=generator).tolist() for n in (30, 5, 17)]
+    shared = gpu.new_cache(1, capacity=32)
+    gpu.extend(torch.tensor([prompt], device=device), shared)
+    cache = shared.select([0, 0, 0])
+    got, place = [[] for _ in texts], [len(prompt)] * 3
+    for counts in ([1, 1, 1], [10, 0, 7], [3, 4, 1], [16, 0, 8]):
+        ids = torch.zeros(3, max(counts), dtype=torch.long)
+        for row, count in enumerate(counts):
+            ids[row, :count] = torch.tensor(texts[row][place[row]:place[row] + count])
+        scores, _ = gpu.extend(ids.to(device), cache, counts)
+        for row, count in enumerate(counts):
+            got[row].append(scores[row, :count].cpu())
+            place[row] += count
+    for row, text in enumerate(texts):
+        assert close(torch.cat(got[row]), ora.forward(torch.tensor([text]))[0, len(prompt):], 2e-2)
+    assert shared.lengths.tolist() == [len(prompt)]
+
+
+class Itself:
+    """The model as its own drafter (the reference's test_sampling.py:82-95):
+    its drafts are always kept."""
+    features, window = (), 0
+
+    def draft(self, model, histories, context, count, probabilities, generator):
+        tokens, distributions = [], []
+        for history in histories:
+            history = list(history)
+            for _ in range(count):
+                p = probabilities(model(torch.tensor([history]))[0, -1])
+                history.append(int(torch.multinomial(p, 1, generator=generator)))
+                distributions.append(p)
+            tokens.append(history[-count:])
+        return torch.tensor(tokens), torch.stack(distributions).view(len(histories), count, -1), None
+
+
+class Uniform:
+    features, window = (), 0
+
+    def draft(self, model, histories, context, count, probabilities, generator):
+        V = model.config.vocab
+        tokens = torch.randint(V, (len(histories), count), generator=generator, device=generator.device)
+        return tokens, torch.full((len(histories), count, V), 1.0 / V, device=generator.device), None
+
+
+def test_the_writer_keeps_every_draft_of_the_model_itself(device):
+    gpu, _ = models(PLUMBING, torch.float32, std=0.05)
+    writer = Writer(gpu, [0, 5, 7], 2, temperature=1.0, top_k=None,
+                    generator=torch.Generator(device=device).manual_seed(0), drafter=Itself())
+    written = writer.write({}, {0: 100, 1: 3})
+    assert len(written[0]) == 5 + 1 and len(written[1]) == 3
+    assert writer.accepted == 5 + 2 and writer.verified == 5 + 2 and writer.rounds == 1
+    stop = written[0][1]
+    writer = Writer(gpu, [0, 5, 7], 2, temperature=1.0, top_k=None,
+                    generator=torch.Generator(device=device).manual_seed(0), drafter=Itself(), stops=[stop])
+    assert writer.write({}, {0: 100, 1: 3})[0] == written[0][:written[0].index(stop) + 1]
+
+
+def test_the_writer_s_cache_holds_each_row_s_text(device):
+    # after speculative steps with uniform drafts, each row's cache reads as
+    # its whole text does (the reference's test_sampling.py:112-121)
+    gpu, _ = models(PLUMBING, torch.float32, std=0.05)
+    writer = Writer(gpu, [0, 5, 7, 9], 3, temperature=1.0, top_k=None,
+                    generator=torch.Generator(device=device).manual_seed(1), drafter=Uniform())
+    for _ in range(4):
+        writer.write({1: [11, 12]} if _ == 2 else {}, {row: 5 for row in range(3)})
+    for row in range(3):
+        history = writer.histories[row]
+        assert int(writer.cache.lengths[row]) == len(history) - 1
+    ids = torch.tensor([[h[-1]] for h in writer.histories], device=device)
+    scores, _ = gpu.extend(ids, writer.cache)
+    for row in range(3):
+        whole = gpu(torch.tensor([writer.histories[row]], device=device))[0, -1]
+        assert close(scores[row, 0].cpu(), whole.cpu(), 1e-5)
+
+
+def test_a_writer_without_drafts_samples_one_token_per_call(device):
+    gpu, _ = models(PLUMBING, torch.float32)
+    writer = Writer(gpu, [1, 2, 3], 2, generator=torch.Generator(device=device).manual_seed(2))
+    for _ in range(3):
+        out = writer.write({}, {0: 1, 1: 1})
+        assert all(len(tokens) == 1 for tokens in out.values())
+    assert [len(h) for h in writer.histories] == [6, 6]
+    assert writer.cache.lengths.tolist() == [5, 5]
+
+
+def test_a_captured_verify_step_replays_as_the_eager_step(device):
+    # greedy steps (no random draws): eager steps on one cache, graph replays
+    # on another with the same prefill, eager work between the replays
+    config = SMALL_BF16
+    w = random_weights(config, seed=7, std=0.05)
+    B, k = 4, 4
+    ids = torch.randint(config.vocab, (B, 90), generator=torch.Generator().manual_seed(8)).to(device)
+    runs = []
+    for captured in (False, True):
+        model = MQADecoder(config, w, dtype=torch.bfloat16)
+        cache = model.new_cache(B, capacity=256)
+        prefill(model, cache, ids[:, :-1], chunk=40)
+        step = VerifyStep(model, cache, k, greedy=True)
+        step.feeds[:, 0] = ids[:, -1]
+        step.feeds[:, 1:] = torch.randint(config.vocab, (B, k), generator=torch.Generator().manual_seed(9)).to(device)
+        out = []
+        if captured:
+            step.capture(warmup=1)  # one eager step on a side stream, then the capture (which runs nothing)
+            for _ in range(5):
+                tokens, counts = step.replay()
+                out.append((tokens.clone(), counts.clone(), cache.lengths.clone()))
+                torch.zeros(1000, device=device).sum()  # eager work between replays
+                torch.cuda.synchronize()
+        else:
+            for _ in range(6):  # the first step is the captured run's warmup
+                tokens, counts = step.run()
+                out.append((tokens.clone(), counts.clone(), cache.lengths.clone()))
+            out = out[1:]
+        runs.append(out)
+    for (te, ce, le), (tg, cg, lg) in zip(*runs):
+        assert torch.equal(te, tg) and torch.equal(ce, cg) and torch.equal(le, lg)

@@ -17,6 +17,7 @@ ABI_VERSION = 1
 WPTV_F32, WPTV_BF16 = 0, 1
 DTYPES = {torch.float32: WPTV_F32, torch.bfloat16: WPTV_BF16}
 FORCE_GENERIC = 1
+RANGE_FROM_POSITIONS = 2
 
 
 class KernelUnavailable(RuntimeError):

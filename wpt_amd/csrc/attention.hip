@@ -791,7 +791,7 @@ extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_str
   const int xcd_map = units % 8 == 0 ? 1 : 0;
   // Full causal attention of a single query group reads the whole table; any
   // other case takes its key range from the positions.
-  const int from_positions = (window > 0 || p.groups > 1) ? 1 : 0;
+  const int from_positions = (window > 0 || p.groups > 1 || (flags & WPTV_ATTN_RANGE_FROM_POSITIONS)) ? 1 : 0;
   const auto* qb = static_cast<const unsigned short*>(q);
   const auto* kb = static_cast<const unsigned short*>(k);
   const auto* vb = static_cast<const unsigned short*>(v);

@@ -1,0 +1,162 @@
+"""An MQA decoder behind the reference's generation protocol (new_cache /
+extend / undo, packages/wpt-model/src/wpt_model/model.py:451-483), running
+its verify-step hot path on libwptv's HIP kernels.
+
+Each layer is the reference's exact layer (ExactAttention, attention.py:
+157-188: q = q_norm(q(x)) per head, the entries [k_norm(k(x)), v(x)] of the
+new tokens appended to the cache, exact attention of every query over the
+rows up to its position, the output projection) in a pre-norm residual
+block, then a SwiGLU feed-forward block; a final norm and the head give
+FP32 scores (model.py:471).  One key/value head is shared by every query
+head (MQA).  RMSNorm's eps is the reference's (layers.py:9).
+
+On the GPU:
+    KV append       wptv_kv_append (at each row's own length, no host sync)
+    verify attention wptv_verify_attention, reading only the rows the query
+                    positions reach in the cache's table
+    projections     the matrix products of the dtype (bf16 on MFMA)
+    sampling        wpt_amd.sampling (wptv_accept), called by the Writer
+The decoder keeps no state between calls but the cache; a step of fixed
+shape can be captured in a HIP graph (wpt_amd.step).
+"""
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import kernels
+from .cache import Cache
+
+EPS = 1e-6
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    layers: int
+    d_model: int
+    heads: int
+    head_dim: int
+    ffn: int
+    vocab: int
+
+    @property
+    def qkv_width(self):
+        return self.heads * self.head_dim + 2 * self.head_dim
+
+
+# The decoders of the verify-step workloads.
+PLUMBING = DecoderConfig(layers=4, d_model=256, heads=4, head_dim=64, ffn=704, vocab=8192)
+LARGE = DecoderConfig(layers=24, d_model=2048, heads=16, head_dim=128, ffn=5632, vocab=32768)
+
+
+def random_weights(config, seed=0, std=0.02, dtype=torch.float32, device="cpu"):
+    """Random-init weights: every matrix ~ N(0, std) drawn from one seeded
+    generator on `device` in a fixed order, every norm weight 1."""
+    generator = torch.Generator(device=device).manual_seed(seed)
+    D, H, c, Fw, V = config.d_model, config.heads, config.head_dim, config.ffn, config.vocab
+
+    def normal(*shape):
+        return (torch.randn(*shape, generator=generator, device=device) * std).to(dtype)
+
+    def ones(n):
+        return torch.ones(n, dtype=torch.float32, device=device)
+
+    weights = {"embedding": normal(V, D)}
+    for i in range(config.layers):
+        weights[f"layers.{i}.attn_norm"] = ones(D)
+        weights[f"layers.{i}.qkv"] = normal(config.qkv_width, D)
+        weights[f"layers.{i}.q_norm"] = ones(c)
+        weights[f"layers.{i}.k_norm"] = ones(c)
+        weights[f"layers.{i}.out"] = normal(D, H * c)
+        weights[f"layers.{i}.ffn_norm"] = ones(D)
+        weights[f"layers.{i}.gate_up"] = normal(2 * Fw, D)
+        weights[f"layers.{i}.down"] = normal(D, Fw)
+    weights["final_norm"] = ones(D)
+    weights["head"] = normal(V, D)
+    return weights
+
+
+def rms_norm(x, weight):
+    """RMSNorm in FP32, the result in x's dtype."""
+    return F.rms_norm(x.float(), (x.shape[-1],), weight, EPS).to(x.dtype)
+
+
+class MQADecoder:
+    """config: DecoderConfig; weights: random_weights' names; dtype: the
+    compute dtype (float32 or bfloat16), on a GPU."""
+
+    def __init__(self, config, weights, dtype=torch.bfloat16, device="cuda"):
+        self.config, self.dtype = config, dtype
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise kernels.KernelUnavailable(f"the decoder's verify step runs on a GPU, not {self.device}")
+        self.w = {}
+        for name, value in weights.items():
+            keep_fp32 = name.endswith("norm")
+            self.w[name] = value.to(device=self.device, dtype=torch.float32 if keep_fp32 else dtype).contiguous()
+
+    def parameters(self):
+        return iter(self.w.values())
+
+    def new_cache(self, rows, routes=False, capacity=256):
+        """An empty cache of `rows` rows (the reference's WPT.new_cache)."""
+        if routes:
+            raise NotImplementedError("this decoder has no routed experts to record")
+        c = self.config.head_dim
+        return Cache(rows, self.config.layers, 2 * c, self.dtype, self.device, capacity)
+
+    def _layer(self, i, h, cache, positions, counts):
+        w = self.w
+        cfg = self.config
+        B, T, _ = h.shape
+        H, c = cfg.heads, cfg.head_dim
+        x = rms_norm(h, w[f"layers.{i}.attn_norm"])
+        qkv = F.linear(x, w[f"layers.{i}.qkv"])
+        q = rms_norm(qkv[..., :H * c].reshape(B, T, H, c), w[f"layers.{i}.q_norm"])
+        k = rms_norm(qkv[..., H * c:H * c + c], w[f"layers.{i}.k_norm"])
+        new = torch.cat([k, qkv[..., H * c + c:]], -1)
+        table = cache.tables[i]
+        kernels.kv_append(table, new, cache.lengths, counts)
+        o = kernels.verify_attention(q, table[..., :c], table[..., c:], positions, c ** -0.5, from_positions=True)
+        h = h + F.linear(o.reshape(B, T, H * c), w[f"layers.{i}.out"])
+        x = rms_norm(h, w[f"layers.{i}.ffn_norm"])
+        gate, up = F.linear(x, w[f"layers.{i}.gate_up"]).chunk(2, -1)
+        return h + F.linear(F.silu(gate) * up, w[f"layers.{i}.down"])
+
+    @torch.no_grad()
+    def extend(self, ids, cache, counts=None, undoable=False, features=()):
+        """Reads ids (B, n), the next tokens of the cache's B rows: the first
+        counts[b] of row b (all n by default), the rest padding.  Returns
+        ((B, n, V) FP32 scores, (B, n, D) final hidden states), as the
+        reference's WPT.extend (model.py:456-473)."""
+        if features:
+            raise NotImplementedError("this decoder gives no intermediate features")
+        ids = ids.to(self.device)
+        B, T = ids.shape
+        if B != cache.rows:
+            raise ValueError(f"ids hold {B} rows; the cache {cache.rows}")
+        if counts is None:
+            counts_ = torch.full((B,), T, dtype=torch.long, device=self.device)
+        else:
+            counts_ = torch.as_tensor(counts, dtype=torch.long).to(self.device)
+        cache.reserve(cache.bound + T)
+        positions = cache.lengths[:, None] + torch.arange(T, device=self.device)
+        h = F.embedding(ids, self.w["embedding"])
+        for i in range(self.config.layers):
+            h = self._layer(i, h, cache, positions, counts_)
+        scores = F.linear(rms_norm(h, self.w["final_norm"]), self.w["head"]).float()
+        cache.finish(counts_, undoable, T)
+        return scores, h
+
+    @torch.no_grad()
+    def undo(self, cache, kept):
+        """After an undoable extend: keeps only its first kept[b] tokens of
+        row b (the reference's WPT.undo, model.py:475-483)."""
+        cache.undo(torch.as_tensor(kept, dtype=torch.long).to(self.device))
+
+    @torch.no_grad()
+    def __call__(self, ids):
+        """The scores (B, T, V) of each row's whole text, read in one pass."""
+        ids = ids.to(self.device)
+        return self.extend(ids, self.new_cache(ids.shape[0], capacity=ids.shape[1]))[0]

@@ -28,7 +28,7 @@ from ._lib import KernelUnavailable, check, ptr
 NAME = "HIP (gfx950)"
 
 __all__ = ["NAME", "KernelUnavailable", "chosen_columns", "exact_attention", "sparse_attention", "verify_attention",
-           "tree_attention", "tree_ancestors"]
+           "tree_attention", "tree_ancestors", "kv_append"]
 
 
 def chosen_columns(top_k, window, N):
@@ -81,7 +81,7 @@ def _long(x, device):
 
 
 def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=None, lse=False, splits=0,
-                     generic=False):
+                     generic=False, from_positions=False):
     """MQA attention of q (B, T, H, c) over k, v (B, N, c): query t of row b
     sees rows max(0, p - window + 1) .. min(p, N - 1), p = positions[b, t]
     (window 0: from row 0), and with tree = (tree_base (B,), ancestors (T,)
@@ -89,7 +89,8 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
     of ancestors[t] is set; sink (H,) joins each head's softmax denominator.
     Returns the output (B, T, H, c) in q's dtype, and with lse=True also the
     (B, T, H) FP32 log-sum-exp.  splits: key-range parts per batch row (0:
-    the library chooses); generic: the wave-per-query kernel."""
+    the library chooses); generic: the wave-per-query kernel; from_positions:
+    read only the rows the positions reach (a cache table with spare rows)."""
     B, T, H, c, N = _check_inputs(q, k, v, positions)
     device = q.device
     library = _lib.lib()
@@ -104,7 +105,7 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
         tree_base, ancestors = (_long(x, device) for x in tree)
         if tree_base.shape != (B,) or ancestors.shape != (T,):
             raise ValueError(f"tree must be (tree_base (B={B},), ancestors (T={T},))")
-    flags = _lib.FORCE_GENERIC if generic else 0
+    flags = (_lib.FORCE_GENERIC if generic else 0) | (_lib.RANGE_FROM_POSITIONS if from_positions else 0)
     parts = _lib.ctypes.c_int(int(splits))
     size = _lib.ctypes.c_size_t(0)
     check(library.wptv_attention_workspace(B, T, H, c, N, int(window), dtype, flags, _lib.ctypes.byref(parts),
@@ -185,3 +186,30 @@ def tree_attention(q, k, v, tree_base, parents, scale, sink=None):
     positions = base[:, None] + torch.arange(M, device=q.device)
     masks = tree_ancestors(parents).to(q.device)
     return verify_attention(q, k, v, positions, scale, sink=sink, tree=(base, masks))
+
+
+def kv_append(table, new, start, counts):
+    """The in-place KV append of the generation cache (the scatter of the
+    reference's Reading.everything, cache.py:110-128): table[b, start[b] + j]
+    = new[b, j] for j < counts[b].  table (B, capacity, width) and new
+    (B, n, width) share a dtype, each row contiguous; start and counts (B,)
+    on the device (no host synchronization).  Rows past the capacity are not
+    written: the caller keeps the table large enough."""
+    if table.dim() != 3 or new.dim() != 3 or table.shape[0] != new.shape[0] or table.shape[2] != new.shape[2]:
+        raise ValueError(f"table (B, capacity, width) and new (B, n, width) do not match: {tuple(table.shape)}, "
+                         f"{tuple(new.shape)}")
+    if table.dtype != new.dtype:
+        raise ValueError(f"table and new must share a dtype; got {table.dtype}, {new.dtype}")
+    if table.device.type != "cuda" or new.device != table.device:
+        raise KernelUnavailable(f"the HIP KV append runs on a GPU; the table is on {table.device}")
+    if table.stride(2) != 1 or new.stride(2) != 1:
+        raise ValueError("each row of the table and of new must be contiguous")
+    B, n, width = new.shape
+    start_ = _long(start, table.device)
+    counts_ = _long(counts, table.device)
+    if start_.shape != (B,) or counts_.shape != (B,):
+        raise ValueError(f"start and counts must be (B={B},)")
+    check(_lib.lib().wptv_kv_append(ptr(table), table.stride(0), table.stride(1), table.shape[1], ptr(new),
+                                    new.stride(0), new.stride(1), ptr(start_), ptr(counts_), B, n, width,
+                                    _lib.dtype_code(table.dtype), _lib.stream(table.device)), "kv_append")
+    return table

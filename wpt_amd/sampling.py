@@ -79,7 +79,13 @@ def accept(scores, q, drafts, u, e, temperature=0.8, top_k=40, lengths=None, fir
         q = u = e = None
     lengths_ = None if lengths is None else torch.as_tensor(lengths, dtype=torch.int32, device=device).contiguous()
     firsts_ = None if firsts is None else torch.as_tensor(firsts, dtype=torch.int32, device=device).contiguous()
-    need = L + 1 + (0 if firsts is None else int(torch.as_tensor(firsts).max()))
+    host_lengths = torch.full((B,), L) if lengths is None else torch.as_tensor(lengths).cpu().long()
+    host_firsts = torch.zeros(B, dtype=torch.long) if firsts is None else torch.as_tensor(firsts).cpu().long()
+    if host_lengths.shape != (B,) or host_firsts.shape != (B,):
+        raise ValueError(f"lengths and firsts must be (B={B},)")
+    if (host_lengths < 0).any() or (host_lengths > L).any() or (host_firsts < 0).any():
+        raise ValueError(f"lengths must lie in [0, {L}] and firsts be non-negative")
+    need = int((host_firsts + host_lengths).max()) + 1
     if scores.shape[1] < need:
         raise ValueError(f"scores hold {scores.shape[1]} positions per row; {need} are read")
     _on_gpu(scores, q, drafts, u, e)

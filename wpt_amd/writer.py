@@ -1,0 +1,148 @@
+"""Speculative writing with the verify step on the GPU: the reference's Writer
+(packages/wpt-inference/src/wpt_inference/__init__.py:71-233) with the same
+signature, protocol and counters, its acceptance loop replaced by the fused
+HIP sampler (wpt_amd.sampling).
+
+What differs from the reference, by design:
+    the draws    the reference draws lazily from `generator` (torch.rand per
+                 draft it looks at, torch.multinomial per row, :214-222);
+                 here each step draws one tape up front from the same
+                 generator (sampling.draws: u (rows, drafts), e (rows, V)),
+                 and every row is decided on the GPU at once.  The tokens
+                 follow the same distribution; a tape made from a lazy run's
+                 draws replays it exactly.
+    host syncs   one per step (the written tokens), instead of one per draft
+                 token (:213, :215, :219, :222).
+    costs        the DSpark prefix scheduler (:236-262) is not built here;
+                 costs raise NotImplementedError rather than be ignored, and
+                 every draft is verified (as the reference does without
+                 costs or confidences).
+"""
+
+import torch
+import torch.nn.functional as F
+
+from . import sampling
+
+DRAFT = 5  # draft tokens per row and step (the reference's DRAFT, :67)
+
+
+def cut(tokens, stops, limit):
+    """tokens up to the first stop token, at most limit of them (:338-344)."""
+    for i, token in enumerate(tokens):
+        if token in stops:
+            tokens = tokens[:i + 1]
+            break
+    return tokens[:limit]
+
+
+class Writer:
+    """Writes for `rows` rows that all start from prompt (a list of ints, at
+    least one); the arguments are the reference's (:71-116)."""
+
+    def __init__(self, model, prompt, rows=1, *, temperature=0.8, top_k=40, generator=None, stops=(), drafter=None,
+                 draft=DRAFT, costs=None, outcomes=None, routes=False):
+        if not prompt:
+            raise ValueError("a prompt holds at least one token")
+        if costs is not None and len(costs) < draft + 1:
+            raise ValueError(f"costs gives {len(costs)} pass times; drafting {draft} tokens needs {draft + 1}")
+        if costs is not None:
+            raise NotImplementedError("the prefix scheduler (costs) is not built in this writer")
+        self.model, self.temperature, self.top_k, self.generator = model, temperature, top_k, generator
+        self.stops, self.drafter, self.draft, self.costs = set(stops), drafter, draft, costs
+        self.outcomes = outcomes
+        self.rounds = self.verified = self.accepted = 0
+        self.device = next(model.parameters()).device
+        self.histories = [list(prompt) for _ in range(rows)]
+        self.pending = [[prompt[-1]] for _ in range(rows)]
+        self.features = tuple(drafter.features) if drafter is not None else ()
+        if self.features:
+            raise NotImplementedError("drafters that read the model's features are not supported by this writer")
+        self.cache = None
+        if hasattr(model, "new_cache"):
+            shared = model.new_cache(1, routes=routes)
+            if len(prompt) > 1:
+                model.extend(self._tensor([prompt[:-1]]), shared)
+            self.cache = shared.select([0] * rows)
+        elif drafter is not None or routes:
+            raise ValueError("drafting and recording routes need a model with a generation cache")
+
+    @torch.no_grad()
+    def write(self, inputs, limits):
+        """inputs: {row: tokens it reads before writing}; limits: {row: the
+        most tokens it may write now, at least 1}.  Returns {row: the tokens
+        it wrote}: at least one, at most its limit, ending at the first stop."""
+        rows = sorted(limits)
+        for row in rows:
+            self.pending[row] += inputs.get(row, [])
+            self.histories[row] += inputs.get(row, [])
+        if self.drafter is not None:
+            written = self._speculate(rows, limits)
+        else:
+            written = {row: [token] for row, token in zip(rows, self._sample(self._scores(rows)))}
+        for row, tokens in written.items():
+            self.histories[row] += tokens
+            self.pending[row] = [tokens[-1]]
+        return written
+
+    def _tensor(self, rows):
+        width = max(len(row) for row in rows)
+        return torch.tensor([row + [0] * (width - len(row)) for row in rows], dtype=torch.long, device=self.device)
+
+    def _read(self, rows, extra=None, undoable=False):
+        feeds = [[] for _ in self.pending]
+        for i, row in enumerate(rows):
+            feeds[row] = self.pending[row] + (extra[i] if extra is not None else [])
+        read = self.model.extend(self._tensor(feeds), self.cache, [len(feed) for feed in feeds], undoable)
+        return read[0][rows], read
+
+    def _scores(self, rows):
+        if self.cache is None:
+            return torch.cat([self.model(self._tensor([self.histories[row]]))[:, -1] for row in rows])
+        scores, _ = self._read(rows)
+        ends = torch.tensor([len(self.pending[row]) - 1 for row in rows], device=self.device)
+        return scores[torch.arange(len(rows), device=self.device), ends]
+
+    def _probabilities(self, scores):
+        """The reference's sampling distribution (:173-179), for drafters."""
+        scores = scores.float() / self.temperature
+        if self.top_k is not None:
+            k = min(self.top_k, scores.size(-1))
+            v, _ = torch.topk(scores, k)
+            scores = scores.masked_fill(scores < v[..., [-1]], float("-inf"))
+        return F.softmax(scores, dim=-1)
+
+    def _sample(self, scores):
+        """One token per row from the distribution of its scores (R, V)."""
+        R, V = scores.shape
+        u, e = sampling.draws(R, 0, V, self.generator, self.device)
+        tokens, counts = sampling.accept(scores[:, None].float(), scores.new_empty(R, 0, V, dtype=torch.float32),
+                                         torch.empty(R, 0, dtype=torch.long, device=self.device), u, e,
+                                         self.temperature, self.top_k)
+        return [row[0] for row in sampling.written(tokens, counts)]
+
+    def _speculate(self, rows, limits):
+        """One step of speculative decoding for rows (:196-233)."""
+        drafted, q, confidences = self.drafter.draft(self.model, [self.histories[row] for row in rows], None,
+                                                     self.draft, self._probabilities, self.generator)
+        drafted, q = drafted.to(self.device), q.to(self.device).float()
+        caps = [min(self.draft, limits[row] - 1) for row in rows]
+        lengths = caps
+        scores, _ = self._read(rows, [drafted[i, :n].tolist() for i, n in enumerate(lengths)], undoable=True)
+        firsts = [len(self.pending[row]) - 1 for row in rows]
+        L = drafted.shape[1]
+        u, e = sampling.draws(len(rows), L, scores.shape[-1], self.generator, self.device)
+        tokens, counts = sampling.accept(scores, q, drafted, u, e, self.temperature, self.top_k, lengths=lengths,
+                                         firsts=firsts)
+        written, kept = {}, [0] * len(self.pending)
+        for i, (row, drawn) in enumerate(zip(rows, sampling.written(tokens, counts))):
+            self.verified += lengths[i]
+            self.accepted += len(drawn) - 1
+            if self.outcomes is not None and confidences is not None:
+                self.outcomes.append((confidences[i, :lengths[i]].tolist(), min(len(drawn) - 1, lengths[i])))
+            drawn = cut(drawn, self.stops, limits[row])
+            written[row] = drawn
+            kept[row] = firsts[i] + len(drawn)
+        self.rounds += 1
+        self.model.undo(self.cache, kept)
+        return written
