@@ -184,8 +184,14 @@ def tree_attention(q, k, v, tree_base, parents, scale, sink=None):
     B, M = q.shape[:2]
     base = tree_base.to(device=q.device, dtype=torch.long)
     positions = base[:, None] + torch.arange(M, device=q.device)
-    masks = tree_ancestors(parents).to(q.device)
+    key = (tuple(int(p) for p in parents), q.device)
+    masks = _TREES.get(key)
+    if masks is None:  # made once per tree and device, outside any graph capture
+        masks = _TREES[key] = tree_ancestors(parents).to(q.device)
     return verify_attention(q, k, v, positions, scale, sink=sink, tree=(base, masks))
+
+
+_TREES = {}  # (parents, device) -> the ancestors-or-self masks on the device
 
 
 def kv_append(table, new, start, counts):

@@ -114,10 +114,13 @@ def greedy_tree(scores, node_tokens, parents):
     scores = _rows_last_contiguous(scores, "scores", 3)
     B, M, V = scores.shape
     device = scores.device
-    parents_ = torch.as_tensor(parents, dtype=torch.int32).to(device)
-    if parents_.shape != (M,) or int(parents_[0]) != -1 or any(not 0 <= int(p) < i for i, p in
-                                                              enumerate(parents_.tolist()) if i > 0):
+    parents = [int(p) for p in parents]
+    if len(parents) != M or parents[0] != -1 or any(not 0 <= p < i for i, p in enumerate(parents) if i > 0):
         raise ValueError("parents must be (M,) with parents[0] = -1 and 0 <= parents[i] < i")
+    key = (tuple(parents), device)
+    parents_ = _PARENTS.get(key)
+    if parents_ is None:  # made once per tree and device, outside any graph capture
+        parents_ = _PARENTS[key] = torch.tensor(parents, dtype=torch.int32, device=device)
     node_tokens = node_tokens.to(device=device, dtype=torch.long).contiguous()
     if node_tokens.shape != (B, M):
         raise ValueError(f"node_tokens must be (B={B}, M={M}); got {tuple(node_tokens.shape)}")
@@ -130,6 +133,9 @@ def greedy_tree(scores, node_tokens, parents):
                                       ptr(parents_), B, M, V, ptr(path), ptr(tokens), ptr(counts), ptr(workspace),
                                       size, _lib.stream(device)), "greedy_tree")
     return path, tokens, counts
+
+
+_PARENTS = {}  # (parents, device) -> the parents on the device
 
 
 def written(tokens, counts):
