@@ -69,16 +69,16 @@ __device__ __forceinline__ bool tree_visible(int n, int64_t tbase, uint64_t anc)
 // ---------------------------------------------------------------------------
 
 template <int C>
-struct Geo {
+struct Tile {
   static constexpr int kSteps = C / 32;             // k-steps of the QK^T product (16x16x32)
   static constexpr int kCBlocks = C / 16;           // 16-wide column blocks of O
-  static constexpr int kBlock = 16 * C;             // one 16-row block of K or V (bf16 elements)
-  static constexpr int kLoads = kBlock * 2 / 1024;  // 1 KiB DMA instructions per block
-  static constexpr int kStage = 2 * kBlock;         // K block then V block
-  static constexpr int kSlots = C == 128 ? 4 : 8;   // 16-row stages per wavefront (32 KiB)
-  static constexpr int kAhead = kSlots / 2 - 1;     // 32-row pairs in flight while one is computed
-  static constexpr int kLdsElems = kWaves * kSlots * kStage;
+  static constexpr int kHalf = 16 * C;              // one 16-row block of K or V (bf16 elements)
+  static constexpr int kElems = 4 * kHalf;          // a 32-row tile: K rows 0-15, 16-31, then V rows 0-15, 16-31
+  static constexpr int kLoads = kElems * 2 / 1024;  // 1 KiB DMA instructions per tile (16 at head width 128)
+  static constexpr int kPerHalf = C / 32;           // DMA instructions per 16-row half
+  static constexpr int kSlots = 4;                  // tiles in each key-set's ring
 };
+constexpr int kKeySets = 2;  // wavefront sets that take alternate tiles of the workgroup's key range
 
 // Softmax rescaling is deferred until a row's maximum grows by more than this
 // many powers of two (the stale maximum stays the reference for p and l, so
@@ -94,6 +94,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 // A raw buffer resource over 4 GiB from `base` (gfx9 dword3 format).
 __device__ __forceinline__ i32x4 buffer_resource(const void* base) {
@@ -113,8 +115,8 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 // Global -> LDS copy of 16 bytes per lane: lane l's bytes land at LDS byte
 // address `lds` + 16 l.  Written as inline assembly so that the compiler's
 // conservative wait (all loads, before any LDS read of the kernel) is not
-// inserted: the kernel waits for each stage itself with wait_vmcnt.  The
-// s_nop covers the M0-write -> LDS-DMA hazard.
+// inserted: the kernel waits for each tile itself.  The s_nop covers the
+// M0-write -> LDS-DMA hazard.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma_16B(i32x4 rsrc, uint32_t voffset, uint32_t lds) {
@@ -132,33 +134,51 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(const float (&p)[8]) {
   return r;
 }
 
-template <int C, int MBW, bool TREE>
-__global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
+// max / sum over the four 16-lane groups (lanes j, j+16, j+32, j+48).
+__device__ __forceinline__ float group_max(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float group_sum(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// One workgroup per (batch row, row group, key split): kKeySets x MB
+// wavefronts; wavefront (s, mb) holds m-block mb (16 query rows) and takes the
+// 32-row key tiles s, s + 2, ... of the split.  The tiles of a key set are
+// DMA'd into its LDS ring by its first DMAW wavefronts and read by all MB of
+// them; a workgroup barrier per iteration hands them over.
+template <int C, int MB, bool TREE>
+__global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     const unsigned short* __restrict__ q, const unsigned short* __restrict__ k, int64_t ksb, int64_t ksn,
     const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn, const int64_t* __restrict__ positions,
     int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
     const float* __restrict__ sink, int T, int H, int N, float scale_log2, int groups, int splits,
     int range_from_positions, int xcd_map, unsigned short* __restrict__ out, float* __restrict__ lse_out,
     float* __restrict__ part_o, float* __restrict__ part_lse) {
-  using G = Geo<C>;
-  constexpr int kRows = 16 * MBW;  // query rows per workgroup
-  static_assert(kRows * C * 4 <= G::kLdsElems * 2, "the merge buffer reuses the stages");
-  static_assert(64 % (C / 8) == 0, "rows per DMA instruction");
-  __shared__ __attribute__((aligned(16))) unsigned short lds[G::kLdsElems];
-  __shared__ __attribute__((aligned(16))) unsigned short qlds[kRows * C];
-  __shared__ float sm_m[kWaves][kRows];
-  __shared__ float sm_l[kWaves][kRows];
-  __shared__ float fin_scale[kRows];
-  __shared__ float fin_lse[kRows];
+  using G = Tile<C>;
+  constexpr int kRows = 16 * MB;
+  constexpr int DMAW = MB >= 4 ? 4 : (MB >= 2 ? 2 : 1);  // wavefronts of a key set that issue its DMA
+  constexpr int kCnt = G::kLoads / DMAW;                 // DMA instructions per such wavefront and tile
+  constexpr int kRing = G::kSlots * G::kElems;           // elements of one key set's ring
+  constexpr int kPitch = C + 4;                          // merge buffer row pitch (floats): distinct banks
+  static_assert(G::kLoads % DMAW == 0, "DMA split");
+  static_assert(MB * (16 * kPitch + 32) * 4 <= kKeySets * kRing * 2, "the merge buffer reuses the rings");
+  __shared__ __attribute__((aligned(16))) unsigned short lds[kKeySets * kRing];
+  __shared__ __attribute__((aligned(16))) unsigned short qlds[MB * 16 * C];  // each m-block's queries
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kset = wid / MB, mb = wid % MB;
   const int j = lane & 15;  // this lane's column: query row (S^T, O^T) or key row (K operand)
   const int g = lane >> 4;  // lane group 0..3
 
-  // Workgroup -> (batch row, row group, split).  With xcd_map the splits of
-  // one (batch row, row group) unit share an XCD (workgroups are dispatched
-  // round-robin over the 8 XCDs), so its queries and parts stay in one L2.
   int unit, split;
   {
     const int L = blockIdx.x;
@@ -176,16 +196,13 @@ __global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
   const int R = T * H;
   const int r_base = grp * kRows;
   const int64_t* pos_b = positions + (int64_t)b * T;
-  const int t_first = r_base / H;
-  const int t_last = ((r_base + kRows < R ? r_base + kRows : R) - 1) / H;
 
-  // The key rows this workgroup's queries can see.  Full causal attention of
-  // one query group reads the whole table, whatever the positions say, so the
-  // first loads need no position (rows past a query are masked below).
+  // The key rows this workgroup's queries can see.
   int u_lo = 0, u_hi = N - 1;
   if (range_from_positions) {
     u_lo = INT_MAX;
     u_hi = -1;
+    const int t_first = r_base / H, t_last = (min(r_base + kRows, R) - 1) / H;
     for (int t = t_first; t <= t_last; ++t) {
       const Bounds bt = query_bounds(pos_b, t, window, N);
       if (bt.hi >= bt.lo) {
@@ -198,293 +215,232 @@ __global__ __launch_bounds__(kThreads, 1) void verify_attention_mfma(
   if (u_hi >= u_lo) {
     const int U = u_hi - u_lo + 1;
     int per = (U + splits - 1) / splits;
-    per = (per + 32 * kWaves - 1) / (32 * kWaves) * (32 * kWaves);
+    per = (per + 32 * kKeySets - 1) / (32 * kKeySets) * (32 * kKeySets);
     s_lo = u_lo + split * per;
     s_hi = min(s_lo + per - 1, u_hi);
   }
-  const int nblocks = s_hi >= s_lo ? (s_hi - s_lo + 1 + 15) / 16 : 0;
-  const int npairs = (nblocks + 1) / 2;
-  const int mine = npairs > wave ? (npairs - wave + kWaves - 1) / kWaves : 0;  // pairs of this wavefront
+  const int ntiles = s_hi >= s_lo ? (s_hi - s_lo + 1 + 31) / 32 : 0;
+  const int niter = (ntiles + kKeySets - 1) / kKeySets;       // workgroup iterations
+  const int mine = ntiles > kset ? (ntiles - kset + kKeySets - 1) / kKeySets : 0;  // tiles of this key set
 
-  // Byte offsets within one batch row's keys and values fit 32 bits: the
-  // host checks that N rows of the table do.
+  // DMA: instruction ii of a tile covers 16 rows x 64 bytes of one half
+  // (part = ii / kPerHalf: K rows 0-15, K rows 16-31, V rows 0-15, V rows 16-31).
+  // LDS layout of a half, chunk-major: the 16-byte chunk x of row r at unit
+  // 16x + r, so lane l of the instruction fills unit 64 (ii % kPerHalf) + l.
   const i32x4 krs = buffer_resource(k + (int64_t)b * ksb);
   const i32x4 vrs = buffer_resource(v + (int64_t)b * vsb);
   const uint32_t krow_bytes = (uint32_t)ksn * 2u, vrow_bytes = (uint32_t)vsn * 2u;
-  unsigned short* const ring = lds + wave * G::kSlots * G::kStage;
+  unsigned short* const ring = lds + kset * kRing;
   const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_address(ring));
-
-  // LDS layout of a 16-row block, chunk-major: the 16-byte chunk x (columns
-  // 8x..8x+7) of row r sits at unit 16x + r.  Lane l of DMA instruction i
-  // fills unit 64i + l, i.e. chunk 4i + (l >> 4) of row l & 15, so every MFMA
-  // operand read below is a per-lane base plus a constant offset.  Pair p of
-  // this wavefront (32 rows) fills slots 2p, 2p + 1 (mod kSlots).
-  auto issue = [&](int it) {
-    const int pair = wave + it * kWaves;
-    const uint32_t slot0 = ring_lds + (uint32_t)((2 * it) % G::kSlots) * (G::kStage * 2);
+  const bool dma_wave = mb < DMAW;
+  auto issue = [&](int it) {  // this wavefront's share of the key set's tile of iteration it
+    const int tile = kset + it * kKeySets;
+    const uint32_t slot = ring_lds + (uint32_t)(it % G::kSlots) * (G::kElems * 2);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      int n = s_lo + (2 * pair + h) * 16 + j;
+    for (int c = 0; c < kCnt; ++c) {
+      const int ii = mb * kCnt + c;
+      const int part = ii / G::kPerHalf, chunk = ii % G::kPerHalf;
+      int n = s_lo + tile * 32 + 16 * (part & 1) + j;
       n = n < s_hi ? n : s_hi;  // rows past the split are masked; read a valid one
-      const uint32_t koff = (uint32_t)n * krow_bytes + 16u * g;
-      const uint32_t voff = (uint32_t)n * vrow_bytes + 16u * g;
-      const uint32_t st = slot0 + h * (G::kStage * 2);
-#pragma unroll
-      for (int i = 0; i < G::kLoads; ++i) {
-        dma_16B(krs, koff + 64u * i, st + 1024u * i);
-        dma_16B(vrs, voff + 64u * i, st + G::kBlock * 2 + 1024u * i);
-      }
+      const uint32_t off = (uint32_t)n * (part < 2 ? krow_bytes : vrow_bytes) + 64u * chunk + 16u * g;
+      dma_16B(part < 2 ? krs : vrs, off, slot + part * (G::kHalf * 2) + 1024u * chunk);
     }
   };
+  // Every load before the loop goes out before the first wait: this
+  // wavefront's 16 query rows (DMA into qlds, laid out like a key half, so
+  // that the Q^T operand of k-step s is unit 64s + lane), the first tiles,
+  // then the bounds.  One explicit wait completes them all, so the compiler
+  // places no waits of its own inside the loop (it cannot count the DMA).
+  const int r = r_base + 16 * mb + j;
+  const bool real = r < R;
+  {
+    const i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
+    const uint32_t qoff = (uint32_t)(real ? r : R - 1) * (uint32_t)(C * 2) + 16u * g;  // a padding row reads row R-1
+    const uint32_t qdst = __builtin_amdgcn_readfirstlane(lds_address(qlds + mb * 16 * C));
 #pragma unroll
-  for (int it = 0; it < G::kAhead; ++it)
-    if (it < mine) issue(it);
-
-  // Workgroup-uniform bounds: the rows every query of the group sees.
-  int f_lo = 0, f_hi = INT_MAX;
-  for (int t = t_first; t <= t_last; ++t) {
-    const Bounds bt = query_bounds(pos_b, t, window, N);
-    f_lo = max(f_lo, bt.lo);
-    f_hi = min(f_hi, bt.hi);
+    for (int s = 0; s < G::kSteps; ++s) dma_16B(qrs, qoff + 64u * s, qdst + 1024u * s);
   }
+  if (dma_wave) {
+#pragma unroll
+    for (int it = 0; it < G::kSlots - 1; ++it)
+      if (it < mine) issue(it);
+  }
+  int lo = 0, hi = -1;
+  uint64_t anc = 0;
   const int64_t tbase = TREE ? tree_base[b] : (int64_t)INT_MAX;
-  if (TREE && tbase <= (int64_t)f_hi) f_hi = (int)tbase - 1;
-
-  // Per-lane query rows (one per m-block) and their bounds.
-  int lo[MBW], hi[MBW];
-  uint64_t anc[TREE ? MBW : 1];
+  if (real) {
+    const int t = r / H;
+    const Bounds bt = query_bounds(pos_b, t, window, N);
+    lo = bt.lo;
+    hi = min(bt.hi, s_hi);
+    if constexpr (TREE) anc = ancestors[t];
+  }
+  wait_vmcnt<0>();
+  bf16x8 qf[G::kSteps];
 #pragma unroll
-  for (int mb = 0; mb < MBW; ++mb) {
-    const int r = r_base + 16 * mb + j;
-    if (r < R) {
-      const int t = r / H;
-      const Bounds bt = query_bounds(pos_b, t, window, N);
-      lo[mb] = bt.lo;
-      hi[mb] = min(bt.hi, s_hi);
-      if constexpr (TREE) anc[mb] = ancestors[t];
+  for (int s = 0; s < G::kSteps; ++s)
+    qf[s] = *reinterpret_cast<const bf16x8*>(qlds + mb * 16 * C + 512 * s + 8 * lane);
+  int f_lo = 0, f_hi = INT_MAX;  // rows every query of the wavefront sees
+  {
+    const int w_first = r_base + 16 * mb;
+    if (w_first < R) {
+      const int t_first = w_first / H, t_last = (min(w_first + 16, R) - 1) / H;
+      for (int t = t_first; t <= t_last; ++t) {
+        const Bounds bt = query_bounds(pos_b, t, window, N);
+        f_lo = max(f_lo, bt.lo);
+        f_hi = min(f_hi, bt.hi);
+      }
     } else {
-      lo[mb] = 0;
-      hi[mb] = -1;
-      if constexpr (TREE) anc[mb] = 0;
+      f_hi = -1;
     }
-  }
-  // The group's queries in LDS, each 16-row m-block laid out like a key
-  // block (chunk-major), zeros past the last row: the Q^T operand of m-block
-  // mb at k-step s is then one conflict-free 16-byte read per lane.
-  for (int u = threadIdx.x; u < kRows * (C / 8); u += kThreads) {
-    const int mb = u / (16 * (C / 8));
-    const int rest = u % (16 * (C / 8));
-    const int x = rest / 16, rr = rest % 16;  // chunk, row within the m-block
-    const int r = r_base + 16 * mb + rr;
-    u16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (r < R) val = *reinterpret_cast<const u16x8*>(q + ((int64_t)b * R + r) * C + 8 * x);
-    *reinterpret_cast<u16x8*>(qlds + u * 8) = val;
-  }
-  __syncthreads();
-
-  f32x4 o[MBW][G::kCBlocks];
-  float m_run[MBW], l_run[MBW];
-#pragma unroll
-  for (int mb = 0; mb < MBW; ++mb) {
-    m_run[mb] = kNegInf;
-    l_run[mb] = 0.f;
-#pragma unroll
-    for (int cb = 0; cb < G::kCBlocks; ++cb) o[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (TREE && tbase <= (int64_t)f_hi) f_hi = (int)tbase - 1;
+    f_hi = min(f_hi, s_hi);
   }
 
-  // One pair: scores of 32 key rows for every query row of the group.
-  float x[MBW][8];
-  float bm[MBW];
-  auto scores = [&](int it) {
-    const unsigned short* st0 = ring + ((2 * it) % G::kSlots) * G::kStage;
-    const unsigned short* st1 = st0 + G::kStage;
-    const int n0 = s_lo + (wave + it * kWaves) * 32;
-    // S^T = K . Q^T: lane (j, g) reads key row j, chunk 4s + g (unit 64s + lane).
-    f32x4 sacc[2][MBW];
+  f32x4 o[G::kCBlocks];
 #pragma unroll
-    for (int mb = 0; mb < MBW; ++mb) sacc[0][mb] = sacc[1][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int cb = 0; cb < G::kCBlocks; ++cb) o[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegInf, l_run = 0.f;
+  // per-lane element offset of the transposed V reads: lane 16g + 4rr + qq
+  // addresses row 4g + rr, columns 4qq..4qq+3 of a 16-column block
+  const int tr_off = 128 * ((lane & 3) >> 1) + 32 * g + 8 * ((lane >> 2) & 3) + 4 * (lane & 1);
+
+#pragma unroll 1
+  for (int it = 0; it < niter; ++it) {
+    const bool have = it < mine;
+    if (dma_wave && have) {
+      // this wavefront's loads of iteration it are done once at most those of
+      // the (up to kSlots - 2) later iterations already issued are in flight
+      const int later = min(G::kSlots - 2, mine - 1 - it);
+      if (later >= 2)
+        wait_vmcnt<2 * kCnt>();
+      else if (later == 1)
+        wait_vmcnt<kCnt>();
+      else
+        wait_vmcnt<0>();
+    }
+    // The tile of iteration it is in LDS; every wavefront is done with
+    // iteration it - 1.  A bare barrier: the DMA-issuing wavefronts waited for
+    // their own loads, and a fence here would wait for the later tiles too.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (dma_wave && it + G::kSlots - 1 < mine) issue(it + G::kSlots - 1);
+    if (!have) continue;
+
+    const unsigned short* st = ring + (it % G::kSlots) * G::kElems;
+    const int n0 = s_lo + (kset + it * kKeySets) * 32;
+    // S^T = K . Q^T for the two 16-row halves: lane (j, g) reads key row j, chunk 4s + g.
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < G::kSteps; ++s) {
-      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(st0 + 512 * s + 8 * lane);
-      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(st1 + 512 * s + 8 * lane);
-#pragma unroll
-      for (int mb = 0; mb < MBW; ++mb) {
-        const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qlds + mb * 16 * C + 512 * s + 8 * lane);
-        sacc[0][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qv, sacc[0][mb], 0, 0, 0);
-        sacc[1][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qv, sacc[1][mb], 0, 0, 0);
-      }
+      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(st + 512 * s + 8 * lane);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(st + G::kHalf + 512 * s + 8 * lane);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[s], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[s], s1, 0, 0, 0);
     }
-    const bool full = n0 >= f_lo && n0 + 31 <= f_hi && n0 + 31 <= s_hi;
+    float x[8];
 #pragma unroll
-    for (int mb = 0; mb < MBW; ++mb) {
+    for (int i = 0; i < 4; ++i) {
+      x[i] = s0[i] * scale_log2;
+      x[4 + i] = s1[i] * scale_log2;
+    }
+    if (!(n0 >= f_lo && n0 + 31 <= f_hi)) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[mb][4 * h + i] = sacc[h][mb][i] * scale_log2;
-      if (!full) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int n = n0 + 16 * h + 4 * g + i;
-            bool vis = n >= lo[mb] && n <= hi[mb];
-            if constexpr (TREE) vis = vis && tree_visible(n, tbase, anc[mb]);
-            x[mb][4 * h + i] = vis ? x[mb][4 * h + i] : kNegInf;
-          }
-      }
-      float t = fmaxf(fmaxf(fmaxf(x[mb][0], x[mb][1]), fmaxf(x[mb][2], x[mb][3])),
-                      fmaxf(fmaxf(x[mb][4], x[mb][5]), fmaxf(x[mb][6], x[mb][7])));
-      t = fmaxf(t, __shfl_xor(t, 16, 64));
-      t = fmaxf(t, __shfl_xor(t, 32, 64));
-      bm[mb] = t;
+        for (int i = 0; i < 4; ++i) {
+          const int n = n0 + 16 * h + 4 * g + i;
+          bool vis = n >= lo && n <= hi;
+          if constexpr (TREE) vis = vis && tree_visible(n, tbase, anc);
+          x[4 * h + i] = vis ? x[4 * h + i] : kNegInf;
+        }
     }
-  };
-  // The probabilities of the pair against the running maxima, and O^T += V^T . P^T.
-  auto accumulate = [&](int it) {
-    const unsigned short* st0 = ring + ((2 * it) % G::kSlots) * G::kStage;
-    bf16x8 pt[MBW];
+    float bm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+    bm = group_max(bm);
+    if (bm > m_run + kRescale) {  // this lane's row: rescale its sums to the new maximum
+      const float alpha = m_run == kNegInf ? 0.f : exp2f(m_run - bm);
+      m_run = bm;
+      l_run *= alpha;
 #pragma unroll
-    for (int mb = 0; mb < MBW; ++mb) {
-      float p[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) p[e] = (m_run[mb] == kNegInf) ? 0.f : exp2f(x[mb][e] - m_run[mb]);
-      l_run[mb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-      pt[mb] = pack_bf16x8(p);
+      for (int cb = 0; cb < G::kCBlocks; ++cb) o[cb] *= alpha;
     }
-    // P^T operand: lane (j, g) holds k-index 8g + e = key 4g + e (e < 4) of
-    // the first 16 rows, key 16 + 4g + e - 4 of the second.  V^T operand:
-    // the same keys at column cb*16 + j: chunk 2cb + (j >> 3), units
-    // 16 (2cb + (j >> 3)) + 4g + i of each stage.
-    const unsigned short* vs = st0 + G::kBlock + 128 * (j >> 3) + 32 * g + (j & 7);
+    float p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p[e] = m_run == kNegInf ? 0.f : exp2f(x[e] - m_run);
+    l_run += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    // P^T operand: lane (j, g) holds k-index 8g + e = key 4g + e of the first
+    // half (e < 4), key 16 + 4g + e - 4 of the second; the V^T operand holds
+    // the same keys at column cb*16 + j, two transposed 4-row reads.
+    const bf16x8 pt = pack_bf16x8(p);
+    const unsigned short* vs = st + 2 * G::kHalf + tr_off;
 #pragma unroll
     for (int cb = 0; cb < G::kCBlocks; ++cb) {
-      const unsigned short* w = vs + 256 * cb;
-      const u16x8 vt = u16x8{w[0], w[8], w[16], w[24], w[G::kStage], w[G::kStage + 8], w[G::kStage + 16],
-                             w[G::kStage + 24]};
-      const bf16x8 vb = __builtin_bit_cast(bf16x8, vt);
-#pragma unroll
-      for (int mb = 0; mb < MBW; ++mb) o[mb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vb, pt[mb], o[mb][cb], 0, 0, 0);
+      const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vs + 256 * cb));
+      const s16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vs + G::kHalf + 256 * cb));
+      typedef short s16x8 __attribute__((ext_vector_type(8)));
+      const s16x8 vt = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+      o[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vt), pt, o[cb], 0, 0, 0);
     }
-  };
-
-  int it = 0;
-  while (it < mine) {
-    // Fast loop: the accumulators are touched by MFMAs only.
-    bool grown = false;
-#pragma unroll 1
-    for (; it < mine; ++it) {
-      asm volatile("" ::: "memory");
-      if (it + G::kAhead < mine) {
-        issue(it + G::kAhead);
-        wait_vmcnt<4 * G::kLoads * G::kAhead>();
-      } else {
-        wait_vmcnt<0>();
-      }
-      scores(it);
-      bool grow = false;
-#pragma unroll
-      for (int mb = 0; mb < MBW; ++mb) grow = grow || (bm[mb] > m_run[mb] + kRescale);
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        grown = true;
-        break;
-      }
-      accumulate(it);
-    }
-    if (!grown) break;
-    // A row's maximum grew: rescale its sums to the new maximum, then finish the pair.
-#pragma unroll
-    for (int mb = 0; mb < MBW; ++mb) {
-      const float m_new = fmaxf(m_run[mb], bm[mb]);
-      const float alpha = (m_new == kNegInf || m_run[mb] == kNegInf) ? 0.f : exp2f(m_run[mb] - m_new);
-      m_run[mb] = m_new;
-      l_run[mb] *= alpha;
-#pragma unroll
-      for (int cb = 0; cb < G::kCBlocks; ++cb) o[mb][cb] *= alpha;
-    }
-    accumulate(it);
-    ++it;
   }
   wait_vmcnt<0>();
+  l_run = group_sum(l_run);
 
-  // ---- merge the four wavefronts (the merge buffer reuses the stages) ----
+  // ---- merge the key sets (the merge buffer reuses the rings) ----
   __syncthreads();
+  float* mbuf = reinterpret_cast<float*>(lds) + mb * (16 * kPitch + 32);  // this m-block's O, then m, l
+  if (kset == 1) {
 #pragma unroll
-  for (int mb = 0; mb < MBW; ++mb) {
-    l_run[mb] += __shfl_xor(l_run[mb], 16, 64);
-    l_run[mb] += __shfl_xor(l_run[mb], 32, 64);
+    for (int cb = 0; cb < G::kCBlocks; ++cb)
+      *reinterpret_cast<f32x4*>(mbuf + j * kPitch + cb * 16 + 4 * g) = o[cb];
     if (g == 0) {
-      sm_m[wave][mb * 16 + j] = m_run[mb];
-      sm_l[wave][mb * 16 + j] = l_run[mb];
+      mbuf[16 * kPitch + j] = m_run;
+      mbuf[16 * kPitch + 16 + j] = l_run;
     }
   }
   __syncthreads();
-  float* obuf = reinterpret_cast<float*>(lds);
-  float wscale[MBW];
+  if (kset != 0) return;
+  {
+    const float m1 = mbuf[16 * kPitch + j], l1 = mbuf[16 * kPitch + 16 + j];
+    const float M = fmaxf(m_run, m1);
+    const float a0 = m_run == kNegInf ? 0.f : exp2f(m_run - M);
+    const float a1 = m1 == kNegInf ? 0.f : exp2f(m1 - M);
 #pragma unroll
-  for (int mb = 0; mb < MBW; ++mb) {
-    float M = kNegInf;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][mb * 16 + j]);
-    wscale[mb] = (m_run[mb] == kNegInf) ? 0.f : exp2f(m_run[mb] - M);
+    for (int cb = 0; cb < G::kCBlocks; ++cb)
+      o[cb] = o[cb] * a0 + *reinterpret_cast<const f32x4*>(mbuf + j * kPitch + cb * 16 + 4 * g) * a1;
+    l_run = l_run * a0 + l1 * a1;
+    m_run = M;
   }
-  for (int w = 0; w < kWaves; ++w) {
-    if (wave == w) {
-#pragma unroll
-      for (int mb = 0; mb < MBW; ++mb) {
-#pragma unroll
-        for (int cb = 0; cb < G::kCBlocks; ++cb) {
-          f32x4* dst = reinterpret_cast<f32x4*>(obuf + (mb * 16 + j) * C + cb * 16 + 4 * g);
-          const f32x4 val = o[mb][cb] * wscale[mb];
-          if (w == 0)
-            *dst = val;
-          else
-            *dst += val;
-        }
-      }
-    }
-    __syncthreads();
-  }
+  if (!real) return;
 
-  // Final statistics per query row (the sink joins the denominator when the
+  // Final statistics of the row (the sink joins the denominator when the
   // split is the whole range), then the output or this split's part.
-  if (threadIdx.x < kRows) {
-    const int rr = threadIdx.x;
-    float M = kNegInf;
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][rr]);
-    float L = 0.f;
-    if (M != kNegInf)
-      for (int w = 0; w < kWaves; ++w)
-        if (sm_m[w][rr] != kNegInf) L += sm_l[w][rr] * exp2f(sm_m[w][rr] - M);
-    float f = 1.f;
-    if (splits == 1 && sink && r_base + rr < R) {
-      const float sl = sink[(r_base + rr) % H] * kLog2e;
-      const float M2 = fmaxf(M, sl);
-      f = (M == kNegInf) ? 0.f : exp2f(M - M2);
-      L = L * f + exp2f(sl - M2);
-      M = M2;
-    }
-    fin_scale[rr] = L > 0.f ? f / L : 0.f;
-    fin_lse[rr] = L > 0.f ? M + log2f(L) : kNegInf;
+  float M = m_run, L = l_run, f = 1.f;
+  if (splits == 1 && sink) {
+    const float sl = sink[r % H] * kLog2e;
+    const float M2 = fmaxf(M, sl);
+    f = (M == kNegInf) ? 0.f : exp2f(M - M2);
+    L = L * f + exp2f(sl - M2);
+    M = M2;
   }
-  __syncthreads();
-
-  const int rows_here = min(kRows, R - r_base);
-  constexpr int kVec = 4;
-  for (int idx = threadIdx.x; idx < rows_here * (C / kVec); idx += kThreads) {
-    const int rr = idx / (C / kVec);
-    const int c4 = (idx % (C / kVec)) * kVec;
-    const int r = r_base + rr;
-    const f32x4 val = *reinterpret_cast<const f32x4*>(obuf + rr * C + c4) * fin_scale[rr];
-    if (splits == 1) {
-      typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
-      *reinterpret_cast<u16x4*>(out + ((int64_t)b * R + r) * C + c4) =
+  const float scale_out = L > 0.f ? f / L : 0.f;
+  const float lse2 = L > 0.f ? M + log2f(L) : kNegInf;
+  if (splits == 1) {
+    typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+    unsigned short* orow = out + ((int64_t)b * R + r) * C;
+#pragma unroll
+    for (int cb = 0; cb < G::kCBlocks; ++cb) {
+      const f32x4 val = o[cb] * scale_out;
+      *reinterpret_cast<u16x4*>(orow + cb * 16 + 4 * g) =
           u16x4{f32_to_bf16(val[0]), f32_to_bf16(val[1]), f32_to_bf16(val[2]), f32_to_bf16(val[3])};
-      if (lse_out && c4 == 0) lse_out[(int64_t)b * R + r] = fin_lse[rr] * kLn2;
-    } else {
-      const int64_t prow = ((int64_t)unit * splits + split) * kRows + rr;
-      *reinterpret_cast<f32x4*>(part_o + prow * C + c4) = val;
-      if (c4 == 0) part_lse[prow] = fin_lse[rr];
     }
+    if (lse_out && g == 0) lse_out[(int64_t)b * R + r] = lse2 * kLn2;
+  } else {
+    const int64_t prow = ((int64_t)unit * splits + split) * kRows + 16 * mb + j;
+#pragma unroll
+    for (int cb = 0; cb < G::kCBlocks; ++cb)
+      *reinterpret_cast<f32x4*>(part_o + prow * C + cb * 16 + 4 * g) = o[cb] * scale_out;
+    if (g == 0) part_lse[prow] = lse2;
   }
 }
 
@@ -692,9 +648,9 @@ int plan(int B, int T, int H, int c, int N, int window, int dtype, int flags, in
   if (splits <= 0) {
     const long long cus = compute_units();
     const long long wgs = (long long)B * p.groups;
-    // Enough workgroups to fill the GPU, each at least 32 key rows per wavefront.
+    // Enough workgroups to fill the GPU, each at least one 32-row tile per key set.
     long long s = (cus + wgs - 1) / wgs;
-    const long long max_s = (span + 32 * kWaves - 1) / (32 * kWaves);
+    const long long max_s = (span + 32 * kKeySets - 1) / (32 * kKeySets);
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
     splits = (int)s;
@@ -717,9 +673,9 @@ void launch_mfma(dim3 grid, hipStream_t stream, const unsigned short* q, const u
                  int window, const int64_t* tree_base, const uint64_t* ancestors, const float* sink, int T, int H,
                  int N, float scale_log2, int groups, int splits, int range_from_positions, int xcd_map,
                  unsigned short* out, float* lse, float* part_o, float* part_lse) {
-  hipLaunchKernelGGL((verify_attention_mfma<C, MBW, TREE>), grid, dim3(kThreads), 0, stream, q, k, ksb, ksn, v, vsb,
-                     vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, groups, splits,
-                     range_from_positions, xcd_map, out, lse, part_o, part_lse);
+  hipLaunchKernelGGL((verify_attention_mfma<C, MBW, TREE>), grid, dim3(kKeySets * MBW * 64), 0, stream, q, k, ksb,
+                     ksn, v, vsb, vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, groups,
+                     splits, range_from_positions, xcd_map, out, lse, part_o, part_lse);
 }
 
 }  // namespace
