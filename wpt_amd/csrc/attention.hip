@@ -246,14 +246,16 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
       dma_16B(part < 2 ? krs : vrs, off, slot + part * (G::kHalf * 2) + 1024u * chunk);
     }
   };
-  // Every load before the loop goes out before the first wait: this
-  // wavefront's 16 query rows (DMA into qlds, laid out like a key half, so
-  // that the Q^T operand of k-step s is unit 64s + lane), the first tiles,
-  // then the bounds.  One explicit wait completes them all, so the compiler
-  // places no waits of its own inside the loop (it cannot count the DMA).
+  // The queries go out first (DMA into qlds, each m-block laid out like a
+  // key half, so that the Q^T operand of k-step s is unit 64s + lane; the
+  // first key set loads them, the second reads them after the first
+  // barrier), then the first tiles.  Waiting for tile 0 then implies the
+  // queries.  The bounds come through scalar loads, on their own counter, so
+  // the compiler needs no vector-memory wait of its own inside the loop (it
+  // cannot count the DMA).
   const int r = r_base + 16 * mb + j;
   const bool real = r < R;
-  {
+  if (kset == 0) {
     const i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
     const uint32_t qoff = (uint32_t)(real ? r : R - 1) * (uint32_t)(C * 2) + 16u * g;  // a padding row reads row R-1
     const uint32_t qdst = __builtin_amdgcn_readfirstlane(lds_address(qlds + mb * 16 * C));
@@ -265,30 +267,30 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     for (int it = 0; it < G::kSlots - 1; ++it)
       if (it < mine) issue(it);
   }
+  // Per-row bounds: the wavefront's 16 rows span positions t_first..t_last;
+  // each position is read with a uniform (scalar) load and the lanes of that
+  // position take it.  f_lo, f_hi: the rows every query of the wavefront sees.
   int lo = 0, hi = -1;
   uint64_t anc = 0;
+  int f_lo = 0, f_hi = INT_MAX;
   const int64_t tbase = TREE ? tree_base[b] : (int64_t)INT_MAX;
-  if (real) {
-    const int t = r / H;
-    const Bounds bt = query_bounds(pos_b, t, window, N);
-    lo = bt.lo;
-    hi = min(bt.hi, s_hi);
-    if constexpr (TREE) anc = ancestors[t];
-  }
-  wait_vmcnt<0>();
-  bf16x8 qf[G::kSteps];
-#pragma unroll
-  for (int s = 0; s < G::kSteps; ++s)
-    qf[s] = *reinterpret_cast<const bf16x8*>(qlds + mb * 16 * C + 512 * s + 8 * lane);
-  int f_lo = 0, f_hi = INT_MAX;  // rows every query of the wavefront sees
   {
     const int w_first = r_base + 16 * mb;
     if (w_first < R) {
       const int t_first = w_first / H, t_last = (min(w_first + 16, R) - 1) / H;
+      const int my_t = real ? r / H : -1;
       for (int t = t_first; t <= t_last; ++t) {
         const Bounds bt = query_bounds(pos_b, t, window, N);
         f_lo = max(f_lo, bt.lo);
         f_hi = min(f_hi, bt.hi);
+        if (my_t == t) {
+          lo = bt.lo;
+          hi = min(bt.hi, s_hi);
+        }
+        if constexpr (TREE) {
+          const uint64_t a = ancestors[t];
+          if (my_t == t) anc = a;
+        }
       }
     } else {
       f_hi = -1;
@@ -297,6 +299,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     f_hi = min(f_hi, s_hi);
   }
 
+  bf16x8 qf[G::kSteps];
   f32x4 o[G::kCBlocks];
 #pragma unroll
   for (int cb = 0; cb < G::kCBlocks; ++cb) o[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -305,13 +308,11 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   // addresses row 4g + rr, columns 4qq..4qq+3 of a 16-column block
   const int tr_off = 128 * ((lane & 3) >> 1) + 32 * g + 8 * ((lane >> 2) & 3) + 4 * (lane & 1);
 
-#pragma unroll 1
-  for (int it = 0; it < niter; ++it) {
-    const bool have = it < mine;
-    if (dma_wave && have) {
-      // this wavefront's loads of iteration it are done once at most those of
-      // the (up to kSlots - 2) later iterations already issued are in flight
-      const int later = min(G::kSlots - 2, mine - 1 - it);
+  // Waits for this key set's tile of iteration t (each DMA wavefront for its
+  // own loads, at most `later` tiles' loads still in flight behind it), then
+  // a bare workgroup barrier: a fence here would wait for the later tiles too.
+  auto arrive = [&](int t, int later) {
+    if (dma_wave && t < mine) {
       if (later >= 2)
         wait_vmcnt<2 * kCnt>();
       else if (later == 1)
@@ -319,19 +320,15 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
       else
         wait_vmcnt<0>();
     }
-    // The tile of iteration it is in LDS; every wavefront is done with
-    // iteration it - 1.  A bare barrier: the DMA-issuing wavefronts waited for
-    // their own loads, and a fence here would wait for the later tiles too.
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (dma_wave && it + G::kSlots - 1 < mine) issue(it + G::kSlots - 1);
-    if (!have) continue;
-
-    const unsigned short* st = ring + (it % G::kSlots) * G::kElems;
-    const int n0 = s_lo + (kset + it * kKeySets) * 32;
-    // S^T = K . Q^T for the two 16-row halves: lane (j, g) reads key row j, chunk 4s + g.
-    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  };
+  // S^T = K . Q^T of a tile's two 16-row halves: lane (j, g) reads key row j, chunk 4s + g.
+  auto qk = [&](int t, f32x4& s0, f32x4& s1) {
+    const unsigned short* st = ring + (t % G::kSlots) * G::kElems;
+    s0 = f32x4{0.f, 0.f, 0.f, 0.f};
+    s1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < G::kSteps; ++s) {
       const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(st + 512 * s + 8 * lane);
@@ -339,6 +336,11 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
       s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[s], s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[s], s1, 0, 0, 0);
     }
+  };
+  // The probabilities of a tile against the running maximum, and O^T += V^T . P^T.
+  auto accumulate = [&](int t, const f32x4& s0, const f32x4& s1) {
+    const unsigned short* st = ring + (t % G::kSlots) * G::kElems;
+    const int n0 = s_lo + (kset + t * kKeySets) * 32;
     float x[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     float bm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
     bm = group_max(bm);
     if (bm > m_run + kRescale) {  // this lane's row: rescale its sums to the new maximum
-      const float alpha = m_run == kNegInf ? 0.f : exp2f(m_run - bm);
+      const float alpha = m_run == kNegInf ? 0.f : __builtin_amdgcn_exp2f(m_run - bm);
       m_run = bm;
       l_run *= alpha;
 #pragma unroll
@@ -367,7 +369,11 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     }
     float p[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) p[e] = m_run == kNegInf ? 0.f : exp2f(x[e] - m_run);
+    for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(x[e] - m_run);  // 0 at -inf; m_run finite here
+    if (m_run == kNegInf) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p[e] = 0.f;
+    }
     l_run += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
     // P^T operand: lane (j, g) holds k-index 8g + e = key 4g + e of the first
     // half (e < 4), key 16 + 4g + e - 4 of the second; the V^T operand holds
@@ -382,6 +388,29 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
       const s16x8 vt = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
       o[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vt), pt, o[cb], 0, 0, 0);
     }
+  };
+
+  // Software pipeline: iteration it multiplies the next tile's keys (QK^T on
+  // the matrix cores) before the softmax and PV of its own tile, whose VALU
+  // work then overlaps them.  Tiles it (PV) and it + 1 (QK) occupy two slots,
+  // it + 2 and it + 3 are in flight.
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  // a first-set wavefront that waits for no tile waits for its queries here
+  if (kset == 0 && !(dma_wave && mine > 0)) wait_vmcnt<0>();
+  arrive(0, min(G::kSlots - 2, mine - 1));  // tile 0 and every m-block's queries are in LDS
+#pragma unroll
+  for (int s = 0; s < G::kSteps; ++s)
+    qf[s] = *reinterpret_cast<const bf16x8*>(qlds + mb * 16 * C + 512 * s + 8 * lane);
+  if (mine > 0) qk(0, s0, s1);
+#pragma unroll 1
+  for (int it = 0; it < niter; ++it) {
+    arrive(it + 1, min(1, mine - 2 - it));  // every wavefront is done with iteration it - 1
+    if (dma_wave && it + G::kSlots - 1 < mine) issue(it + G::kSlots - 1);
+    f32x4 n0v = {0.f, 0.f, 0.f, 0.f}, n1v = {0.f, 0.f, 0.f, 0.f};
+    if (it + 1 < mine) qk(it + 1, n0v, n1v);
+    if (it < mine) accumulate(it, s0, s1);
+    s0 = n0v;
+    s1 = n1v;
   }
   wait_vmcnt<0>();
   l_run = group_sum(l_run);
