@@ -120,6 +120,32 @@ int wptv_kv_append(void* table, int64_t table_stride_b, int64_t table_stride_n, 
                    hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * The decoder layer's memory-bound steps around its matrix products (the
+ * reference's extend runs them as torch operations: model.py:394-436,
+ * attention.py:157-188, layers.py:45-61).  dtype WPTV_F32 or WPTV_BF16 for
+ * every activation; norm weights fp32; rows contiguous and 16-byte aligned.
+ *
+ * wptv_add_rms_norm: h [M, D] += delta (when delta is not NULL; the residual
+ *   add, rounded to dtype), then y = h * rsqrt(mean(h^2) + eps) * weight in
+ *   FP32 (nn.RMSNorm, layers.py:9 eps 1e-6).  D a multiple of 8, <= 4096.
+ * wptv_qkv_post: the exact layer after its projection (attention.py:182-185):
+ *   qkv [B*T, >= (H + 2) c] (row stride qkv_row_stride) holds q, k, v;
+ *   q_out [B, T, H, c] = q_norm(q) per head; for t < counts[b] the entry
+ *   [k_norm(k), v] is written at table row start[b] + t (the KV append of
+ *   Reading.everything, cache.py:110-128; rows past capacity are skipped).
+ * wptv_swiglu: out [M, F] = silu(gate) * up of gate_up [M, 2F] (gate first).
+ * ------------------------------------------------------------------------- */
+int wptv_add_rms_norm(void* h, const void* delta, const float* weight, void* y, int M, int D, int dtype, float eps,
+                      hipStream_t stream);
+
+int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const float* q_norm, const float* k_norm, void* q_out,
+                  void* table, int64_t table_stride_b, int64_t table_stride_n, int64_t capacity,
+                  const int64_t* start, const int64_t* counts, int B, int T, int H, int c, int dtype, float eps,
+                  hipStream_t stream);
+
+int wptv_swiglu(const void* gate_up, void* out, int M, int F, int dtype, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Acceptance: the reference's per-row verification loop of
  * Writer._speculate (packages/wpt-inference/src/wpt_inference/__init__.py:
  * 210-229) with its sampling distribution Writer._probabilities (:173-179),

@@ -1,0 +1,235 @@
+// The decoder layer's memory-bound pieces around the matrix products, each
+// one pass over its rows (the reference's extend runs them as separate torch
+// operations: model.py:394-436, attention.py:157-188, layers.py:45-61):
+//
+//   add_rms_norm  h += delta (the residual add of the sublayer before, when
+//                 given), then y = RMSNorm(h) * weight in FP32
+//   qkv_post      the exact layer after its q/k/v projection: q = q_norm(q)
+//                 per head into (B, T, H, c); the entries [k_norm(k), v] of
+//                 each row's first counts[b] tokens appended to the cache
+//                 table at start[b] + t (the KV append, cache.py:110-128)
+//   swiglu        silu(gate) * up of the feed-forward block's two halves
+//
+// One wavefront per row for the norms (16-byte vector loads, FP32 sums with
+// wavefront reductions); one thread per 8 elements for SwiGLU.
+#include "wptv_common.h"
+
+namespace wptv {
+namespace {
+
+template <typename T>
+struct Vec8;
+template <>
+struct Vec8<unsigned short> {  // 8 bf16
+  typedef unsigned short raw __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ void load(const unsigned short* p, float (&x)[8]) {
+    const raw v = *reinterpret_cast<const raw*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = bf16_to_f32(v[e]);
+  }
+  static __device__ __forceinline__ void store(unsigned short* p, const float (&x)[8]) {
+    raw v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = f32_to_bf16(x[e]);
+    *reinterpret_cast<raw*>(p) = v;
+  }
+};
+template <>
+struct Vec8<float> {
+  static __device__ __forceinline__ void load(const float* p, float (&x)[8]) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = a[e], x[4 + e] = b[e];
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&x)[8]) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
+  }
+};
+
+// x rounded to T and back (the value a T tensor holds).
+template <typename T>
+__device__ __forceinline__ float rounded(float x);
+template <>
+__device__ __forceinline__ float rounded<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ float rounded<unsigned short>(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// Values of one row held by a lane: D / 8 / 64 chunks of 8, at most kChunks.
+constexpr int kChunks = 8;  // rows up to 64 * 8 * 8 = 4096 wide
+
+template <typename T>
+__global__ __launch_bounds__(256) void add_rms_norm(T* __restrict__ h, const T* __restrict__ delta,
+                                                    const float* __restrict__ weight, T* __restrict__ y, int M,
+                                                    int D, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  T* hrow = h + (int64_t)row * D;
+  const T* drow = delta ? delta + (int64_t)row * D : nullptr;
+  float x[kChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) {
+    const int col = (k * 64 + lane) * 8;
+    if (col < D) {
+      Vec8<T>::load(hrow + col, x[k]);
+      if (drow) {
+        float d[8];
+        Vec8<T>::load(drow + col, d);
+        // the residual stream keeps the activation dtype, as the reference's h = h + out does
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[k][e] = rounded<T>(x[k][e] + d[e]);
+        Vec8<T>::store(hrow + col, x[k]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[k][e] * x[k][e];
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / (float)D + eps);
+  T* yrow = y + (int64_t)row * D;
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) {
+    const int col = (k * 64 + lane) * 8;
+    if (col < D) {
+      float out[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = x[k][e] * inv * weight[col + e];
+      Vec8<T>::store(yrow + col, out);
+    }
+  }
+}
+
+// One workgroup of 4 wavefronts per token row; wavefront w takes heads w,
+// w + 4, ... of the H query heads, then the key (head H) and value (H + 1).
+template <typename T>
+__global__ __launch_bounds__(256) void qkv_post(const T* __restrict__ qkv, int64_t qkv_row,
+                                                const float* __restrict__ q_norm, const float* __restrict__ k_norm,
+                                                T* __restrict__ q_out, T* __restrict__ table, int64_t tsb,
+                                                int64_t tsn, int64_t capacity, const int64_t* __restrict__ start,
+                                                const int64_t* __restrict__ counts, int T_, int H, int C, float eps) {
+  const int row = blockIdx.x;
+  const int b = row / T_, t = row % T_;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const T* src = qkv + (int64_t)row * qkv_row;
+  const bool append = t < counts[b];
+  const int64_t dst_row = start[b] + t;
+  T* entry = (append && dst_row >= 0 && dst_row < capacity) ? table + b * tsb + dst_row * tsn : nullptr;
+  for (int head = wave; head < H + 2; head += 4) {
+    const T* x = src + (int64_t)head * C;
+    if (head == H + 1) {  // the value: copied as it is
+      if (entry)
+        for (int col = lane; col < C; col += 64) entry[C + col] = x[col];
+      continue;
+    }
+    float v[4];  // C <= 256: 4 values per lane
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int col = lane + 64 * k;
+      v[k] = col < C ? load_f32(x + col) : 0.f;
+      ss += v[k] * v[k];
+    }
+    ss = wave_sum(ss);
+    const float inv = rsqrtf(ss / (float)C + eps);
+    const float* w = head < H ? q_norm : k_norm;
+    T* dst = head < H ? q_out + ((int64_t)row * H + head) * C : entry;
+    if (!dst) continue;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int col = lane + 64 * k;
+      if (col < C) dst[col] = from_f32<T>(v[k] * inv * w[col]);
+    }
+  }
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
+
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu(const T* __restrict__ gu, T* __restrict__ out, int M, int F) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i >= (int64_t)M * F) return;
+  const int64_t m = i / F, f = i % F;
+  float g[8], u[8], o[8];
+  Vec8<T>::load(gu + m * 2 * F + f, g);
+  Vec8<T>::load(gu + m * 2 * F + F + f, u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = silu(g[e]) * u[e];
+  Vec8<T>::store(out + i, o);
+}
+
+}  // namespace
+}  // namespace wptv
+
+using namespace wptv;
+
+namespace {
+bool vec_aligned(const void* p) { return p == nullptr || aligned(p, 16); }
+}  // namespace
+
+extern "C" int wptv_add_rms_norm(void* h, const void* delta, const float* weight, void* y, int M, int D, int dtype,
+                                 float eps, hipStream_t stream) {
+  if (!h || !weight || !y) return fail(WPTV_E_INVALID, "add_rms_norm: h, weight and y must be given");
+  if (M < 0 || D <= 0) return fail(WPTV_E_INVALID, "add_rms_norm: bad shape M=%d D=%d", M, D);
+  if (D % 8 != 0 || D > 64 * 8 * kChunks)
+    return fail(WPTV_E_UNSUPPORTED, "add_rms_norm: width %d is not a multiple of 8 up to %d", D, 64 * 8 * kChunks);
+  if (!vec_aligned(h) || !vec_aligned(delta) || !vec_aligned(y))
+    return fail(WPTV_E_INVALID, "add_rms_norm: rows must be 16-byte aligned");
+  if (M == 0) return WPTV_OK;
+  dim3 grid((M + 3) / 4);
+  if (dtype == WPTV_BF16)
+    hipLaunchKernelGGL(add_rms_norm<unsigned short>, grid, dim3(256), 0, stream, static_cast<unsigned short*>(h),
+                       static_cast<const unsigned short*>(delta), weight, static_cast<unsigned short*>(y), M, D, eps);
+  else if (dtype == WPTV_F32)
+    hipLaunchKernelGGL(add_rms_norm<float>, grid, dim3(256), 0, stream, static_cast<float*>(h),
+                       static_cast<const float*>(delta), weight, static_cast<float*>(y), M, D, eps);
+  else
+    return fail(WPTV_E_UNSUPPORTED, "add_rms_norm: dtype %d is neither fp32 nor bf16", dtype);
+  return launched("add_rms_norm");
+}
+
+extern "C" int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const float* q_norm, const float* k_norm,
+                             void* q_out, void* table, int64_t table_stride_b, int64_t table_stride_n,
+                             int64_t capacity, const int64_t* start, const int64_t* counts, int B, int T, int H,
+                             int c, int dtype, float eps, hipStream_t stream) {
+  if (!qkv || !q_norm || !k_norm || !q_out || !table || !start || !counts)
+    return fail(WPTV_E_INVALID, "qkv_post: every pointer must be given");
+  if (B < 0 || T < 0 || H <= 0 || c <= 0 || c > 256)
+    return fail(WPTV_E_INVALID, "qkv_post: bad shape B=%d T=%d H=%d c=%d", B, T, H, c);
+  if (qkv_row_stride < (int64_t)(H + 2) * c || table_stride_n < 2 * c)
+    return fail(WPTV_E_INVALID, "qkv_post: a row stride below its width");
+  if (B == 0 || T == 0) return WPTV_OK;
+  dim3 grid(B * T);
+  if (dtype == WPTV_BF16)
+    hipLaunchKernelGGL(qkv_post<unsigned short>, grid, dim3(256), 0, stream, static_cast<const unsigned short*>(qkv),
+                       qkv_row_stride, q_norm, k_norm, static_cast<unsigned short*>(q_out),
+                       static_cast<unsigned short*>(table), table_stride_b, table_stride_n, capacity, start, counts, T,
+                       H, c, eps);
+  else if (dtype == WPTV_F32)
+    hipLaunchKernelGGL(qkv_post<float>, grid, dim3(256), 0, stream, static_cast<const float*>(qkv), qkv_row_stride,
+                       q_norm, k_norm, static_cast<float*>(q_out), static_cast<float*>(table), table_stride_b,
+                       table_stride_n, capacity, start, counts, T, H, c, eps);
+  else
+    return fail(WPTV_E_UNSUPPORTED, "qkv_post: dtype %d is neither fp32 nor bf16", dtype);
+  return launched("qkv_post");
+}
+
+extern "C" int wptv_swiglu(const void* gate_up, void* out, int M, int F, int dtype, hipStream_t stream) {
+  if (!gate_up || !out) return fail(WPTV_E_INVALID, "swiglu: gate_up and out must be given");
+  if (M < 0 || F <= 0) return fail(WPTV_E_INVALID, "swiglu: bad shape M=%d F=%d", M, F);
+  if (F % 8 != 0) return fail(WPTV_E_UNSUPPORTED, "swiglu: width %d is not a multiple of 8", F);
+  if (!vec_aligned(gate_up) || !vec_aligned(out)) return fail(WPTV_E_INVALID, "swiglu: rows must be 16-byte aligned");
+  if (M == 0) return WPTV_OK;
+  const int64_t threads = (int64_t)M * F / 8;
+  dim3 grid((unsigned)((threads + 255) / 256));
+  if (dtype == WPTV_BF16)
+    hipLaunchKernelGGL(swiglu<unsigned short>, grid, dim3(256), 0, stream, static_cast<const unsigned short*>(gate_up),
+                       static_cast<unsigned short*>(out), M, F);
+  else if (dtype == WPTV_F32)
+    hipLaunchKernelGGL(swiglu<float>, grid, dim3(256), 0, stream, static_cast<const float*>(gate_up),
+                       static_cast<float*>(out), M, F);
+  else
+    return fail(WPTV_E_UNSUPPORTED, "swiglu: dtype %d is neither fp32 nor bf16", dtype);
+  return launched("swiglu");
+}

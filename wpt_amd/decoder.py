@@ -11,7 +11,9 @@ FP32 scores (model.py:471).  One key/value head is shared by every query
 head (MQA).  RMSNorm's eps is the reference's (layers.py:9).
 
 On the GPU:
-    KV append       wptv_kv_append (at each row's own length, no host sync)
+    KV append       wptv_qkv_post: q/k norms, and the new entries written at
+                    each row's own length (no host sync)
+    norms, SwiGLU   wptv_add_rms_norm (residual add + RMSNorm), wptv_swiglu
     verify attention wptv_verify_attention, reading only the rows the query
                     positions reach in the cache's table
     projections     the matrix products of the dtype (bf16 on MFMA)
@@ -25,7 +27,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from . import kernels
+from . import kernels, layers
 from .cache import Cache
 
 EPS = 1e-6
@@ -77,11 +79,6 @@ def random_weights(config, seed=0, std=0.02, dtype=torch.float32, device="cpu"):
     return weights
 
 
-def rms_norm(x, weight):
-    """RMSNorm in FP32, the result in x's dtype."""
-    return F.rms_norm(x.float(), (x.shape[-1],), weight, EPS).to(x.dtype)
-
-
 class MQADecoder:
     """config: DecoderConfig; weights: random_weights' names; dtype: the
     compute dtype (float32 or bfloat16), on a GPU."""
@@ -106,23 +103,21 @@ class MQADecoder:
         c = self.config.head_dim
         return Cache(rows, self.config.layers, 2 * c, self.dtype, self.device, capacity)
 
-    def _layer(self, i, h, cache, positions, counts):
+    def _layer(self, i, h, x, cache, positions, counts, next_norm):
+        """One layer on the residual stream h (B, T, D), x = RMSNorm(h) with the
+        layer's attention norm; leaves h updated and x = RMSNorm(h) with
+        next_norm (the next layer's attention norm, or the final norm)."""
         w = self.w
         cfg = self.config
         B, T, _ = h.shape
         H, c = cfg.heads, cfg.head_dim
-        x = rms_norm(h, w[f"layers.{i}.attn_norm"])
-        qkv = F.linear(x, w[f"layers.{i}.qkv"])
-        q = rms_norm(qkv[..., :H * c].reshape(B, T, H, c), w[f"layers.{i}.q_norm"])
-        k = rms_norm(qkv[..., H * c:H * c + c], w[f"layers.{i}.k_norm"])
-        new = torch.cat([k, qkv[..., H * c + c:]], -1)
         table = cache.tables[i]
-        kernels.kv_append(table, new, cache.lengths, counts)
+        qkv = F.linear(x, w[f"layers.{i}.qkv"])
+        q = layers.qkv_post(qkv, w[f"layers.{i}.q_norm"], w[f"layers.{i}.k_norm"], table, cache.lengths, counts, H)
         o = kernels.verify_attention(q, table[..., :c], table[..., c:], positions, c ** -0.5, from_positions=True)
-        h = h + F.linear(o.reshape(B, T, H * c), w[f"layers.{i}.out"])
-        x = rms_norm(h, w[f"layers.{i}.ffn_norm"])
-        gate, up = F.linear(x, w[f"layers.{i}.gate_up"]).chunk(2, -1)
-        return h + F.linear(F.silu(gate) * up, w[f"layers.{i}.down"])
+        layers.add_rms_norm(h, F.linear(o.reshape(B, T, H * c), w[f"layers.{i}.out"]), w[f"layers.{i}.ffn_norm"], x)
+        act = layers.swiglu(F.linear(x, w[f"layers.{i}.gate_up"]))
+        layers.add_rms_norm(h, F.linear(act, w[f"layers.{i}.down"]), next_norm, x)
 
     @torch.no_grad()
     def extend(self, ids, cache, counts=None, undoable=False, features=()):
@@ -143,9 +138,13 @@ class MQADecoder:
         cache.reserve(cache.bound + T)
         positions = cache.lengths[:, None] + torch.arange(T, device=self.device)
         h = F.embedding(ids, self.w["embedding"])
+        x = torch.empty_like(h)
+        layers.add_rms_norm(h, None, self.w["layers.0.attn_norm"], x)
         for i in range(self.config.layers):
-            h = self._layer(i, h, cache, positions, counts_)
-        scores = F.linear(rms_norm(h, self.w["final_norm"]), self.w["head"]).float()
+            last = i + 1 == self.config.layers
+            next_norm = self.w["final_norm"] if last else self.w[f"layers.{i + 1}.attn_norm"]
+            self._layer(i, h, x, cache, positions, counts_, next_norm)
+        scores = F.linear(x, self.w["head"]).float()
         cache.finish(counts_, undoable, T)
         return scores, h
 

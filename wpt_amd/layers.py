@@ -1,0 +1,68 @@
+"""Python entry points of libwptv's decoder-layer kernels (include/wptv.h):
+the residual add + RMSNorm, the exact layer's q/k norms + KV append, and
+SwiGLU, each one pass over its rows on the GPU (the reference runs them as
+separate torch operations: model.py:394-436, attention.py:157-188,
+layers.py:45-61)."""
+
+import torch
+
+from . import _lib
+from ._lib import KernelUnavailable, check, ptr
+
+EPS = 1e-6
+
+
+def _gpu(*tensors):
+    for x in tensors:
+        if x is not None and x.device.type != "cuda":
+            raise KernelUnavailable(f"the HIP layer kernels run on a GPU; a tensor is on {x.device}")
+
+
+def _rows(x, name):
+    if not x.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return x
+
+
+def add_rms_norm(h, delta, weight, y, eps=EPS):
+    """h += delta (None: no add), then y = RMSNorm(h) * weight (FP32 math).
+    h, delta, y share shape (..., D) and dtype; weight (D,) FP32."""
+    _gpu(h, delta, weight, y)
+    D = h.shape[-1]
+    if y.shape != h.shape or (delta is not None and delta.shape != h.shape) or weight.shape != (D,):
+        raise ValueError(f"h {tuple(h.shape)}, delta, y and weight ({D},) do not match")
+    if weight.dtype != torch.float32 or (delta is not None and delta.dtype != h.dtype) or y.dtype != h.dtype:
+        raise ValueError("h, delta and y share a dtype; weight is float32")
+    check(_lib.lib().wptv_add_rms_norm(ptr(_rows(h, "h")), ptr(None if delta is None else _rows(delta, "delta")),
+                                       ptr(weight), ptr(_rows(y, "y")), h.numel() // D, D, _lib.dtype_code(h.dtype),
+                                       float(eps), _lib.stream(h.device)), "add_rms_norm")
+    return y
+
+
+def qkv_post(qkv, q_norm, k_norm, table, start, counts, heads, eps=EPS):
+    """qkv (B, T, (H + 2) c) -> q (B, T, H, c) = q_norm per head; the entries
+    [k_norm(k), v] of row b's first counts[b] tokens written into table
+    (B, capacity, 2c) at start[b] + t."""
+    _gpu(qkv, table)
+    B, T, width = qkv.shape
+    c = table.shape[-1] // 2
+    if width != (heads + 2) * c or qkv.stride(-1) != 1 or qkv.stride(0) != T * qkv.stride(1):
+        raise ValueError(f"qkv must be (B, T, (H + 2) c) with rows one after another; got {tuple(qkv.shape)}")
+    if table.dtype != qkv.dtype or table.stride(-1) != 1 or table.shape[0] != B:
+        raise ValueError("the table must be (B, capacity, 2c) in qkv's dtype, rows contiguous")
+    q = torch.empty(B, T, heads, c, dtype=qkv.dtype, device=qkv.device)
+    check(_lib.lib().wptv_qkv_post(ptr(qkv), qkv.stride(1), ptr(q_norm), ptr(k_norm), ptr(q), ptr(table),
+                                   table.stride(0), table.stride(1), table.shape[1], ptr(start), ptr(counts), B, T,
+                                   heads, c, _lib.dtype_code(qkv.dtype), float(eps), _lib.stream(qkv.device)),
+          "qkv_post")
+    return q
+
+
+def swiglu(gate_up):
+    """silu(gate) * up of gate_up (..., 2F): (..., F)."""
+    _gpu(gate_up)
+    F = gate_up.shape[-1] // 2
+    out = torch.empty(*gate_up.shape[:-1], F, dtype=gate_up.dtype, device=gate_up.device)
+    check(_lib.lib().wptv_swiglu(ptr(_rows(gate_up, "gate_up")), ptr(out), gate_up.numel() // (2 * F), F,
+                                 _lib.dtype_code(gate_up.dtype), _lib.stream(gate_up.device)), "swiglu")
+    return out
