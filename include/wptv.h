@@ -43,9 +43,12 @@ enum { WPTV_F32 = 0, WPTV_BF16 = 1 };
 /* wptv_verify_attention flags */
 enum {
   WPTV_ATTN_FORCE_GENERIC = 1,        /* run the wave-per-query VALU kernel even where the MFMA kernel applies */
-  WPTV_ATTN_RANGE_FROM_POSITIONS = 2  /* read only the rows the positions reach (a table with spare capacity
-                                         past its rows); by default a single full-causal query group reads
-                                         rows 0..N-1 and masks the ones past each query */
+  WPTV_ATTN_RANGE_FROM_POSITIONS = 2, /* read only the rows the positions reach (a table with spare capacity
+                                         past its rows); by default the row-block kernel's single full-causal
+                                         query group reads rows 0..N-1 and masks the ones past each query (the
+                                         key-parallel kernel always reads only the rows the positions reach) */
+  WPTV_ATTN_KEY_SPLIT = 4             /* where T*H <= 80: the key-parallel MFMA kernel (each wavefront owns key
+                                         tiles and holds every query row) instead of the row-block one */
 };
 
 int wptv_abi_version(void);

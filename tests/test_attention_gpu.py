@@ -36,8 +36,10 @@ def on(device, *tensors):
     (2, 7, 12, 128, 300, 0),     # 84 query rows: five 16-row blocks, the last partly padding
     (2, 5, 16, 64, 777, 0),      # head width 64
     (1, 1, 4, 64, 1, 0),         # a single row
+    (64, 5, 16, 128, 2048, 0),   # the end-to-end step's layer shape
 ])
-def test_exact_attention_matches_the_oracle(device, B, T, H, c, N, splits):
+@pytest.mark.parametrize("key_split", [False, True], ids=["row-blocks", "key-parallel"])
+def test_exact_attention_matches_the_oracle(device, B, T, H, c, N, splits, key_split):
     q = draw(B, T, H, c, seed=1)
     _, k, v = entries_table(B, N, c, seed=2)
     positions = (N - T + torch.arange(T)).clamp(min=0).expand(B, T).contiguous()
@@ -45,7 +47,8 @@ def test_exact_attention_matches_the_oracle(device, B, T, H, c, N, splits):
     qd, kd, vd, pd = on(device, q, k, v, positions)
     # the strided halves of the device table, as the model's cache gives them
     table = torch.cat([kd, vd], -1)
-    got = kernels.verify_attention(qd, table[..., :c], table[..., c:], pd, c ** -0.5, splits=splits)
+    got = kernels.verify_attention(qd, table[..., :c], table[..., c:], pd, c ** -0.5, splits=splits,
+                                   key_split=key_split)
     assert got.dtype == torch.bfloat16 and got.shape == (B, T, H, c)
     assert relative_error(got.cpu(), expected) < 1e-2
 
@@ -80,9 +83,51 @@ def test_the_generic_and_mfma_kernels_agree(device):
     q, (_, k, v) = draw(B, T, H, c, seed=5), entries_table(B, N, c, seed=6)
     positions = (N - T + torch.arange(T)).expand(B, T).contiguous()
     args = on(device, q, k, v, positions)
-    mfma = kernels.verify_attention(*args, c ** -0.5)
-    generic = kernels.verify_attention(*args, c ** -0.5, generic=True)
-    assert relative_error(mfma.cpu(), generic.cpu().float()) < 1e-2
+    generic = kernels.verify_attention(*args, c ** -0.5, generic=True).cpu().float()
+    for key_split in (False, True):
+        mfma = kernels.verify_attention(*args, c ** -0.5, key_split=key_split)
+        assert relative_error(mfma.cpu(), generic) < 1e-2
+
+
+@pytest.mark.parametrize("key_split", [False, True], ids=["row-blocks", "key-parallel"])
+def test_scores_growing_along_the_keys(device, key_split):
+    # every query along one direction u, key n = f_n u with f_n rising over
+    # the rows: each row's maximum grows by far more than 2^32 across the
+    # tiles, so the running maximum moves and the partial sums are rescaled
+    B, T, H, c, N = 2, 5, 16, 128, 2000
+    generator = torch.Generator().manual_seed(31)
+    u = torch.randn(c, generator=generator)
+    u = u / u.norm()
+    q = (8 * u).expand(B, T, H, c) * (1 + 0.1 * torch.randn(B, T, H, 1, generator=generator))
+    f = torch.linspace(0, 100, N)
+    k = f[None, :, None] * u + 0.05 * torch.randn(B, N, c, generator=generator)
+    v = torch.randn(B, N, c, generator=generator)
+    q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
+    positions = (N - T + torch.arange(T)).expand(B, T).contiguous()
+    expected, _ = oracle.exact_attention(q, k, v, positions, c ** -0.5, 0, 128)
+    for splits in (1, 0):
+        got = kernels.verify_attention(*on(device, q, k, v, positions), c ** -0.5, splits=splits,
+                                       key_split=key_split)
+        assert relative_error(got.cpu(), expected) < 1e-2
+
+
+def test_a_small_tree_on_both_mfma_kernels(device):
+    # a draft tree of 5 nodes (root, two children, two grandchildren under
+    # the first child): 80 query rows
+    B, H, c, prefix = 3, 16, 128, 700
+    parents = [-1, 0, 0, 1, 1]
+    M = len(parents)
+    q = draw(B, M, H, c, seed=32)
+    _, k, v = entries_table(B, prefix + M, c, seed=33)
+    prefixes = torch.tensor([prefix, prefix - 37, prefix - 300])
+    expected = oracle.tree_attention(q, k, v, prefixes, parents, c ** -0.5)
+    qd, kd, vd, bd = on(device, q, k, v, prefixes)
+    got = kernels.tree_attention(qd, kd, vd, bd, parents, c ** -0.5)
+    assert relative_error(got.cpu(), expected) < 1e-2
+    positions = bd[:, None] + torch.arange(M, device=device)
+    masks = kernels.tree_ancestors(parents).to(device)
+    got = kernels.verify_attention(qd, kd, vd, positions, c ** -0.5, tree=(bd, masks), key_split=True)
+    assert relative_error(got.cpu(), expected) < 1e-2
 
 
 @pytest.mark.parametrize("with_sink", [False, True])
@@ -130,6 +175,10 @@ def test_tree_attention_matches_the_oracle(device):
     expected = oracle.tree_attention(q, k, v, prefixes, parents, c ** -0.5)
     qd, kd, vd, bd = on(device, q, k, v, prefixes)
     got = kernels.tree_attention(qd, kd, vd, bd, parents, c ** -0.5)
+    assert relative_error(got.cpu(), expected) < 1e-2
+    positions = bd[:, None] + torch.arange(M, device=device)
+    masks = kernels.tree_ancestors(parents).to(device)
+    got = kernels.verify_attention(qd, kd, vd, positions, c ** -0.5, tree=(bd, masks), key_split=True)
     assert relative_error(got.cpu(), expected) < 1e-2
 
 

@@ -35,8 +35,12 @@ def test_the_workspace_query_plans_the_verify_attention_workload():
     status = library.wptv_attention_workspace(32, 5, 16, 128, 4096, 0, _lib.WPTV_BF16, 0, ctypes.byref(splits),
                                               ctypes.byref(size))
     assert status == 0 and splits.value == 8
-    # eight parts of 80 query rows x 128 FP32 values plus a log-sum-exp each
-    assert size.value >= 32 * 8 * 80 * (128 + 1) * 4
+    # eight parts of 80 query rows x 128 bf16 values plus an FP32
+    # log-sum-exp each
+    assert size.value >= 32 * 8 * 80 * (128 * 2 + 4)
+    status = library.wptv_attention_workspace(32, 5, 16, 128, 4096, 0, _lib.WPTV_BF16, _lib.KEY_SPLIT,
+                                              ctypes.byref(splits), ctypes.byref(size))
+    assert status == 0 and size.value >= 32 * 8 * 80 * (128 * 2 + 4)
 
 
 def test_bad_arguments_are_reported_with_a_message():

@@ -18,6 +18,7 @@ WPTV_F32, WPTV_BF16 = 0, 1
 DTYPES = {torch.float32: WPTV_F32, torch.bfloat16: WPTV_BF16}
 FORCE_GENERIC = 1
 RANGE_FROM_POSITIONS = 2
+KEY_SPLIT = 4
 
 
 class KernelUnavailable(RuntimeError):

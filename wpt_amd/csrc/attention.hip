@@ -34,6 +34,7 @@
 #include "wptv_common.h"
 
 #include <climits>
+#include <type_traits>
 
 namespace wptv {
 namespace {
@@ -80,10 +81,13 @@ struct Tile {
 };
 constexpr int kKeySets = 2;  // wavefront sets that take alternate tiles of the workgroup's key range
 
-// Softmax rescaling is deferred until a row's maximum grows by more than this
-// many powers of two (the stale maximum stays the reference for p and l, so
-// the result is exact; p stays below 2^8).
-constexpr float kRescale = 8.f;
+// A row's softmax reference maximum is its first finite tile maximum and
+// moves only when a later tile's maximum exceeds it by more than this many
+// powers of two (p then stays below 2^32, far inside the fp32 and bf16
+// range; the stale maximum stays the reference for p and l, so the result is
+// exact either way).  Moving it from -inf needs no rescale (O and l are still
+// 0); a real rescale is rare and done in one uniform branch.
+constexpr float kRescaleLog2 = 32.f;
 
 // s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding).
 template <int n>
@@ -161,7 +165,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
     const float* __restrict__ sink, int T, int H, int N, float scale_log2, int groups, int splits,
     int range_from_positions, int xcd_map, unsigned short* __restrict__ out, float* __restrict__ lse_out,
-    float* __restrict__ part_o, float* __restrict__ part_lse) {
+    unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
   using G = Tile<C>;
   constexpr int kRows = 16 * MB;
   constexpr int DMAW = MB >= 4 ? 4 : (MB >= 2 ? 2 : 1);  // wavefronts of a key set that issue its DMA
@@ -341,11 +345,11 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   auto accumulate = [&](int t, const f32x4& s0, const f32x4& s1) {
     const unsigned short* st = ring + (t % G::kSlots) * G::kElems;
     const int n0 = s_lo + (kset + t * kKeySets) * 32;
-    float x[8];
+    float x[8];  // raw scores (the scale is positive: maxima commute with it)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      x[i] = s0[i] * scale_log2;
-      x[4 + i] = s1[i] * scale_log2;
+      x[i] = s0[i];
+      x[4 + i] = s1[i];
     }
     if (!(n0 >= f_lo && n0 + 31 <= f_hi)) {
 #pragma unroll
@@ -358,22 +362,23 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
           x[4 * h + i] = vis ? x[4 * h + i] : kNegInf;
         }
     }
-    float bm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-    bm = group_max(bm);
-    if (bm > m_run + kRescale) {  // this lane's row: rescale its sums to the new maximum
-      const float alpha = m_run == kNegInf ? 0.f : __builtin_amdgcn_exp2f(m_run - bm);
-      m_run = bm;
+    const float bm =
+        group_max(fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])))) *
+        scale_log2;
+    const bool grow = bm > m_run + kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(grow && m_run != kNegInf)) {
+      const float alpha = (grow && m_run != kNegInf) ? __builtin_amdgcn_exp2f(m_run - bm) : 1.f;
       l_run *= alpha;
 #pragma unroll
       for (int cb = 0; cb < G::kCBlocks; ++cb) o[cb] *= alpha;
     }
+    m_run = grow ? bm : m_run;
+    // a row with no visible key so far has every score at -inf: any finite
+    // reference gives p = 0
+    const float neg_m = m_run == kNegInf ? 0.f : -m_run;
     float p[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(x[e] - m_run);  // 0 at -inf; m_run finite here
-    if (m_run == kNegInf) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) p[e] = 0.f;
-    }
+    for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(fmaf(x[e], scale_log2, neg_m));
     l_run += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
     // P^T operand: lane (j, g) holds k-index 8g + e = key 4g + e of the first
     // half (e < 4), key 16 + 4g + e - 4 of the second; the V^T operand holds
@@ -465,70 +470,570 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     }
     if (lse_out && g == 0) lse_out[(int64_t)b * R + r] = lse2 * kLn2;
   } else {
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
     const int64_t prow = ((int64_t)unit * splits + split) * kRows + 16 * mb + j;
 #pragma unroll
-    for (int cb = 0; cb < G::kCBlocks; ++cb)
-      *reinterpret_cast<f32x4*>(part_o + prow * C + cb * 16 + 4 * g) = o[cb] * scale_out;
+    for (int cb = 0; cb < G::kCBlocks; ++cb) {
+      const f32x4 val = o[cb] * scale_out;
+      *reinterpret_cast<bf16x4*>(part_o + prow * C + cb * 16 + 4 * g) =
+          bf16x4{static_cast<__bf16>(val[0]), static_cast<__bf16>(val[1]), static_cast<__bf16>(val[2]),
+                 static_cast<__bf16>(val[3])};
+    }
     if (g == 0) part_lse[prow] = lse2;
   }
 }
 
+// ---------------------------------------------------------------------------
+// Key-parallel MFMA kernel (at most 80 query rows, no tree mask)
+// ---------------------------------------------------------------------------
+//
+// One workgroup of four wavefronts (one per SIMD) per (batch row, key split).
+// Every wavefront holds all R <= 16 MB query rows of the batch row (Q^T in
+// registers, the O^T accumulators of every row) and owns every fourth
+// 32-row key tile of the split: it DMAs its tiles into a private LDS ring and
+// reads each byte of them once, so the loop has no workgroup barrier and the
+// LDS traffic is the key/value bytes themselves.  The four partial softmaxes
+// are merged through LDS at the end; each wavefront then finishes a quarter
+// of the head columns.
+//
+// LDS layouts (bank-conflict free for the reads that use them):
+//   K and Q rows: the 16-byte chunk q of row r at chunk position q ^ fk(r),
+//     so the 16 lanes of a 128-bit operand read (16 rows, one chunk) hit 16
+//     distinct 16-byte bank groups;
+//   V rows: the 32-byte segment s of row r at segment position s ^ fv(r), so
+//     a transposed 64-bit read (8 rows x 32 bytes per half-wavefront) hits
+//     distinct 32-byte bank groups.
+// The DMA writes 1 KiB of LDS per instruction (lane l at +16 l), so each lane
+// fetches the global chunk that belongs at its LDS position.
+
+template <int C>
+struct KTile {
+  static constexpr int kRowBytes = 2 * C;            // one bf16 key, value or query row
+  static constexpr int kLoads = 32 * kRowBytes / 1024;  // DMA instructions per 32 rows of K (or V)
+  static constexpr int kRowsPerLoad = 1024 / kRowBytes;
+  static constexpr int kChunks = C / 8;              // 16-byte chunks per row
+  static constexpr int kSteps = C / 32;              // k-steps of the QK^T product
+  static constexpr int kCBlocks = C / 16;            // 16-column blocks of O
+  static constexpr int kSlots = C == 64 ? 4 : 2;     // ring depth (tiles) per wavefront
+  static constexpr int kSlotBytes = 2 * 32 * kRowBytes;  // K tile then V tile
+};
+constexpr int kKeyWaves = 4;
+
+template <int C>
+__device__ __forceinline__ int swz_k(int r) {
+  return (r / (128 / C)) & (C / 8 - 1);
+}
+template <int C>
+__device__ __forceinline__ int swz_v(int r) {
+  return (r / (128 / C)) & (C / 16 - 1);
+}
+
+// vmcnt wait for a runtime count n in [0, 3 * kLoads]: the tiles still
+// allowed in flight behind the one needed.
+template <int kPer>
+__device__ __forceinline__ void wait_tiles_behind(int tiles) {
+  if (tiles >= 3)
+    wait_vmcnt<6 * kPer>();
+  else if (tiles == 2)
+    wait_vmcnt<4 * kPer>();
+  else if (tiles == 1)
+    wait_vmcnt<2 * kPer>();
+  else
+    wait_vmcnt<0>();
+}
+
+// Global -> LDS copy of 16 bytes per lane at base + soffset + voffset
+// (soffset uniform): lane l's bytes land at LDS byte address `lds` + 16 l.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_16B_at(i32x4 rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(soffset), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int C, int MB, bool TREE>
+__global__ __launch_bounds__(kKeyWaves * 64, 1) void verify_attention_keys(
+    const unsigned short* __restrict__ q, const unsigned short* __restrict__ k, int64_t ksb, int64_t ksn,
+    const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn, const int64_t* __restrict__ positions,
+    int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
+    const float* __restrict__ sink, int T, int H, int N, float scale_log2, int splits, int xcd_map,
+    unsigned short* __restrict__ out, float* __restrict__ lse_out, unsigned short* __restrict__ part_o,
+    float* __restrict__ part_lse) {
+  using G = KTile<C>;
+  constexpr int kRows = 16 * MB;
+  constexpr int kQLoads = kRows * G::kRowBytes / 1024;
+  constexpr int kOwn = G::kCBlocks / kKeyWaves;  // column blocks each wavefront finishes
+  constexpr int kBlockFloats = kRows * 16;       // one column block of O for every row
+  constexpr int kPerK = 16 / G::kRowsPerLoad;    // K DMA pieces after which the swizzle repeats
+  constexpr int kPerV = G::kRowsPerLoad >= 8 ? 1 : 8 / G::kRowsPerLoad;
+  static_assert(G::kLoads <= 16 && 6 * G::kLoads < 64, "vmcnt range");
+  static_assert(kOwn >= 1, "head width");
+  static_assert(kKeyWaves * (G::kCBlocks - kOwn) * kBlockFloats * 4 + kKeyWaves * kRows * 8 <=
+                    kKeyWaves * G::kSlots * G::kSlotBytes,
+                "the merge buffers reuse the rings");
+  __shared__ __attribute__((aligned(16))) unsigned char ring_all[kKeyWaves * G::kSlots * G::kSlotBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char qlds[kRows * G::kRowBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15;
+  const int g = lane >> 4;
+
+  int b, split;
+  {
+    const int L = blockIdx.x;
+    if (xcd_map) {  // the splits of one batch row on one XCD (workgroups go round-robin over the 8)
+      const int kk = L >> 3;
+      b = (L & 7) + 8 * (kk / splits);
+      split = kk % splits;
+    } else {
+      b = L / splits;
+      split = L % splits;
+    }
+  }
+  const int R = T * H;
+  const int64_t* pos_b = positions + (int64_t)b * T;
+  // DMA lane roles: lane l fills row rr of a piece (kRowsPerLoad whole rows), 16-byte position p.
+  const int rr = lane / G::kChunks, p = lane % G::kChunks;
+
+  // Queries first: wavefront w DMAs the 1 KiB pieces w, w + 4, ... of the
+  // R rows (padding rows repeat row R - 1).
+  {
+    const i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
+    const uint32_t qdst = __builtin_amdgcn_readfirstlane(lds_address(qlds));
+#pragma unroll
+    for (int ii = 0; ii < kQLoads; ++ii) {
+      if (ii % kKeyWaves != w) continue;
+      const int row = ii * G::kRowsPerLoad + rr;
+      const int src = row < R ? row : R - 1;
+      dma_16B(qrs, (uint32_t)src * G::kRowBytes + 16u * (uint32_t)(p ^ swz_k<C>(row)), qdst + 1024u * ii);
+    }
+  }
+
+  // Per-position bounds through scalar loads: the union u_lo..u_hi of the
+  // rows any query sees, the rows f_lo..f_hi every query sees, and for each
+  // of this lane's query rows (row 16 mb + j) its own range.
+  int u_lo = INT_MAX, u_hi = -1, f_lo = 0, f_hi = INT_MAX;
+  int lo[MB], hi[MB];
+  int row_t[MB];
+  uint64_t anc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int row = 16 * mb + j;
+    row_t[mb] = row < R ? row / H : -1;
+    lo[mb] = 0;
+    hi[mb] = -1;
+    anc[mb] = 0;
+  }
+  const int64_t tbase = TREE ? tree_base[b] : (int64_t)INT_MAX;
+  for (int t = 0; t < T; ++t) {
+    const Bounds bt = query_bounds(pos_b, t, window, N);
+    f_lo = max(f_lo, bt.lo);
+    f_hi = min(f_hi, bt.hi);
+    if (bt.hi >= bt.lo) {
+      u_lo = min(u_lo, bt.lo);
+      u_hi = max(u_hi, bt.hi);
+    }
+    uint64_t a = 0;
+    if constexpr (TREE) a = ancestors[t];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      if (row_t[mb] == t) {
+        lo[mb] = bt.lo;
+        hi[mb] = bt.hi;
+        anc[mb] = a;
+      }
+  }
+  if (TREE && tbase <= (int64_t)f_hi) f_hi = (int)tbase - 1;  // tree nodes are masked per query
+  int s_lo = 0, s_hi = -1;
+  if (u_hi >= u_lo) {
+    const int U = u_hi - u_lo + 1;
+    int per = (U + splits - 1) / splits;
+    per = (per + 32 * kKeyWaves - 1) / (32 * kKeyWaves) * (32 * kKeyWaves);
+    s_lo = u_lo + split * per;
+    s_hi = min(s_lo + per - 1, u_hi);
+  }
+  f_hi = min(f_hi, s_hi);
+  const int ntiles = s_hi >= s_lo ? (s_hi - s_lo + 1 + 31) / 32 : 0;
+  const int mine = ntiles > w ? (ntiles - w + kKeyWaves - 1) / kKeyWaves : 0;  // tiles w, w + 4, ...
+
+  // This wavefront's ring and its tile DMA: K rows then V rows, kLoads
+  // pieces each.  A whole tile inside the split goes with per-lane offsets
+  // fixed at the start and the tile's row offset as the scalar offset; the
+  // last, partial tile clamps each row to the split (the extra rows are
+  // masked).
+  unsigned char* const ring = ring_all + w * G::kSlots * G::kSlotBytes;
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_address(ring));
+  const i32x4 krs = buffer_resource(k + (int64_t)b * ksb);
+  const i32x4 vrs = buffer_resource(v + (int64_t)b * vsb);
+  const uint32_t krow_bytes = (uint32_t)ksn * 2u, vrow_bytes = (uint32_t)vsn * 2u;
+  uint32_t kvo[kPerK], vvo[kPerV];
+#pragma unroll
+  for (int m = 0; m < kPerK; ++m) kvo[m] = (uint32_t)rr * krow_bytes + 16u * (uint32_t)(p ^ swz_k<C>(m * G::kRowsPerLoad + rr));
+#pragma unroll
+  for (int m = 0; m < kPerV; ++m)
+    vvo[m] = (uint32_t)rr * vrow_bytes + 32u * (uint32_t)((p >> 1) ^ swz_v<C>(m * G::kRowsPerLoad + rr)) + 16u * (uint32_t)(p & 1);
+  auto issue_k = [&](int i) {
+    const uint32_t slot = ring_lds + (uint32_t)(i % G::kSlots) * G::kSlotBytes;
+    const int n0 = s_lo + (w + kKeyWaves * i) * 32;
+    if (n0 + 31 <= s_hi) {
+#pragma unroll
+      for (int ii = 0; ii < G::kLoads; ++ii)
+        dma_16B_at(krs, kvo[ii % kPerK], (uint32_t)(n0 + ii * G::kRowsPerLoad) * krow_bytes, slot + 1024u * ii);
+    } else {
+#pragma unroll
+      for (int ii = 0; ii < G::kLoads; ++ii) {
+        const int tr = ii * G::kRowsPerLoad + rr;
+        const int n = min(n0 + tr, s_hi);
+        dma_16B(krs, (uint32_t)n * krow_bytes + 16u * (uint32_t)(p ^ swz_k<C>(tr)), slot + 1024u * ii);
+      }
+    }
+  };
+  auto issue_v = [&](int i) {
+    const uint32_t slot = ring_lds + (uint32_t)(i % G::kSlots) * G::kSlotBytes + 32u * G::kRowBytes;
+    const int n0 = s_lo + (w + kKeyWaves * i) * 32;
+    if (n0 + 31 <= s_hi) {
+#pragma unroll
+      for (int ii = 0; ii < G::kLoads; ++ii)
+        dma_16B_at(vrs, vvo[ii % kPerV], (uint32_t)(n0 + ii * G::kRowsPerLoad) * vrow_bytes, slot + 1024u * ii);
+    } else {
+#pragma unroll
+      for (int ii = 0; ii < G::kLoads; ++ii) {
+        const int tr = ii * G::kRowsPerLoad + rr;
+        const int n = min(n0 + tr, s_hi);
+        const int seg = (p >> 1) ^ swz_v<C>(tr);
+        dma_16B(vrs, (uint32_t)n * vrow_bytes + 32u * (uint32_t)seg + 16u * (uint32_t)(p & 1), slot + 1024u * ii);
+      }
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < G::kSlots; ++i)
+    if (i < mine) {
+      issue_k(i);
+      issue_v(i);
+    }
+
+  // Queries: every wavefront's share is in LDS once each has waited for its
+  // own (everything but its tiles) and the workgroup has met.
+  wait_tiles_behind<G::kLoads>(min(mine, G::kSlots));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  // Per-lane LDS offsets.  K operand of k-step s (and Q^T, with the query
+  // rows): row j, chunk 4 s + g.  Transposed V read of column block cb: lane
+  // 16 g + 4 y + qq addresses row 4 g + y, columns 16 cb + 4 qq .. + 3 (the
+  // second read adds 16 rows; the swizzles repeat every 16 rows).
+  uint32_t ko[G::kSteps], vo[G::kCBlocks];
+#pragma unroll
+  for (int s = 0; s < G::kSteps; ++s) ko[s] = (uint32_t)(j * G::kRowBytes + 16 * ((4 * s + g) ^ swz_k<C>(j)));
+  {
+    const int vy = 4 * g + ((lane >> 2) & 3), vqq = lane & 3;
+#pragma unroll
+    for (int cb = 0; cb < G::kCBlocks; ++cb)
+      vo[cb] = (uint32_t)(vy * G::kRowBytes + 32 * (cb ^ swz_v<C>(vy)) + 8 * vqq);
+  }
+
+  f32x4 o[G::kCBlocks][MB];
+  float m_run[MB], l_run[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    m_run[mb] = kNegInf;
+    l_run[mb] = 0.f;
+  }
+
+  // One 32-key tile.  FIRST: the wavefront's first tile, which starts the
+  // O^T accumulators (no rescale can be needed: every row's reference
+  // maximum is still -inf).
+  auto step = [&](int i, auto first_c) {
+    constexpr bool FIRST = decltype(first_c)::value;
+    wait_tiles_behind<G::kLoads>(min(mine - 1 - i, G::kSlots - 1));
+    const unsigned char* st = ring + (i % G::kSlots) * G::kSlotBytes;
+    const unsigned char* sv = st + 32 * G::kRowBytes;
+    const int n0 = s_lo + (w + kKeyWaves * i) * 32;
+
+    // S^T = K . Q^T for every row block: K is the A operand (lane (j, g)
+    // holds key row 16 kb + j, chunk 4 s + g), Q^T the B operand.
+    bf16x8 kop[2][G::kSteps];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int s = 0; s < G::kSteps; ++s)
+        kop[kb][s] = *reinterpret_cast<const bf16x8*>(st + 16 * kb * G::kRowBytes + ko[s]);
+    f32x4 sacc[MB][2];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int s = 0; s < G::kSteps; ++s) {
+        const bf16x8 qs = *reinterpret_cast<const bf16x8*>(qlds + 16 * mb * G::kRowBytes + ko[s]);
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        sacc[mb][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0][s], qs, s == 0 ? z : sacc[mb][0], 0, 0, 0);
+        sacc[mb][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[1][s], qs, s == 0 ? z : sacc[mb][1], 0, 0, 0);
+      }
+    }
+    // The keys of the slot are read: refill them while the softmax runs.
+    if (i + G::kSlots < mine) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue_k(i + G::kSlots);
+    }
+
+    // Row maxima on the raw scores (the scale is positive; lane column j is
+    // the query row, lane (j, g) holds keys n0 + 16 kb + 4 g + e).  A row's
+    // reference maximum is its first finite tile maximum and moves only when
+    // a later one exceeds it by more than 2^kRescaleLog2 (p then stays below
+    // 2^32, far inside the fp32 and bf16 range; the result is exact either
+    // way).  Moving it from -inf needs no rescale (O and l are still 0); a
+    // real rescale is rare and done in one branch for the whole tile.
+    const bool full = n0 >= f_lo && n0 + 31 <= f_hi;
+    float x[MB][8], tmax[MB];
+    bool grow[MB];
+    bool rescale = false;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[mb][e] = sacc[mb][0][e];
+        x[mb][4 + e] = sacc[mb][1][e];
+      }
+      if (!full) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int n = n0 + 16 * (e >> 2) + 4 * g + (e & 3);
+          bool vis = n >= lo[mb] && n <= hi[mb] && n <= s_hi;
+          if constexpr (TREE) vis = vis && tree_visible(n, tbase, anc[mb]);
+          x[mb][e] = vis ? x[mb][e] : kNegInf;
+        }
+      }
+      const float* xm = x[mb];
+      const float bm =
+          group_max(fmaxf(fmaxf(fmaxf(xm[0], xm[1]), fmaxf(xm[2], xm[3])), fmaxf(fmaxf(xm[4], xm[5]), fmaxf(xm[6], xm[7])))) *
+          scale_log2;
+      tmax[mb] = bm;
+      grow[mb] = bm > m_run[mb] + kRescaleLog2;
+      if constexpr (!FIRST) rescale = rescale || (grow[mb] && m_run[mb] != kNegInf);
+    }
+    if constexpr (!FIRST) {
+      if (__builtin_amdgcn_ballot_w64(rescale)) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const float alpha =
+              (grow[mb] && m_run[mb] != kNegInf) ? __builtin_amdgcn_exp2f(m_run[mb] - tmax[mb]) : 1.f;
+          l_run[mb] *= alpha;
+#pragma unroll
+          for (int cb = 0; cb < G::kCBlocks; ++cb) {
+            // the empty asm pins the accumulators in AGPRs up to here, so the
+            // compiler copies them to VGPRs inside this branch, not every tile
+            f32x4 t = o[cb][mb];
+            asm volatile("" : "+a"(t));
+            o[cb][mb] = t * alpha;
+          }
+        }
+      }
+    }
+
+    // O^T += V^T . P^T: V^T is the A operand (two transposed reads per
+    // column block), P^T the B operand, which the S^T accumulator layout
+    // already is (k-index 8 g + e = key 4 g + e of the first 16, 16 + 4 g +
+    // e - 4 of the second).
+    bf16x8 vop[G::kCBlocks];
+#pragma unroll
+    for (int cb = 0; cb < G::kCBlocks; ++cb) {
+      const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(sv + vo[cb]));
+      const s16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(sv + 16 * G::kRowBytes + vo[cb]));
+      vop[cb] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      m_run[mb] = grow[mb] ? tmax[mb] : m_run[mb];
+      // a row with no visible key so far has every score at -inf: any finite
+      // reference gives p = 0
+      const float neg_m = m_run[mb] == kNegInf ? 0.f : -m_run[mb];
+      float pe[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pe[e] = __builtin_amdgcn_exp2f(fmaf(x[mb][e], scale_log2, neg_m));
+      l_run[mb] += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
+      const bf16x8 pt = pack_bf16x8(pe);
+#pragma unroll
+      for (int cb = 0; cb < G::kCBlocks; ++cb) {
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        o[cb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[cb], pt, FIRST ? z : o[cb][mb], 0, 0, 0);
+      }
+    }
+    // The values of the slot are read: refill them.
+    if (i + G::kSlots < mine) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue_v(i + G::kSlots);
+    }
+  };
+
+  if (mine > 0) {
+    step(0, std::integral_constant<bool, true>{});
+#pragma unroll 1
+    for (int i = 1; i < mine; ++i) step(i, std::integral_constant<bool, false>{});
+  } else {
+#pragma unroll
+    for (int cb = 0; cb < G::kCBlocks; ++cb)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) o[cb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  wait_vmcnt<0>();
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) l_run[mb] = group_sum(l_run[mb]);
+
+  // ---- merge the four wavefronts (the buffers reuse the rings) ----
+  __syncthreads();
+  float* stats = reinterpret_cast<float*>(ring_all);  // [wave][row]: m, then l
+  float* xbuf = stats + kKeyWaves * kRows * 2;        // [column block][slot 0..2][kBlockFloats]
+  if (g == 0) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      stats[(w * kRows + 16 * mb + j) * 2] = m_run[mb];
+      stats[(w * kRows + 16 * mb + j) * 2 + 1] = l_run[mb];
+    }
+  }
+  __syncthreads();
+  float fac[MB], lse2[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int row = 16 * mb + j;
+    float mw[kKeyWaves], lw[kKeyWaves];
+    float M = kNegInf;
+#pragma unroll
+    for (int u = 0; u < kKeyWaves; ++u) {
+      mw[u] = stats[(u * kRows + row) * 2];
+      lw[u] = stats[(u * kRows + row) * 2 + 1];
+      M = fmaxf(M, mw[u]);
+    }
+    float L = 0.f;
+    if (M != kNegInf) {
+#pragma unroll
+      for (int u = 0; u < kKeyWaves; ++u)
+        if (mw[u] != kNegInf) L += lw[u] * exp2f(mw[u] - M);
+    }
+    // The sink joins the denominator when the split is the whole range.
+    if (splits == 1 && sink && row < R) {
+      const float sl = sink[row % H] * kLog2e;
+      const float M2 = fmaxf(M, sl);
+      L = (M == kNegInf ? 0.f : L * exp2f(M - M2)) + exp2f(sl - M2);
+      M = M2;
+    }
+    fac[mb] = (L > 0.f && m_run[mb] != kNegInf) ? exp2f(m_run[mb] - M) / L : 0.f;
+    lse2[mb] = L > 0.f ? M + log2f(L) : kNegInf;
+  }
+  // Column block cb is finished by wavefront cb / kOwn; the other three
+  // leave their scaled share in its slots.
+#pragma unroll
+  for (int cb = 0; cb < G::kCBlocks; ++cb) {
+    const int owner = cb / kOwn;
+    if (owner == w) continue;
+    const int slot = w < owner ? w : w - 1;
+    float* dst = xbuf + (cb * (kKeyWaves - 1) + slot) * kBlockFloats;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) *reinterpret_cast<f32x4*>(dst + (64 * mb + lane) * 4) = o[cb][mb] * fac[mb];
+  }
+  __syncthreads();
+  typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int cb = 0; cb < G::kCBlocks; ++cb) {
+    if (cb / kOwn != w) continue;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int row = 16 * mb + j;
+      f32x4 acc = o[cb][mb] * fac[mb];
+#pragma unroll
+      for (int sl = 0; sl < kKeyWaves - 1; ++sl)
+        acc += *reinterpret_cast<const f32x4*>(xbuf + (cb * (kKeyWaves - 1) + sl) * kBlockFloats + (64 * mb + lane) * 4);
+      if (row >= R) continue;
+      const bf16x4 val = {static_cast<__bf16>(acc[0]), static_cast<__bf16>(acc[1]), static_cast<__bf16>(acc[2]),
+                          static_cast<__bf16>(acc[3])};
+      unsigned short* dst = splits == 1 ? out + ((int64_t)b * R + row) * C
+                                        : part_o + (((int64_t)b * splits + split) * kRows + row) * C;
+      *reinterpret_cast<bf16x4*>(dst + cb * 16 + 4 * g) = val;
+    }
+  }
+  if (w == 0 && g == 0) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int row = 16 * mb + j;
+      if (row >= R) continue;
+      if (splits == 1) {
+        if (lse_out) lse_out[(int64_t)b * R + row] = lse2[mb] * kLn2;
+      } else {
+        part_lse[((int64_t)b * splits + split) * kRows + row] = lse2[mb];
+      }
+    }
+  }
+}
+
 // Merges the splits of each query row: fixed order, log-sum-exp weights,
-// the sink joining the denominator.  One thread per (batch row, query row,
-// 4 columns); the parts of one row are read with independent loads.
-template <typename OutT>
-__global__ __launch_bounds__(256) void combine_splits(const float* __restrict__ part_o,
-                                                       const float* __restrict__ part_lse,
-                                                       const float* __restrict__ sink, int B, int R, int H, int C,
-                                                       int rows_per_group, int groups, int splits,
-                                                       OutT* __restrict__ out, float* __restrict__ lse_out) {
-  const int per_row = C / 4;
+// the sink joining the denominator.  One thread per (batch row, query row, 8
+// columns); the parts of a row are read eight at a time, every load of a
+// group issued before any is used (a part count up to 8 costs one memory
+// round trip), with a running maximum across groups.
+__global__ __launch_bounds__(256) void combine_splits(const unsigned short* __restrict__ part_o,
+                                                      const float* __restrict__ part_lse,
+                                                      const float* __restrict__ sink, int B, int R, int H, int C,
+                                                      int rows_per_group, int groups, int splits,
+                                                      unsigned short* __restrict__ out, float* __restrict__ lse_out) {
+  constexpr int kGroup = 8;
+  const int per_row = C / 8;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)B * R * per_row) return;
   const int b = (int)(idx / ((int64_t)R * per_row));
   const int rem = (int)(idx % ((int64_t)R * per_row));
   const int r = rem / per_row;
-  const int c4 = (rem % per_row) * 4;
+  const int c8 = (rem % per_row) * 8;
   const int grp = r / rows_per_group, rr = r % rows_per_group;
   const int64_t row0 = ((int64_t)(b * groups + grp) * splits) * rows_per_group + rr;  // split 0's part
-  constexpr int kUnroll = 8;
-  float M = kNegInf;
-  for (int s0 = 0; s0 < splits; s0 += kUnroll) {
-    float ls[kUnroll];
+  float M = kNegInf, L = 0.f;
+  float acc[8];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) ls[u] = s0 + u < splits ? part_lse[row0 + (int64_t)(s0 + u) * rows_per_group] : kNegInf;
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += kGroup) {
+    float ls[kGroup];
+    u16x8 po[kGroup];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) M = fmaxf(M, ls[u]);
-  }
-  const float sl = sink ? sink[r % H] * kLog2e : kNegInf;
-  const float M2 = fmaxf(M, sl);
-  float L = 0.f;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  if (M2 != kNegInf) {
-    for (int s0 = 0; s0 < splits; s0 += kUnroll) {
-      float ls[kUnroll];
-      f32x4 po[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int64_t prow = row0 + (int64_t)(s0 + u) * rows_per_group;
-        const bool in = s0 + u < splits;
-        ls[u] = in ? part_lse[prow] : kNegInf;
-        po[u] = in ? *reinterpret_cast<const f32x4*>(part_o + prow * C + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (ls[u] == kNegInf) continue;
-        const float w = exp2f(ls[u] - M2);
-        L += w;
-        acc += w * po[u];
-      }
+    for (int u = 0; u < kGroup; ++u) {
+      const int64_t prow = row0 + (int64_t)(s0 + u) * rows_per_group;
+      const bool in = s0 + u < splits;
+      ls[u] = in ? part_lse[prow] : kNegInf;
+      po[u] = in ? *reinterpret_cast<const u16x8*>(part_o + prow * C + c8) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
-    if (sink) L += exp2f(sl - M2);
+    float m = M;
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) m = fmaxf(m, ls[u]);
+    if (m == kNegInf) continue;  // nothing seen yet
+    const float f = M == kNegInf ? 0.f : exp2f(M - m);
+    L *= f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= f;
+    M = m;
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      if (ls[u] == kNegInf) continue;
+      const float wgt = exp2f(ls[u] - M);
+      L += wgt;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += wgt * bf16_to_f32(po[u][e]);
+    }
+  }
+  if (sink) {
+    const float sl = sink[r % H] * kLog2e;
+    const float M2 = fmaxf(M, sl);
+    const float f = M == kNegInf ? 0.f : exp2f(M - M2);
+    L = L * f + exp2f(sl - M2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= f;
+    M = M2;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  OutT* dst = out + ((int64_t)b * R + r) * C + c4;
-  for (int e = 0; e < 4; ++e) dst[e] = from_f32<OutT>(acc[e] * inv);
-  if (lse_out && c4 == 0) lse_out[(int64_t)b * R + r] = L > 0.f ? (M2 + log2f(L)) * kLn2 : kNegInf;
+  u16x8 res;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) res[e] = f32_to_bf16(acc[e] * inv);
+  *reinterpret_cast<u16x8*>(out + ((int64_t)b * R + r) * C + c8) = res;
+  if (lse_out && c8 == 0) lse_out[(int64_t)b * R + r] = L > 0.f ? (M + log2f(L)) * kLn2 : kNegInf;
 }
 
 // ---------------------------------------------------------------------------
@@ -628,9 +1133,11 @@ __global__ __launch_bounds__(64) void attention_generic(
 // Host side
 // ---------------------------------------------------------------------------
 
+enum Kind { kGeneric = 0, kRowBlocks = 1, kKeySplit = 2 };
+
 struct Plan {
-  bool mfma;
-  int mbw;      // m-blocks per workgroup
+  Kind kind;
+  int mbw;      // m-blocks per workgroup (row-block kernel) or per wavefront (key-parallel kernel)
   int groups;   // query-row groups per batch row
   int splits;   // key-range parts per batch row
   size_t bytes; // workspace
@@ -657,8 +1164,9 @@ int plan(int B, int T, int H, int c, int N, int window, int dtype, int flags, in
     return fail(WPTV_E_UNSUPPORTED, "verify_attention: dtype %d is neither fp32 nor bf16", dtype);
   if (c > kMaxC) return fail(WPTV_E_UNSUPPORTED, "verify_attention: head width %d above %d", c, kMaxC);
   Plan p{};
-  p.mfma = dtype == WPTV_BF16 && (c == 64 || c == 128) && !(flags & WPTV_ATTN_FORCE_GENERIC);
-  if (!p.mfma) {
+  const bool mfma = dtype == WPTV_BF16 && (c == 64 || c == 128) && !(flags & WPTV_ATTN_FORCE_GENERIC);
+  if (!mfma) {
+    p.kind = kGeneric;
     p.mbw = 0;
     p.groups = 1;
     p.splits = 1;
@@ -667,19 +1175,29 @@ int plan(int B, int T, int H, int c, int N, int window, int dtype, int flags, in
     return WPTV_OK;
   }
   const int R = T * H;
-  p.mbw = pick_mbw(R);
-  p.groups = (R + 16 * p.mbw - 1) / (16 * p.mbw);
+  const int blocks = (R + 15) / 16;
+  p.kind = (blocks <= 5 && (flags & WPTV_ATTN_KEY_SPLIT)) ? kKeySplit : kRowBlocks;
+  if (p.kind == kKeySplit) {
+    p.mbw = blocks;
+    p.groups = 1;
+  } else {
+    p.mbw = pick_mbw(R);
+    p.groups = (R + 16 * p.mbw - 1) / (16 * p.mbw);
+  }
   // Key rows a group reads: the whole table, or the window plus the span of
   // the query positions (T - 1 for consecutive positions).
   long long span = N;
   if (window > 0 && (long long)window + T - 1 < span) span = (long long)window + T - 1;
+  // The smallest useful part: one 32-row tile per wavefront (key-parallel
+  // kernel) or per key set (row-block kernel).
+  const long long quantum = p.kind == kKeySplit ? 32 * kKeyWaves : 32 * kKeySets;
   int splits = requested;
   if (splits <= 0) {
     const long long cus = compute_units();
     const long long wgs = (long long)B * p.groups;
-    // Enough workgroups to fill the GPU, each at least one 32-row tile per key set.
+    // One workgroup per compute unit.
     long long s = (cus + wgs - 1) / wgs;
-    const long long max_s = (span + 32 * kKeySets - 1) / (32 * kKeySets);
+    const long long max_s = (span + quantum - 1) / quantum;
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
     splits = (int)s;
@@ -687,8 +1205,9 @@ int plan(int B, int T, int H, int c, int N, int window, int dtype, int flags, in
   if (splits > 4096) return fail(WPTV_E_INVALID, "verify_attention: splits %d above 4096", splits);
   p.splits = splits;
   if (splits > 1) {
+    // parts: bf16 outputs (normalized per part) and fp32 log-sum-exps
     const size_t rows = (size_t)B * p.groups * splits * 16 * p.mbw;
-    p.bytes = align_up(rows * c * sizeof(float), 256) + align_up(rows * sizeof(float), 256);
+    p.bytes = align_up(rows * c * 2, 256) + align_up(rows * sizeof(float), 256);
   } else {
     p.bytes = 0;
   }
@@ -696,12 +1215,23 @@ int plan(int B, int T, int H, int c, int N, int window, int dtype, int flags, in
   return WPTV_OK;
 }
 
+template <int C, int MB, bool TREE>
+void launch_keys(dim3 grid, hipStream_t stream, const unsigned short* q, const unsigned short* k, int64_t ksb,
+                 int64_t ksn, const unsigned short* v, int64_t vsb, int64_t vsn, const int64_t* positions,
+                 int window, const int64_t* tree_base, const uint64_t* ancestors, const float* sink, int T, int H,
+                 int N, float scale_log2, int splits, int xcd_map, unsigned short* out, float* lse,
+                 unsigned short* part_o, float* part_lse) {
+  hipLaunchKernelGGL((verify_attention_keys<C, MB, TREE>), grid, dim3(kKeyWaves * 64), 0, stream, q, k, ksb, ksn,
+                     v, vsb, vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, splits,
+                     xcd_map, out, lse, part_o, part_lse);
+}
+
 template <int C, int MBW, bool TREE>
 void launch_mfma(dim3 grid, hipStream_t stream, const unsigned short* q, const unsigned short* k, int64_t ksb,
                  int64_t ksn, const unsigned short* v, int64_t vsb, int64_t vsn, const int64_t* positions,
                  int window, const int64_t* tree_base, const uint64_t* ancestors, const float* sink, int T, int H,
                  int N, float scale_log2, int groups, int splits, int range_from_positions, int xcd_map,
-                 unsigned short* out, float* lse, float* part_o, float* part_lse) {
+                 unsigned short* out, float* lse, unsigned short* part_o, float* part_lse) {
   hipLaunchKernelGGL((verify_attention_mfma<C, MBW, TREE>), grid, dim3(kKeySets * MBW * 64), 0, stream, q, k, ksb,
                      ksn, v, vsb, vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, groups,
                      splits, range_from_positions, xcd_map, out, lse, part_o, part_lse);
@@ -739,14 +1269,15 @@ extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_str
   int st = plan(B, T, H, c, N, window, dtype, flags, splits, &p);
   if (st != WPTV_OK) return st;
   const float scale_log2 = scale * kLog2e;
-  if (p.mfma) {
+  if (p.kind != kGeneric && !(scale > 0.f && scale < 1e30f)) p.kind = kGeneric, p.splits = 1, p.bytes = 0;  // the MFMA kernels take row maxima on unscaled scores
+  if (p.kind != kGeneric) {
     // 32-bit byte offsets within one batch row's table (buffer loads).
     const bool ok_range = (double)N * (double)(k_stride_n > v_stride_n ? k_stride_n : v_stride_n) * 2.0 < 4.0e9;
     const bool ok_align = ok_range && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && (k_stride_b % 8 == 0) &&
                           (k_stride_n % 8 == 0) && (v_stride_b % 8 == 0) && (v_stride_n % 8 == 0);
-    if (!ok_align) p.mfma = false, p.splits = 1, p.bytes = 0;
+    if (!ok_align) p.kind = kGeneric, p.splits = 1, p.bytes = 0;
   }
-  if (!p.mfma) {
+  if (p.kind == kGeneric) {
     dim3 grid(T * H, B);
     if (dtype == WPTV_F32)
       hipLaunchKernelGGL(attention_generic<float>, grid, dim3(64), 0, stream, (const float*)q, (const float*)k,
@@ -764,53 +1295,83 @@ extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_str
                 workspace_bytes, p.bytes, p.splits);
   const int R = T * H;
   const int rows_per_group = 16 * p.mbw;
-  float* part_o = nullptr;
+  const size_t part_elem = 2;
+  void* part_o = nullptr;
   float* part_lse = nullptr;
   if (p.splits > 1) {
     const size_t rows = (size_t)B * p.groups * p.splits * rows_per_group;
-    part_o = static_cast<float*>(workspace);
-    part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(rows * c * sizeof(float), 256));
+    part_o = workspace;
+    part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(rows * c * part_elem, 256));
   }
   const int units = B * p.groups;
   dim3 grid(units * p.splits);
   const int xcd_map = units % 8 == 0 ? 1 : 0;
-  // Full causal attention of a single query group reads the whole table; any
-  // other case takes its key range from the positions.
-  const int from_positions = (window > 0 || p.groups > 1 || (flags & WPTV_ATTN_RANGE_FROM_POSITIONS)) ? 1 : 0;
   const auto* qb = static_cast<const unsigned short*>(q);
   const auto* kb = static_cast<const unsigned short*>(k);
   const auto* vb = static_cast<const unsigned short*>(v);
   auto* ob = static_cast<unsigned short*>(out);
+  if (p.kind == kKeySplit) {
+    auto* po = static_cast<unsigned short*>(part_o);
+#define WPTV_LAUNCH(CC, MM)                                                                                       \
+  (tree_base ? launch_keys<CC, MM, true> : launch_keys<CC, MM, false>)(                                           \
+      grid, stream, qb, kb, k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, positions, window, tree_base,     \
+      tree_ancestors, sink, T, H, N, scale_log2, p.splits, xcd_map, ob, lse, po, part_lse)
+    if (c == 128) {
+      switch (p.mbw) {
+        case 1: WPTV_LAUNCH(128, 1); break;
+        case 2: WPTV_LAUNCH(128, 2); break;
+        case 3: WPTV_LAUNCH(128, 3); break;
+        case 4: WPTV_LAUNCH(128, 4); break;
+        default: WPTV_LAUNCH(128, 5); break;
+      }
+    } else {
+      switch (p.mbw) {
+        case 1: WPTV_LAUNCH(64, 1); break;
+        case 2: WPTV_LAUNCH(64, 2); break;
+        case 3: WPTV_LAUNCH(64, 3); break;
+        case 4: WPTV_LAUNCH(64, 4); break;
+        default: WPTV_LAUNCH(64, 5); break;
+      }
+    }
+#undef WPTV_LAUNCH
+    st = launched("verify_attention_keys");
+  } else {
+    // Full causal attention of a single query group reads the whole table; any
+    // other case takes its key range from the positions.
+    const int from_positions = (window > 0 || p.groups > 1 || (flags & WPTV_ATTN_RANGE_FROM_POSITIONS)) ? 1 : 0;
+    auto* po = static_cast<unsigned short*>(part_o);
 #define WPTV_LAUNCH(CC, MM)                                                                                     \
   (tree_base ? launch_mfma<CC, MM, true> : launch_mfma<CC, MM, false>)(                                         \
       grid, stream, qb, kb, k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, positions, window, tree_base,   \
-      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_map, ob, lse, part_o, \
+      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_map, ob, lse, po, \
       part_lse)
-  if (c == 128) {
-    switch (p.mbw) {
-      case 1: WPTV_LAUNCH(128, 1); break;
-      case 2: WPTV_LAUNCH(128, 2); break;
-      case 3: WPTV_LAUNCH(128, 3); break;
-      case 4: WPTV_LAUNCH(128, 4); break;
-      default: WPTV_LAUNCH(128, 5); break;
+    if (c == 128) {
+      switch (p.mbw) {
+        case 1: WPTV_LAUNCH(128, 1); break;
+        case 2: WPTV_LAUNCH(128, 2); break;
+        case 3: WPTV_LAUNCH(128, 3); break;
+        case 4: WPTV_LAUNCH(128, 4); break;
+        default: WPTV_LAUNCH(128, 5); break;
+      }
+    } else {
+      switch (p.mbw) {
+        case 1: WPTV_LAUNCH(64, 1); break;
+        case 2: WPTV_LAUNCH(64, 2); break;
+        case 3: WPTV_LAUNCH(64, 3); break;
+        case 4: WPTV_LAUNCH(64, 4); break;
+        default: WPTV_LAUNCH(64, 5); break;
+      }
     }
-  } else {
-    switch (p.mbw) {
-      case 1: WPTV_LAUNCH(64, 1); break;
-      case 2: WPTV_LAUNCH(64, 2); break;
-      case 3: WPTV_LAUNCH(64, 3); break;
-      case 4: WPTV_LAUNCH(64, 4); break;
-      default: WPTV_LAUNCH(64, 5); break;
-    }
-  }
 #undef WPTV_LAUNCH
-  st = launched("verify_attention_mfma");
+    st = launched("verify_attention_mfma");
+  }
   if (st != WPTV_OK || p.splits == 1) return st;
   const int threads = 256;
-  const long long items = (long long)B * R * (c / 4);
+  const long long items = (long long)B * R * (c / 8);
   dim3 cgrid((unsigned)((items + threads - 1) / threads));
-  hipLaunchKernelGGL(combine_splits<unsigned short>, cgrid, dim3(threads), 0, stream, part_o, part_lse, sink, B, R, H, c,
-                     rows_per_group, p.groups, p.splits, ob, lse);
+  hipLaunchKernelGGL(combine_splits, cgrid, dim3(threads), 0, stream,
+                     static_cast<const unsigned short*>(part_o), part_lse, sink, B, R, H, c, rows_per_group, p.groups,
+                     p.splits, ob, lse);
   return launched("combine_splits");
 }
 

@@ -81,7 +81,7 @@ def _long(x, device):
 
 
 def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=None, lse=False, splits=0,
-                     generic=False, from_positions=False):
+                     generic=False, from_positions=False, key_split=False):
     """MQA attention of q (B, T, H, c) over k, v (B, N, c): query t of row b
     sees rows max(0, p - window + 1) .. min(p, N - 1), p = positions[b, t]
     (window 0: from row 0), and with tree = (tree_base (B,), ancestors (T,)
@@ -90,7 +90,9 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
     Returns the output (B, T, H, c) in q's dtype, and with lse=True also the
     (B, T, H) FP32 log-sum-exp.  splits: key-range parts per batch row (0:
     the library chooses); generic: the wave-per-query kernel; from_positions:
-    read only the rows the positions reach (a cache table with spare rows)."""
+    read only the rows the positions reach (a cache table with spare rows);
+    key_split: where T*H <= 80, the key-parallel MFMA kernel instead of the
+    row-block one."""
     B, T, H, c, N = _check_inputs(q, k, v, positions)
     device = q.device
     library = _lib.lib()
@@ -105,7 +107,8 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
         tree_base, ancestors = (_long(x, device) for x in tree)
         if tree_base.shape != (B,) or ancestors.shape != (T,):
             raise ValueError(f"tree must be (tree_base (B={B},), ancestors (T={T},))")
-    flags = (_lib.FORCE_GENERIC if generic else 0) | (_lib.RANGE_FROM_POSITIONS if from_positions else 0)
+    flags = ((_lib.FORCE_GENERIC if generic else 0) | (_lib.RANGE_FROM_POSITIONS if from_positions else 0)
+             | (_lib.KEY_SPLIT if key_split else 0))
     parts = _lib.ctypes.c_int(int(splits))
     size = _lib.ctypes.c_size_t(0)
     check(library.wptv_attention_workspace(B, T, H, c, N, int(window), dtype, flags, _lib.ctypes.byref(parts),
