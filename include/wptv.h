@@ -149,6 +149,26 @@ int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const float* q_norm, 
 int wptv_swiglu(const void* gate_up, void* out, int M, int F, int dtype, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Skinny matrix products on the matrix cores: out[M, N] = x[M, K] . w[N, K]^T
+ * in bf16 with FP32 accumulation -- the reference's nn.Linear projections and
+ * lm_head under bf16 autocast (packages/wpt-model/src/wpt_model/
+ * attention.py:113-124,157-168, layers.py:45-61, model.py:267,471), at the
+ * verify step's few rows (M <= 512; N a multiple of 64, K of 64).
+ *
+ *   x, w       row-major bf16 with leading dimensions ldx, ldw (elements)
+ *   out        [M, N] with leading dimension ldo: bf16 (out_dtype
+ *              WPTV_BF16) or FP32 holding the bf16-rounded product
+ *              (WPTV_F32: the reference's bf16 logits cast to FP32)
+ *   splits     parts of K (0 = chosen from M, N, K and the GPU); the FP32
+ *              part products go through the workspace,
+ *              wptv_gemm_workspace() bytes for the same M, N, K and splits
+ * ------------------------------------------------------------------------- */
+int wptv_gemm_workspace(int M, int N, int K, int* splits, size_t* bytes);
+
+int wptv_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K, void* out, int64_t ldo,
+              int out_dtype, int splits, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Acceptance: the reference's per-row verification loop of
  * Writer._speculate (packages/wpt-inference/src/wpt_inference/__init__.py:
  * 210-229) with its sampling distribution Writer._probabilities (:173-179),

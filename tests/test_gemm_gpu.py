@@ -1,0 +1,70 @@
+"""The skinny bf16 matrix product (wptv_gemm, through wpt_amd.layers.linear)
+against a plain PyTorch FP32 product of the same bf16 operands, on the GPU:
+within 1e-2 of the largest expected value (bf16 output rounding and the FP32
+accumulation order), and the FP32 output exactly the bf16-rounded product's
+value as FP32 where the two round alike."""
+
+import pytest
+import torch
+
+from tests.formulas import relative_error
+from wpt_amd import layers
+
+pytestmark = pytest.mark.gpu
+
+
+def operands(M, N, K, seed, device):
+    generator = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=generator).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=generator) * 0.02).to(torch.bfloat16)
+    return x.to(device), w.to(device)
+
+
+@pytest.mark.parametrize("M, N, K, splits", [
+    (160, 2304, 2048, 0),    # the q/k/v projection at batch 32, k+1 = 5
+    (160, 2048, 2048, 0),    # the output projection
+    (160, 11264, 2048, 0),   # SwiGLU gate and up
+    (160, 2048, 5632, 0),    # the down projection
+    (320, 2048, 2048, 0),    # batch 64
+    (496, 1024, 2048, 0),    # the tree's 16 x 31 rows (lm_head shape, fewer columns)
+    (17, 192, 320, 3),       # rows that are not a multiple of 16, an uneven K split
+    (64, 128, 64, 1),        # one K chunk
+])
+def test_linear_matches_the_fp32_product(device, M, N, K, splits):
+    x, w = operands(M, N, K, seed=M + N + K, device=device)
+    expected = x.float() @ w.float().T
+    got = layers.linear(x, w, splits=splits)
+    assert got.dtype == torch.bfloat16 and got.shape == (M, N)
+    assert relative_error(got.float().cpu(), expected.cpu()) < 1e-2
+
+
+def test_fp32_output_is_the_bf16_rounded_product(device):
+    M, N, K = 160, 4096, 2048
+    x, w = operands(M, N, K, seed=5, device=device)
+    got = layers.linear(x, w, out_dtype=torch.float32)
+    bf16 = layers.linear(x, w)
+    assert got.dtype == torch.float32
+    # the same FP32 sums rounded once: identical to the bf16 output's values
+    assert torch.equal(got, bf16.float())
+    assert relative_error(got.cpu(), (x.float() @ w.float().T).cpu()) < 1e-2
+
+
+def test_splits_agree(device):
+    M, N, K = 160, 512, 2048
+    x, w = operands(M, N, K, seed=6, device=device)
+    one = layers.linear(x, w, splits=1).float()
+    for splits in (2, 5, 32):
+        assert (layers.linear(x, w, splits=splits).float() - one).abs().max() <= 2e-2 * one.abs().max()
+
+
+def test_batched_rows_and_bad_shapes(device):
+    x, w = operands(160, 256, 128, seed=7, device=device)
+    got = layers.linear(x.reshape(32, 5, 128), w)
+    assert got.shape == (32, 5, 256)
+    assert relative_error(got.reshape(160, 256).float().cpu(), (x.float() @ w.float().T).cpu()) < 1e-2
+    with pytest.raises(NotImplementedError):
+        layers.linear(x, w[:100])            # N not a multiple of 64
+    with pytest.raises(NotImplementedError):
+        layers.linear(torch.zeros(600, 128, dtype=torch.bfloat16, device=device), w)  # above 512 rows
+    with pytest.raises(ValueError):
+        layers.linear(x.float(), w)

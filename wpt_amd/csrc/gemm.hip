@@ -1,0 +1,317 @@
+// Skinny matrix products of the verify step on the matrix cores:
+//
+//   C[M, N] = X[M, K] . W[N, K]^T        bf16 in, FP32 accumulation
+//
+// The reference's projections and lm_head are nn.Linear products under bf16
+// autocast (attention.py:113-124,157-168, layers.py:45-61, model.py:267,471):
+// the verify step multiplies M = B (k+1) rows (160 at batch 32, k = 4) by
+// weights of 8 to 134 MB, so each product streams its weight matrix once and
+// the rows X stay in the L2.
+//
+// One workgroup (4 wavefronts) per 64 output columns and one part of K (a
+// "split"; the splits of a column tile add their FP32 products into the
+// workspace, and wptv_gemm's reduction, or the consumer, sums them).  The
+// workgroup stages 64-wide K chunks of W (64 rows) and of X (all M rows,
+// padded to 64 MBW) through a ring in LDS by DMA; wavefront w multiplies its
+// MBW 16-row blocks of X by the four 16-column blocks of W:
+//
+//   C^T[n, m] += W[n, k] . X^T[k, m]     v_mfma_f32_16x16x32_bf16, W as the A
+//                                       operand, so lane (j, g) ends with 4
+//                                       consecutive columns of row m = j
+//
+// LDS rows are 128 bytes (64 bf16); the 16-byte piece q of row r sits at
+// position q ^ ((r >> 1) & 7), so the 16 lanes of an operand read (16 rows,
+// one piece) hit distinct bank groups.  The DMA writes 1 KiB (8 rows) per
+// instruction, each lane fetching the piece that belongs at its position.
+#include "wptv_common.h"
+
+#include <climits>
+
+namespace wptv {
+namespace {
+
+constexpr int kGemmWaves = 4;
+constexpr int kTileN = 64;         // output columns per workgroup
+constexpr int kChunkK = 64;        // K per staged chunk (two k-steps of 32)
+constexpr int kRowBytes = kChunkK * 2;
+
+template <int MBW>
+struct GemmTile {
+  static constexpr int kRows = 64 * MBW;                 // staged X rows (all M, padded)
+  static constexpr int kWBytes = kTileN * kRowBytes;     // 8 KiB
+  static constexpr int kSlotBytes = kWBytes + kRows * kRowBytes;
+  static constexpr int kSlots = (160 * 1024) / kSlotBytes < 4 ? (160 * 1024) / kSlotBytes : 4;
+  static constexpr int kPieces = kSlotBytes / 1024;      // 1 KiB DMA instructions per chunk
+  static constexpr int kPerWave = kPieces / kGemmWaves;  // 2 + 2 MBW
+  static_assert(kPieces % kGemmWaves == 0, "pieces per wave");
+  static_assert(kSlots >= 2, "ring");
+  static_assert((kSlots - 1) * kPerWave < 64, "vmcnt range");
+};
+
+__device__ __forceinline__ int gemm_swz(int r) { return (r >> 1) & 7; }
+
+// vmcnt wait for this wavefront's pieces of one chunk, `behind` chunks
+// (0 .. kSlots - 1) still allowed in flight after it.
+template <int kPer>
+__device__ __forceinline__ void wait_chunks_behind(int behind) {
+  if (behind >= 3)
+    wait_vmcnt<(3 * kPer < 64 ? 3 * kPer : 63)>();
+  else if (behind == 2)
+    wait_vmcnt<2 * kPer>();
+  else if (behind == 1)
+    wait_vmcnt<kPer>();
+  else
+    wait_vmcnt<0>();
+}
+
+enum GemmOut { kPartF32 = 0, kOutBf16 = 1, kOutF32 = 2 };
+
+// grid: (N / 64, splits).  Split z multiplies K chunks [z cps, min((z + 1) cps, K / 64)).
+// OUT: kPartF32 -> part[z][m][n] FP32; kOutBf16 -> out bf16; kOutF32 -> out
+// FP32 holding the bf16-rounded product (the reference's bf16 product cast to
+// FP32).
+template <int MBW, int OUT>
+__global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned short* __restrict__ x, int64_t ldx,
+                                                               const unsigned short* __restrict__ w, int64_t ldw,
+                                                               int M, int N, int K, int cps, void* __restrict__ out,
+                                                               int64_t ldo) {
+  using G = GemmTile<MBW>;
+  __shared__ __attribute__((aligned(16))) unsigned char ring[G::kSlots * G::kSlotBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * kTileN;
+  const int z = blockIdx.y;
+  const int chunks = K / kChunkK;
+  const int c0 = z * cps;
+  const int nch = max(0, min(chunks, c0 + cps) - c0);
+
+  // DMA: piece p of a chunk is 8 rows x 128 bytes (W rows for p < 8, then X
+  // rows); lane l fills row rr = l / 8, position pos = l % 8.  The row part of
+  // the offset and the chunk's K offset go in the scalar offset.
+  const i32x4 wrs = buffer_resource(w);
+  const i32x4 xrs = buffer_resource(x);
+  const int rr = lane >> 3, pos = lane & 7;
+  const uint32_t ldw_b = (uint32_t)ldw * 2u, ldx_b = (uint32_t)ldx * 2u;
+  // the swizzle of row 8 p' + rr depends on p' only through p' & 1
+  const uint32_t wv_off[2] = {(uint32_t)rr * ldw_b + 16u * (uint32_t)(pos ^ gemm_swz(rr)),
+                              (uint32_t)rr * ldw_b + 16u * (uint32_t)(pos ^ gemm_swz(8 + rr))};
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_address(ring));
+  auto issue = [&](int i) {  // this wavefront's pieces of chunk c0 + i
+    const uint32_t slot = ring_lds + (uint32_t)(i % G::kSlots) * G::kSlotBytes;
+    const uint32_t kb = (uint32_t)(c0 + i) * kRowBytes;
+#pragma unroll
+    for (int u = 0; u < G::kPerWave; ++u) {
+      const int p = wv + kGemmWaves * u;
+      if (p < 8) {
+        const uint32_t sbase = (uint32_t)(n0 + 8 * p) * ldw_b + kb;
+        dma_16B_at(wrs, wv_off[p & 1], sbase, slot + 1024u * p);
+      } else {
+        const int row = 8 * (p - 8) + rr;
+        const int src = row < M ? row : M - 1;  // padding rows repeat row M - 1
+        dma_16B(xrs, (uint32_t)src * ldx_b + kb + 16u * (uint32_t)(pos ^ gemm_swz(row)), slot + 1024u * p);
+      }
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < G::kSlots - 1; ++i)
+    if (i < nch) issue(i);
+
+  // operand offsets within a slot: W row 16 nb + j and X row 16 mb + j,
+  // piece 4 s + g (s = k-step within the chunk)
+  uint32_t op_off[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) op_off[s] = (uint32_t)(j * kRowBytes + 16 * ((4 * s + g) ^ gemm_swz(j)));
+  const int mb0 = wv * MBW;  // this wavefront's first 16-row block
+  f32x4 acc[MBW][4];
+#pragma unroll
+  for (int i = 0; i < MBW; ++i)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) acc[i][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll 1
+  for (int i = 0; i < nch; ++i) {
+    // chunk i has landed (this wavefront's pieces; the barrier covers the others')
+    wait_chunks_behind<G::kPerWave>(min(nch - 1 - i, G::kSlots - 2));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // the slot of chunk i - 1 is free (every wavefront is past it): refill it
+    if (i + G::kSlots - 1 < nch) issue(i + G::kSlots - 1);
+    const unsigned char* st = ring + (i % G::kSlots) * G::kSlotBytes;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      bf16x8 wf[4];
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        wf[nb] = *reinterpret_cast<const bf16x8*>(st + 16 * nb * kRowBytes + op_off[s]);
+#pragma unroll
+      for (int ii = 0; ii < MBW; ++ii) {
+        if (16 * (mb0 + ii) >= M) break;  // a block of padding rows only
+        const bf16x8 xf = *reinterpret_cast<const bf16x8*>(st + G::kWBytes + 16 * (mb0 + ii) * kRowBytes + op_off[s]);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          acc[ii][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[nb], xf, acc[ii][nb], 0, 0, 0);
+      }
+    }
+  }
+  wait_vmcnt<0>();
+
+  // lane (j, g) holds columns n0 + 16 nb + 4 g .. + 3 of row 16 mb + j
+#pragma unroll
+  for (int ii = 0; ii < MBW; ++ii) {
+    const int m = 16 * (mb0 + ii) + j;
+    if (m >= M) continue;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int n = n0 + 16 * nb + 4 * g;
+      const f32x4 a = acc[ii][nb];
+      if constexpr (OUT == kPartF32) {
+        float* dst = static_cast<float*>(out) + ((int64_t)z * M + m) * N + n;
+        *reinterpret_cast<f32x4*>(dst) = a;
+      } else if constexpr (OUT == kOutBf16) {
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        unsigned short* dst = static_cast<unsigned short*>(out) + (int64_t)m * ldo + n;
+        *reinterpret_cast<bf16x4*>(dst) = bf16x4{static_cast<__bf16>(a[0]), static_cast<__bf16>(a[1]),
+                                                 static_cast<__bf16>(a[2]), static_cast<__bf16>(a[3])};
+      } else {
+        float* dst = static_cast<float*>(out) + (int64_t)m * ldo + n;
+        *reinterpret_cast<f32x4*>(dst) =
+            f32x4{bf16_to_f32(f32_to_bf16(a[0])), bf16_to_f32(f32_to_bf16(a[1])), bf16_to_f32(f32_to_bf16(a[2])),
+                  bf16_to_f32(f32_to_bf16(a[3]))};
+      }
+    }
+  }
+}
+
+// out[m, n] = sum over the splits of part[z][m][n], as bf16, or as FP32
+// holding the bf16-rounded sum.  One thread per 4 columns.
+template <bool F32>
+__global__ __launch_bounds__(256) void gemm_reduce(const float* __restrict__ part, int splits, int M, int N,
+                                                   void* __restrict__ out, int64_t ldo) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per_row = N / 4;
+  if (idx >= (int64_t)M * per_row) return;
+  const int m = (int)(idx / per_row), n = (int)(idx % per_row) * 4;
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < splits; ++z) s += *reinterpret_cast<const f32x4*>(part + ((int64_t)z * M + m) * N + n);
+  if constexpr (F32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + (int64_t)m * ldo + n) =
+        f32x4{bf16_to_f32(f32_to_bf16(s[0])), bf16_to_f32(f32_to_bf16(s[1])), bf16_to_f32(f32_to_bf16(s[2])),
+              bf16_to_f32(f32_to_bf16(s[3]))};
+  } else {
+    typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<u16x4*>(static_cast<unsigned short*>(out) + (int64_t)m * ldo + n) =
+        u16x4{f32_to_bf16(s[0]), f32_to_bf16(s[1]), f32_to_bf16(s[2]), f32_to_bf16(s[3])};
+  }
+}
+
+constexpr int kMaxGemmRows = 512;  // 8 row blocks per wavefront
+
+struct GemmPlan {
+  int mbw;     // 16-row blocks per wavefront
+  int splits;  // parts of K
+  int cps;     // K chunks per split
+  size_t bytes;
+};
+
+int gemm_plan(int M, int N, int K, int requested, GemmPlan* p) {
+  if (M <= 0 || N <= 0 || K <= 0)
+    return fail(WPTV_E_INVALID, "gemm: M, N and K must be positive (got %d, %d, %d)", M, N, K);
+  if (M > kMaxGemmRows) return fail(WPTV_E_UNSUPPORTED, "gemm: M = %d above %d rows", M, kMaxGemmRows);
+  if (N % kTileN || K % kChunkK)
+    return fail(WPTV_E_UNSUPPORTED, "gemm: N (%d) must be a multiple of %d and K (%d) of %d", N, kTileN, K, kChunkK);
+  const int blocks = (M + 15) / 16;
+  int mbw = (blocks + kGemmWaves - 1) / kGemmWaves;
+  if (mbw == 4) mbw = 5;  // instantiated widths: 1, 2, 3, 5, 8
+  if (mbw > 5) mbw = 8;
+  const int tiles = N / kTileN, chunks = K / kChunkK;
+  int s = requested;
+  if (s <= 0) {
+    s = compute_units() / tiles;  // one workgroup per compute unit
+    if (s < 1) s = 1;
+  }
+  if (s > chunks) s = chunks;
+  const int cps = (chunks + s - 1) / s;
+  s = (chunks + cps - 1) / cps;  // no empty split
+  p->mbw = mbw;
+  p->splits = s;
+  p->cps = cps;
+  p->bytes = s > 1 ? align_up((size_t)s * M * N * sizeof(float), 256) : 0;
+  return WPTV_OK;
+}
+
+template <int MBW, int OUT>
+void launch_gemm(dim3 grid, hipStream_t stream, const unsigned short* x, int64_t ldx, const unsigned short* w,
+                 int64_t ldw, int M, int N, int K, int cps, void* out, int64_t ldo) {
+  hipLaunchKernelGGL((gemm_xwt<MBW, OUT>), grid, dim3(kGemmWaves * 64), 0, stream, x, ldx, w, ldw, M, N, K, cps, out,
+                     ldo);
+}
+
+template <int OUT>
+void launch_gemm_mbw(int mbw, dim3 grid, hipStream_t stream, const unsigned short* x, int64_t ldx,
+                     const unsigned short* w, int64_t ldw, int M, int N, int K, int cps, void* out, int64_t ldo) {
+  switch (mbw) {
+    case 1: launch_gemm<1, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo); break;
+    case 2: launch_gemm<2, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo); break;
+    case 3: launch_gemm<3, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo); break;
+    case 5: launch_gemm<5, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo); break;
+    default: launch_gemm<8, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo); break;
+  }
+}
+
+}  // namespace
+}  // namespace wptv
+
+using namespace wptv;
+
+extern "C" int wptv_gemm_workspace(int M, int N, int K, int* splits, size_t* bytes) {
+  if (!splits || !bytes) return fail(WPTV_E_INVALID, "gemm_workspace: null output pointer");
+  GemmPlan p;
+  const int st = gemm_plan(M, N, K, *splits, &p);
+  if (st != WPTV_OK) return st;
+  *splits = p.splits;
+  *bytes = p.bytes;
+  return WPTV_OK;
+}
+
+extern "C" int wptv_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K, void* out,
+                         int64_t ldo, int out_dtype, int splits, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
+  if (!x || !w || !out) return fail(WPTV_E_INVALID, "gemm: x, w and out must be given");
+  if (out_dtype != WPTV_BF16 && out_dtype != WPTV_F32)
+    return fail(WPTV_E_UNSUPPORTED, "gemm: output dtype %d is neither bf16 nor fp32", out_dtype);
+  GemmPlan p;
+  int st = gemm_plan(M, N, K, splits, &p);
+  if (st != WPTV_OK) return st;
+  if (ldx < K || ldw < K || ldo < N) return fail(WPTV_E_INVALID, "gemm: a leading dimension below the row width");
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16) || ldx % 8 || ldw % 8 || ldo % 4)
+    return fail(WPTV_E_INVALID, "gemm: x, w and out must be 16-byte aligned with leading dimensions of 8 elements");
+  if ((double)N * (double)ldw * 2.0 >= 4.0e9 || (double)M * (double)ldx * 2.0 >= 4.0e9)
+    return fail(WPTV_E_UNSUPPORTED, "gemm: operands above 4 GB");
+  if (p.splits > 1 && (!workspace || workspace_bytes < p.bytes))
+    return fail(WPTV_E_INVALID, "gemm: workspace of %zu bytes, %zu needed for %d splits", workspace_bytes, p.bytes,
+                p.splits);
+  const auto* xb = static_cast<const unsigned short*>(x);
+  const auto* wb = static_cast<const unsigned short*>(w);
+  dim3 grid(N / kTileN, p.splits);
+  if (p.splits == 1) {
+    if (out_dtype == WPTV_BF16)
+      launch_gemm_mbw<kOutBf16>(p.mbw, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, out, ldo);
+    else
+      launch_gemm_mbw<kOutF32>(p.mbw, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, out, ldo);
+    return launched("gemm_xwt");
+  }
+  launch_gemm_mbw<kPartF32>(p.mbw, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, workspace, 0);
+  st = launched("gemm_xwt");
+  if (st != WPTV_OK) return st;
+  const long long items = (long long)M * (N / 4);
+  dim3 rgrid((unsigned)((items + 255) / 256));
+  if (out_dtype == WPTV_BF16)
+    hipLaunchKernelGGL(gemm_reduce<false>, rgrid, dim3(256), 0, stream, static_cast<const float*>(workspace), p.splits,
+                       M, N, out, ldo);
+  else
+    hipLaunchKernelGGL(gemm_reduce<true>, rgrid, dim3(256), 0, stream, static_cast<const float*>(workspace), p.splits,
+                       M, N, out, ldo);
+  return launched("gemm_reduce");
+}

@@ -73,4 +73,60 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+
+// ---- LDS DMA (global -> LDS without registers) -----------------------------
+
+// s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+  asm volatile("" ::: "memory");
+}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// A raw buffer resource over 4 GiB from `base` (gfx9 dword3 format).
+__device__ __forceinline__ i32x4 buffer_resource(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = static_cast<int>(static_cast<uint32_t>(a));
+  r[1] = static_cast<int>(static_cast<uint32_t>(a >> 32));  // stride 0
+  r[2] = -1;
+  r[3] = 0x00020000;
+  return r;
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
+// Global -> LDS copy of 16 bytes per lane: lane l's bytes land at LDS byte
+// address `lds` + 16 l.  Written as inline assembly so that the compiler's
+// conservative wait (all loads, before any LDS read of the kernel) is not
+// inserted: the kernel waits for each tile itself.  The s_nop covers the
+// M0-write -> LDS-DMA hazard.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_16B(i32x4 rsrc, uint32_t voffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Global -> LDS copy of 16 bytes per lane at base + soffset + voffset
+// (soffset uniform): lane l's bytes land at LDS byte address `lds` + 16 l.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_16B_at(i32x4 rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(soffset), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 }  // namespace wptv

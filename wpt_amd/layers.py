@@ -66,3 +66,32 @@ def swiglu(gate_up):
     check(_lib.lib().wptv_swiglu(ptr(_rows(gate_up, "gate_up")), ptr(out), gate_up.numel() // (2 * F), F,
                                  _lib.dtype_code(gate_up.dtype), _lib.stream(gate_up.device)), "swiglu")
     return out
+
+
+def linear(x, w, out_dtype=None, splits=0):
+    """x (..., K) . w (N, K)^T on the matrix cores (the projections' and the
+    lm_head's nn.Linear under bf16 autocast): bf16 operands, FP32
+    accumulation; out_dtype bfloat16 (default) or float32 (the bf16-rounded
+    product as FP32).  At most 512 rows; N and K multiples of 64."""
+    _gpu(x, w)
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise ValueError(f"linear takes bf16 operands; got {x.dtype} and {w.dtype}")
+    K = x.shape[-1]
+    N = w.shape[0]
+    if w.dim() != 2 or w.shape[1] != K or w.stride(1) != 1:
+        raise ValueError(f"w must be (N, K={K}) with contiguous rows; got {tuple(w.shape)}")
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    out_dtype = torch.bfloat16 if out_dtype is None else out_dtype
+    code = _lib.dtype_code(out_dtype)
+    library = _lib.lib()
+    parts = _lib.ctypes.c_int(int(splits))
+    size = _lib.ctypes.c_size_t(0)
+    check(library.wptv_gemm_workspace(M, N, K, _lib.ctypes.byref(parts), _lib.ctypes.byref(size)), "gemm")
+    workspace = torch.empty(size.value, dtype=torch.uint8, device=x.device) if size.value else None
+    out = torch.empty(M, N, dtype=out_dtype, device=x.device)
+    check(library.wptv_gemm(ptr(x2), x2.stride(0), ptr(w), w.stride(0), M, N, K, ptr(out), out.stride(0), code,
+                            parts.value, ptr(workspace), size.value, _lib.stream(x.device)), "gemm")
+    return out.reshape(*x.shape[:-1], N)
