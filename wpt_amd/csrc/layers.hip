@@ -10,8 +10,9 @@
 //                 table at start[b] + t (the KV append, cache.py:110-128)
 //   swiglu        silu(gate) * up of the feed-forward block's two halves
 //
-// One wavefront per row for the norms (16-byte vector loads, FP32 sums with
-// wavefront reductions); one thread per 8 elements for SwiGLU.
+// One wavefront per row (norm) or per (row, head) (q/k norms), every load
+// issued before the first use (16-byte vector loads, FP32 sums with wavefront
+// reductions); one thread per 8 elements for SwiGLU.
 #include "wptv_common.h"
 
 namespace wptv {
@@ -58,90 +59,129 @@ __device__ __forceinline__ float rounded<unsigned short>(float x) { return bf16_
 // Values of one row held by a lane: D / 8 / 64 chunks of 8, at most kChunks.
 constexpr int kChunks = 8;  // rows up to 64 * 8 * 8 = 4096 wide
 
-template <typename T>
-__global__ __launch_bounds__(256) void add_rms_norm(T* __restrict__ h, const T* __restrict__ delta,
-                                                    const float* __restrict__ weight, T* __restrict__ y, int M,
-                                                    int D, float eps) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= M) return;
+// One wavefront (one workgroup) per row: every load of the row -- h, delta
+// and the norm weight -- is issued before the first is used (NCH chunks of
+// 512 columns, straight-line code: a chunk past the row end re-reads the
+// row's last 8 columns and is ignored), so a row costs one memory round
+// trip, then the wavefront sum.
+template <typename T, int NCH, bool DELTA>
+__global__ __launch_bounds__(64) void add_rms_norm(T* __restrict__ h, const T* __restrict__ delta,
+                                                   const float* __restrict__ weight, T* __restrict__ y, int M, int D,
+                                                   float eps) {
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
   T* hrow = h + (int64_t)row * D;
-  const T* drow = delta ? delta + (int64_t)row * D : nullptr;
-  float x[kChunks][8];
+  const T* drow = DELTA ? delta + (int64_t)row * D : nullptr;
+  float x[NCH][8], d[NCH][8], wt[NCH][8];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int col = min((k * 64 + lane) * 8, D - 8);
+    Vec8<T>::load(hrow + col, x[k]);
+    if constexpr (DELTA) Vec8<T>::load(drow + col, d[k]);
+    Vec8<float>::load(weight + col, wt[k]);
+  }
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < kChunks; ++k) {
-    const int col = (k * 64 + lane) * 8;
-    if (col < D) {
-      Vec8<T>::load(hrow + col, x[k]);
-      if (drow) {
-        float d[8];
-        Vec8<T>::load(drow + col, d);
-        // the residual stream keeps the activation dtype, as the reference's h = h + out does
+  for (int k = 0; k < NCH; ++k) {
+    const bool in = (k * 64 + lane) * 8 < D;
+    if constexpr (DELTA) {
+      // the residual stream keeps the activation dtype, as the reference's h = h + out does
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[k][e] = rounded<T>(x[k][e] + d[e]);
-        Vec8<T>::store(hrow + col, x[k]);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss += x[k][e] * x[k][e];
+      for (int e = 0; e < 8; ++e) x[k][e] = rounded<T>(x[k][e] + d[k][e]);
     }
+    float part = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part += x[k][e] * x[k][e];
+    ss += in ? part : 0.f;
   }
   ss = wave_sum(ss);
   const float inv = rsqrtf(ss / (float)D + eps);
   T* yrow = y + (int64_t)row * D;
 #pragma unroll
-  for (int k = 0; k < kChunks; ++k) {
+  for (int k = 0; k < NCH; ++k) {
     const int col = (k * 64 + lane) * 8;
     if (col < D) {
+      if constexpr (DELTA) Vec8<T>::store(hrow + col, x[k]);
       float out[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) out[e] = x[k][e] * inv * weight[col + e];
+      for (int e = 0; e < 8; ++e) out[e] = x[k][e] * inv * wt[k][e];
       Vec8<T>::store(yrow + col, out);
     }
   }
 }
 
-// One workgroup of 4 wavefronts per token row; wavefront w takes heads w,
-// w + 4, ... of the H query heads, then the key (head H) and value (H + 1).
-template <typename T>
+// EPL consecutive elements per lane (a head of 64 EPL values per wavefront).
+template <typename T, int EPL>
+struct Lane {
+  static __device__ __forceinline__ void load(const T* p, float (&v)[EPL]) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) v[e] = load_f32(p + e);
+  }
+  static __device__ __forceinline__ void store(T* p, const float (&v)[EPL]) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) p[e] = from_f32<T>(v[e]);
+  }
+};
+template <int EPL>
+struct Lane<unsigned short, EPL> {
+  typedef unsigned short raw __attribute__((ext_vector_type(EPL)));
+  static __device__ __forceinline__ void load(const unsigned short* p, float (&v)[EPL]) {
+    const raw r = *reinterpret_cast<const raw*>(p);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) v[e] = bf16_to_f32(r[e]);
+  }
+  static __device__ __forceinline__ void store(unsigned short* p, const float (&v)[EPL]) {
+    raw r;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) r[e] = f32_to_bf16(v[e]);
+    *reinterpret_cast<raw*>(p) = r;
+  }
+};
+template <>
+struct Lane<unsigned short, 1> {
+  static __device__ __forceinline__ void load(const unsigned short* p, float (&v)[1]) { v[0] = bf16_to_f32(*p); }
+  static __device__ __forceinline__ void store(unsigned short* p, const float (&v)[1]) { *p = f32_to_bf16(v[0]); }
+};
+
+// One wavefront per (token row, head) of the H query heads, the key (head
+// H) and the value (head H + 1); lane l holds elements EPL l .. EPL l + EPL - 1.
+template <typename T, int EPL>
 __global__ __launch_bounds__(256) void qkv_post(const T* __restrict__ qkv, int64_t qkv_row,
                                                 const float* __restrict__ q_norm, const float* __restrict__ k_norm,
                                                 T* __restrict__ q_out, T* __restrict__ table, int64_t tsb,
                                                 int64_t tsn, int64_t capacity, const int64_t* __restrict__ start,
-                                                const int64_t* __restrict__ counts, int T_, int H, int C, float eps) {
-  const int row = blockIdx.x;
+                                                const int64_t* __restrict__ counts, int rows, int T_, int H,
+                                                float eps) {
+  constexpr int C = 64 * EPL;
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (gw >= rows * (H + 2)) return;
+  const int row = gw / (H + 2), head = gw % (H + 2);
   const int b = row / T_, t = row % T_;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const T* src = qkv + (int64_t)row * qkv_row;
-  const bool append = t < counts[b];
-  const int64_t dst_row = start[b] + t;
-  T* entry = (append && dst_row >= 0 && dst_row < capacity) ? table + b * tsb + dst_row * tsn : nullptr;
-  for (int head = wave; head < H + 2; head += 4) {
-    const T* x = src + (int64_t)head * C;
-    if (head == H + 1) {  // the value: copied as it is
-      if (entry)
-        for (int col = lane; col < C; col += 64) entry[C + col] = x[col];
-      continue;
-    }
-    float v[4];  // C <= 256: 4 values per lane
+  const T* x = qkv + (int64_t)row * qkv_row + (int64_t)head * C + EPL * lane;
+  float v[EPL], wt[EPL];
+  Lane<T, EPL>::load(x, v);
+  const float* w = (head < H ? q_norm : k_norm) + EPL * lane;  // the value (head H + 1) reads k_norm unused
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) wt[e] = w[e];
+  T* dst;
+  if (head < H) {
+    dst = q_out + ((int64_t)row * H + head) * C;
+  } else {
+    const int64_t dst_row = start[b] + t;
+    if (!(t < counts[b] && dst_row >= 0 && dst_row < capacity)) return;
+    dst = table + b * tsb + dst_row * tsn + (head == H ? 0 : C);  // [k_norm(k), v]
+  }
+  if (head <= H) {
     float ss = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int col = lane + 64 * k;
-      v[k] = col < C ? load_f32(x + col) : 0.f;
-      ss += v[k] * v[k];
-    }
+    for (int e = 0; e < EPL; ++e) ss += v[e] * v[e];
     ss = wave_sum(ss);
     const float inv = rsqrtf(ss / (float)C + eps);
-    const float* w = head < H ? q_norm : k_norm;
-    T* dst = head < H ? q_out + ((int64_t)row * H + head) * C : entry;
-    if (!dst) continue;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int col = lane + 64 * k;
-      if (col < C) dst[col] = from_f32<T>(v[k] * inv * w[col]);
-    }
+    for (int e = 0; e < EPL; ++e) v[e] = v[e] * inv * wt[e];
   }
+  Lane<T, EPL>::store(dst + EPL * lane, v);
 }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
@@ -177,15 +217,31 @@ extern "C" int wptv_add_rms_norm(void* h, const void* delta, const float* weight
   if (!vec_aligned(h) || !vec_aligned(delta) || !vec_aligned(y))
     return fail(WPTV_E_INVALID, "add_rms_norm: rows must be 16-byte aligned");
   if (M == 0) return WPTV_OK;
-  dim3 grid((M + 3) / 4);
-  if (dtype == WPTV_BF16)
-    hipLaunchKernelGGL(add_rms_norm<unsigned short>, grid, dim3(256), 0, stream, static_cast<unsigned short*>(h),
-                       static_cast<const unsigned short*>(delta), weight, static_cast<unsigned short*>(y), M, D, eps);
-  else if (dtype == WPTV_F32)
-    hipLaunchKernelGGL(add_rms_norm<float>, grid, dim3(256), 0, stream, static_cast<float*>(h),
-                       static_cast<const float*>(delta), weight, static_cast<float*>(y), M, D, eps);
-  else
+  dim3 grid(M);
+  const int nch = (D + 511) / 512;
+#define WPTV_ARN(TT, NN)                                                                                           \
+  do {                                                                                                             \
+    if (delta)                                                                                                     \
+      hipLaunchKernelGGL((add_rms_norm<TT, NN, true>), grid, dim3(64), 0, stream, static_cast<TT*>(h),             \
+                         static_cast<const TT*>(delta), weight, static_cast<TT*>(y), M, D, eps);                   \
+    else                                                                                                           \
+      hipLaunchKernelGGL((add_rms_norm<TT, NN, false>), grid, dim3(64), 0, stream, static_cast<TT*>(h), nullptr,   \
+                         weight, static_cast<TT*>(y), M, D, eps);                                                  \
+  } while (0)
+#define WPTV_ARN_N(TT)            \
+  if (nch <= 1) WPTV_ARN(TT, 1);  \
+  else if (nch <= 2) WPTV_ARN(TT, 2); \
+  else if (nch <= 4) WPTV_ARN(TT, 4); \
+  else WPTV_ARN(TT, 8)
+  if (dtype == WPTV_BF16) {
+    WPTV_ARN_N(unsigned short);
+  } else if (dtype == WPTV_F32) {
+    WPTV_ARN_N(float);
+  } else {
     return fail(WPTV_E_UNSUPPORTED, "add_rms_norm: dtype %d is neither fp32 nor bf16", dtype);
+  }
+#undef WPTV_ARN_N
+#undef WPTV_ARN
   return launched("add_rms_norm");
 }
 
@@ -195,23 +251,36 @@ extern "C" int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const floa
                              int c, int dtype, float eps, hipStream_t stream) {
   if (!qkv || !q_norm || !k_norm || !q_out || !table || !start || !counts)
     return fail(WPTV_E_INVALID, "qkv_post: every pointer must be given");
-  if (B < 0 || T < 0 || H <= 0 || c <= 0 || c > 256)
+  if (B < 0 || T < 0 || H <= 0 || c <= 0)
     return fail(WPTV_E_INVALID, "qkv_post: bad shape B=%d T=%d H=%d c=%d", B, T, H, c);
+  if (c != 64 && c != 128 && c != 256)
+    return fail(WPTV_E_UNSUPPORTED, "qkv_post: head width %d is not 64, 128 or 256", c);
   if (qkv_row_stride < (int64_t)(H + 2) * c || table_stride_n < 2 * c)
     return fail(WPTV_E_INVALID, "qkv_post: a row stride below its width");
+  const int epl = c / 64;
+  const int esize = dtype == WPTV_F32 ? 4 : 2;
+  if (qkv_row_stride % epl || table_stride_b % epl || table_stride_n % epl || !aligned(qkv, epl * esize) ||
+      !aligned(table, epl * esize) || !aligned(q_out, epl * esize))
+    return fail(WPTV_E_INVALID, "qkv_post: rows must be aligned to %d elements", epl);
   if (B == 0 || T == 0) return WPTV_OK;
-  dim3 grid(B * T);
-  if (dtype == WPTV_BF16)
-    hipLaunchKernelGGL(qkv_post<unsigned short>, grid, dim3(256), 0, stream, static_cast<const unsigned short*>(qkv),
-                       qkv_row_stride, q_norm, k_norm, static_cast<unsigned short*>(q_out),
-                       static_cast<unsigned short*>(table), table_stride_b, table_stride_n, capacity, start, counts, T,
-                       H, c, eps);
-  else if (dtype == WPTV_F32)
-    hipLaunchKernelGGL(qkv_post<float>, grid, dim3(256), 0, stream, static_cast<const float*>(qkv), qkv_row_stride,
-                       q_norm, k_norm, static_cast<float*>(q_out), static_cast<float*>(table), table_stride_b,
-                       table_stride_n, capacity, start, counts, T, H, c, eps);
-  else
+  const int rows = B * T;
+  dim3 grid((unsigned)(((int64_t)rows * (H + 2) + 3) / 4));
+#define WPTV_QKV(TT, EE)                                                                                           \
+  hipLaunchKernelGGL((qkv_post<TT, EE>), grid, dim3(256), 0, stream, static_cast<const TT*>(qkv), qkv_row_stride, \
+                     q_norm, k_norm, static_cast<TT*>(q_out), static_cast<TT*>(table), table_stride_b,           \
+                     table_stride_n, capacity, start, counts, rows, T, H, eps)
+  if (dtype == WPTV_BF16) {
+    if (epl == 1) WPTV_QKV(unsigned short, 1);
+    else if (epl == 2) WPTV_QKV(unsigned short, 2);
+    else WPTV_QKV(unsigned short, 4);
+  } else if (dtype == WPTV_F32) {
+    if (epl == 1) WPTV_QKV(float, 1);
+    else if (epl == 2) WPTV_QKV(float, 2);
+    else WPTV_QKV(float, 4);
+  } else {
     return fail(WPTV_E_UNSUPPORTED, "qkv_post: dtype %d is neither fp32 nor bf16", dtype);
+  }
+#undef WPTV_QKV
   return launched("qkv_post");
 }
 
