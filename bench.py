@@ -323,6 +323,41 @@ def cpu_baseline(pieces, rows=2, budget_s=20.0):
                       f"length and drafts, fastest of {passes} passes on {cpu_name()}"}
 
 
+def pmc_workload():
+    import torch
+
+    from wpt_amd import kernels
+
+    B, T, H, c, N = 32, 5, 16, 128, 4096
+    device = torch.device("cuda", 0)
+    generator = torch.Generator().manual_seed(0)
+    q = torch.randn(B, T, H, c, generator=generator).to(torch.bfloat16).to(device)
+    table = torch.randn(B, N, 2 * c, generator=generator).to(torch.bfloat16).to(device)
+    positions = (N - T + torch.arange(T)).expand(B, T).contiguous().to(device)
+    for _ in range(5):
+        kernels.verify_attention(q, table[..., :c], table[..., c:], positions, c ** -0.5)
+    torch.cuda.synchronize()
+    src = torch.ones(32 * 1024 * 1024, dtype=torch.bfloat16, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("pmc workload done")
+
+
+def traffic_bytes():
+    """HBM bytes per verify-attention call from the committed counter summary
+    (two rocprofv3 --pmc passes, calibrated by a plain copy), or None."""
+    import re
+
+    path = ROOT / "profiles" / "verify_attention_B32_KV4096.md"
+    try:
+        found = re.search(r"HBM traffic per call: (\d+) bytes", path.read_text())
+    except OSError:
+        return None
+    return int(found.group(1)) if found else None
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -330,7 +365,13 @@ def main():
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--quick", action="store_true",
                         help="the headline step and its roofline only (no other configs, no CPU baseline)")
+    parser.add_argument("--pmc-workload", action="store_true",
+                        help="for a counter pass: five verify-attention calls of the roofline shape, then five "
+                             "plain 64 MiB device copies (the counters' calibration); prints no JSON")
     args = parser.parse_args()
+    if args.pmc_workload:
+        pmc_workload()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the verify step here is built and timed on a single MI355X "
               f"(--gpus {args.gpus} is not supported)", file=sys.stderr)
@@ -369,7 +410,7 @@ def main():
                                "rejection sampling T=0.8, HIP graph", "global_batch": B, "seq_len": KV,
                    "draft": K, "tokens_per_row_step": head["tokens_per_row_step"]},
         "roofline": {"bound": "hbm", "achieved": attn["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": attn["GBps"] / HBM_PEAK_GBS, "traffic": None,
+                     "frac": attn["GBps"] / HBM_PEAK_GBS, "traffic": traffic_bytes(),
                      "kernel": "verify attention, batch 32 x 4096 rows x 5 queries x 16 heads x 128, bf16",
                      "ms": attn["ms"]},
         "cpu_baseline": cpu,
