@@ -141,6 +141,12 @@ int wptv_kv_append(void* table, int64_t table_stride_b, int64_t table_stride_n, 
 int wptv_add_rms_norm(void* h, const void* delta, const float* weight, void* y, int M, int D, int dtype, float eps,
                       hipStream_t stream);
 
+/* wptv_add_rms_norm_parts: as wptv_add_rms_norm with delta = the sum over
+ * z < splits of parts[z] (FP32 [splits, M, D], e.g. wptv_gemm_parts' output),
+ * rounded to the dtype before the residual add; splits <= 8, D <= 8192. */
+int wptv_add_rms_norm_parts(void* h, const float* parts, int splits, const float* weight, void* y, int M, int D,
+                            int dtype, float eps, hipStream_t stream);
+
 int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const float* q_norm, const float* k_norm, void* q_out,
                   void* table, int64_t table_stride_b, int64_t table_stride_n, int64_t capacity,
                   const int64_t* start, const int64_t* counts, int B, int T, int H, int c, int dtype, float eps,
@@ -167,6 +173,13 @@ int wptv_gemm_workspace(int M, int N, int K, int* splits, size_t* bytes);
 
 int wptv_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K, void* out, int64_t ldo,
               int out_dtype, int splits, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* wptv_gemm_parts: the split products only, FP32 parts [splits, M, N] (each
+ * the product over one part of K; their sum is x . w^T), for a consumer that
+ * sums them itself (wptv_add_rms_norm_parts); splits as wptv_gemm_workspace
+ * returns it. */
+int wptv_gemm_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K, int splits,
+                    float* parts, size_t parts_bytes, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Acceptance: the reference's per-row verification loop of

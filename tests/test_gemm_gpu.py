@@ -68,3 +68,23 @@ def test_batched_rows_and_bad_shapes(device):
         layers.linear(torch.zeros(600, 128, dtype=torch.bfloat16, device=device), w)  # above 512 rows
     with pytest.raises(ValueError):
         layers.linear(x.float(), w)
+
+
+def test_parts_sum_to_the_product_and_feed_the_norm(device):
+    # the down projection's shape: parts summed by add_rms_norm_parts equal
+    # the reduced product fed to add_rms_norm
+    M, N, K = 160, 2048, 5632
+    x, w = operands(M, N, K, seed=8, device=device)
+    parts = layers.linear_parts(x, w)
+    assert parts.dtype == torch.float32 and parts.shape[1:] == (M, N) and 1 <= parts.shape[0] <= 8
+    assert relative_error(parts.sum(0).cpu(), (x.float() @ w.float().T).cpu()) < 1e-3
+    generator = torch.Generator().manual_seed(9)
+    h0 = torch.randn(M, N, generator=generator).to(torch.bfloat16).to(device)
+    weight = (1 + 0.1 * torch.randn(N, generator=generator)).to(device)
+    h1, y1 = h0.clone(), torch.empty_like(h0)
+    layers.add_rms_norm_parts(h1, parts, weight, y1)
+    h2, y2 = h0.clone(), torch.empty_like(h0)
+    layers.add_rms_norm(h2, parts.sum(0).to(torch.bfloat16), weight, y2)
+    # the same bf16 delta up to the order of the FP32 part sums
+    assert (h1.float() - h2.float()).abs().max() <= 2e-2 * h2.float().abs().max()
+    assert relative_error(y1.float().cpu(), y2.float().cpu()) < 1e-2

@@ -275,6 +275,29 @@ extern "C" int wptv_gemm_workspace(int M, int N, int K, int* splits, size_t* byt
   return WPTV_OK;
 }
 
+extern "C" int wptv_gemm_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K,
+                               int splits, float* parts, size_t parts_bytes, hipStream_t stream) {
+  if (!x || !w || !parts) return fail(WPTV_E_INVALID, "gemm_parts: x, w and parts must be given");
+  GemmPlan p;
+  const int st = gemm_plan(M, N, K, splits, &p);
+  if (st != WPTV_OK) return st;
+  if (p.splits != splits) return fail(WPTV_E_INVALID, "gemm_parts: %d splits do not cut K = %d evenly into chunks "
+                                                      "(%d would); take the count from wptv_gemm_workspace",
+                                      splits, K, p.splits);
+  if (ldx < K || ldw < K) return fail(WPTV_E_INVALID, "gemm_parts: a leading dimension below the row width");
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(parts, 16) || ldx % 8 || ldw % 8)
+    return fail(WPTV_E_INVALID, "gemm_parts: x, w and parts must be 16-byte aligned with leading dimensions of 8");
+  if ((double)N * (double)ldw * 2.0 >= 4.0e9 || (double)M * (double)ldx * 2.0 >= 4.0e9)
+    return fail(WPTV_E_UNSUPPORTED, "gemm_parts: operands above 4 GB");
+  const size_t need = (size_t)p.splits * M * N * sizeof(float);
+  if (parts_bytes < need)
+    return fail(WPTV_E_INVALID, "gemm_parts: %zu bytes of parts, %zu needed", parts_bytes, need);
+  dim3 grid(N / kTileN, p.splits);
+  launch_gemm_mbw<kPartF32>(p.mbw, grid, stream, static_cast<const unsigned short*>(x), ldx,
+                            static_cast<const unsigned short*>(w), ldw, M, N, K, p.cps, parts, 0);
+  return launched("gemm_xwt");
+}
+
 extern "C" int wptv_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K, void* out,
                          int64_t ldo, int out_dtype, int splits, void* workspace, size_t workspace_bytes,
                          hipStream_t stream) {

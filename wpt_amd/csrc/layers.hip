@@ -110,6 +110,49 @@ __global__ __launch_bounds__(64) void add_rms_norm(T* __restrict__ h, const T* _
   }
 }
 
+// add_rms_norm with delta = the sum of S FP32 parts [S][M][D] (a split-K
+// matrix product's parts, summed in a fixed order): one workgroup of D / 8
+// threads per row, 8 columns a thread; every load -- the parts, h and the
+// norm weight -- issued before the first use.
+template <typename T, int S>
+__global__ __launch_bounds__(1024) void add_rms_norm_parts(T* __restrict__ h, const float* __restrict__ parts,
+                                                           const float* __restrict__ weight, T* __restrict__ y, int M,
+                                                           int D, float eps) {
+  __shared__ float wsum[16];
+  const int row = blockIdx.x;
+  const int col = threadIdx.x * 8;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  T* hrow = h + (int64_t)row * D;
+  float x[8], d[S][8], wt[8];
+  Vec8<T>::load(hrow + col, x);
+#pragma unroll
+  for (int z = 0; z < S; ++z) Vec8<float>::load(parts + ((int64_t)z * M + row) * D + col, d[z]);
+  Vec8<float>::load(weight + col, wt);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float delta = 0.f;
+#pragma unroll
+    for (int z = 0; z < S; ++z) delta += d[z][e];
+    // the product rounded to the activation dtype, then the residual add in it,
+    // as the reference's h = h + out of a bf16 product does
+    x[e] = rounded<T>(x[e] + rounded<T>(delta));
+    ss += x[e] * x[e];
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) wsum[wv] = ss;
+  __syncthreads();
+  float total = 0.f;
+  const int waves = (blockDim.x + 63) / 64;
+  for (int u = 0; u < waves; ++u) total += wsum[u];
+  const float inv = rsqrtf(total / (float)D + eps);
+  Vec8<T>::store(hrow + col, x);
+  float out[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = x[e] * inv * wt[e];
+  Vec8<T>::store(y + (int64_t)row * D + col, out);
+}
+
 // EPL consecutive elements per lane (a head of 64 EPL values per wavefront).
 template <typename T, int EPL>
 struct Lane {
@@ -243,6 +286,44 @@ extern "C" int wptv_add_rms_norm(void* h, const void* delta, const float* weight
 #undef WPTV_ARN_N
 #undef WPTV_ARN
   return launched("add_rms_norm");
+}
+
+extern "C" int wptv_add_rms_norm_parts(void* h, const float* parts, int splits, const float* weight, void* y, int M,
+                                       int D, int dtype, float eps, hipStream_t stream) {
+  if (!h || !parts || !weight || !y) return fail(WPTV_E_INVALID, "add_rms_norm_parts: every pointer must be given");
+  if (M < 0 || D <= 0 || splits <= 0)
+    return fail(WPTV_E_INVALID, "add_rms_norm_parts: bad shape M=%d D=%d splits=%d", M, D, splits);
+  if (D % 8 != 0 || D > 8 * 1024)
+    return fail(WPTV_E_UNSUPPORTED, "add_rms_norm_parts: width %d is not a multiple of 8 up to 8192", D);
+  if (splits > 8) return fail(WPTV_E_UNSUPPORTED, "add_rms_norm_parts: %d parts above 8", splits);
+  if (!vec_aligned(h) || !vec_aligned(parts) || !vec_aligned(y))
+    return fail(WPTV_E_INVALID, "add_rms_norm_parts: rows must be 16-byte aligned");
+  if (M == 0) return WPTV_OK;
+  dim3 grid(M), block(D / 8);
+#define WPTV_ARNP(TT, SS)                                                                                       \
+  hipLaunchKernelGGL((add_rms_norm_parts<TT, SS>), grid, block, 0, stream, static_cast<TT*>(h), parts, weight, \
+                     static_cast<TT*>(y), M, D, eps)
+#define WPTV_ARNP_S(TT)             \
+  switch (splits) {                 \
+    case 1: WPTV_ARNP(TT, 1); break; \
+    case 2: WPTV_ARNP(TT, 2); break; \
+    case 3: WPTV_ARNP(TT, 3); break; \
+    case 4: WPTV_ARNP(TT, 4); break; \
+    case 5: WPTV_ARNP(TT, 5); break; \
+    case 6: WPTV_ARNP(TT, 6); break; \
+    case 7: WPTV_ARNP(TT, 7); break; \
+    default: WPTV_ARNP(TT, 8); break; \
+  }
+  if (dtype == WPTV_BF16) {
+    WPTV_ARNP_S(unsigned short);
+  } else if (dtype == WPTV_F32) {
+    WPTV_ARNP_S(float);
+  } else {
+    return fail(WPTV_E_UNSUPPORTED, "add_rms_norm_parts: dtype %d is neither fp32 nor bf16", dtype);
+  }
+#undef WPTV_ARNP_S
+#undef WPTV_ARNP
+  return launched("add_rms_norm_parts");
 }
 
 extern "C" int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const float* q_norm, const float* k_norm,

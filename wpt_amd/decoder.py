@@ -16,7 +16,8 @@ On the GPU:
     norms, SwiGLU   wptv_add_rms_norm (residual add + RMSNorm), wptv_swiglu
     verify attention wptv_verify_attention, reading only the rows the query
                     positions reach in the cache's table
-    projections     the matrix products of the dtype (bf16 on MFMA)
+    projections     the matrix products of the dtype (bf16 on MFMA: hipBLASLt,
+                    and wptv_gemm for the down projection at few rows)
     sampling        wpt_amd.sampling (wptv_accept), called by the Writer
 The decoder keeps no state between calls but the cache; a step of fixed
 shape can be captured in a HIP graph (wpt_amd.step).
@@ -117,7 +118,14 @@ class MQADecoder:
         o = kernels.verify_attention(q, table[..., :c], table[..., c:], positions, c ** -0.5, from_positions=True)
         layers.add_rms_norm(h, F.linear(o.reshape(B, T, H * c), w[f"layers.{i}.out"]), w[f"layers.{i}.ffn_norm"], x)
         act = layers.swiglu(F.linear(x, w[f"layers.{i}.gate_up"]))
-        layers.add_rms_norm(h, F.linear(act, w[f"layers.{i}.down"]), next_norm, x)
+        down = w[f"layers.{i}.down"]
+        if act.dtype == torch.bfloat16 and B * T <= layers.LINEAR_MAX_ROWS:
+            # the build's split-K MFMA product (it reads the 23 MB weight once;
+            # measured faster than hipBLASLt's tiles at these rows), its parts
+            # summed by the residual add + norm
+            layers.add_rms_norm_parts(h, layers.linear_parts(act, down), next_norm, x)
+        else:
+            layers.add_rms_norm(h, F.linear(act, down), next_norm, x)
 
     @torch.no_grad()
     def extend(self, ids, cache, counts=None, undoable=False, features=()):

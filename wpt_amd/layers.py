@@ -10,6 +10,7 @@ from . import _lib
 from ._lib import KernelUnavailable, check, ptr
 
 EPS = 1e-6
+LINEAR_MAX_ROWS = 512  # rows wptv_gemm takes
 
 
 def _gpu(*tensors):
@@ -95,3 +96,44 @@ def linear(x, w, out_dtype=None, splits=0):
     check(library.wptv_gemm(ptr(x2), x2.stride(0), ptr(w), w.stride(0), M, N, K, ptr(out), out.stride(0), code,
                             parts.value, ptr(workspace), size.value, _lib.stream(x.device)), "gemm")
     return out.reshape(*x.shape[:-1], N)
+
+
+def linear_parts(x, w, splits=0):
+    """The split-K parts of x (..., K) . w (N, K)^T: FP32 (S, rows, N) whose
+    sum over S is the product (wptv_gemm_parts), for a consumer that sums them
+    (add_rms_norm_parts)."""
+    _gpu(x, w)
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise ValueError(f"linear_parts takes bf16 operands; got {x.dtype} and {w.dtype}")
+    K = x.shape[-1]
+    N = w.shape[0]
+    if w.dim() != 2 or w.shape[1] != K or w.stride(1) != 1:
+        raise ValueError(f"w must be (N, K={K}) with contiguous rows; got {tuple(w.shape)}")
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    library = _lib.lib()
+    parts = _lib.ctypes.c_int(int(splits))
+    size = _lib.ctypes.c_size_t(0)
+    check(library.wptv_gemm_workspace(M, N, K, _lib.ctypes.byref(parts), _lib.ctypes.byref(size)), "gemm_parts")
+    out = torch.empty(parts.value, M, N, dtype=torch.float32, device=x.device)
+    check(library.wptv_gemm_parts(ptr(x2), x2.stride(0), ptr(w), w.stride(0), M, N, K, parts.value, ptr(out),
+                                  out.numel() * 4, _lib.stream(x.device)), "gemm_parts")
+    return out
+
+
+def add_rms_norm_parts(h, parts, weight, y, eps=EPS):
+    """add_rms_norm with delta = parts.sum(0) (FP32 (S, rows, D), S <= 8),
+    rounded to h's dtype before the residual add."""
+    _gpu(h, parts, weight, y)
+    D = h.shape[-1]
+    M = h.numel() // D
+    if parts.dim() != 3 or parts.shape[1:] != (M, D) or parts.dtype != torch.float32 or not parts.is_contiguous():
+        raise ValueError(f"parts must be contiguous FP32 (S, {M}, {D}); got {tuple(parts.shape)} {parts.dtype}")
+    if y.shape != h.shape or y.dtype != h.dtype or weight.shape != (D,) or weight.dtype != torch.float32:
+        raise ValueError("h and y share shape and dtype; weight is float32 (D,)")
+    check(_lib.lib().wptv_add_rms_norm_parts(ptr(_rows(h, "h")), ptr(parts), parts.shape[0], ptr(weight),
+                                             ptr(_rows(y, "y")), M, D, _lib.dtype_code(h.dtype), float(eps),
+                                             _lib.stream(h.device)), "add_rms_norm_parts")
+    return y
