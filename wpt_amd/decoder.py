@@ -116,10 +116,15 @@ class MQADecoder:
         qkv = F.linear(x, w[f"layers.{i}.qkv"])
         q = layers.qkv_post(qkv, w[f"layers.{i}.q_norm"], w[f"layers.{i}.k_norm"], table, cache.lengths, counts, H)
         o = kernels.verify_attention(q, table[..., :c], table[..., c:], positions, c ** -0.5, from_positions=True)
-        layers.add_rms_norm(h, F.linear(o.reshape(B, T, H * c), w[f"layers.{i}.out"]), w[f"layers.{i}.ffn_norm"], x)
+        few = x.dtype == torch.bfloat16 and B * T <= layers.LINEAR_MAX_ROWS
+        if few:
+            layers.add_rms_norm_parts(h, layers.linear_parts(o.reshape(B, T, H * c), w[f"layers.{i}.out"]),
+                                      w[f"layers.{i}.ffn_norm"], x)
+        else:
+            layers.add_rms_norm(h, F.linear(o.reshape(B, T, H * c), w[f"layers.{i}.out"]), w[f"layers.{i}.ffn_norm"], x)
         act = layers.swiglu(F.linear(x, w[f"layers.{i}.gate_up"]))
         down = w[f"layers.{i}.down"]
-        if act.dtype == torch.bfloat16 and B * T <= layers.LINEAR_MAX_ROWS:
+        if few:
             # the build's split-K MFMA product (it reads the 23 MB weight once;
             # measured faster than hipBLASLt's tiles at these rows), its parts
             # summed by the residual add + norm

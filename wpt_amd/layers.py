@@ -98,10 +98,11 @@ def linear(x, w, out_dtype=None, splits=0):
     return out.reshape(*x.shape[:-1], N)
 
 
-def linear_parts(x, w, splits=0):
+def linear_parts(x, w, splits=0, max_splits=8):
     """The split-K parts of x (..., K) . w (N, K)^T: FP32 (S, rows, N) whose
     sum over S is the product (wptv_gemm_parts), for a consumer that sums them
-    (add_rms_norm_parts)."""
+    (add_rms_norm_parts, which takes up to 8).  splits 0: the library's
+    choice, at most max_splits."""
     _gpu(x, w)
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
         raise ValueError(f"linear_parts takes bf16 operands; got {x.dtype} and {w.dtype}")
@@ -117,6 +118,9 @@ def linear_parts(x, w, splits=0):
     parts = _lib.ctypes.c_int(int(splits))
     size = _lib.ctypes.c_size_t(0)
     check(library.wptv_gemm_workspace(M, N, K, _lib.ctypes.byref(parts), _lib.ctypes.byref(size)), "gemm_parts")
+    if parts.value > max_splits:
+        parts = _lib.ctypes.c_int(int(max_splits))
+        check(library.wptv_gemm_workspace(M, N, K, _lib.ctypes.byref(parts), _lib.ctypes.byref(size)), "gemm_parts")
     out = torch.empty(parts.value, M, N, dtype=torch.float32, device=x.device)
     check(library.wptv_gemm_parts(ptr(x2), x2.stride(0), ptr(w), w.stride(0), M, N, K, parts.value, ptr(out),
                                   out.numel() * 4, _lib.stream(x.device)), "gemm_parts")
