@@ -152,6 +152,14 @@ int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const float* q_norm, 
                   const int64_t* start, const int64_t* counts, int B, int T, int H, int c, int dtype, float eps,
                   hipStream_t stream);
 
+/* wptv_qkv_post_parts: as wptv_qkv_post with the projection given as FP32
+ * split-K parts [splits, B*T, (H + 2) c] (wptv_gemm_parts' output), summed and
+ * rounded to the dtype first; splits <= 8. */
+int wptv_qkv_post_parts(const float* parts, int splits, const float* q_norm, const float* k_norm, void* q_out,
+                        void* table, int64_t table_stride_b, int64_t table_stride_n, int64_t capacity,
+                        const int64_t* start, const int64_t* counts, int B, int T, int H, int c, int dtype, float eps,
+                        hipStream_t stream);
+
 int wptv_swiglu(const void* gate_up, void* out, int M, int F, int dtype, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------

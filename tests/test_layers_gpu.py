@@ -82,3 +82,25 @@ def test_kv_append_writes_each_row_at_its_length(device, dtype):
     td = table.to(device)
     kernels.kv_append(td, new.to(device), start.to(device), counts.to(device))
     assert torch.equal(td.cpu(), expected)
+
+
+@pytest.mark.parametrize("splits", [1, 3, 7])
+def test_qkv_post_parts_equals_qkv_post_on_the_summed_product(device, splits):
+    # the projection as FP32 split-K parts: summed in order and rounded to
+    # bf16, then exactly qkv_post's work
+    B, T, H, c, cap = 2, 5, 16, 128, 32
+    g = torch.Generator().manual_seed(3)
+    parts = torch.randn(splits, B * T, (H + 2) * c, generator=g)
+    summed = parts[0].clone()
+    for z in range(1, splits):
+        summed += parts[z]
+    qkv = summed.to(torch.bfloat16).reshape(B, T, (H + 2) * c)
+    qn, kn = 1 + 0.1 * torch.randn(c, generator=g), 1 + 0.1 * torch.randn(c, generator=g)
+    table = torch.randn(B, cap, 2 * c, generator=g).to(torch.bfloat16)
+    start, counts = torch.tensor([3, 20]), torch.tensor([5, 4])
+    t1, t2 = table.to(device), table.to(device)
+    args = (qn.to(device), kn.to(device))
+    q1 = layers.qkv_post(qkv.to(device), *args, t1, start.to(device), counts.to(device), H)
+    q2 = layers.qkv_post_parts(parts.to(device), *args, t2, start.to(device), counts.to(device), H, T)
+    assert torch.equal(q1, q2)
+    assert torch.equal(t1, t2)

@@ -46,6 +46,7 @@ SIGNATURES = {
     "wptv_gemm": [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _I, _I, _P, _SZ, _P],
     "wptv_gemm_parts": [_P, _I64, _P, _I64, _I, _I, _I, _I, _P, _SZ, _P],
     "wptv_add_rms_norm_parts": [_P, _P, _I, _P, _P, _I, _I, _I, _F, _P],
+    "wptv_qkv_post_parts": [_P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I, _I, _F, _P],
     "wptv_accept_workspace": [_I, _I, ctypes.POINTER(_SZ)],
     "wptv_accept": [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P, _P, _P,
                     _SZ, _P],

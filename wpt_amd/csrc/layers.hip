@@ -188,8 +188,12 @@ struct Lane<unsigned short, 1> {
 
 // One wavefront per (token row, head) of the H query heads, the key (head
 // H) and the value (head H + 1); lane l holds elements EPL l .. EPL l + EPL - 1.
-template <typename T, int EPL>
+// S > 0: the projection comes as S FP32 split-K parts [S][rows][(H + 2) c]
+// (qkv_parts), summed in a fixed order and rounded to T, as the reference's
+// bf16 product is.
+template <typename T, int EPL, int S>
 __global__ __launch_bounds__(256) void qkv_post(const T* __restrict__ qkv, int64_t qkv_row,
+                                                const float* __restrict__ qkv_parts,
                                                 const float* __restrict__ q_norm, const float* __restrict__ k_norm,
                                                 T* __restrict__ q_out, T* __restrict__ table, int64_t tsb,
                                                 int64_t tsn, int64_t capacity, const int64_t* __restrict__ start,
@@ -201,9 +205,26 @@ __global__ __launch_bounds__(256) void qkv_post(const T* __restrict__ qkv, int64
   if (gw >= rows * (H + 2)) return;
   const int row = gw / (H + 2), head = gw % (H + 2);
   const int b = row / T_, t = row % T_;
-  const T* x = qkv + (int64_t)row * qkv_row + (int64_t)head * C + EPL * lane;
   float v[EPL], wt[EPL];
-  Lane<T, EPL>::load(x, v);
+  if constexpr (S == 0) {
+    Lane<T, EPL>::load(qkv + (int64_t)row * qkv_row + (int64_t)head * C + EPL * lane, v);
+  } else {
+    const int64_t width = (int64_t)(H + 2) * C;
+    float d[S][EPL];
+#pragma unroll
+    for (int z = 0; z < S; ++z) {
+      const float* src = qkv_parts + ((int64_t)z * rows + row) * width + (int64_t)head * C + EPL * lane;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) d[z][e] = src[e];
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float sum = 0.f;
+#pragma unroll
+      for (int z = 0; z < S; ++z) sum += d[z][e];
+      v[e] = rounded<T>(sum);
+    }
+  }
   const float* w = (head < H ? q_norm : k_norm) + EPL * lane;  // the value (head H + 1) reads k_norm unused
 #pragma unroll
   for (int e = 0; e < EPL; ++e) wt[e] = w[e];
@@ -346,10 +367,10 @@ extern "C" int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const floa
   if (B == 0 || T == 0) return WPTV_OK;
   const int rows = B * T;
   dim3 grid((unsigned)(((int64_t)rows * (H + 2) + 3) / 4));
-#define WPTV_QKV(TT, EE)                                                                                           \
-  hipLaunchKernelGGL((qkv_post<TT, EE>), grid, dim3(256), 0, stream, static_cast<const TT*>(qkv), qkv_row_stride, \
-                     q_norm, k_norm, static_cast<TT*>(q_out), static_cast<TT*>(table), table_stride_b,           \
-                     table_stride_n, capacity, start, counts, rows, T, H, eps)
+#define WPTV_QKV(TT, EE)                                                                                          \
+  hipLaunchKernelGGL((qkv_post<TT, EE, 0>), grid, dim3(256), 0, stream, static_cast<const TT*>(qkv),             \
+                     qkv_row_stride, nullptr, q_norm, k_norm, static_cast<TT*>(q_out), static_cast<TT*>(table),  \
+                     table_stride_b, table_stride_n, capacity, start, counts, rows, T, H, eps)
   if (dtype == WPTV_BF16) {
     if (epl == 1) WPTV_QKV(unsigned short, 1);
     else if (epl == 2) WPTV_QKV(unsigned short, 2);
@@ -363,6 +384,57 @@ extern "C" int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const floa
   }
 #undef WPTV_QKV
   return launched("qkv_post");
+}
+
+extern "C" int wptv_qkv_post_parts(const float* parts, int splits, const float* q_norm, const float* k_norm,
+                                   void* q_out, void* table, int64_t table_stride_b, int64_t table_stride_n,
+                                   int64_t capacity, const int64_t* start, const int64_t* counts, int B, int T, int H,
+                                   int c, int dtype, float eps, hipStream_t stream) {
+  if (!parts || !q_norm || !k_norm || !q_out || !table || !start || !counts)
+    return fail(WPTV_E_INVALID, "qkv_post_parts: every pointer must be given");
+  if (B < 0 || T < 0 || H <= 0 || c <= 0 || splits <= 0)
+    return fail(WPTV_E_INVALID, "qkv_post_parts: bad shape B=%d T=%d H=%d c=%d splits=%d", B, T, H, c, splits);
+  if (c != 64 && c != 128 && c != 256)
+    return fail(WPTV_E_UNSUPPORTED, "qkv_post_parts: head width %d is not 64, 128 or 256", c);
+  if (splits > 8) return fail(WPTV_E_UNSUPPORTED, "qkv_post_parts: %d parts above 8", splits);
+  if (table_stride_n < 2 * c) return fail(WPTV_E_INVALID, "qkv_post_parts: a row stride below its width");
+  const int epl = c / 64;
+  const int esize = dtype == WPTV_F32 ? 4 : 2;
+  if (table_stride_b % epl || table_stride_n % epl || !aligned(table, epl * esize) || !aligned(q_out, epl * esize) ||
+      !aligned(parts, 4 * epl))
+    return fail(WPTV_E_INVALID, "qkv_post_parts: rows must be aligned to %d elements", epl);
+  if (B == 0 || T == 0) return WPTV_OK;
+  const int rows = B * T;
+  dim3 grid((unsigned)(((int64_t)rows * (H + 2) + 3) / 4));
+#define WPTV_QKVP(TT, EE, SS)                                                                                     \
+  hipLaunchKernelGGL((qkv_post<TT, EE, SS>), grid, dim3(256), 0, stream, nullptr, 0, parts, q_norm, k_norm,       \
+                     static_cast<TT*>(q_out), static_cast<TT*>(table), table_stride_b, table_stride_n, capacity, \
+                     start, counts, rows, T, H, eps)
+#define WPTV_QKVP_S(TT, EE)               \
+  switch (splits) {                       \
+    case 1: WPTV_QKVP(TT, EE, 1); break;  \
+    case 2: WPTV_QKVP(TT, EE, 2); break;  \
+    case 3: WPTV_QKVP(TT, EE, 3); break;  \
+    case 4: WPTV_QKVP(TT, EE, 4); break;  \
+    case 5: WPTV_QKVP(TT, EE, 5); break;  \
+    case 6: WPTV_QKVP(TT, EE, 6); break;  \
+    case 7: WPTV_QKVP(TT, EE, 7); break;  \
+    default: WPTV_QKVP(TT, EE, 8); break; \
+  }
+  if (dtype == WPTV_BF16) {
+    if (epl == 1) { WPTV_QKVP_S(unsigned short, 1); }
+    else if (epl == 2) { WPTV_QKVP_S(unsigned short, 2); }
+    else { WPTV_QKVP_S(unsigned short, 4); }
+  } else if (dtype == WPTV_F32) {
+    if (epl == 1) { WPTV_QKVP_S(float, 1); }
+    else if (epl == 2) { WPTV_QKVP_S(float, 2); }
+    else { WPTV_QKVP_S(float, 4); }
+  } else {
+    return fail(WPTV_E_UNSUPPORTED, "qkv_post_parts: dtype %d is neither fp32 nor bf16", dtype);
+  }
+#undef WPTV_QKVP_S
+#undef WPTV_QKVP
+  return launched("qkv_post_parts");
 }
 
 extern "C" int wptv_swiglu(const void* gate_up, void* out, int M, int F, int dtype, hipStream_t stream) {

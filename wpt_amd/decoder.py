@@ -113,10 +113,19 @@ class MQADecoder:
         B, T, _ = h.shape
         H, c = cfg.heads, cfg.head_dim
         table = cache.tables[i]
-        qkv = F.linear(x, w[f"layers.{i}.qkv"])
-        q = layers.qkv_post(qkv, w[f"layers.{i}.q_norm"], w[f"layers.{i}.k_norm"], table, cache.lengths, counts, H)
-        o = kernels.verify_attention(q, table[..., :c], table[..., c:], positions, c ** -0.5, from_positions=True)
+        # at the verify step's few bf16 rows, the projections run as the
+        # build's split-K MFMA products (each weight read once; measured faster
+        # than hipBLASLt's tiles there), their FP32 parts summed by the kernel
+        # that consumes them; torch's products otherwise
         few = x.dtype == torch.bfloat16 and B * T <= layers.LINEAR_MAX_ROWS
+        if few:
+            q = layers.qkv_post_parts(layers.linear_parts(x, w[f"layers.{i}.qkv"]), w[f"layers.{i}.q_norm"],
+                                      w[f"layers.{i}.k_norm"], table, cache.lengths, counts, H, T)
+        else:
+            qkv = F.linear(x, w[f"layers.{i}.qkv"])
+            q = layers.qkv_post(qkv, w[f"layers.{i}.q_norm"], w[f"layers.{i}.k_norm"], table, cache.lengths, counts,
+                                H)
+        o = kernels.verify_attention(q, table[..., :c], table[..., c:], positions, c ** -0.5, from_positions=True)
         if few:
             layers.add_rms_norm_parts(h, layers.linear_parts(o.reshape(B, T, H * c), w[f"layers.{i}.out"]),
                                       w[f"layers.{i}.ffn_norm"], x)
@@ -125,9 +134,6 @@ class MQADecoder:
         act = layers.swiglu(F.linear(x, w[f"layers.{i}.gate_up"]))
         down = w[f"layers.{i}.down"]
         if few:
-            # the build's split-K MFMA product (it reads the 23 MB weight once;
-            # measured faster than hipBLASLt's tiles at these rows), its parts
-            # summed by the residual add + norm
             layers.add_rms_norm_parts(h, layers.linear_parts(act, down), next_norm, x)
         else:
             layers.add_rms_norm(h, F.linear(act, down), next_norm, x)

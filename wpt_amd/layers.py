@@ -59,6 +59,26 @@ def qkv_post(qkv, q_norm, k_norm, table, start, counts, heads, eps=EPS):
     return q
 
 
+def qkv_post_parts(parts, q_norm, k_norm, table, start, counts, heads, T, eps=EPS):
+    """qkv_post with the projection as FP32 split-K parts (S, B*T, (H + 2) c)
+    (linear_parts' output), summed and rounded to the table's dtype first."""
+    _gpu(parts, table)
+    S, rows, width = parts.shape
+    B = table.shape[0]
+    c = table.shape[-1] // 2
+    if rows != B * T or width != (heads + 2) * c or parts.dtype != torch.float32 or not parts.is_contiguous():
+        raise ValueError(f"parts must be contiguous FP32 (S, B*T={B * T}, (H + 2) c={(heads + 2) * c}); "
+                         f"got {tuple(parts.shape)}")
+    if table.stride(-1) != 1:
+        raise ValueError("the table must be (B, capacity, 2c) with contiguous rows")
+    q = torch.empty(B, T, heads, c, dtype=table.dtype, device=table.device)
+    check(_lib.lib().wptv_qkv_post_parts(ptr(parts), S, ptr(q_norm), ptr(k_norm), ptr(q), ptr(table),
+                                         table.stride(0), table.stride(1), table.shape[1], ptr(start), ptr(counts), B,
+                                         T, heads, c, _lib.dtype_code(table.dtype), float(eps),
+                                         _lib.stream(table.device)), "qkv_post_parts")
+    return q
+
+
 def swiglu(gate_up):
     """silu(gate) * up of gate_up (..., 2F): (..., F)."""
     _gpu(gate_up)
