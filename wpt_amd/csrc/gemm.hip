@@ -12,8 +12,9 @@
 // "split"; the splits of a column tile add their FP32 products into the
 // workspace, and wptv_gemm's reduction, or the consumer, sums them).  The
 // workgroup stages 64-wide K chunks of W (64 rows) and of X (all M rows,
-// padded to 64 MBW) through a ring in LDS by DMA; wavefront w multiplies its
-// MBW 16-row blocks of X by the four 16-column blocks of W:
+// padded to a multiple of 32) through a ring in LDS by DMA; each wavefront
+// multiplies its share of the 16-row blocks of X by the four 16-column blocks
+// of W:
 //
 //   C^T[n, m] += W[n, k] . X^T[k, m]     v_mfma_f32_16x16x32_bf16, W as the A
 //                                       operand, so lane (j, g) ends with 4
@@ -35,14 +36,17 @@ constexpr int kTileN = 64;         // output columns per workgroup
 constexpr int kChunkK = 64;        // K per staged chunk (two k-steps of 32)
 constexpr int kRowBytes = kChunkK * 2;
 
-template <int MBW>
+// R32: the staged X rows, 32 R32 (all M rows, padded to a multiple of 32).
+template <int R32>
 struct GemmTile {
-  static constexpr int kRows = 64 * MBW;                 // staged X rows (all M, padded)
-  static constexpr int kWBytes = kTileN * kRowBytes;     // 8 KiB
+  static constexpr int kRows = 32 * R32;
+  static constexpr int kBlocks = kRows / 16;                        // 16-row blocks
+  static constexpr int kMaxPerWave = (kBlocks + kGemmWaves - 1) / kGemmWaves;
+  static constexpr int kWBytes = kTileN * kRowBytes;                // 8 KiB
   static constexpr int kSlotBytes = kWBytes + kRows * kRowBytes;
   static constexpr int kSlots = (160 * 1024) / kSlotBytes < 4 ? (160 * 1024) / kSlotBytes : 4;
-  static constexpr int kPieces = kSlotBytes / 1024;      // 1 KiB DMA instructions per chunk
-  static constexpr int kPerWave = kPieces / kGemmWaves;  // 2 + 2 MBW
+  static constexpr int kPieces = kSlotBytes / 1024;                 // 1 KiB DMA instructions per chunk
+  static constexpr int kPerWave = kPieces / kGemmWaves;             // 2 + R32
   static_assert(kPieces % kGemmWaves == 0, "pieces per wave");
   static_assert(kSlots >= 2, "ring");
   static_assert((kSlots - 1) * kPerWave < 64, "vmcnt range");
@@ -70,12 +74,13 @@ enum GemmOut { kPartF32 = 0, kOutBf16 = 1, kOutF32 = 2 };
 // OUT: kPartF32 -> part[z][m][n] FP32; kOutBf16 -> out bf16; kOutF32 -> out
 // FP32 holding the bf16-rounded product (the reference's bf16 product cast to
 // FP32).
-template <int MBW, int OUT>
+template <int R32, int OUT>
 __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned short* __restrict__ x, int64_t ldx,
                                                                const unsigned short* __restrict__ w, int64_t ldw,
                                                                int M, int N, int K, int cps, void* __restrict__ out,
                                                                int64_t ldo) {
-  using G = GemmTile<MBW>;
+  using G = GemmTile<R32>;
+  constexpr int MBW = G::kMaxPerWave;
   __shared__ __attribute__((aligned(16))) unsigned char ring[G::kSlots * G::kSlotBytes];
 
   const int lane = threadIdx.x & 63;
@@ -123,7 +128,11 @@ __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned sh
   uint32_t op_off[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) op_off[s] = (uint32_t)(j * kRowBytes + 16 * ((4 * s + g) ^ gemm_swz(j)));
-  const int mb0 = wv * MBW;  // this wavefront's first 16-row block
+  // this wavefront's 16-row blocks: mb0 .. mb0 + nblk - 1 (the blocks are
+  // dealt out as evenly as they go)
+  constexpr int kBase = G::kBlocks / kGemmWaves, kExtra = G::kBlocks % kGemmWaves;
+  const int nblk = kBase + (wv < kExtra ? 1 : 0);
+  const int mb0 = wv * kBase + min(wv, kExtra);
   f32x4 acc[MBW][4];
 #pragma unroll
   for (int i = 0; i < MBW; ++i)
@@ -147,7 +156,7 @@ __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned sh
         wf[nb] = *reinterpret_cast<const bf16x8*>(st + 16 * nb * kRowBytes + op_off[s]);
 #pragma unroll
       for (int ii = 0; ii < MBW; ++ii) {
-        if (16 * (mb0 + ii) >= M) break;  // a block of padding rows only
+        if (ii >= nblk || 16 * (mb0 + ii) >= M) break;  // not this wavefront's, or padding rows only
         const bf16x8 xf = *reinterpret_cast<const bf16x8*>(st + G::kWBytes + 16 * (mb0 + ii) * kRowBytes + op_off[s]);
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
@@ -161,7 +170,7 @@ __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned sh
 #pragma unroll
   for (int ii = 0; ii < MBW; ++ii) {
     const int m = 16 * (mb0 + ii) + j;
-    if (m >= M) continue;
+    if (ii >= nblk || m >= M) continue;
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int n = n0 + 16 * nb + 4 * g;
@@ -209,7 +218,7 @@ __global__ __launch_bounds__(256) void gemm_reduce(const float* __restrict__ par
 constexpr int kMaxGemmRows = 512;  // 8 row blocks per wavefront
 
 struct GemmPlan {
-  int mbw;     // 16-row blocks per wavefront
+  int r32;     // staged X rows / 32
   int splits;  // parts of K
   int cps;     // K chunks per split
   size_t bytes;
@@ -221,10 +230,9 @@ int gemm_plan(int M, int N, int K, int requested, GemmPlan* p) {
   if (M > kMaxGemmRows) return fail(WPTV_E_UNSUPPORTED, "gemm: M = %d above %d rows", M, kMaxGemmRows);
   if (N % kTileN || K % kChunkK)
     return fail(WPTV_E_UNSUPPORTED, "gemm: N (%d) must be a multiple of %d and K (%d) of %d", N, kTileN, K, kChunkK);
-  const int blocks = (M + 15) / 16;
-  int mbw = (blocks + kGemmWaves - 1) / kGemmWaves;
-  if (mbw == 4) mbw = 5;  // instantiated widths: 1, 2, 3, 5, 8
-  if (mbw > 5) mbw = 8;
+  // instantiated row counts: 32 r32 for r32 in 1-6, 8, 10, 12, 16
+  int r32 = (M + 31) / 32;
+  if (r32 > 6) r32 = r32 <= 8 ? 8 : r32 <= 10 ? 10 : r32 <= 12 ? 12 : 16;
   const int tiles = N / kTileN, chunks = K / kChunkK;
   int s = requested;
   if (s <= 0) {
@@ -234,30 +242,37 @@ int gemm_plan(int M, int N, int K, int requested, GemmPlan* p) {
   if (s > chunks) s = chunks;
   const int cps = (chunks + s - 1) / s;
   s = (chunks + cps - 1) / cps;  // no empty split
-  p->mbw = mbw;
+  p->r32 = r32;
   p->splits = s;
   p->cps = cps;
   p->bytes = s > 1 ? align_up((size_t)s * M * N * sizeof(float), 256) : 0;
   return WPTV_OK;
 }
 
-template <int MBW, int OUT>
+template <int R32, int OUT>
 void launch_gemm(dim3 grid, hipStream_t stream, const unsigned short* x, int64_t ldx, const unsigned short* w,
                  int64_t ldw, int M, int N, int K, int cps, void* out, int64_t ldo) {
-  hipLaunchKernelGGL((gemm_xwt<MBW, OUT>), grid, dim3(kGemmWaves * 64), 0, stream, x, ldx, w, ldw, M, N, K, cps, out,
+  hipLaunchKernelGGL((gemm_xwt<R32, OUT>), grid, dim3(kGemmWaves * 64), 0, stream, x, ldx, w, ldw, M, N, K, cps, out,
                      ldo);
 }
 
 template <int OUT>
-void launch_gemm_mbw(int mbw, dim3 grid, hipStream_t stream, const unsigned short* x, int64_t ldx,
-                     const unsigned short* w, int64_t ldw, int M, int N, int K, int cps, void* out, int64_t ldo) {
-  switch (mbw) {
-    case 1: launch_gemm<1, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo); break;
-    case 2: launch_gemm<2, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo); break;
-    case 3: launch_gemm<3, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo); break;
-    case 5: launch_gemm<5, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo); break;
-    default: launch_gemm<8, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo); break;
+void launch_gemm_rows(int r32, dim3 grid, hipStream_t stream, const unsigned short* x, int64_t ldx,
+                      const unsigned short* w, int64_t ldw, int M, int N, int K, int cps, void* out, int64_t ldo) {
+#define WPTV_G(RR) launch_gemm<RR, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo)
+  switch (r32) {
+    case 1: WPTV_G(1); break;
+    case 2: WPTV_G(2); break;
+    case 3: WPTV_G(3); break;
+    case 4: WPTV_G(4); break;
+    case 5: WPTV_G(5); break;
+    case 6: WPTV_G(6); break;
+    case 8: WPTV_G(8); break;
+    case 10: WPTV_G(10); break;
+    case 12: WPTV_G(12); break;
+    default: WPTV_G(16); break;
   }
+#undef WPTV_G
 }
 
 }  // namespace
@@ -293,7 +308,7 @@ extern "C" int wptv_gemm_parts(const void* x, int64_t ldx, const void* w, int64_
   if (parts_bytes < need)
     return fail(WPTV_E_INVALID, "gemm_parts: %zu bytes of parts, %zu needed", parts_bytes, need);
   dim3 grid(N / kTileN, p.splits);
-  launch_gemm_mbw<kPartF32>(p.mbw, grid, stream, static_cast<const unsigned short*>(x), ldx,
+  launch_gemm_rows<kPartF32>(p.r32, grid, stream, static_cast<const unsigned short*>(x), ldx,
                             static_cast<const unsigned short*>(w), ldw, M, N, K, p.cps, parts, 0);
   return launched("gemm_xwt");
 }
@@ -320,12 +335,12 @@ extern "C" int wptv_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw,
   dim3 grid(N / kTileN, p.splits);
   if (p.splits == 1) {
     if (out_dtype == WPTV_BF16)
-      launch_gemm_mbw<kOutBf16>(p.mbw, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, out, ldo);
+      launch_gemm_rows<kOutBf16>(p.r32, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, out, ldo);
     else
-      launch_gemm_mbw<kOutF32>(p.mbw, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, out, ldo);
+      launch_gemm_rows<kOutF32>(p.r32, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, out, ldo);
     return launched("gemm_xwt");
   }
-  launch_gemm_mbw<kPartF32>(p.mbw, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, workspace, 0);
+  launch_gemm_rows<kPartF32>(p.r32, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, workspace, 0);
   st = launched("gemm_xwt");
   if (st != WPTV_OK) return st;
   const long long items = (long long)M * (N / 4);
