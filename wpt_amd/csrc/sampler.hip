@@ -173,12 +173,13 @@ __global__ __launch_bounds__(kT) void accept_stats(const float* __restrict__ sco
   const int64_t first = firsts ? firsts[b] : 0;
   const float* row = scores + b * sb + (first + j) * st;
   const int tid = threadIdx.x;
+  // every load issued before the first use: indices past the row read its
+  // last entry, masked after
   float x[ITEMS];
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    const int v = tid + i * kT;
-    x[i] = v < V ? row[v] : kNegInfS;
-  }
+  for (int i = 0; i < ITEMS; ++i) x[i] = row[min(tid + i * kT, V - 1)];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) x[i] = tid + i * kT < V ? x[i] : kNegInfS;
   // first maximal index of the raw scores
   float bv = kNegInfS;
   int bi = INT_MAX;
@@ -253,19 +254,25 @@ __global__ __launch_bounds__(kT) void accept_finish(const float* __restrict__ sc
   const float* row = scores + b * sb + (first + js) * st;
   const float m = stats.m[idx], zinv = 1.f / stats.z[idx], thr = stats.thr[idx];
   const bool rejected = js < n;
-  const float* qrow = rejected ? q + b * qb + js * qt : nullptr;
+  const float* qrow = rejected ? q + b * qb + js * qt : row;  // (row: a valid address, unused)
   const float* erow = e + (int64_t)b * V;
-  float w[ITEMS];
+  // every load issued before the first use: indices past the row read its
+  // last entry, masked after
+  float w[ITEMS], qv[ITEMS], ev[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int vc = min(tid + i * kT, V - 1);
+    w[i] = row[vc];
+    qv[i] = qrow[vc];
+    ev[i] = erow[vc];
+  }
   float part = 0.f;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    const int v = tid + i * kT;
-    float p = 0.f;
-    if (v < V) {
-      const float s = row[v] / temperature;
-      p = s >= thr ? expf(s - m) * zinv : 0.f;
-      if (rejected) p = fmaxf(p - qrow[v], 0.f);
-    }
+    const float s = w[i] / temperature;
+    float p = s >= thr ? expf(s - m) * zinv : 0.f;
+    if (rejected) p = fmaxf(p - qv[i], 0.f);
+    p = tid + i * kT < V ? p : 0.f;
     w[i] = p;
     part += p;
   }
@@ -276,7 +283,7 @@ __global__ __launch_bounds__(kT) void accept_finish(const float* __restrict__ sc
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const int v = tid + i * kT;
-    if (v < V) arg_better(bv, bi, (rejected ? w[i] / S : w[i]) / erow[v], v);
+    if (v < V) arg_better(bv, bi, (rejected ? w[i] / S : w[i]) / ev[i], v);
   }
   const int token = block_argmax(bv, bi, redv, redi);
   if (tid == 0) {
