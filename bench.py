@@ -19,8 +19,9 @@ write (kept drafts + 1 per row) over the timed steps' wall time.
 split attention and the split combine), timed with HIP events on their stream
 over a graph of 20 back-to-back calls, against 8 TB/s.  `configs` reports the other
 workloads: the FP32 plumbing decoder's greedy step (checked bit-exact against
-the oracle), sliding-window and tree verification, and the 24-layer step at
-batch 64 / KV 2048.  `cpu_baseline` is the oracle (the reference's PyTorch
+the oracle), sliding-window and tree verification, the step's matrix products
+(MFMA TFLOP/s against the bf16 peak), and the 24-layer step at batch 64 / KV
+2048.  `cpu_baseline` is the oracle (the reference's PyTorch
 algorithm restated in FP32 on the CPU) running the headline step for a sample
 of rows on this host's cores.
 """
@@ -282,6 +283,48 @@ def plumbing_c1():
             "bit_exact_vs_oracle": got == expected, "tokens": got}
 
 
+def projections(model, rows, steps, warmup):
+    """The step's matrix products at `rows` rows over the decoder's own 24
+    layers of weights (each graph replay walks the layers, so every weight is
+    cold, as in the step): per product, time per call, TFLOP/s against the bf16
+    MFMA peak, and weight GB/s against HBM."""
+    import torch
+    import torch.nn.functional as F
+
+    from wpt_amd import layers
+
+    cfg = model.config
+    device = model.device
+    generator = torch.Generator(device=device).manual_seed(7)
+    out = {}
+    kinds = [("qkv", cfg.d_model, "build split-K (parts)"), ("out", cfg.heads * cfg.head_dim, "build split-K (parts)"),
+             ("gate_up", cfg.d_model, "hipBLASLt"), ("down", cfg.ffn, "build split-K (parts)")]
+    for name, K, engine in kinds:
+        x = torch.randn(rows, K, generator=generator, device=device).to(torch.bfloat16)
+        ws = [model.w[f"layers.{i}.{name}"] for i in range(cfg.layers)]
+        if engine == "hipBLASLt":
+            calls = [lambda w=w: F.linear(x, w) for w in ws]
+        else:
+            calls = [lambda w=w: layers.linear_parts(x, w) for w in ws]
+        replay = graphed(lambda: [f() for f in calls])
+        ms = timed(replay, max(1, steps // 5), max(1, warmup // 5)) / len(ws)
+        N = ws[0].shape[0]
+        flops, nbytes = 2 * rows * N * K, N * K * 2
+        out[name] = {"engine": engine, "N": N, "K": K, "us": ms * 1e3, "TFLOPs": flops / (ms * 1e-3) / 1e12,
+                     "frac_bf16_peak": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                     "weight_GBps": nbytes / (ms * 1e-3) / 1e9}
+    x = torch.randn(rows, cfg.d_model, generator=generator, device=device).to(torch.bfloat16)
+    replay = graphed(lambda: F.linear(x, model.w["head"]).float())
+    ms = timed(replay, steps, warmup)
+    N, K = model.w["head"].shape
+    flops = 2 * rows * N * K
+    out["lm_head"] = {"engine": "hipBLASLt + FP32 cast", "N": N, "K": K, "us": ms * 1e3,
+                      "TFLOPs": flops / (ms * 1e-3) / 1e12,
+                      "frac_bf16_peak": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                      "weight_GBps": N * K * 2 / (ms * 1e-3) / 1e9}
+    return out
+
+
 # ---------------------------------------------------------------------------
 # the CPU baseline: the oracle running the headline step for sampled rows
 # ---------------------------------------------------------------------------
@@ -392,6 +435,9 @@ def main():
         configs["tree_B16_KV8192_31nodes_lm_head"] = tree_c4(args.steps, args.warmup)
         log("configs c1-c4 done")
     pieces = head.pop("_pieces")
+    if not args.quick:
+        configs["projections_rows160"] = projections(pieces[0], B * (K + 1), args.steps, args.warmup)
+        log("projections done")
     cpu = None if args.quick else cpu_baseline(pieces)
     del pieces
     torch.cuda.empty_cache()
