@@ -16,8 +16,11 @@ On the GPU:
     norms, SwiGLU   wptv_add_rms_norm (residual add + RMSNorm), wptv_swiglu
     verify attention wptv_verify_attention, reading only the rows the query
                     positions reach in the cache's table
-    projections     the matrix products of the dtype (bf16 on MFMA: hipBLASLt,
-                    and wptv_gemm for the down projection at few rows)
+    projections     the matrix products of the dtype on MFMA: wptv_gemm's
+                    split-K parts for q/k/v, output and down at up to
+                    SPLIT_K_ROWS bf16 rows (summed by qkv_post and the
+                    residual add + norm), hipBLASLt otherwise and for the
+                    gate/up product and the lm_head
     sampling        wpt_amd.sampling (wptv_accept), called by the Writer
 The decoder keeps no state between calls but the cache; a step of fixed
 shape can be captured in a HIP graph (wpt_amd.step).
@@ -32,6 +35,10 @@ from . import kernels, layers
 from .cache import Cache
 
 EPS = 1e-6
+# Rows up to which the projections run as the build's split-K products: at
+# 160 rows (batch 32, k = 4) the step takes 2.53 ms with them against 2.81 ms
+# with hipBLASLt; at 320 rows the two tie (3.19 vs 3.16 ms).
+SPLIT_K_ROWS = 256
 
 
 @dataclass(frozen=True)
@@ -114,10 +121,9 @@ class MQADecoder:
         H, c = cfg.heads, cfg.head_dim
         table = cache.tables[i]
         # at the verify step's few bf16 rows, the projections run as the
-        # build's split-K MFMA products (each weight read once; measured faster
-        # than hipBLASLt's tiles there), their FP32 parts summed by the kernel
-        # that consumes them; torch's products otherwise
-        few = x.dtype == torch.bfloat16 and B * T <= layers.LINEAR_MAX_ROWS
+        # build's split-K MFMA products (each weight read once), their FP32
+        # parts summed by the kernel that consumes them; torch's otherwise
+        few = x.dtype == torch.bfloat16 and B * T <= SPLIT_K_ROWS
         if few:
             q = layers.qkv_post_parts(layers.linear_parts(x, w[f"layers.{i}.qkv"]), w[f"layers.{i}.q_norm"],
                                       w[f"layers.{i}.k_norm"], table, cache.lengths, counts, H, T)
