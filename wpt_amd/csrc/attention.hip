@@ -65,6 +65,66 @@ __device__ __forceinline__ bool tree_visible(int n, int64_t tbase, uint64_t anc)
   return node < 64 && ((anc >> node) & 1ull);
 }
 
+// Merges the parts of one query row's 8 columns c8 .. c8 + 7: fixed split
+// order, log-sum-exp weights, the sink (log2 units; -inf: none) joining the
+// denominator.  Part s of the row is at row0 + s * stride (bf16 output,
+// normalized within the part, and its log2-sum-exp).  The parts are read
+// eight at a time, every load of a group issued before any is used, with a
+// running maximum across groups.  Writes the 8 outputs and, when lse is
+// given and c8 == 0, the row's natural-log log-sum-exp.
+__device__ __forceinline__ void merge_parts(const unsigned short* __restrict__ part_o,
+                                            const float* __restrict__ part_lse, int64_t row0, int64_t stride,
+                                            int splits, int C, int c8, float sink_log2,
+                                            unsigned short* __restrict__ orow, float* __restrict__ lse) {
+  constexpr int kGroup = 8;
+  float M = kNegInf, L = 0.f;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += kGroup) {
+    float ls[kGroup];
+    u16x8 po[kGroup];
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const int64_t prow = row0 + (int64_t)(s0 + u) * stride;
+      const bool in = s0 + u < splits;
+      ls[u] = in ? part_lse[prow] : kNegInf;
+      po[u] = in ? *reinterpret_cast<const u16x8*>(part_o + prow * C + c8) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+    float m = M;
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) m = fmaxf(m, ls[u]);
+    if (m == kNegInf) continue;  // nothing seen yet
+    const float f = M == kNegInf ? 0.f : exp2f(M - m);
+    L *= f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= f;
+    M = m;
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      if (ls[u] == kNegInf) continue;
+      const float wgt = exp2f(ls[u] - M);
+      L += wgt;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += wgt * bf16_to_f32(po[u][e]);
+    }
+  }
+  if (sink_log2 != kNegInf) {
+    const float M2 = fmaxf(M, sink_log2);
+    const float f = M == kNegInf ? 0.f : exp2f(M - M2);
+    L = L * f + exp2f(sink_log2 - M2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= f;
+    M = M2;
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  u16x8 res;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) res[e] = f32_to_bf16(acc[e] * inv);
+  *reinterpret_cast<u16x8*>(orow + c8) = res;
+  if (lse && c8 == 0) *lse = L > 0.f ? (M + log2f(L)) * kLn2 : kNegInf;
+}
+
 // ---------------------------------------------------------------------------
 // MFMA kernel
 // ---------------------------------------------------------------------------
@@ -913,17 +973,13 @@ __global__ __launch_bounds__(kKeyWaves * 64, 1) void verify_attention_keys(
   }
 }
 
-// Merges the splits of each query row: fixed order, log-sum-exp weights,
-// the sink joining the denominator.  One thread per (batch row, query row, 8
-// columns); the parts of a row are read eight at a time, every load of a
-// group issued before any is used (a part count up to 8 costs one memory
-// round trip), with a running maximum across groups.
+// Merges the splits of each query row in a kernel of its own: one thread
+// per (batch row, query row, 8 columns).
 __global__ __launch_bounds__(256) void combine_splits(const unsigned short* __restrict__ part_o,
                                                       const float* __restrict__ part_lse,
                                                       const float* __restrict__ sink, int B, int R, int H, int C,
                                                       int rows_per_group, int groups, int splits,
                                                       unsigned short* __restrict__ out, float* __restrict__ lse_out) {
-  constexpr int kGroup = 8;
   const int per_row = C / 8;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)B * R * per_row) return;
@@ -933,53 +989,8 @@ __global__ __launch_bounds__(256) void combine_splits(const unsigned short* __re
   const int c8 = (rem % per_row) * 8;
   const int grp = r / rows_per_group, rr = r % rows_per_group;
   const int64_t row0 = ((int64_t)(b * groups + grp) * splits) * rows_per_group + rr;  // split 0's part
-  float M = kNegInf, L = 0.f;
-  float acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  for (int s0 = 0; s0 < splits; s0 += kGroup) {
-    float ls[kGroup];
-    u16x8 po[kGroup];
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) {
-      const int64_t prow = row0 + (int64_t)(s0 + u) * rows_per_group;
-      const bool in = s0 + u < splits;
-      ls[u] = in ? part_lse[prow] : kNegInf;
-      po[u] = in ? *reinterpret_cast<const u16x8*>(part_o + prow * C + c8) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
-    float m = M;
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) m = fmaxf(m, ls[u]);
-    if (m == kNegInf) continue;  // nothing seen yet
-    const float f = M == kNegInf ? 0.f : exp2f(M - m);
-    L *= f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] *= f;
-    M = m;
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) {
-      if (ls[u] == kNegInf) continue;
-      const float wgt = exp2f(ls[u] - M);
-      L += wgt;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += wgt * bf16_to_f32(po[u][e]);
-    }
-  }
-  if (sink) {
-    const float sl = sink[r % H] * kLog2e;
-    const float M2 = fmaxf(M, sl);
-    const float f = M == kNegInf ? 0.f : exp2f(M - M2);
-    L = L * f + exp2f(sl - M2);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] *= f;
-    M = M2;
-  }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  u16x8 res;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) res[e] = f32_to_bf16(acc[e] * inv);
-  *reinterpret_cast<u16x8*>(out + ((int64_t)b * R + r) * C + c8) = res;
-  if (lse_out && c8 == 0) lse_out[(int64_t)b * R + r] = L > 0.f ? (M + log2f(L)) * kLn2 : kNegInf;
+  merge_parts(part_o, part_lse, row0, rows_per_group, splits, C, c8, sink ? sink[r % H] * kLog2e : kNegInf,
+              out + ((int64_t)b * R + r) * C, lse_out ? lse_out + (int64_t)b * R + r : nullptr);
 }
 
 // ---------------------------------------------------------------------------
