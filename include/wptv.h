@@ -107,6 +107,33 @@ int wptv_sparse_attention(const void* q, const void* k, int64_t k_stride_b, int6
                           void* out, float* lse, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Exact attention's choice of rows: the top_k rows each query weighs most
+ * among those at least `window` tokens back, which the sparse layers after an
+ * exact layer read.  Replaces the choice of the reference's exact_attention
+ * (packages/wpt-model/src/wpt_model/pytorch_kernels.py:112-117, columns
+ * chosen_columns :73-77; the Triton form's _choose, triton_kernels.py:
+ * 222-239,393-508).
+ *
+ *   q, k, positions, B, T, H, c, N, scale  as wptv_verify_attention (k rows
+ *            16-byte aligned for the bf16 matrix-core path)
+ *   lse      [B, T, H] fp32: each query head's natural-log log-sum-exp over
+ *            the rows it sees (wptv_verify_attention's lse output)
+ *   chosen   [B, T, K] int64 out, K = max(0, min(top_k, N - window)): the K
+ *            rows n <= p - window (n < N) with the largest score
+ *            max_h (q_h . k_n * scale - lse_h); a query with fewer such rows
+ *            gets all of them, then -1.  Rows above the K-th largest score
+ *            come first in row order, then rows equal to it, lowest first.
+ *   workspace  wptv_choice_workspace(B, T, N) bytes (the scores)
+ * H <= 128, c <= 256; nothing is launched when K = 0.
+ * ------------------------------------------------------------------------- */
+int wptv_choice_workspace(int B, int T, int N, size_t* bytes);
+
+int wptv_exact_choice(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n, int dtype,
+                      const int64_t* positions, const float* lse, int B, int T, int H, int c, int N, float scale,
+                      int top_k, int window, int64_t* chosen, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
  * KV append: table[b, start[b] + j, :] = rows[b, j, :] for j < counts[b].
  * Replaces the scatter of the reference's Reading.everything
  * (packages/wpt-model/src/wpt_model/cache.py:110-128; the index_put at :126).

@@ -19,6 +19,35 @@ def exact_by_formula(q, k, v, positions, scale):
     return out
 
 
+def choice_by_formula(q, k, positions, scale, top_k, window):
+    """The set of rows each query chooses (the reference's exact_by_formula,
+    test_kernels.py:23-40): the top_k rows among 0 .. p - window by their
+    largest softmax weight over the heads, in FP64; all of them when fewer."""
+    B, T, H, c = q.shape
+    N = k.shape[1]
+    chosen = [[set() for _ in range(T)] for _ in range(B)]
+    for b in range(B):
+        for t in range(T):
+            p = min(int(positions[b, t]), N - 1)
+            weights = torch.softmax((q[b, t].double() @ k[b, :p + 1].double().T) * scale, -1)  # (H, p + 1)
+            far = min(int(positions[b, t]) + 1 - window, N)
+            if far > 0:
+                score = weights[:, :far].amax(0)
+                chosen[b][t] = set(score.topk(min(top_k, far)).indices.tolist())
+    return chosen
+
+
+def choice_scores(q, k, positions, scale, window):
+    """(B, T, N) FP64: each row's largest log-weight over the heads for each
+    query, -inf at rows that are not candidates (n > p - window)."""
+    B, T, H, c = q.shape
+    N = k.shape[1]
+    z = torch.einsum("bthc,bnc->bthn", q.double(), k.double()) * scale
+    z = z.masked_fill(torch.arange(N) > positions[..., None, None], float("-inf"))
+    score = (z - z.logsumexp(-1, keepdim=True)).amax(2)
+    return score.masked_fill(torch.arange(N) > positions[..., None] - window, float("-inf"))
+
+
 def sparse_by_formula(q, k, v, sink, idx, positions, scale, window):
     """Each query over its rows idx and its last window rows (a set: the
     reference's chosen rows never meet its window), each head's sink in the

@@ -201,11 +201,3 @@ def test_bad_shapes_raise_value_error(device):
         kernels.verify_attention(q, k, k, positions, 0.1)
     with pytest.raises(ValueError):
         kernels.verify_attention(q, k.float(), k.float(), positions[:, :1].expand(2, 5), 0.1)
-
-
-def test_the_choice_is_not_built_yet(device):
-    q = torch.zeros(1, 2, 4, 128, dtype=torch.bfloat16, device=device)
-    k = torch.zeros(1, 300, 128, dtype=torch.bfloat16, device=device)
-    positions = torch.tensor([[298, 299]], device=device)
-    with pytest.raises(NotImplementedError):
-        kernels.exact_attention(q, k, k, positions, 0.1, 16, 128)

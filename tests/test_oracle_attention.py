@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from oracle import attention as oracle
-from tests.formulas import exact_by_formula, inputs, sparse_by_formula, tree_by_formula
+from tests.formulas import choice_by_formula, exact_by_formula, inputs, sparse_by_formula, tree_by_formula
 
 
 def test_exact_attention_follows_the_formula_across_block_joins(monkeypatch):
@@ -26,6 +26,19 @@ def test_the_choice_picks_the_rows_of_largest_weight_outside_the_window():
     assert chosen.shape == (2, 12, 8)
     for t in range(12):
         assert set(chosen[0, t][chosen[0, t] >= 0].tolist()) == set(range(max(0, t - 3)))
+
+
+@pytest.mark.parametrize("top_k, window", [(5, 8), (1, 3), (20, 1), (3, 0)])
+def test_the_choice_is_the_top_k_by_the_largest_weight_over_the_heads(monkeypatch, top_k, window):
+    # the reference's formula test of the choice (test_kernels.py:70-79): the
+    # chosen sets equal the brute-force top_k of max-over-heads weights, in
+    # blocks of a few queries
+    monkeypatch.setattr(oracle, "BLOCK_VALUES", 4 * 3 * 50)
+    q, k, v, _, positions = inputs(T=30, N=50)
+    _, chosen = oracle.exact_attention(q, k, v, positions, 0.3, top_k, window)
+    assert chosen.shape == (2, 30, oracle.chosen_columns(top_k, window, 50))
+    expected = choice_by_formula(q, k, positions, 0.3, top_k, window)
+    assert [[set(row[row >= 0].tolist()) for row in query] for query in chosen] == expected
 
 
 def test_padding_queries_past_the_table_read_up_to_its_last_row():

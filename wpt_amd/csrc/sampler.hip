@@ -39,15 +39,6 @@ struct Stats {  // per (batch row, position); arrays of B * P in the workspace
   int* keep;    // 1 if the draft at this position is kept
 };
 
-__device__ __forceinline__ uint32_t order_key(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ float key_value(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
-
 __device__ __forceinline__ float block_max(float x, float* red) {
   x = wave_max(x);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;

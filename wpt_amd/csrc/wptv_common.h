@@ -61,6 +61,17 @@ __device__ __forceinline__ float from_f32<float>(float f) { return f; }
 template <>
 __device__ __forceinline__ unsigned short from_f32<unsigned short>(float f) { return f32_to_bf16(f); }
 
+// An order-preserving unsigned key of a float (larger float, larger key;
+// -0 below +0), and its inverse: radix selection runs on these keys.
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));

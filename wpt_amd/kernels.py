@@ -14,8 +14,7 @@ scores and softmax in FP32.
 These forms are forward-only: the verify step runs under torch.no_grad
 (wpt_model.WPT.extend, model.py:456).  Their backward raises
 NotImplementedError, which the reference's kernel tests read as "not
-written yet" (test_kernels.py:149-154); so does the exact layer's top-k
-choice (top_k > 0 with rows outside the window) until it is built.
+written yet" (test_kernels.py:149-154).
 A bad shape or dtype is ValueError; a device without the library is
 KernelUnavailable, never a fall back to another form.
 """
@@ -27,8 +26,8 @@ from ._lib import KernelUnavailable, check, ptr
 
 NAME = "HIP (gfx950)"
 
-__all__ = ["NAME", "KernelUnavailable", "chosen_columns", "exact_attention", "sparse_attention", "verify_attention",
-           "tree_attention", "tree_ancestors", "kv_append"]
+__all__ = ["NAME", "KernelUnavailable", "chosen_columns", "exact_attention", "choose_rows", "sparse_attention",
+           "verify_attention", "tree_attention", "tree_ancestors", "kv_append"]
 
 
 def chosen_columns(top_k, window, N):
@@ -127,15 +126,50 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
 
 def exact_attention(q, k, v, positions, scale, top_k, window):
     """(output (B, T, H, c), the chosen rows (B, T, K)): every query attends
-    to every row up to its position (pytorch_kernels.py:98-121,142-146).
-    K = chosen_columns(top_k, window, N); a choice (K > 0) is not built yet
-    and raises NotImplementedError."""
+    to every row up to its position, and chooses the top_k rows it weighs
+    most among those at least window tokens back, by their largest
+    log-weight over the heads (pytorch_kernels.py:98-121,142-146).  K =
+    chosen_columns(top_k, window, N); a query with fewer such rows holds all
+    of them, then -1.  The rows are in no particular order (here: those above
+    the K-th largest score in row order, then those equal to it)."""
     B, T, H, c, N = _check_inputs(q, k, v, positions)
     K = chosen_columns(top_k, window, N)
-    if K:
-        raise NotImplementedError("the exact layer's top-k choice of rows is not built in the HIP form yet")
-    out = verify_attention(q, k, v, positions, scale)
-    return out, torch.full((B, T, 0), -1, dtype=torch.long, device=q.device)
+    if not K:
+        out = verify_attention(q, k, v, positions, scale)
+        return out, torch.full((B, T, 0), -1, dtype=torch.long, device=q.device)
+    out, lse = verify_attention(q, k, v, positions, scale, lse=True)
+    return out, choose_rows(q, k, positions, lse, scale, top_k, window)
+
+
+def choose_rows(q, k, positions, lse, scale, top_k, window):
+    """The exact layer's choice (B, T, K) from the forward pass's lse
+    (B, T, H): each query's K = chosen_columns(top_k, window, N) rows among
+    0 .. p - window with the largest max_h (q_h . k_n * scale - lse_h), -1
+    past a query's candidates (pytorch_kernels.py:112-117)."""
+    if q.dim() != 4 or k.dim() != 3:
+        raise ValueError(f"q must be (B, T, H, c) and k (B, N, c); got {tuple(q.shape)}, {tuple(k.shape)}")
+    B, T, H, c = q.shape
+    N = k.shape[1]
+    if tuple(lse.shape) != (B, T, H) or lse.dtype != torch.float32:
+        raise ValueError(f"lse must be FP32 (B={B}, T={T}, H={H}); got {lse.dtype} {tuple(lse.shape)}")
+    if k.shape[0] != B or k.shape[2] != c or k.stride(2) != 1 or k.dtype != q.dtype:
+        raise ValueError(f"k must be (B={B}, N, c={c}) in q's dtype with contiguous rows")
+    K = chosen_columns(top_k, window, N)
+    device = q.device
+    chosen = torch.empty(B, T, K, dtype=torch.long, device=device)
+    if not K:
+        return chosen
+    library = _lib.lib()
+    size = _lib.ctypes.c_size_t(0)
+    check(library.wptv_choice_workspace(B, T, N, _lib.ctypes.byref(size)), "choose_rows")
+    workspace = torch.empty(size.value, dtype=torch.uint8, device=device)
+    q_ = q.contiguous()
+    positions_ = _long(positions, device)
+    check(library.wptv_exact_choice(ptr(q_), ptr(k), k.stride(0), k.stride(1), _lib.dtype_code(q.dtype),
+                                    ptr(positions_), ptr(lse.contiguous()), B, T, H, c, N, float(scale), int(top_k),
+                                    int(window), ptr(chosen), ptr(workspace), size.value, _lib.stream(device)),
+          "choose_rows")
+    return chosen
 
 
 def sparse_attention(q, k, v, sink, idx, positions, scale, window):
