@@ -95,6 +95,34 @@ int wptv_verify_attention(const void* q, const void* k, int64_t k_stride_b, int6
                           int N, float scale, int splits, int flags, void* out, float* lse,
                           void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Window attention: each query at position p reads the rows of positions
+ * max(0, p - window + 1) .. p, itself included and none before the text, with
+ * a per-head sink in the denominator and the layer's output gate -- a window
+ * layer's attention at decode (packages/wpt-model/src/wpt_model/
+ * attention.py:85-107 window_attention, :142-151 WindowAttention.forward,
+ * the gate of :128-130).  Where the reference reads a (B, window - 1 + T, 2c)
+ * table of the carried tail and the new entries (carry.py:43-63), the table
+ * here is addressed by token position:
+ *   row_base NULL: a ring of ring_rows (a power of 2, >= window + T - 1) rows
+ *            per batch row, position n at row n mod ring_rows (the build's
+ *            window-layer cache; wptv_window_qkv_post appends to it)
+ *   row_base [B] int64: position n at row n - row_base[b] of a table of
+ *            ring_rows rows (the reference's tail + new table: row_base =
+ *            the position of its first row)
+ *   gate     NULL, or [B*T, >= H*c] in dtype (row stride gate_stride): the
+ *            output is o * sigmoid(gate), each factor rounded to the dtype
+ *   workspace  wptv_window_attention_workspace() bytes for the same splits
+ * The T positions of a batch row are consecutive (a pass of new tokens).
+ * ------------------------------------------------------------------------- */
+int wptv_window_attention_workspace(int B, int T, int H, int c, int window, int dtype, int* splits, size_t* bytes);
+
+int wptv_window_attention(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n, const void* v,
+                          int64_t v_stride_b, int64_t v_stride_n, int dtype, const int64_t* positions,
+                          const int64_t* row_base, int ring_rows, int window, const float* sink, const void* gate,
+                          int64_t gate_stride, int B, int T, int H, int c, float scale, int splits, void* out,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Sparse attention over chosen rows plus the last `window` rows, with a sink:
  * the reference's sparse_attention with chosen rows
  * (pytorch_kernels.py:171-187,213-217).  idx [B, T, K] int64, -1 = none;
@@ -186,6 +214,20 @@ int wptv_qkv_post_parts(const float* parts, int splits, const float* q_norm, con
                         void* table, int64_t table_stride_b, int64_t table_stride_n, int64_t capacity,
                         const int64_t* start, const int64_t* counts, int B, int T, int H, int c, int dtype, float eps,
                         hipStream_t stream);
+
+/* wptv_window_qkv_post: a window layer after its projection (attention.py:
+ *   113-135 queries / entries): as wptv_qkv_post, then the last rope_dims
+ *   dimensions of each normed query head and key turned by the token's
+ *   position p = start[b] + t (rotate, attention.py:59-71: adjacent pairs
+ *   (2i, 2i + 1) by the angle p / rope_div[i], in FP32 from the normed values
+ *   rounded to the dtype); rope_div [rope_dims / 2] fp32 on the device, the
+ *   reference's base^(2i / rope_dims); the entry [rotate(k_norm(k)), v] of
+ *   t < counts[b] written at ring row (start[b] + t) mod ring_rows (a power
+ *   of 2). */
+int wptv_window_qkv_post(const void* qkv, int64_t qkv_row_stride, const float* q_norm, const float* k_norm,
+                         void* q_out, void* ring, int64_t ring_stride_b, int64_t ring_stride_n, int ring_rows,
+                         const int64_t* start, const int64_t* counts, int B, int T, int H, int c, int rope_dims,
+                         const float* rope_div, int dtype, float eps, hipStream_t stream);
 
 int wptv_swiglu(const void* gate_up, void* out, int M, int F, int dtype, hipStream_t stream);
 

@@ -7,6 +7,10 @@ CPU (test infrastructure; see oracle/__init__.py).
     sparse_attention  pytorch_kernels.py:149-153 (_window), :156-161
                       (_gather), :171-187 (_Sparse.forward), :213-217
     dense_attention   attention.py:74-82
+    window_attention  attention.py:85-107: each query over the last `window`
+                      rows of a (B, window - 1 + T) table of the carried tail
+                      and the new entries, none before the text, with a sink
+    rotate            attention.py:59-71, the window layers' rotary encoding
     tree_visible      the mask "prefix plus ancestors-or-self" of a draft tree
 
 Forward passes only: the verify step runs under no_grad.
@@ -101,6 +105,45 @@ def dense_attention(q, k, v, sink, visible, scale):
     z = z.masked_fill(~visible[..., None, :, :], float("-inf"))
     lse = torch.logaddexp(torch.logsumexp(z, -1), sink.float()[:, None])
     return torch.einsum("...hqk,...kc->...qhc", (z - lse[..., None]).exp(), v.float())
+
+
+ROPE_DIMS = 64  # attention.py:53-54
+ROPE_BASE = 10000
+
+
+def rotate(x, positions, dims=ROPE_DIMS, base=ROPE_BASE):
+    """Rotary encoding of the last `dims` dimensions of x (B, T, d) or
+    (B, T, H, d) at positions (T,) or (B, T): adjacent pairs (2i, 2i + 1)
+    turned by the angle p / base^(2i / dims), computed in FP32 from x's values
+    and returned in x's dtype, the other dimensions untouched."""
+    pairs = torch.arange(dims // 2, dtype=torch.float32)
+    angles = positions.float()[..., None] / base ** (2 * pairs / dims)
+    cos, sin = angles.cos(), angles.sin()
+    if x.ndim == 4:
+        cos, sin = cos[..., None, :], sin[..., None, :]
+    kept, turning = x[..., :-dims], x[..., -dims:].float()
+    even, odd = turning[..., 0::2], turning[..., 1::2]
+    turned = torch.stack([even * cos - odd * sin, even * sin + odd * cos], -1).flatten(-2)
+    return torch.cat([kept, turned.to(x.dtype)], -1)
+
+
+def window_visible(positions, window, T):
+    """(B, T, window - 1 + T) bool: query t (its own entry at table row
+    window - 1 + t) sees the rows window - 1 + t - d for distances
+    0 <= d < window with d <= its position (nothing before the text)."""
+    rows = torch.arange(window - 1 + T)
+    distance = (window - 1 + torch.arange(T))[:, None] - rows  # (T, rows)
+    return (distance >= 0) & (distance < window) & (distance <= positions[..., None])
+
+
+def window_attention(q, k, v, sink, positions, scale, window):
+    """q (B, T, H, c) at positions (B, T); k, v (B, window - 1 + T, c): the
+    window - 1 rows before the pass's first token, then its own.  Output
+    (B, T, H, c) in FP32 (scores and softmax in FP32, the sink (H,) in each
+    head's denominator)."""
+    B, T = q.shape[:2]
+    positions = positions.expand(B, T)
+    return dense_attention(q, k, v, sink, window_visible(positions, window, T), scale)
 
 
 def binary_tree_parents(nodes):

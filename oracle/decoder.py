@@ -10,6 +10,13 @@ extend reads it (model.py:456-473: scores = head(final_norm(hidden)), FP32).
 RMSNorm's eps is the reference's (layers.py:9).  extend / undo / new_cache
 follow the reference's generation protocol through oracle.cache.
 
+A layer may instead be the reference's window layer (WindowAttention,
+attention.py:109-151): q = rotate(q_norm(q(x))), entries
+[rotate(k_norm(k(x))), v(x)] at the tokens' positions, the window - 1 entries
+carried from before (the cache's tail, cache.py:97-108) joined in front,
+window attention with a sink per head, and the output times sigmoid(gate(x))
+before the output projection.
+
 Weights are a dict of tensors (any dtype; used in FP32):
     embedding (V, D); head (V, D); final_norm (D,)
     layers.{i}.attn_norm (D,)   layers.{i}.qkv (H*c + 2c, D): q rows, k, v
@@ -17,6 +24,7 @@ Weights are a dict of tensors (any dtype; used in FP32):
     layers.{i}.out (D, H*c)     layers.{i}.ffn_norm (D,)
     layers.{i}.gate_up (2F, D): gate rows, then up rows
     layers.{i}.down (D, F)
+    window layers also: layers.{i}.gate (H*c, D), layers.{i}.sink (H,)
 """
 
 import torch
@@ -32,9 +40,11 @@ def rms_norm(x, weight):
 
 
 class Decoder:
-    def __init__(self, weights, layers, heads, head_dim):
+    def __init__(self, weights, layers, heads, head_dim, kinds=(), window=128, rope_dims=64, rope_base=10000.0):
         self.w = {name: value.float() for name, value in weights.items()}
         self.layers, self.heads, self.head_dim = layers, heads, head_dim
+        self.kinds = tuple(kinds) or ("exact",) * layers
+        self.window, self.rope_dims, self.rope_base = window, rope_dims, rope_base
 
     def new_cache(self, rows):
         return cache.Rows(rows)
@@ -48,8 +58,17 @@ class Decoder:
         q = rms_norm(qkv[..., :H * c].reshape(B, T, H, c), w("q_norm"))
         k = rms_norm(qkv[..., H * c:H * c + c], w("k_norm"))
         v = qkv[..., H * c + c:]
-        table = reading.everything(("entries", i), torch.cat([k, v], -1))
-        o, _ = attention.exact_attention(q, table[..., :c], table[..., c:], reading.positions(T), c ** -0.5, 0, 128)
+        positions = reading.positions(T)
+        if self.kinds[i] == "window":
+            W = self.window
+            q = attention.rotate(q, positions, self.rope_dims, self.rope_base)
+            entries = torch.cat([attention.rotate(k, positions, self.rope_dims, self.rope_base), v], -1)
+            table = torch.cat([reading.before(("window", i), W - 1, entries), entries], 1)
+            o = attention.window_attention(q, table[..., :c], table[..., c:], w("sink"), positions, c ** -0.5, W)
+            o = o * torch.sigmoid(x @ w("gate").T).reshape(B, T, H, c)
+        else:
+            table = reading.everything(("entries", i), torch.cat([k, v], -1))
+            o, _ = attention.exact_attention(q, table[..., :c], table[..., c:], positions, c ** -0.5, 0, 128)
         h = h + o.reshape(B, T, H * c) @ w("out").T
         x = rms_norm(h, w("ffn_norm"))
         gate, up = (x @ w("gate_up").T).chunk(2, -1)

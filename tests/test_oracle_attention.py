@@ -1,6 +1,8 @@
 """Pins the oracle's attention (CPU): against brute-force formulas, a closed
 form, causality and padding queries past the table."""
 
+import math
+
 import pytest
 import torch
 
@@ -123,3 +125,56 @@ def test_the_tree_of_a_chain_is_causal_attention():
     tree = oracle.tree_attention(q, k, v, torch.tensor([7, 7]), parents, 0.3)
     exact, _ = oracle.exact_attention(q, k, v, positions, 0.3, 0, 4)
     assert torch.allclose(tree, exact, atol=1e-6)
+
+
+@pytest.mark.parametrize("start, T, window", [(300, 5, 128), (3, 5, 16), (0, 7, 8), (40, 1, 8)])
+def test_window_attention_is_sparse_attention_over_the_last_window_rows(start, T, window):
+    # the window layer's form (a table of the carried tail, zeros before the
+    # text, and the new entries) against the pinned sparse form over the
+    # whole text at the same positions, with no chosen rows
+    generator = torch.Generator().manual_seed(7)
+    B, H, c = 2, 4, 32
+    L = start + T
+    q = torch.randn(B, T, H, c, generator=generator)
+    full = torch.randn(B, L, 2 * c, generator=generator)
+    sink = torch.randn(H, generator=generator)
+    positions = (start + torch.arange(T)).expand(B, T)
+    tail = torch.zeros(B, window - 1, 2 * c)
+    before = full[:, max(0, start - window + 1):start]
+    if before.shape[1]:
+        tail[:, -before.shape[1]:] = before
+    table = torch.cat([tail, full[:, start:]], 1)
+    got = oracle.window_attention(q, table[..., :c], table[..., c:], sink, positions, c ** -0.5, window)
+    expected = oracle.sparse_attention(q, full[..., :c], full[..., c:], sink, torch.empty(B, T, 0, dtype=torch.long),
+                                       positions, c ** -0.5, window)
+    assert torch.allclose(got, expected, atol=1e-5)
+    assert torch.allclose(got.double(), sparse_by_formula(q, full[..., :c], full[..., c:], sink,
+                                                          torch.empty(B, T, 0, dtype=torch.long), positions,
+                                                          c ** -0.5, window), atol=1e-5)
+
+
+def test_rotate_turns_pairs_by_the_position_over_the_frequency():
+    # RoPE (attention.py:59-71) from what fixes it: position 0 is the
+    # identity; the first pair of the turned dimensions turns by p radians
+    # (frequency base^0 = 1) and the last by p / base^(62/64); every pair
+    # keeps its length; the dimensions before the last 64 are untouched; and
+    # a query-key product depends on the positions' difference only
+    generator = torch.Generator().manual_seed(8)
+    x = torch.randn(1, 3, 2, 128, generator=generator)
+    assert torch.equal(oracle.rotate(x, torch.zeros(3, dtype=torch.long)), x)
+    unit = torch.zeros(1, 1, 128)
+    unit[..., 64] = 1.0
+    unit[..., 126] = 1.0
+    p = torch.tensor([5])
+    turned = oracle.rotate(unit, p)
+    assert torch.allclose(turned[0, 0, 64:66], torch.tensor([math.cos(5.0), math.sin(5.0)]), atol=1e-6)
+    angle = 5.0 / 10000 ** (62 / 64)
+    assert torch.allclose(turned[0, 0, 126:128], torch.tensor([math.cos(angle), math.sin(angle)]), atol=1e-6)
+    y = oracle.rotate(x, torch.tensor([7, 100, 12345]))
+    assert torch.equal(y[..., :64], x[..., :64])
+    pairs = lambda t: t[..., 64:].reshape(*t.shape[:-1], 32, 2).norm(dim=-1)  # noqa: E731
+    assert torch.allclose(pairs(y), pairs(x), atol=1e-5)
+    qv, kv = torch.randn(2, 1, 1, 128, generator=generator)
+    dots = [float((oracle.rotate(qv, torch.tensor([a])) * oracle.rotate(kv, torch.tensor([b]))).sum())
+            for a, b in ((10, 3), (57, 50), (1007, 1000))]
+    assert max(dots) - min(dots) < 1e-3

@@ -2,8 +2,11 @@
 pieces gives the scores of reading it whole (the reference's
 test_cache.py:74-143), rows sharing one prompt go on apart (:173-203), and
 undoing rejected drafts leaves the cache as if only the kept tokens had been
-read (:206-238); tails cut back as carry.last says."""
+read (:206-238); tails cut back as carry.last says.  Each holds for the
+exact layers' entries and for the window layers' carried tails (a window of
+8 rows, smaller than the pieces, so that the tails matter)."""
 
+import pytest
 import torch
 
 from oracle import cache, decoder
@@ -25,19 +28,25 @@ def weights(seed=0):
         w[f"layers.{i}.ffn_norm"] = 1 + 0.1 * torch.randn(D, generator=generator)
         w[f"layers.{i}.gate_up"] = torch.randn(2 * FFN, D, generator=generator) * 0.2
         w[f"layers.{i}.down"] = torch.randn(D, FFN, generator=generator) * 0.1
+        w[f"layers.{i}.gate"] = torch.randn(H * C, D, generator=generator) * 0.2
+        w[f"layers.{i}.sink"] = torch.randn(H, generator=generator)
     return w
 
 
-def model():
-    return decoder.Decoder(weights(), LAYERS, H, C)
+KINDS = [(), ("window", "exact")]
+
+
+def model(kinds=()):
+    return decoder.Decoder(weights(), LAYERS, H, C, kinds=kinds, window=8, rope_dims=8)
 
 
 def close(got, expected, share=1e-5):
     return (got - expected).abs().max() <= share * expected.abs().max()
 
 
-def test_reading_in_pieces_gives_the_whole_text_s_scores():
-    m = model()
+@pytest.mark.parametrize("kinds", KINDS, ids=["exact", "window+exact"])
+def test_reading_in_pieces_gives_the_whole_text_s_scores(kinds):
+    m = model(kinds)
     ids = torch.randint(V, (2, sum(PIECES)), generator=torch.Generator().manual_seed(1))
     whole = m.forward(ids)
     rows, got, start = m.new_cache(2), [], 0
@@ -48,8 +57,9 @@ def test_reading_in_pieces_gives_the_whole_text_s_scores():
     assert close(torch.cat(got, 1), whole)
 
 
-def test_a_shared_prompt_and_rows_at_different_places():
-    m = model()
+@pytest.mark.parametrize("kinds", KINDS, ids=["exact", "window+exact"])
+def test_a_shared_prompt_and_rows_at_different_places(kinds):
+    m = model(kinds)
     generator = torch.Generator().manual_seed(2)
     prompt = torch.randint(V, (40,), generator=generator).tolist()
     texts = [prompt + torch.randint(V, (n,), generator=generator).tolist() for n in (30, 5, 17)]
@@ -71,8 +81,9 @@ def test_a_shared_prompt_and_rows_at_different_places():
     assert shared.lengths.tolist() == [len(prompt)]
 
 
-def test_undoing_rejected_drafts_leaves_only_the_kept_tokens():
-    m = model()
+@pytest.mark.parametrize("kinds", KINDS, ids=["exact", "window+exact"])
+def test_undoing_rejected_drafts_leaves_only_the_kept_tokens(kinds):
+    m = model(kinds)
     generator = torch.Generator().manual_seed(3)
     texts = [torch.randint(V, (200,), generator=generator).tolist() for _ in range(2)]
     rows = m.new_cache(2)
@@ -94,8 +105,9 @@ def test_undoing_rejected_drafts_leaves_only_the_kept_tokens():
         assert close(torch.cat(got[row]), whole[60:])
 
 
-def test_later_tokens_never_change_earlier_scores():
-    m = model()
+@pytest.mark.parametrize("kinds", KINDS, ids=["exact", "window+exact"])
+def test_later_tokens_never_change_earlier_scores(kinds):
+    m = model(kinds)
     ids = torch.randint(V, (1, 50), generator=torch.Generator().manual_seed(4))
     changed = ids.clone()
     changed[0, 30] = (changed[0, 30] + 7) % V

@@ -38,11 +38,15 @@ SIGNATURES = {
                               _I, _P, _P, _P, _SZ, _P],
     "wptv_sparse_attention": [_P, _P, _I64, _I64, _P, _I64, _I64, _I, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _F, _P,
                               _P, _P],
+    "wptv_window_attention_workspace": [_I, _I, _I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_SZ)],
+    "wptv_window_attention": [_P, _P, _I64, _I64, _P, _I64, _I64, _I, _P, _P, _I, _I, _P, _P, _I64, _I, _I, _I, _I,
+                              _F, _I, _P, _P, _SZ, _P],
     "wptv_choice_workspace": [_I, _I, _I, ctypes.POINTER(_SZ)],
     "wptv_exact_choice": [_P, _P, _I64, _I64, _I, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P, _P, _SZ, _P],
     "wptv_kv_append": [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _I, _I, _I, _P],
     "wptv_add_rms_norm": [_P, _P, _P, _P, _I, _I, _I, _F, _P],
     "wptv_qkv_post": [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I, _I, _F, _P],
+    "wptv_window_qkv_post": [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I, _P, _P, _I, _I, _I, _I, _I, _P, _I, _F, _P],
     "wptv_swiglu": [_P, _P, _I, _I, _I, _P],
     "wptv_gemm_workspace": [_I, _I, _I, _P, _P],
     "wptv_gemm": [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _I, _I, _P, _SZ, _P],

@@ -1,7 +1,17 @@
 """The generation cache of the MQA decoder on the GPU: the reference's Rows /
 Reading / Cache (packages/wpt-model/src/wpt_model/cache.py:54-174) for exact
 layers, whose carried value is every token's key and value side by side
-(carry.Entries, carry.py:66-71).
+(carry.Entries, carry.py:66-71), and for window layers, whose carried value
+is the last window - 1 tokens' (carry.Tail, carry.py:30-63).
+
+A window layer's entries live in a ring of R rows per batch row (R a power
+of 2 of at least window - 1 + the widest reading), token p at row p mod R: a
+reading writes its tokens over ones more than R - 1 tokens back, which no
+query of it or of a later reading sees, so the ring holds the reference's
+tail (the window - 1 rows before each row's length, tail(layer) gathers it)
+with no copy per step, and undo, which only restores the lengths, cuts it
+back as carry.Tail.undo does (rows past a length are written again before
+any query reads them).
 
 Each layer's entries live in one (B, capacity, 2c) table, keys first, token p
 of row b at row p.  A reading appends each row's own new entries at its own
@@ -21,10 +31,17 @@ import torch
 
 
 class Cache:
-    def __init__(self, rows, layers, width, dtype, device, capacity=256):
+    """rings: the layers whose table is a ring of ring_rows rows (window
+    layers); every other layer's table grows with the text."""
+
+    def __init__(self, rows, layers, width, dtype, device, capacity=256, rings=(), ring_rows=256):
+        if ring_rows <= 0 or ring_rows & (ring_rows - 1):
+            raise ValueError(f"a ring holds a power of 2 of rows, not {ring_rows}")
         self.lengths = torch.zeros(rows, dtype=torch.long, device=device)
         self.before = torch.zeros_like(self.lengths)  # the lengths before the last undoable reading
-        self.tables = [torch.zeros(rows, capacity, width, dtype=dtype, device=device) for _ in range(layers)]
+        self.rings = frozenset(rings)
+        self.tables = [torch.zeros(rows, ring_rows if i in self.rings else capacity, width, dtype=dtype,
+                                   device=device) for i in range(layers)]
         self.pending = False
         self.bound = 0
         self.routes = None
@@ -35,18 +52,40 @@ class Cache:
 
     @property
     def capacity(self):
-        return self.tables[0].shape[1] if self.tables else 0
+        grown = [t.shape[1] for i, t in enumerate(self.tables) if i not in self.rings]
+        return grown[0] if grown else None
+
+    @property
+    def ring_rows(self):
+        rings = [self.tables[i].shape[1] for i in sorted(self.rings)]
+        return rings[0] if rings else None
 
     def reserve(self, need):
-        """Tables of at least `need` rows (grown to max(need, 2 x capacity))."""
-        if need <= self.capacity:
+        """Growing tables of at least `need` rows (grown to max(need, 2 x
+        capacity)); the rings keep their size."""
+        if self.capacity is None or need <= self.capacity:
             return
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError(f"the cache needs {need} rows but holds {self.capacity}: reserve them before "
                                "capturing a step")
         grown = max(need, 2 * self.capacity)
-        self.tables = [torch.cat([t, t.new_zeros(t.shape[0], grown - t.shape[1], t.shape[2])], 1)
-                       for t in self.tables]
+        self.tables = [t if i in self.rings else torch.cat([t, t.new_zeros(t.shape[0], grown - t.shape[1],
+                                                                           t.shape[2])], 1)
+                       for i, t in enumerate(self.tables)]
+
+    def tail(self, layer, steps):
+        """A window layer's carried tail (B, steps, width): the entries of the
+        steps tokens before each row's length, zeros before the text (the
+        reference's Reading.before, cache.py:97-108)."""
+        if layer not in self.rings:
+            raise ValueError(f"layer {layer} keeps every entry, not a tail")
+        ring = self.tables[layer]
+        R = ring.shape[1]
+        if steps > R:
+            raise ValueError(f"the ring holds {R} rows, fewer than {steps}")
+        positions = self.lengths[:, None] - steps + torch.arange(steps, device=ring.device)
+        rows = ring.gather(1, (positions % R)[..., None].expand(-1, -1, ring.shape[2]))
+        return rows.masked_fill((positions < 0)[..., None], 0)
 
     def finish(self, counts, undoable, width):
         """The rows have read their tokens (the reference's Reading.finish).
@@ -75,5 +114,6 @@ class Cache:
         copy.lengths = self.lengths[index]
         copy.before = torch.zeros_like(copy.lengths)
         copy.tables = [t[index] for t in self.tables]
+        copy.rings = self.rings
         copy.pending, copy.bound, copy.routes = False, self.bound, None
         return copy

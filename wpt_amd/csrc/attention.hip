@@ -65,17 +65,53 @@ __device__ __forceinline__ bool tree_visible(int n, int64_t tbase, uint64_t anc)
   return node < 64 && ((anc >> node) & 1ull);
 }
 
+// Where logical row n (a token's position) of batch row b sits in the table:
+// physical row (n - base[b]) & mask.  The default (base NULL, mask all ones)
+// is token p at row p; a window layer's ring of 2^r rows per batch row has
+// mask 2^r - 1; a table that starts at a later token has base[b] = that
+// token's position.
+struct RowMap {
+  const int64_t* base;
+  uint32_t mask;
+};
+
+__device__ __forceinline__ int row_base(const RowMap& m, int b) { return m.base ? (int)m.base[b] : 0; }
+
+// A window or sparse layer's output gate (attention.py:128-130): the output
+// o (rounded to bf16, the attention's dtype) times sigmoid(gate) (rounded to
+// bf16, as torch.sigmoid of a bf16 tensor), rounded again.  Row (b*T + t) of
+// the gate at g + (b*T + t)*stride, head h's columns at + h*c; g NULL: none.
+struct OutGate {
+  const void* g;  // in the attention's dtype
+  int64_t stride;
+  template <typename E>
+  __device__ __forceinline__ const E* row(int b, int T, int r, int H, int C) const {
+    return g ? static_cast<const E*>(g) + ((int64_t)b * T + r / H) * stride + (int64_t)(r % H) * C : nullptr;
+  }
+};
+
+__device__ __forceinline__ float gate_factor(unsigned short g) {
+  return bf16_to_f32(f32_to_bf16(1.f / (1.f + __expf(-bf16_to_f32(g)))));
+}
+
+// o rounded to bf16, times the gate factor, rounded again.
+__device__ __forceinline__ unsigned short gated_bf16(float o, unsigned short g) {
+  return f32_to_bf16(bf16_to_f32(f32_to_bf16(o)) * gate_factor(g));
+}
+
 // Merges the parts of one query row's 8 columns c8 .. c8 + 7: fixed split
 // order, log-sum-exp weights, the sink (log2 units; -inf: none) joining the
 // denominator.  Part s of the row is at row0 + s * stride (bf16 output,
 // normalized within the part, and its log2-sum-exp).  The parts are read
 // eight at a time, every load of a group issued before any is used, with a
 // running maximum across groups.  Writes the 8 outputs and, when lse is
-// given and c8 == 0, the row's natural-log log-sum-exp.
+// given and c8 == 0, the row's natural-log log-sum-exp.  grow: the row's
+// output gate (NULL: none).
 __device__ __forceinline__ void merge_parts(const unsigned short* __restrict__ part_o,
                                             const float* __restrict__ part_lse, int64_t row0, int64_t stride,
                                             int splits, int C, int c8, float sink_log2,
-                                            unsigned short* __restrict__ orow, float* __restrict__ lse) {
+                                            unsigned short* __restrict__ orow, float* __restrict__ lse,
+                                            const unsigned short* __restrict__ grow) {
   constexpr int kGroup = 8;
   float M = kNegInf, L = 0.f;
   float acc[8];
@@ -119,8 +155,14 @@ __device__ __forceinline__ void merge_parts(const unsigned short* __restrict__ p
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   u16x8 res;
+  if (grow) {
+    const u16x8 gv = *reinterpret_cast<const u16x8*>(grow + c8);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) res[e] = f32_to_bf16(acc[e] * inv);
+    for (int e = 0; e < 8; ++e) res[e] = gated_bf16(acc[e] * inv, gv[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) res[e] = f32_to_bf16(acc[e] * inv);
+  }
   *reinterpret_cast<u16x8*>(orow + c8) = res;
   if (lse && c8 == 0) *lse = L > 0.f ? (M + log2f(L)) * kLn2 : kNegInf;
 }
@@ -182,8 +224,8 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn, const int64_t* __restrict__ positions,
     int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
     const float* __restrict__ sink, int T, int H, int N, float scale_log2, int groups, int splits,
-    int range_from_positions, int xcd_map, unsigned short* __restrict__ out, float* __restrict__ lse_out,
-    unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
+    int range_from_positions, int xcd_map, RowMap rows, OutGate gate, unsigned short* __restrict__ out,
+    float* __restrict__ lse_out, unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
   using G = Tile<C>;
   constexpr int kRows = 16 * MB;
   constexpr int DMAW = MB >= 4 ? 4 : (MB >= 2 ? 2 : 1);  // wavefronts of a key set that issue its DMA
@@ -255,6 +297,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   unsigned short* const ring = lds + kset * kRing;
   const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_address(ring));
   const bool dma_wave = mb < DMAW;
+  const int rbase = row_base(rows, b);
   auto issue = [&](int it) {  // this wavefront's share of the key set's tile of iteration it
     const int tile = kset + it * kKeySets;
     const uint32_t slot = ring_lds + (uint32_t)(it % G::kSlots) * (G::kElems * 2);
@@ -264,7 +307,8 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
       const int part = ii / G::kPerHalf, chunk = ii % G::kPerHalf;
       int n = s_lo + tile * 32 + 16 * (part & 1) + j;
       n = n < s_hi ? n : s_hi;  // rows past the split are masked; read a valid one
-      const uint32_t off = (uint32_t)n * (part < 2 ? krow_bytes : vrow_bytes) + 64u * chunk + 16u * g;
+      const uint32_t phys = (uint32_t)(n - rbase) & rows.mask;
+      const uint32_t off = phys * (part < 2 ? krow_bytes : vrow_bytes) + 64u * chunk + 16u * g;
       dma_16B(part < 2 ? krs : vrs, off, slot + part * (G::kHalf * 2) + 1024u * chunk);
     }
   };
@@ -480,11 +524,19 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   if (splits == 1) {
     typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
     unsigned short* orow = out + ((int64_t)b * R + r) * C;
+    const unsigned short* grow = gate.row<unsigned short>(b, T, r, H, C);
 #pragma unroll
     for (int cb = 0; cb < G::kCBlocks; ++cb) {
       const f32x4 val = o[cb] * scale_out;
-      *reinterpret_cast<u16x4*>(orow + cb * 16 + 4 * g) =
-          u16x4{f32_to_bf16(val[0]), f32_to_bf16(val[1]), f32_to_bf16(val[2]), f32_to_bf16(val[3])};
+      u16x4 res;
+      if (grow) {
+        const u16x4 gv = *reinterpret_cast<const u16x4*>(grow + cb * 16 + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) res[e] = gated_bf16(val[e], gv[e]);
+      } else {
+        res = u16x4{f32_to_bf16(val[0]), f32_to_bf16(val[1]), f32_to_bf16(val[2]), f32_to_bf16(val[3])};
+      }
+      *reinterpret_cast<u16x4*>(orow + cb * 16 + 4 * g) = res;
     }
     if (lse_out && g == 0) lse_out[(int64_t)b * R + r] = lse2 * kLn2;
   } else {
@@ -977,9 +1029,10 @@ __global__ __launch_bounds__(kKeyWaves * 64, 1) void verify_attention_keys(
 // per (batch row, query row, 8 columns).
 __global__ __launch_bounds__(256) void combine_splits(const unsigned short* __restrict__ part_o,
                                                       const float* __restrict__ part_lse,
-                                                      const float* __restrict__ sink, int B, int R, int H, int C,
-                                                      int rows_per_group, int groups, int splits,
+                                                      const float* __restrict__ sink, int B, int T, int H, int C,
+                                                      int rows_per_group, int groups, int splits, OutGate gate,
                                                       unsigned short* __restrict__ out, float* __restrict__ lse_out) {
+  const int R = T * H;
   const int per_row = C / 8;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)B * R * per_row) return;
@@ -989,8 +1042,9 @@ __global__ __launch_bounds__(256) void combine_splits(const unsigned short* __re
   const int c8 = (rem % per_row) * 8;
   const int grp = r / rows_per_group, rr = r % rows_per_group;
   const int64_t row0 = ((int64_t)(b * groups + grp) * splits) * rows_per_group + rr;  // split 0's part
+  const unsigned short* grow = gate.row<unsigned short>(b, T, r, H, C);
   merge_parts(part_o, part_lse, row0, rows_per_group, splits, C, c8, sink ? sink[r % H] * kLog2e : kNegInf,
-              out + ((int64_t)b * R + r) * C, lse_out ? lse_out + (int64_t)b * R + r : nullptr);
+              out + ((int64_t)b * R + r) * C, lse_out ? lse_out + (int64_t)b * R + r : nullptr, grow);
 }
 
 // ---------------------------------------------------------------------------
@@ -1004,8 +1058,8 @@ __global__ __launch_bounds__(64) void attention_generic(
     const T* __restrict__ q, const T* __restrict__ k, int64_t ksb, int64_t ksn, const T* __restrict__ v,
     int64_t vsb, int64_t vsn, const int64_t* __restrict__ idx, int K, const int64_t* __restrict__ positions,
     int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
-    const float* __restrict__ sink, int T_, int H, int C, int N, float scale_log2, T* __restrict__ out,
-    float* __restrict__ lse_out) {
+    const float* __restrict__ sink, int T_, int H, int C, int N, float scale_log2, RowMap rows, OutGate gate,
+    T* __restrict__ out, float* __restrict__ lse_out) {
   const int lane = threadIdx.x;
   const int h = blockIdx.x % H;
   const int t = blockIdx.x / H;
@@ -1024,6 +1078,7 @@ __global__ __launch_bounds__(64) void attention_generic(
   const int n_window = hi >= lo ? hi - lo + 1 : 0;
   const int total = K + n_window;
   const int64_t* idx_row = idx ? idx + ((int64_t)b * T_ + t) * K : nullptr;
+  const int rbase = row_base(rows, b);
 
   float m_run = kNegInf, l_run = 0.f;
   float acc[kMaxC / 64];
@@ -1044,7 +1099,7 @@ __global__ __launch_bounds__(64) void attention_generic(
     }
     float z = kNegInf;
     if (n >= 0) {
-      const T* krow = k + (int64_t)b * ksb + (int64_t)n * ksn;
+      const T* krow = k + (int64_t)b * ksb + (int64_t)((uint32_t)(n - rbase) & rows.mask) * ksn;
       float dot = 0.f;
       for (int c = 0; c < C; ++c) dot += load_f32(qrow + c) * load_f32(krow + c);
       z = dot * scale_log2;
@@ -1062,7 +1117,7 @@ __global__ __launch_bounds__(64) void attention_generic(
       const float pi = __shfl(pz, i, 64);
       const int ni = __shfl(n, i, 64);
       if (ni < 0) continue;
-      const T* vrow = v + (int64_t)b * vsb + (int64_t)ni * vsn;
+      const T* vrow = v + (int64_t)b * vsb + (int64_t)((uint32_t)(ni - rbase) & rows.mask) * vsn;
       for (int u = 0; u < per_lane; ++u) {
         const int c = lane + 64 * u;
         if (c < C) acc[u] += pi * load_f32(vrow + c);
@@ -1079,9 +1134,14 @@ __global__ __launch_bounds__(64) void attention_generic(
   }
   const float inv = L > 0.f ? f / L : 0.f;
   T* orow = out + row * C;
+  const T* grow = gate.row<T>(b, T_, t * H + h, H, C);
   for (int u = 0; u < per_lane; ++u) {
     const int c = lane + 64 * u;
-    if (c < C) orow[c] = from_f32<T>(acc[u] * inv);
+    if (c >= C) continue;
+    float val = acc[u] * inv;
+    if (grow)  // o in the dtype, times sigmoid(gate) in the dtype, rounded again
+      val = rounded<T>(val) * rounded<T>(1.f / (1.f + __expf(-load_f32(grow + c))));
+    orow[c] = from_f32<T>(val);
   }
   if (lse_out && lane == 0) lse_out[row] = L > 0.f ? (M + log2f(L)) * kLn2 : kNegInf;
 }
@@ -1188,10 +1248,11 @@ void launch_mfma(dim3 grid, hipStream_t stream, const unsigned short* q, const u
                  int64_t ksn, const unsigned short* v, int64_t vsb, int64_t vsn, const int64_t* positions,
                  int window, const int64_t* tree_base, const uint64_t* ancestors, const float* sink, int T, int H,
                  int N, float scale_log2, int groups, int splits, int range_from_positions, int xcd_map,
-                 unsigned short* out, float* lse, unsigned short* part_o, float* part_lse) {
+                 RowMap rows, OutGate gate, unsigned short* out, float* lse, unsigned short* part_o,
+                 float* part_lse) {
   hipLaunchKernelGGL((verify_attention_mfma<C, MBW, TREE>), grid, dim3(kKeySets * MBW * 64), 0, stream, q, k, ksb,
                      ksn, v, vsb, vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, groups,
-                     splits, range_from_positions, xcd_map, out, lse, part_o, part_lse);
+                     splits, range_from_positions, xcd_map, rows, gate, out, lse, part_o, part_lse);
 }
 
 }  // namespace
@@ -1210,12 +1271,14 @@ extern "C" int wptv_attention_workspace(int B, int T, int H, int c, int N, int w
   return WPTV_OK;
 }
 
-extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
-                                     const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
-                                     const int64_t* positions, int window, const int64_t* tree_base,
-                                     const uint64_t* tree_ancestors, const float* sink, int B, int T, int H, int c,
-                                     int N, float scale, int splits, int flags, void* out, float* lse,
-                                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+namespace {
+// Every attention entry point: the table is addressed through `rows`
+// (physical rows phys_rows per batch row), the output optionally gated.
+int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n, const void* v, int64_t v_stride_b,
+           int64_t v_stride_n, int dtype, const int64_t* positions, int window, const int64_t* tree_base,
+           const uint64_t* tree_ancestors, const float* sink, int B, int T, int H, int c, int N, float scale,
+           int splits, int flags, RowMap rows, int64_t phys_rows, OutGate gate, void* out, float* lse,
+           void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (!q || !k || !v || !positions || !out)
     return fail(WPTV_E_INVALID, "verify_attention: q, k, v, positions and out must be given");
   if ((tree_base == nullptr) != (tree_ancestors == nullptr))
@@ -1229,7 +1292,8 @@ extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_str
   if (p.kind != kGeneric && !(scale > 0.f && scale < 1e30f)) p.kind = kGeneric, p.splits = 1, p.bytes = 0;  // the MFMA kernels take row maxima on unscaled scores
   if (p.kind != kGeneric) {
     // 32-bit byte offsets within one batch row's table (buffer loads).
-    const bool ok_range = (double)N * (double)(k_stride_n > v_stride_n ? k_stride_n : v_stride_n) * 2.0 < 4.0e9;
+    const bool ok_range =
+        (double)phys_rows * (double)(k_stride_n > v_stride_n ? k_stride_n : v_stride_n) * 2.0 < 4.0e9;
     const bool ok_align = ok_range && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && (k_stride_b % 8 == 0) &&
                           (k_stride_n % 8 == 0) && (v_stride_b % 8 == 0) && (v_stride_n % 8 == 0);
     if (!ok_align) p.kind = kGeneric, p.splits = 1, p.bytes = 0;
@@ -1239,12 +1303,13 @@ extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_str
     if (dtype == WPTV_F32)
       hipLaunchKernelGGL(attention_generic<float>, grid, dim3(64), 0, stream, (const float*)q, (const float*)k,
                          k_stride_b, k_stride_n, (const float*)v, v_stride_b, v_stride_n, nullptr, 0, positions,
-                         window, tree_base, tree_ancestors, sink, T, H, c, N, scale_log2, (float*)out, lse);
+                         window, tree_base, tree_ancestors, sink, T, H, c, N, scale_log2, rows, gate, (float*)out,
+                         lse);
     else
       hipLaunchKernelGGL(attention_generic<unsigned short>, grid, dim3(64), 0, stream, (const unsigned short*)q,
                          (const unsigned short*)k, k_stride_b, k_stride_n, (const unsigned short*)v, v_stride_b,
                          v_stride_n, nullptr, 0, positions, window, tree_base, tree_ancestors, sink, T, H, c, N,
-                         scale_log2, (unsigned short*)out, lse);
+                         scale_log2, rows, gate, (unsigned short*)out, lse);
     return launched("attention_generic");
   }
   if (p.bytes > 0 && (!workspace || workspace_bytes < p.bytes))
@@ -1300,8 +1365,8 @@ extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_str
 #define WPTV_LAUNCH(CC, MM)                                                                                     \
   (tree_base ? launch_mfma<CC, MM, true> : launch_mfma<CC, MM, false>)(                                         \
       grid, stream, qb, kb, k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, positions, window, tree_base,   \
-      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_map, ob, lse, po, \
-      part_lse)
+      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_map, rows, gate, ob, lse, \
+      po, part_lse)
     if (c == 128) {
       switch (p.mbw) {
         case 1: WPTV_LAUNCH(128, 1); break;
@@ -1327,10 +1392,57 @@ extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_str
   const long long items = (long long)B * R * (c / 8);
   dim3 cgrid((unsigned)((items + threads - 1) / threads));
   hipLaunchKernelGGL(combine_splits, cgrid, dim3(threads), 0, stream,
-                     static_cast<const unsigned short*>(part_o), part_lse, sink, B, R, H, c, rows_per_group, p.groups,
-                     p.splits, ob, lse);
+                     static_cast<const unsigned short*>(part_o), part_lse, sink, B, T, H, c, rows_per_group, p.groups,
+                     p.splits, gate, ob, lse);
   return launched("combine_splits");
 }
+}  // namespace
+
+extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
+                                     const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
+                                     const int64_t* positions, int window, const int64_t* tree_base,
+                                     const uint64_t* tree_ancestors, const float* sink, int B, int T, int H, int c,
+                                     int N, float scale, int splits, int flags, void* out, float* lse,
+                                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return attend(q, k, k_stride_b, k_stride_n, v, v_stride_b, v_stride_n, dtype, positions, window, tree_base,
+                tree_ancestors, sink, B, T, H, c, N, scale, splits, flags, RowMap{nullptr, 0xffffffffu}, N,
+                OutGate{nullptr, 0}, out, lse, workspace, workspace_bytes, stream);
+}
+
+extern "C" int wptv_window_attention_workspace(int B, int T, int H, int c, int window, int dtype, int* splits,
+                                               size_t* bytes) {
+  if (!splits || !bytes) return fail(WPTV_E_INVALID, "window_attention_workspace: null output pointer");
+  if (window <= 0) return fail(WPTV_E_INVALID, "window_attention_workspace: window %d must be > 0", window);
+  Plan p;
+  const int st = plan(B, T, H, c, window + T - 1, window, dtype, 0, *splits, &p);
+  if (st != WPTV_OK) return st;
+  *splits = p.splits;
+  *bytes = p.bytes;
+  return WPTV_OK;
+}
+
+extern "C" int wptv_window_attention(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
+                                     const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
+                                     const int64_t* positions, const int64_t* row_base, int ring_rows, int window,
+                                     const float* sink, const void* gate, int64_t gate_stride, int B, int T, int H,
+                                     int c, float scale, int splits, void* out, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream) {
+  if (window <= 0) return fail(WPTV_E_INVALID, "window_attention: window %d must be > 0", window);
+  if (ring_rows <= 0) return fail(WPTV_E_INVALID, "window_attention: ring_rows %d must be > 0", ring_rows);
+  if (row_base == nullptr && (ring_rows & (ring_rows - 1)) != 0)
+    return fail(WPTV_E_INVALID, "window_attention: a ring of %d rows is not a power of 2", ring_rows);
+  if (row_base == nullptr && ring_rows < window + T - 1)
+    return fail(WPTV_E_INVALID, "window_attention: a ring of %d rows holds less than window + T - 1 = %d", ring_rows,
+                window + T - 1);
+  if (gate && gate_stride < (int64_t)H * c)
+    return fail(WPTV_E_INVALID, "window_attention: gate row stride %lld below H*c", (long long)gate_stride);
+  // Logical rows: token positions; the upper bound only keeps hi = p.
+  const RowMap rows{row_base, row_base ? 0xffffffffu : (uint32_t)(ring_rows - 1)};
+  return attend(q, k, k_stride_b, k_stride_n, v, v_stride_b, v_stride_n, dtype, positions, window, nullptr, nullptr,
+                sink, B, T, H, c, INT_MAX / 2, scale, splits, WPTV_ATTN_RANGE_FROM_POSITIONS, rows, ring_rows,
+                OutGate{gate, gate_stride}, out, nullptr, workspace, workspace_bytes, stream);
+}
+
 
 extern "C" int wptv_sparse_attention(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
                                      const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
@@ -1351,12 +1463,13 @@ extern "C" int wptv_sparse_attention(const void* q, const void* k, int64_t k_str
   if (dtype == WPTV_F32)
     hipLaunchKernelGGL(attention_generic<float>, grid, dim3(64), 0, stream, (const float*)q, (const float*)k, k_stride_b,
                        k_stride_n, (const float*)v, v_stride_b, v_stride_n, rows, K, positions, window, nullptr,
-                       nullptr, sink, T, H, c, N, scale_log2, (float*)out, lse);
+                       nullptr, sink, T, H, c, N, scale_log2, RowMap{nullptr, 0xffffffffu}, OutGate{nullptr, 0},
+                       (float*)out, lse);
   else if (dtype == WPTV_BF16)
     hipLaunchKernelGGL(attention_generic<unsigned short>, grid, dim3(64), 0, stream, (const unsigned short*)q,
                        (const unsigned short*)k, k_stride_b, k_stride_n, (const unsigned short*)v, v_stride_b,
                        v_stride_n, rows, K, positions, window, nullptr, nullptr, sink, T, H, c, N, scale_log2,
-                       (unsigned short*)out, lse);
+                       RowMap{nullptr, 0xffffffffu}, OutGate{nullptr, 0}, (unsigned short*)out, lse);
   else
     return fail(WPTV_E_UNSUPPORTED, "sparse_attention: dtype %d is neither fp32 nor bf16", dtype);
   return launched("attention_generic");

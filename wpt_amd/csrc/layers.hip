@@ -48,14 +48,6 @@ struct Vec8<float> {
   }
 };
 
-// x rounded to T and back (the value a T tensor holds).
-template <typename T>
-__device__ __forceinline__ float rounded(float x);
-template <>
-__device__ __forceinline__ float rounded<float>(float x) { return x; }
-template <>
-__device__ __forceinline__ float rounded<unsigned short>(float x) { return bf16_to_f32(f32_to_bf16(x)); }
-
 // Values of one row held by a lane: D / 8 / 64 chunks of 8, at most kChunks.
 constexpr int kChunks = 8;  // rows up to 64 * 8 * 8 = 4096 wide
 
@@ -191,6 +183,20 @@ struct Lane<unsigned short, 1> {
 // S > 0: the projection comes as S FP32 split-K parts [S][rows][(H + 2) c]
 // (qkv_parts), summed in a fixed order and rounded to T, as the reference's
 // bf16 product is.
+//
+// A window layer (Rope, attention.py:113-135) also turns the last rope.dims
+// dimensions of every query head and of the key by the token's position
+// start[b] + t (rotate, attention.py:59-71: adjacent pairs (2i, 2i + 1) by
+// the angle p / div[i], div[i] = base^(2i / dims), from the normed values in
+// T, in FP32) and writes the entry at ring slot (start[b] + t) & ring_mask.
+// The divisors come from the host, computed as the reference computes them,
+// so that both divide the same numbers.
+struct Rope {
+  int dims;            // 0: no rotation (an exact layer)
+  const float* div;    // [dims / 2]
+  uint32_t ring_mask;  // 0: the entry at row start[b] + t (no ring)
+};
+
 template <typename T, int EPL, int S>
 __global__ __launch_bounds__(256) void qkv_post(const T* __restrict__ qkv, int64_t qkv_row,
                                                 const float* __restrict__ qkv_parts,
@@ -198,7 +204,7 @@ __global__ __launch_bounds__(256) void qkv_post(const T* __restrict__ qkv, int64
                                                 T* __restrict__ q_out, T* __restrict__ table, int64_t tsb,
                                                 int64_t tsn, int64_t capacity, const int64_t* __restrict__ start,
                                                 const int64_t* __restrict__ counts, int rows, int T_, int H,
-                                                float eps) {
+                                                float eps, Rope rope) {
   constexpr int C = 64 * EPL;
   const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -228,13 +234,14 @@ __global__ __launch_bounds__(256) void qkv_post(const T* __restrict__ qkv, int64
   const float* w = (head < H ? q_norm : k_norm) + EPL * lane;  // the value (head H + 1) reads k_norm unused
 #pragma unroll
   for (int e = 0; e < EPL; ++e) wt[e] = w[e];
+  const int64_t pos = start[b] + t;
   T* dst;
   if (head < H) {
     dst = q_out + ((int64_t)row * H + head) * C;
   } else {
-    const int64_t dst_row = start[b] + t;
-    if (!(t < counts[b] && dst_row >= 0 && dst_row < capacity)) return;
-    dst = table + b * tsb + dst_row * tsn + (head == H ? 0 : C);  // [k_norm(k), v]
+    const int64_t slot = rope.ring_mask ? (pos & (int64_t)rope.ring_mask) : pos;
+    if (!(t < counts[b] && pos >= 0 && slot < capacity)) return;
+    dst = table + b * tsb + slot * tsn + (head == H ? 0 : C);  // [k_norm(k), v]
   }
   if (head <= H) {
     float ss = 0.f;
@@ -244,6 +251,30 @@ __global__ __launch_bounds__(256) void qkv_post(const T* __restrict__ qkv, int64
     const float inv = rsqrtf(ss / (float)C + eps);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) v[e] = v[e] * inv * wt[e];
+    if (rope.dims > 0) {
+      // element d = EPL lane + e; rotated when d >= C - dims, pair i = (d - first) / 2
+      const int first = C - rope.dims;
+      float mine[EPL], other[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) mine[e] = rounded<T>(v[e]);
+      if constexpr (EPL == 1) {
+        other[0] = __shfl_xor(mine[0], 1, 64);  // the pair's other element sits on the next lane
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) other[e] = mine[e ^ 1];
+      }
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const int d = EPL * lane + e;
+        if (d < first) continue;
+        const int i = (d - first) >> 1;
+        const float angle = (float)pos / rope.div[i];
+        float sn, cs;
+        sincosf(angle, &sn, &cs);
+        // (even, odd) -> (even cos - odd sin, even sin + odd cos)
+        v[e] = (d & 1) == 0 ? mine[e] * cs - other[e] * sn : other[e] * sn + mine[e] * cs;
+      }
+    }
   }
   Lane<T, EPL>::store(dst + EPL * lane, v);
 }
@@ -370,7 +401,8 @@ extern "C" int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const floa
 #define WPTV_QKV(TT, EE)                                                                                          \
   hipLaunchKernelGGL((qkv_post<TT, EE, 0>), grid, dim3(256), 0, stream, static_cast<const TT*>(qkv),             \
                      qkv_row_stride, nullptr, q_norm, k_norm, static_cast<TT*>(q_out), static_cast<TT*>(table),  \
-                     table_stride_b, table_stride_n, capacity, start, counts, rows, T, H, eps)
+                     table_stride_b, table_stride_n, capacity, start, counts, rows, T, H, eps, rope)
+  const Rope rope{0, nullptr, 0u};
   if (dtype == WPTV_BF16) {
     if (epl == 1) WPTV_QKV(unsigned short, 1);
     else if (epl == 2) WPTV_QKV(unsigned short, 2);
@@ -384,6 +416,51 @@ extern "C" int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const floa
   }
 #undef WPTV_QKV
   return launched("qkv_post");
+}
+
+extern "C" int wptv_window_qkv_post(const void* qkv, int64_t qkv_row_stride, const float* q_norm, const float* k_norm,
+                                    void* q_out, void* ring, int64_t ring_stride_b, int64_t ring_stride_n,
+                                    int ring_rows, const int64_t* start, const int64_t* counts, int B, int T, int H,
+                                    int c, int rope_dims, const float* rope_div, int dtype, float eps,
+                                    hipStream_t stream) {
+  if (!qkv || !q_norm || !k_norm || !q_out || !ring || !start || !counts || (rope_dims > 0 && !rope_div))
+    return fail(WPTV_E_INVALID, "window_qkv_post: every pointer must be given");
+  if (B < 0 || T < 0 || H <= 0 || c <= 0)
+    return fail(WPTV_E_INVALID, "window_qkv_post: bad shape B=%d T=%d H=%d c=%d", B, T, H, c);
+  if (c != 64 && c != 128 && c != 256)
+    return fail(WPTV_E_UNSUPPORTED, "window_qkv_post: head width %d is not 64, 128 or 256", c);
+  if (ring_rows <= 0 || (ring_rows & (ring_rows - 1)) != 0)
+    return fail(WPTV_E_INVALID, "window_qkv_post: ring of %d rows is not a power of 2", ring_rows);
+  if (rope_dims < 0 || rope_dims > c || rope_dims % 2 != 0)
+    return fail(WPTV_E_INVALID, "window_qkv_post: rope dims %d must be even and at most %d", rope_dims, c);
+  if (qkv_row_stride < (int64_t)(H + 2) * c || ring_stride_n < 2 * c)
+    return fail(WPTV_E_INVALID, "window_qkv_post: a row stride below its width");
+  const int epl = c / 64;
+  const int esize = dtype == WPTV_F32 ? 4 : 2;
+  if (qkv_row_stride % epl || ring_stride_b % epl || ring_stride_n % epl || !aligned(qkv, epl * esize) ||
+      !aligned(ring, epl * esize) || !aligned(q_out, epl * esize))
+    return fail(WPTV_E_INVALID, "window_qkv_post: rows must be aligned to %d elements", epl);
+  if (B == 0 || T == 0) return WPTV_OK;
+  const int rows = B * T;
+  const Rope rope{rope_dims, rope_div, (uint32_t)(ring_rows - 1)};
+  dim3 grid((unsigned)(((int64_t)rows * (H + 2) + 3) / 4));
+#define WPTV_WQKV(TT, EE)                                                                                         \
+  hipLaunchKernelGGL((qkv_post<TT, EE, 0>), grid, dim3(256), 0, stream, static_cast<const TT*>(qkv),             \
+                     qkv_row_stride, nullptr, q_norm, k_norm, static_cast<TT*>(q_out), static_cast<TT*>(ring),   \
+                     ring_stride_b, ring_stride_n, (int64_t)ring_rows, start, counts, rows, T, H, eps, rope)
+  if (dtype == WPTV_BF16) {
+    if (epl == 1) WPTV_WQKV(unsigned short, 1);
+    else if (epl == 2) WPTV_WQKV(unsigned short, 2);
+    else WPTV_WQKV(unsigned short, 4);
+  } else if (dtype == WPTV_F32) {
+    if (epl == 1) WPTV_WQKV(float, 1);
+    else if (epl == 2) WPTV_WQKV(float, 2);
+    else WPTV_WQKV(float, 4);
+  } else {
+    return fail(WPTV_E_UNSUPPORTED, "window_qkv_post: dtype %d is neither fp32 nor bf16", dtype);
+  }
+#undef WPTV_WQKV
+  return launched("window_qkv_post");
 }
 
 extern "C" int wptv_qkv_post_parts(const float* parts, int splits, const float* q_norm, const float* k_norm,
@@ -409,7 +486,7 @@ extern "C" int wptv_qkv_post_parts(const float* parts, int splits, const float* 
 #define WPTV_QKVP(TT, EE, SS)                                                                                     \
   hipLaunchKernelGGL((qkv_post<TT, EE, SS>), grid, dim3(256), 0, stream, nullptr, 0, parts, q_norm, k_norm,       \
                      static_cast<TT*>(q_out), static_cast<TT*>(table), table_stride_b, table_stride_n, capacity, \
-                     start, counts, rows, T, H, eps)
+                     start, counts, rows, T, H, eps, Rope{0, nullptr, 0u})
 #define WPTV_QKVP_S(TT, EE)               \
   switch (splits) {                       \
     case 1: WPTV_QKVP(TT, EE, 1); break;  \

@@ -61,6 +61,14 @@ __device__ __forceinline__ float from_f32<float>(float f) { return f; }
 template <>
 __device__ __forceinline__ unsigned short from_f32<unsigned short>(float f) { return f32_to_bf16(f); }
 
+// f rounded to the element type T and read back.
+template <typename T>
+__device__ __forceinline__ float rounded(float f);
+template <>
+__device__ __forceinline__ float rounded<float>(float f) { return f; }
+template <>
+__device__ __forceinline__ float rounded<unsigned short>(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
 // An order-preserving unsigned key of a float (larger float, larger key;
 // -0 below +0), and its inverse: radix selection runs on these keys.
 __device__ __forceinline__ uint32_t order_key(float f) {

@@ -8,7 +8,10 @@ new tokens appended to the cache, exact attention of every query over the
 rows up to its position, the output projection) in a pre-norm residual
 block, then a SwiGLU feed-forward block; a final norm and the head give
 FP32 scores (model.py:471).  One key/value head is shared by every query
-head (MQA).  RMSNorm's eps is the reference's (layers.py:9).
+head (MQA).  RMSNorm's eps is the reference's (layers.py:9).  A layer may
+instead be the reference's window layer (WindowAttention, attention.py:
+109-151): rotary encoding of the normed queries and key, a window of the last
+`window` tokens with a sink per head, and the output gated by sigmoid(gate(x)).
 
 On the GPU:
     KV append       wptv_qkv_post: q/k norms, and the new entries written at
@@ -21,6 +24,9 @@ On the GPU:
                     SPLIT_K_ROWS bf16 rows (summed by qkv_post and the
                     residual add + norm), hipBLASLt otherwise and for the
                     gate/up product and the lm_head
+    window layers   wptv_window_qkv_post (norms, rotary encoding, the ring
+                    append), wptv_window_attention over the cache's ring with
+                    the sink and the output gate fused
     sampling        wpt_amd.sampling (wptv_accept), called by the Writer
 The decoder keeps no state between calls but the cache; a step of fixed
 shape can be captured in a HIP graph (wpt_amd.step).
@@ -49,10 +55,22 @@ class DecoderConfig:
     head_dim: int
     ffn: int
     vocab: int
+    kinds: tuple = ()          # "exact" or "window" per layer; () = every layer exact
+    window: int = 128          # WINDOW, attention.py:51
+    rope_dims: int = 64        # ROPE_DIMS, attention.py:53
+    rope_base: float = 10000.0
 
     @property
     def qkv_width(self):
         return self.heads * self.head_dim + 2 * self.head_dim
+
+    def kind(self, i):
+        return self.kinds[i] if self.kinds else "exact"
+
+    @property
+    def windows(self):
+        """The window layers' indices."""
+        return tuple(i for i in range(self.layers) if self.kind(i) == "window")
 
 
 # The decoders of the verify-step workloads.
@@ -82,6 +100,10 @@ def random_weights(config, seed=0, std=0.02, dtype=torch.float32, device="cpu"):
         weights[f"layers.{i}.ffn_norm"] = ones(D)
         weights[f"layers.{i}.gate_up"] = normal(2 * Fw, D)
         weights[f"layers.{i}.down"] = normal(D, Fw)
+        if config.kind(i) == "window":
+            weights[f"layers.{i}.gate"] = normal(H * c, D)
+            # the reference starts its sinks at 0; drawn here so that they matter
+            weights[f"layers.{i}.sink"] = torch.randn(H, generator=generator, device=device)
     weights["final_norm"] = ones(D)
     weights["head"] = normal(V, D)
     return weights
@@ -98,25 +120,69 @@ class MQADecoder:
             raise kernels.KernelUnavailable(f"the decoder's verify step runs on a GPU, not {self.device}")
         self.w = {}
         for name, value in weights.items():
-            keep_fp32 = name.endswith("norm")
+            keep_fp32 = name.endswith("norm") or name.endswith("sink")
             self.w[name] = value.to(device=self.device, dtype=torch.float32 if keep_fp32 else dtype).contiguous()
+        for i in config.windows:  # one projection for q, k, v and the gate
+            self.w[f"layers.{i}.qkvg"] = torch.cat([self.w[f"layers.{i}.qkv"], self.w[f"layers.{i}.gate"]]).contiguous()
 
     def parameters(self):
         return iter(self.w.values())
 
-    def new_cache(self, rows, routes=False, capacity=256):
-        """An empty cache of `rows` rows (the reference's WPT.new_cache)."""
+    def new_cache(self, rows, routes=False, capacity=256, widest=129):
+        """An empty cache of `rows` rows (the reference's WPT.new_cache); its
+        window layers' rings hold readings of up to `widest` tokens (wider
+        ones are read in pieces)."""
         if routes:
             raise NotImplementedError("this decoder has no routed experts to record")
         c = self.config.head_dim
-        return Cache(rows, self.config.layers, 2 * c, self.dtype, self.device, capacity)
+        ring = 1 << max(0, (self.config.window - 1 + widest - 1).bit_length())
+        return Cache(rows, self.config.layers, 2 * c, self.dtype, self.device, capacity, self.config.windows, ring)
+
+    def widest(self, cache):
+        """The most tokens one reading of the cache takes (its rings' size)."""
+        ring = cache.ring_rows
+        return None if ring is None else ring - self.config.window + 1
 
     def _layer(self, i, h, x, cache, positions, counts, next_norm):
         """One layer on the residual stream h (B, T, D), x = RMSNorm(h) with the
         layer's attention norm; leaves h updated and x = RMSNorm(h) with
         next_norm (the next layer's attention norm, or the final norm)."""
         w = self.w
-        cfg = self.config
+        B, T, _ = h.shape
+        if self.config.kind(i) == "window":
+            self._window_attention(i, h, x, cache, positions, counts)
+        else:
+            self._exact_attention(i, h, x, cache, positions, counts)
+        act = layers.swiglu(F.linear(x, w[f"layers.{i}.gate_up"]))
+        down = w[f"layers.{i}.down"]
+        if x.dtype == torch.bfloat16 and B * T <= SPLIT_K_ROWS:
+            layers.add_rms_norm_parts(h, layers.linear_parts(act, down), next_norm, x)
+        else:
+            layers.add_rms_norm(h, F.linear(act, down), next_norm, x)
+
+    def _window_attention(self, i, h, x, cache, positions, counts):
+        """A window layer's attention block: h += out(o * sigmoid(gate(x))),
+        x = RMSNorm(h) with the feed-forward norm."""
+        w, cfg = self.w, self.config
+        B, T, _ = h.shape
+        H, c = cfg.heads, cfg.head_dim
+        ring = cache.tables[i]
+        proj = F.linear(x, w[f"layers.{i}.qkvg"])  # (B, T, (2H + 2) c): q, k, v, gate
+        q = layers.window_qkv_post(proj, w[f"layers.{i}.q_norm"], w[f"layers.{i}.k_norm"], ring, cache.lengths,
+                                   counts, H, cfg.rope_dims, cfg.rope_base)
+        o = kernels.ring_attention(q, ring, positions, c ** -0.5, cfg.window, w[f"layers.{i}.sink"],
+                                   gate=proj[..., (H + 2) * c:])
+        out = w[f"layers.{i}.out"]
+        if x.dtype == torch.bfloat16 and B * T <= SPLIT_K_ROWS:
+            layers.add_rms_norm_parts(h, layers.linear_parts(o.reshape(B, T, H * c), out), w[f"layers.{i}.ffn_norm"],
+                                      x)
+        else:
+            layers.add_rms_norm(h, F.linear(o.reshape(B, T, H * c), out), w[f"layers.{i}.ffn_norm"], x)
+
+    def _exact_attention(self, i, h, x, cache, positions, counts):
+        """An exact layer's attention block: h += out(o), x = RMSNorm(h) with
+        the feed-forward norm."""
+        w, cfg = self.w, self.config
         B, T, _ = h.shape
         H, c = cfg.heads, cfg.head_dim
         table = cache.tables[i]
@@ -137,12 +203,6 @@ class MQADecoder:
                                       w[f"layers.{i}.ffn_norm"], x)
         else:
             layers.add_rms_norm(h, F.linear(o.reshape(B, T, H * c), w[f"layers.{i}.out"]), w[f"layers.{i}.ffn_norm"], x)
-        act = layers.swiglu(F.linear(x, w[f"layers.{i}.gate_up"]))
-        down = w[f"layers.{i}.down"]
-        if few:
-            layers.add_rms_norm_parts(h, layers.linear_parts(act, down), next_norm, x)
-        else:
-            layers.add_rms_norm(h, F.linear(act, down), next_norm, x)
 
     @torch.no_grad()
     def extend(self, ids, cache, counts=None, undoable=False, features=()):
@@ -160,6 +220,16 @@ class MQADecoder:
             counts_ = torch.full((B,), T, dtype=torch.long, device=self.device)
         else:
             counts_ = torch.as_tensor(counts, dtype=torch.long).to(self.device)
+        widest = self.widest(cache)
+        if widest is not None and T > widest:
+            if undoable:
+                raise ValueError(f"an undoable reading of {T} tokens is wider than the cache's rings take ({widest})")
+            # in pieces that the window layers' rings hold; every layer is causal
+            pieces = []
+            for start in range(0, T, widest):
+                part = self.extend(ids[:, start:start + widest], cache, (counts_ - start).clamp(0, widest))
+                pieces.append(part)
+            return torch.cat([p[0] for p in pieces], 1), torch.cat([p[1] for p in pieces], 1)
         cache.reserve(cache.bound + T)
         positions = cache.lengths[:, None] + torch.arange(T, device=self.device)
         h = F.embedding(ids, self.w["embedding"])

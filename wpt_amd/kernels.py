@@ -27,7 +27,7 @@ from ._lib import KernelUnavailable, check, ptr
 NAME = "HIP (gfx950)"
 
 __all__ = ["NAME", "KernelUnavailable", "chosen_columns", "exact_attention", "choose_rows", "sparse_attention",
-           "verify_attention", "tree_attention", "tree_ancestors", "kv_append"]
+           "verify_attention", "window_attention", "ring_attention", "tree_attention", "tree_ancestors", "kv_append"]
 
 
 def chosen_columns(top_k, window, N):
@@ -197,6 +197,65 @@ def sparse_attention(q, k, v, sink, idx, positions, scale, window):
                                         H, c, N, float(scale), ptr(out), None, _lib.stream(device)),
           "sparse_attention")
     return _forward_only(out, q, k, v, sink)
+
+
+def _window_call(q, k, v, sink, positions, scale, window, row_base, ring_rows, gate):
+    B, T, H, c = q.shape
+    device = q.device
+    if not (q.dtype == k.dtype == v.dtype) or k.dim() != 3 or k.shape != v.shape or k.shape[0] != B or \
+            k.shape[2] != c:
+        raise ValueError(f"k and v must be (B={B}, rows, c={c}) in q's dtype; got {tuple(k.shape)}, {tuple(v.shape)}")
+    if q.device.type != "cuda" or k.device != device or v.device != device:
+        raise KernelUnavailable(f"the HIP window attention runs on a GPU; q is on {q.device}")
+    if k.stride(2) != 1 or v.stride(2) != 1:
+        raise ValueError("each row of k and v must be contiguous")
+    if sink.shape != (H,):
+        raise ValueError(f"sink must be (H={H},); got {tuple(sink.shape)}")
+    positions_ = _long(positions.expand(B, T), device)
+    sink_ = sink.to(device=device, dtype=torch.float32).contiguous()
+    gate_stride = 0
+    if gate is not None:
+        if gate.dtype != q.dtype or gate.shape[:2] != (B, T) or gate.stride(-1) != 1 or \
+                gate.stride(0) != T * gate.stride(1) or gate.shape[-1] < H * c:
+            raise ValueError(f"gate must be (B={B}, T={T}, >= H*c) in q's dtype, rows one after another")
+        gate_stride = gate.stride(1)
+    library = _lib.lib()
+    dtype = _lib.dtype_code(q.dtype)
+    parts = _lib.ctypes.c_int(0)
+    size = _lib.ctypes.c_size_t(0)
+    check(library.wptv_window_attention_workspace(B, T, H, c, int(window), dtype, _lib.ctypes.byref(parts),
+                                                  _lib.ctypes.byref(size)), "window_attention")
+    workspace = torch.empty(size.value, dtype=torch.uint8, device=device) if size.value else None
+    q_ = q.contiguous()
+    out = torch.empty_like(q_)
+    check(library.wptv_window_attention(ptr(q_), ptr(k), k.stride(0), k.stride(1), ptr(v), v.stride(0), v.stride(1),
+                                        dtype, ptr(positions_), ptr(row_base), int(ring_rows), int(window), ptr(sink_),
+                                        ptr(gate), gate_stride, B, T, H, c, float(scale), parts.value, ptr(out),
+                                        ptr(workspace), size.value, _lib.stream(device)), "window_attention")
+    return _forward_only(out, q, k, v, sink)
+
+
+def window_attention(q, k, v, sink, positions, scale, window=128, gate=None):
+    """The reference's window_attention (attention.py:85-107): q (B, T, H, c)
+    at positions (T,) or (B, T), consecutive within a row; k, v
+    (B, window - 1 + T, c), the window - 1 tokens before the pass's first,
+    then its own.  Each query reads the last `window` rows, itself included,
+    none before the text, the sink (H,) in each head's denominator.  gate
+    (B, T, >= H*c): the output times sigmoid(gate) (attention.py:128-130)."""
+    B, T = q.shape[:2]
+    if k.dim() != 3 or k.shape[1] != window - 1 + T:
+        raise ValueError(f"k must hold window - 1 + T = {window - 1 + T} rows; got {tuple(k.shape)}")
+    positions = positions.to(q.device).expand(B, T)
+    row_base = _long(positions[:, 0] - (window - 1), q.device)
+    return _window_call(q, k, v, sink, positions, scale, window, row_base, k.shape[1], gate)
+
+
+def ring_attention(q, ring, positions, scale, window, sink, gate=None):
+    """A window layer's attention over its cache ring (B, R, 2c), R a power
+    of 2 of at least window - 1 + T, token n at row n mod R (keys then
+    values): window_attention's result from the build's ring cache."""
+    c = q.shape[-1]
+    return _window_call(q, ring[..., :c], ring[..., c:], sink, positions, scale, window, None, ring.shape[1], gate)
 
 
 def tree_ancestors(parents):

@@ -1,6 +1,6 @@
 """Python entry points of libwptv's decoder-layer kernels (include/wptv.h):
-the residual add + RMSNorm, the exact layer's q/k norms + KV append, and
-SwiGLU, each one pass over its rows on the GPU (the reference runs them as
+the residual add + RMSNorm, the exact layer's q/k norms + KV append, the
+window layer's q/k norms + rotary encoding + ring append, and SwiGLU, each one pass over its rows on the GPU (the reference runs them as
 separate torch operations: model.py:394-436, attention.py:157-188,
 layers.py:45-61)."""
 
@@ -76,6 +76,43 @@ def qkv_post_parts(parts, q_norm, k_norm, table, start, counts, heads, T, eps=EP
                                          table.stride(0), table.stride(1), table.shape[1], ptr(start), ptr(counts), B,
                                          T, heads, c, _lib.dtype_code(table.dtype), float(eps),
                                          _lib.stream(table.device)), "qkv_post_parts")
+    return q
+
+
+def rope_divisors(dims=64, base=10000.0, device="cpu"):
+    """The rotary encoding's divisors base^(2i / dims), i < dims / 2, computed
+    in FP32 on the CPU as the reference's rotate computes them
+    (attention.py:63-64), so that the kernel divides the same numbers."""
+    pairs = torch.arange(dims // 2, dtype=torch.float32)
+    return (base ** (2 * pairs / dims)).to(device)
+
+
+_DIVISORS = {}  # (dims, base, device) -> rope_divisors
+
+
+def window_qkv_post(proj, q_norm, k_norm, ring, start, counts, heads, rope_dims=64, rope_base=10000.0, eps=EPS):
+    """A window layer after its projection: proj (B, T, >= (H + 2) c) holds
+    q, k, v first (the gate may follow in the same rows) -> q (B, T, H, c) =
+    rotate(q_norm(q)) at positions start[b] + t; the entries
+    [rotate(k_norm(k)), v] of row b's first counts[b] tokens written into the
+    ring (B, R, 2c) (R a power of 2) at row (start[b] + t) mod R
+    (attention.py:113-135, rotate :59-71)."""
+    _gpu(proj, ring)
+    key = (int(rope_dims), float(rope_base), proj.device)
+    div = _DIVISORS.get(key)
+    if div is None:  # made once per setting and device, outside any graph capture
+        div = _DIVISORS[key] = rope_divisors(rope_dims, rope_base, proj.device)
+    B, T, width = proj.shape
+    c = ring.shape[-1] // 2
+    if width < (heads + 2) * c or proj.stride(-1) != 1 or proj.stride(0) != T * proj.stride(1):
+        raise ValueError(f"proj must be (B, T, >= (H + 2) c) with rows one after another; got {tuple(proj.shape)}")
+    if ring.dtype != proj.dtype or ring.stride(-1) != 1 or ring.shape[0] != B:
+        raise ValueError("the ring must be (B, R, 2c) in proj's dtype, rows contiguous")
+    q = torch.empty(B, T, heads, c, dtype=proj.dtype, device=proj.device)
+    check(_lib.lib().wptv_window_qkv_post(ptr(proj), proj.stride(1), ptr(q_norm), ptr(k_norm), ptr(q), ptr(ring),
+                                          ring.stride(0), ring.stride(1), ring.shape[1], ptr(start), ptr(counts), B,
+                                          T, heads, c, int(rope_dims), ptr(div), _lib.dtype_code(proj.dtype),
+                                          float(eps), _lib.stream(proj.device)), "window_qkv_post")
     return q
 
 
