@@ -125,14 +125,24 @@ int wptv_window_attention(const void* q, const void* k, int64_t k_stride_b, int6
 
 /* Sparse attention over chosen rows plus the last `window` rows, with a sink:
  * the reference's sparse_attention with chosen rows
- * (pytorch_kernels.py:171-187,213-217).  idx [B, T, K] int64, -1 = none;
- * a row named both in idx and in the window is counted twice, as the
- * reference's concatenation of the two lists counts it. */
+ * (pytorch_kernels.py:171-187,213-217) and the sparse layer's output gate
+ * (attention.py:128-130,190-): idx [B, T, K] int64, -1 = none; a row named
+ * both in idx and in the window is counted twice, as the reference's
+ * concatenation of the two lists counts it.  gate NULL or [B*T, >= H*c] in
+ * dtype (row stride gate_stride): the output times sigmoid(gate).  bf16 with
+ * head width 64 or 128 and H <= 16 runs the MFMA gather kernel (the query's
+ * rows cut into `splits` parts, merged by a second kernel through the
+ * workspace, wptv_sparse_attention_workspace() bytes for the same arguments);
+ * anything else the wave-per-query kernel (no workspace). */
+int wptv_sparse_attention_workspace(int B, int T, int H, int c, int K, int window, int N, int dtype, int* splits,
+                                    size_t* bytes);
+
 int wptv_sparse_attention(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
                           const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
                           const int64_t* idx, int K, const int64_t* positions, int window,
-                          const float* sink, int B, int T, int H, int c, int N, float scale,
-                          void* out, float* lse, hipStream_t stream);
+                          const float* sink, const void* gate, int64_t gate_stride, int B, int T, int H, int c,
+                          int N, float scale, int splits, void* out, float* lse, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Exact attention's choice of rows: the top_k rows each query weighs most

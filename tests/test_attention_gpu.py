@@ -164,6 +164,36 @@ def test_chosen_rows_with_a_window_and_sink_match_the_oracle(device):
     assert relative_error(got.cpu(), expected) < 1e-2
 
 
+@pytest.mark.parametrize("B, T, H, c, N, W, K, splits", [
+    (32, 5, 16, 128, 4096, 128, 1024, 0),   # a WPT sparse layer at the verify step (TOP_K 1024, WINDOW 128)
+    (2, 6, 12, 128, 300, 32, 16, 1),        # 12 heads, one part: no combine
+    (3, 5, 16, 64, 500, 40, 100, 3),        # head width 64, three parts
+    (2, 4, 16, 128, 200, 16, 300, 0),       # more chosen entries than rows: many -1
+])
+@pytest.mark.parametrize("gated", [False, True], ids=["plain", "gated"])
+def test_the_sparse_gather_kernel_matches_the_oracle(device, B, T, H, c, N, W, K, splits, gated):
+    # chosen rows outside each query's window, some -1, some named twice and
+    # some also in the window (each counts twice, as the reference's
+    # concatenation counts it); the last row's queries past the table
+    q = draw(B, T, H, c, seed=40)
+    _, k, v = entries_table(B, N, c, seed=41)
+    sink = draw(H, seed=42, dtype=torch.float32)
+    positions = (N - T + torch.arange(T)).expand(B, T).clone()
+    positions[-1] += 2
+    generator = torch.Generator().manual_seed(43)
+    idx = torch.randint(-1, N, (B, T, K), generator=generator)
+    idx[:, :, :2] = positions[..., None].clamp(max=N - 1) - torch.tensor([0, 1])  # also in the window
+    idx[:, :, 2] = idx[:, :, 3]                                                   # named twice
+    gate = draw(B, T, H * c, seed=44) if gated else None
+    expected = oracle.sparse_attention(q, k, v, sink, idx, positions, c ** -0.5, W)
+    if gated:
+        expected = expected * torch.sigmoid(gate.float()).reshape(B, T, H, c)
+    qd, kd, vd, sd, id_, pd = on(device, q, k, v, sink, idx, positions)
+    got = kernels.sparse_attention(qd, kd, vd, sd, id_, pd, c ** -0.5, W, splits=splits,
+                                   gate=None if gate is None else gate.to(device))
+    assert relative_error(got.cpu(), expected) < 1e-2
+
+
 def test_tree_attention_matches_the_oracle(device):
     # the tree workload's shape at a smaller prefix: a binary draft tree of 31
     # nodes (depth 5) after the prefix, ancestor-only mask

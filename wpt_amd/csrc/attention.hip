@@ -562,6 +562,228 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
 }
 
 // ---------------------------------------------------------------------------
+// Sparse MFMA kernel: chosen rows plus the window (at most 16 heads)
+// ---------------------------------------------------------------------------
+//
+// One workgroup of four wavefronts per (query, split).  The query's rows --
+// its chosen rows idx[b, t, :], then its window max(0, p - window + 1) ..
+// min(p, N - 1), the reference's concatenation (pytorch_kernels.py:213-217)
+// -- are a list; the split takes a contiguous part of it, copies the row
+// numbers into LDS and cuts it into 32-row tiles, and wavefront w gathers the
+// tiles w, w + 4, ... into its own two-tile LDS ring (each lane of an LDS DMA
+// fetches the row its list entry names: the gather costs nothing beyond the
+// DMA) and multiplies them with the H <= 16 heads of the query as one MFMA
+// block (S^T = K . Q^T, O^T += V^T . P^T, as the row-block kernel, with its
+// swizzled tile layout).  A missing row (-1, or past the table) is fetched as
+// a valid one and masked.  The four wavefronts merge through LDS; the splits
+// merge in combine_splits.
+
+constexpr int kSparseWaves = 4;
+constexpr int kSparseSlots = 2;     // tiles in each wavefront's ring
+constexpr int kSparseList = 4096;   // list entries a split holds
+
+template <int C>
+__global__ __launch_bounds__(kSparseWaves * 64, 1) void sparse_attention_mfma(
+    const unsigned short* __restrict__ q, const unsigned short* __restrict__ k, int64_t ksb, int64_t ksn,
+    const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn, const int64_t* __restrict__ idx, int K,
+    const int64_t* __restrict__ positions, int window, const float* __restrict__ sink, int T, int H, int N,
+    float scale_log2, int splits, int per_split, OutGate gate, unsigned short* __restrict__ out,
+    float* __restrict__ lse_out, unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
+  using G = Tile<C>;
+  constexpr int kWaveRing = kSparseSlots * G::kElems;  // elements of one wavefront's ring
+  constexpr int kPitch = C + 4;                        // merge buffer row pitch (floats)
+  static_assert(16 * kPitch + 32 <= kWaveRing / 2, "a wavefront's merge buffer fits in its ring");
+  __shared__ __attribute__((aligned(16))) unsigned short ring_all[kSparseWaves * kWaveRing];
+  __shared__ __attribute__((aligned(16))) int rows_lds[kSparseList];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int unit = blockIdx.x / splits, split = blockIdx.x % splits;  // unit = b T + t
+  const int b = unit / T;
+  const int64_t p = positions[unit];
+  const int64_t lo64 = p - window + 1;
+  const int lo = lo64 > 0 ? (int)lo64 : 0;
+  const int hi = p < (int64_t)N - 1 ? (int)p : N - 1;
+  const int nwin = hi >= lo ? hi - lo + 1 : 0;
+  const int e0 = split * per_split;
+  const int cnt = max(0, min(K + nwin, e0 + per_split) - e0);
+  for (int i = threadIdx.x; i < per_split; i += kSparseWaves * 64) {
+    const int e = e0 + i;
+    int n = -1;
+    if (i < cnt) {
+      if (e < K) {
+        const int64_t chosen = idx[(int64_t)unit * K + e];
+        n = chosen >= 0 && chosen < N ? (int)chosen : -1;
+      } else {
+        n = lo + (e - K);
+      }
+    }
+    rows_lds[i] = n;
+  }
+  __syncthreads();
+  const int ntiles = (cnt + 31) / 32;
+  const int mine = ntiles > w ? (ntiles - w + kSparseWaves - 1) / kSparseWaves : 0;  // tiles w, w + 4, ...
+  const int fallback = nwin > 0 ? lo : 0;  // a valid row for a missing entry's DMA
+
+  const i32x4 krs = buffer_resource(k + (int64_t)b * ksb);
+  const i32x4 vrs = buffer_resource(v + (int64_t)b * vsb);
+  const uint32_t krow_bytes = (uint32_t)ksn * 2u, vrow_bytes = (uint32_t)vsn * 2u;
+  unsigned short* const ring = ring_all + w * kWaveRing;
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_address(ring));
+  auto issue = [&](int i) {  // tile w + 4 i into slot i % 2
+    const int tile = w + kSparseWaves * i;
+    const uint32_t slot = ring_lds + (uint32_t)(i % kSparseSlots) * (G::kElems * 2);
+#pragma unroll
+    for (int ii = 0; ii < G::kLoads; ++ii) {
+      const int part = ii / G::kPerHalf, chunk = ii % G::kPerHalf;
+      const int le = tile * 32 + 16 * (part & 1) + (j ^ (12 * (g & 1)));
+      int n = le < cnt ? rows_lds[le] : -1;
+      n = n < 0 ? fallback : n;
+      const uint32_t off = (uint32_t)n * (part < 2 ? krow_bytes : vrow_bytes) + 64u * chunk + 16u * g;
+      dma_16B(part < 2 ? krs : vrs, off, slot + part * (G::kHalf * 2) + 1024u * chunk);
+    }
+  };
+  for (int i = 0; i < kSparseSlots; ++i)
+    if (i < mine) issue(i);
+
+  // Q^T operand: head j of the query (a padding head repeats head H - 1)
+  bf16x8 qf[G::kSteps];
+  const unsigned short* qrow = q + ((int64_t)unit * H + min(j, H - 1)) * C;
+#pragma unroll
+  for (int s = 0; s < G::kSteps; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g);
+  const int tr_off =
+      128 * ((lane & 3) >> 1) + 8 * ((4 * g + ((lane >> 2) & 3)) ^ (12 * ((lane >> 1) & 1))) + 4 * (lane & 1);
+  const int k_off = 128 * g + 8 * (j ^ (12 * (g & 1)));
+
+  f32x4 o[G::kCBlocks];
+#pragma unroll
+  for (int cb = 0; cb < G::kCBlocks; ++cb) o[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegInf, l_run = 0.f;
+#pragma unroll 1
+  for (int i = 0; i < mine; ++i) {
+    if (i + 1 < mine)
+      wait_vmcnt<G::kLoads>();
+    else
+      wait_vmcnt<0>();
+    const unsigned short* st = ring + (i % kSparseSlots) * G::kElems;
+    const int tile = w + kSparseWaves * i;
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < G::kSteps; ++s) {
+      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(st + 512 * s + k_off);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(st + G::kHalf + 512 * s + k_off);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[s], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[s], s1, 0, 0, 0);
+    }
+    // keys 4g + i of each half: masked where the entry names no row
+    float x[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int le = tile * 32 + 16 * h + 4 * g;
+      const int4 ns = *reinterpret_cast<const int4*>(rows_lds + le);  // le + 3 < per_split: a whole tile
+      const f32x4 sv = h ? s1 : s0;
+      x[4 * h + 0] = le + 0 < cnt && ns.x >= 0 ? sv[0] : kNegInf;
+      x[4 * h + 1] = le + 1 < cnt && ns.y >= 0 ? sv[1] : kNegInf;
+      x[4 * h + 2] = le + 2 < cnt && ns.z >= 0 ? sv[2] : kNegInf;
+      x[4 * h + 3] = le + 3 < cnt && ns.w >= 0 ? sv[3] : kNegInf;
+    }
+    const float bm =
+        group_max(fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])))) *
+        scale_log2;
+    const bool grow = bm > m_run + kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(grow && m_run != kNegInf)) {
+      const float alpha = (grow && m_run != kNegInf) ? __builtin_amdgcn_exp2f(m_run - bm) : 1.f;
+      l_run *= alpha;
+#pragma unroll
+      for (int cb = 0; cb < G::kCBlocks; ++cb) o[cb] *= alpha;
+    }
+    m_run = grow ? bm : m_run;
+    const float neg_m = m_run == kNegInf ? 0.f : -m_run;
+    float pr[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pr[e] = __builtin_amdgcn_exp2f(fmaf(x[e], scale_log2, neg_m));
+    l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+    const bf16x8 pt = pack_bf16x8(pr);
+    const unsigned short* vs = st + 2 * G::kHalf + tr_off;
+#pragma unroll
+    for (int cb = 0; cb < G::kCBlocks; ++cb) {
+      const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vs + 256 * cb));
+      const s16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vs + G::kHalf + 256 * cb));
+      typedef short s16x8 __attribute__((ext_vector_type(8)));
+      const s16x8 vt = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+      o[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vt), pt, o[cb], 0, 0, 0);
+    }
+    // the slot is free once its values have reached the matrix cores
+    if (i + kSparseSlots < mine) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue(i + kSparseSlots);
+    }
+  }
+  wait_vmcnt<0>();
+  l_run = group_sum(l_run);
+
+  // ---- merge the four wavefronts (each one's buffer in its own ring) ----
+  float* mine_buf = reinterpret_cast<float*>(ring);
+#pragma unroll
+  for (int cb = 0; cb < G::kCBlocks; ++cb)
+    *reinterpret_cast<f32x4*>(mine_buf + j * kPitch + cb * 16 + 4 * g) = o[cb];
+  if (g == 0) {
+    mine_buf[16 * kPitch + j] = m_run;
+    mine_buf[16 * kPitch + 16 + j] = l_run;
+  }
+  __syncthreads();
+  constexpr int kQuads8 = C / 8;
+  const int item = threadIdx.x;
+  if (item >= 16 * kQuads8) return;
+  const int jr = item / kQuads8, c8 = (item % kQuads8) * 8;
+  if (jr >= H) return;
+  float M = kNegInf;
+#pragma unroll
+  for (int ww = 0; ww < kSparseWaves; ++ww)
+    M = fmaxf(M, reinterpret_cast<const float*>(ring_all + ww * kWaveRing)[16 * kPitch + jr]);
+  float L = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (M != kNegInf) {
+#pragma unroll
+    for (int ww = 0; ww < kSparseWaves; ++ww) {
+      const float* buf = reinterpret_cast<const float*>(ring_all + ww * kWaveRing);
+      const float mw = buf[16 * kPitch + jr];
+      if (mw == kNegInf) continue;
+      const float a = exp2f(mw - M);
+      L += buf[16 * kPitch + 16 + jr] * a;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += buf[jr * kPitch + c8 + e] * a;
+    }
+  }
+  const int r = (unit % T) * H + jr;  // query row within the batch row
+  if (splits == 1) {
+    float f = 1.f;
+    if (sink) {
+      const float sl = sink[jr] * kLog2e;
+      const float M2 = fmaxf(M, sl);
+      f = M == kNegInf ? 0.f : exp2f(M - M2);
+      L = L * f + exp2f(sl - M2);
+      M = M2;
+    }
+    const float inv = L > 0.f ? f / L : 0.f;
+    const unsigned short* grow = gate.row<unsigned short>(b, T, r, H, C);
+    u16x8 res;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) res[e] = grow ? gated_bf16(acc[e] * inv, grow[c8 + e]) : f32_to_bf16(acc[e] * inv);
+    *reinterpret_cast<u16x8*>(out + ((int64_t)unit * H + jr) * C + c8) = res;
+    if (lse_out && c8 == 0) lse_out[(int64_t)unit * H + jr] = L > 0.f ? (M + log2f(L)) * kLn2 : kNegInf;
+  } else {
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const int64_t prow = ((int64_t)unit * splits + split) * H + jr;
+    u16x8 res;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) res[e] = f32_to_bf16(acc[e] * inv);
+    *reinterpret_cast<u16x8*>(part_o + prow * C + c8) = res;
+    if (c8 == 0) part_lse[prow] = L > 0.f ? M + log2f(L) : kNegInf;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Key-parallel MFMA kernel (at most 80 query rows, no tree mask)
 // ---------------------------------------------------------------------------
 //
@@ -1452,33 +1674,127 @@ extern "C" int wptv_window_attention(const void* q, const void* k, int64_t k_str
 }
 
 
+namespace {
+struct SparsePlan {
+  bool mfma;
+  int splits, per_split;
+  size_t bytes;
+};
+
+int sparse_plan(int B, int T, int H, int c, int K, int window, int N, int dtype, int requested, SparsePlan* p) {
+  if (B <= 0 || T <= 0 || H <= 0 || c <= 0 || K < 0 || window < 0)
+    return fail(WPTV_E_INVALID, "sparse_attention: bad shape B=%d T=%d H=%d c=%d K=%d window=%d", B, T, H, c, K,
+                window);
+  if (dtype != WPTV_F32 && dtype != WPTV_BF16)
+    return fail(WPTV_E_UNSUPPORTED, "sparse_attention: dtype %d is neither fp32 nor bf16", dtype);
+  if (c > kMaxC) return fail(WPTV_E_UNSUPPORTED, "sparse_attention: head width %d above %d", c, kMaxC);
+  p->mfma = dtype == WPTV_BF16 && (c == 64 || c == 128) && H <= 16;
+  p->splits = 1;
+  p->per_split = 0;
+  p->bytes = 0;
+  if (!p->mfma) return WPTV_OK;
+  const long long total = (long long)K + (window < N ? window : N);  // the longest list of a query
+  long long s = requested;
+  if (s <= 0) {
+    s = (compute_units() + (long long)B * T - 1) / ((long long)B * T);  // a workgroup per compute unit
+    const long long most = (total + 127) / 128;  // at least one tile per wavefront
+    if (s > most) s = most;
+  }
+  const long long least = (total + kSparseList - 1) / kSparseList;  // the list of a split fits its LDS
+  if (s < least) s = least;
+  if (s < 1) s = 1;
+  if (s > 4096) return fail(WPTV_E_INVALID, "sparse_attention: splits %lld above 4096", s);
+  long long per = (total + s - 1) / s;
+  per = (per + 31) / 32 * 32;
+  if (per > kSparseList) return fail(WPTV_E_INVALID, "sparse_attention: %lld rows per split above %d", per, kSparseList);
+  p->splits = (int)s;
+  p->per_split = (int)(per > 0 ? per : 32);
+  if (s > 1) {
+    const size_t rows = (size_t)B * T * s * H;
+    p->bytes = align_up(rows * c * 2, 256) + align_up(rows * sizeof(float), 256);
+  }
+  return WPTV_OK;
+}
+}  // namespace
+
+extern "C" int wptv_sparse_attention_workspace(int B, int T, int H, int c, int K, int window, int N, int dtype,
+                                               int* splits, size_t* bytes) {
+  if (!splits || !bytes) return fail(WPTV_E_INVALID, "sparse_attention_workspace: null output pointer");
+  SparsePlan p;
+  const int st = sparse_plan(B, T, H, c, K, window, N, dtype, *splits, &p);
+  if (st != WPTV_OK) return st;
+  *splits = p.splits;
+  *bytes = p.bytes;
+  return WPTV_OK;
+}
+
 extern "C" int wptv_sparse_attention(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
                                      const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
                                      const int64_t* idx, int K, const int64_t* positions, int window,
-                                     const float* sink, int B, int T, int H, int c, int N, float scale, void* out,
-                                     float* lse, hipStream_t stream) {
+                                     const float* sink, const void* gate, int64_t gate_stride, int B, int T, int H,
+                                     int c, int N, float scale, int splits, void* out, float* lse, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream) {
   if (!q || !k || !v || !positions || !out || (K > 0 && !idx))
     return fail(WPTV_E_INVALID, "sparse_attention: q, k, v, positions, out (and idx when K > 0) must be given");
-  if (B <= 0 || T <= 0 || H <= 0 || c <= 0 || N <= 0 || K < 0 || window < 0)
-    return fail(WPTV_E_INVALID, "sparse_attention: bad shape B=%d T=%d H=%d c=%d N=%d K=%d window=%d", B, T, H, c,
-                N, K, window);
-  if (c > kMaxC) return fail(WPTV_E_UNSUPPORTED, "sparse_attention: head width %d above %d", c, kMaxC);
+  if (N <= 0) return fail(WPTV_E_INVALID, "sparse_attention: the table is empty");
   if (k_stride_n < c || v_stride_n < c)
     return fail(WPTV_E_INVALID, "sparse_attention: a row stride below the head width");
+  if (gate && gate_stride < (int64_t)H * c)
+    return fail(WPTV_E_INVALID, "sparse_attention: gate row stride %lld below H*c", (long long)gate_stride);
+  SparsePlan p;
+  int st = sparse_plan(B, T, H, c, K, window, N, dtype, splits, &p);
+  if (st != WPTV_OK) return st;
   const float scale_log2 = scale * kLog2e;
+  const bool ok_range = (double)N * (double)(k_stride_n > v_stride_n ? k_stride_n : v_stride_n) * 2.0 < 4.0e9;
+  if (p.mfma && !(scale > 0.f && scale < 1e30f && ok_range && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
+                  k_stride_b % 8 == 0 && k_stride_n % 8 == 0 && v_stride_b % 8 == 0 && v_stride_n % 8 == 0 &&
+                  (!gate || (aligned(gate, 16) && gate_stride % 8 == 0))))
+    p.mfma = false;
   const int64_t* rows = K > 0 ? idx : nullptr;
-  dim3 grid(T * H, B);
-  if (dtype == WPTV_F32)
-    hipLaunchKernelGGL(attention_generic<float>, grid, dim3(64), 0, stream, (const float*)q, (const float*)k, k_stride_b,
-                       k_stride_n, (const float*)v, v_stride_b, v_stride_n, rows, K, positions, window, nullptr,
-                       nullptr, sink, T, H, c, N, scale_log2, RowMap{nullptr, 0xffffffffu}, OutGate{nullptr, 0},
-                       (float*)out, lse);
-  else if (dtype == WPTV_BF16)
-    hipLaunchKernelGGL(attention_generic<unsigned short>, grid, dim3(64), 0, stream, (const unsigned short*)q,
-                       (const unsigned short*)k, k_stride_b, k_stride_n, (const unsigned short*)v, v_stride_b,
-                       v_stride_n, rows, K, positions, window, nullptr, nullptr, sink, T, H, c, N, scale_log2,
-                       RowMap{nullptr, 0xffffffffu}, OutGate{nullptr, 0}, (unsigned short*)out, lse);
+  const OutGate og{gate, gate_stride};
+  if (!p.mfma) {
+    dim3 grid(T * H, B);
+    if (dtype == WPTV_F32)
+      hipLaunchKernelGGL(attention_generic<float>, grid, dim3(64), 0, stream, (const float*)q, (const float*)k,
+                         k_stride_b, k_stride_n, (const float*)v, v_stride_b, v_stride_n, rows, K, positions, window,
+                         nullptr, nullptr, sink, T, H, c, N, scale_log2, RowMap{nullptr, 0xffffffffu}, og,
+                         (float*)out, lse);
+    else
+      hipLaunchKernelGGL(attention_generic<unsigned short>, grid, dim3(64), 0, stream, (const unsigned short*)q,
+                         (const unsigned short*)k, k_stride_b, k_stride_n, (const unsigned short*)v, v_stride_b,
+                         v_stride_n, rows, K, positions, window, nullptr, nullptr, sink, T, H, c, N, scale_log2,
+                         RowMap{nullptr, 0xffffffffu}, og, (unsigned short*)out, lse);
+    return launched("attention_generic");
+  }
+  if (p.bytes > 0 && (!workspace || workspace_bytes < p.bytes))
+    return fail(WPTV_E_INVALID, "sparse_attention: workspace of %zu bytes, %zu needed for %d splits", workspace_bytes,
+                p.bytes, p.splits);
+  unsigned short* part_o = nullptr;
+  float* part_lse = nullptr;
+  if (p.splits > 1) {
+    const size_t rows_n = (size_t)B * T * p.splits * H;
+    part_o = static_cast<unsigned short*>(workspace);
+    part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(rows_n * c * 2, 256));
+  }
+  const long long wgs = (long long)B * T * p.splits;
+  if (wgs > INT_MAX) return fail(WPTV_E_INVALID, "sparse_attention: grid too large");
+  const auto* qb = static_cast<const unsigned short*>(q);
+  const auto* kb = static_cast<const unsigned short*>(k);
+  const auto* vb = static_cast<const unsigned short*>(v);
+  auto* ob = static_cast<unsigned short*>(out);
+  if (c == 128)
+    hipLaunchKernelGGL(sparse_attention_mfma<128>, dim3((unsigned)wgs), dim3(kSparseWaves * 64), 0, stream, qb, kb,
+                       k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, rows, K, positions, window, sink, T, H, N,
+                       scale_log2, p.splits, p.per_split, og, ob, lse, part_o, part_lse);
   else
-    return fail(WPTV_E_UNSUPPORTED, "sparse_attention: dtype %d is neither fp32 nor bf16", dtype);
-  return launched("attention_generic");
+    hipLaunchKernelGGL(sparse_attention_mfma<64>, dim3((unsigned)wgs), dim3(kSparseWaves * 64), 0, stream, qb, kb,
+                       k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, rows, K, positions, window, sink, T, H, N,
+                       scale_log2, p.splits, p.per_split, og, ob, lse, part_o, part_lse);
+  st = launched("sparse_attention_mfma");
+  if (st != WPTV_OK || p.splits == 1) return st;
+  const long long items = (long long)B * T * H * (c / 8);
+  dim3 cgrid((unsigned)((items + 255) / 256));
+  hipLaunchKernelGGL(combine_splits, cgrid, dim3(256), 0, stream, part_o, part_lse, sink, B, T, H, c, H, T, p.splits,
+                     og, ob, lse);
+  return launched("combine_splits");
 }

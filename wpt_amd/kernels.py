@@ -172,18 +172,19 @@ def choose_rows(q, k, positions, lse, scale, top_k, window):
     return chosen
 
 
-def sparse_attention(q, k, v, sink, idx, positions, scale, window):
+def sparse_attention(q, k, v, sink, idx, positions, scale, window, *, gate=None, splits=0):
     """The output (B, T, H, c) of attention over each query's rows idx
     (B, T, K) and its last window tokens, with sink (H,) added to each
     head's denominator (pytorch_kernels.py:149-153,171-187,213-217).  A row
-    in both lists counts twice, as the reference's concatenation counts it."""
+    in both lists counts twice, as the reference's concatenation counts it.
+    gate (B, T, >= H*c): the sparse layer's output gate, o * sigmoid(gate)
+    (attention.py:128-130).  splits: parts of each query's rows (0: the
+    library chooses)."""
     B, T, H, c, N = _check_inputs(q, k, v, positions)
     if idx.dim() != 3 or tuple(idx.shape[:2]) != (B, T):
         raise ValueError(f"idx must be (B={B}, T={T}, K); got {tuple(idx.shape)}")
     if window <= 0:
         raise ValueError(f"the sparse form reads a window of at least one row; got {window}")
-    if idx.shape[2] == 0:
-        return verify_attention(q, k, v, positions, scale, window=window, sink=sink)
     device = q.device
     library = _lib.lib()
     dtype = _lib.dtype_code(q.dtype)
@@ -191,11 +192,25 @@ def sparse_attention(q, k, v, sink, idx, positions, scale, window):
     idx_ = _long(idx, device)
     positions_ = _long(positions, device)
     sink_ = sink.to(device=device, dtype=torch.float32).contiguous()
+    if sink_.shape != (H,):
+        raise ValueError(f"sink must be (H={H},); got {tuple(sink_.shape)}")
+    gate_stride = 0
+    if gate is not None:
+        if gate.dtype != q.dtype or gate.shape[:2] != (B, T) or gate.stride(-1) != 1 or \
+                gate.stride(0) != T * gate.stride(1) or gate.shape[-1] < H * c:
+            raise ValueError(f"gate must be (B={B}, T={T}, >= H*c) in q's dtype, rows one after another")
+        gate_stride = gate.stride(1)
+    K = idx_.shape[2]
+    parts = _lib.ctypes.c_int(int(splits))
+    size = _lib.ctypes.c_size_t(0)
+    check(library.wptv_sparse_attention_workspace(B, T, H, c, K, int(window), N, dtype, _lib.ctypes.byref(parts),
+                                                  _lib.ctypes.byref(size)), "sparse_attention")
+    workspace = torch.empty(size.value, dtype=torch.uint8, device=device) if size.value else None
     out = torch.empty_like(q_)
     check(library.wptv_sparse_attention(ptr(q_), ptr(k), k.stride(0), k.stride(1), ptr(v), v.stride(0), v.stride(1),
-                                        dtype, ptr(idx_), idx_.shape[2], ptr(positions_), int(window), ptr(sink_), B, T,
-                                        H, c, N, float(scale), ptr(out), None, _lib.stream(device)),
-          "sparse_attention")
+                                        dtype, ptr(idx_), K, ptr(positions_), int(window), ptr(sink_), ptr(gate),
+                                        gate_stride, B, T, H, c, N, float(scale), parts.value, ptr(out), None,
+                                        ptr(workspace), size.value, _lib.stream(device)), "sparse_attention")
     return _forward_only(out, q, k, v, sink)
 
 
