@@ -587,7 +587,7 @@ __global__ __launch_bounds__(kSparseWaves * 64, 1) void sparse_attention_mfma(
     const unsigned short* __restrict__ q, const unsigned short* __restrict__ k, int64_t ksb, int64_t ksn,
     const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn, const int64_t* __restrict__ idx, int K,
     const int64_t* __restrict__ positions, int window, const float* __restrict__ sink, int T, int H, int N,
-    float scale_log2, int splits, int per_split, OutGate gate, unsigned short* __restrict__ out,
+    float scale_log2, int splits, int per_split, int xcd_map, OutGate gate, unsigned short* __restrict__ out,
     float* __restrict__ lse_out, unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
   using G = Tile<C>;
   constexpr int kWaveRing = kSparseSlots * G::kElems;  // elements of one wavefront's ring
@@ -599,7 +599,20 @@ __global__ __launch_bounds__(kSparseWaves * 64, 1) void sparse_attention_mfma(
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
-  const int unit = blockIdx.x / splits, split = blockIdx.x % splits;  // unit = b T + t
+  // unit = b T + t.  With xcd_map (B a multiple of 8), every workgroup of a
+  // batch row lands on one XCD (the dispatcher deals workgroups out to the 8
+  // XCDs in turn), so rows that several of its queries chose are read from
+  // HBM once and from that XCD's L2 after.
+  int unit, split;
+  if (xcd_map) {
+    const int per_row = T * splits, kk = blockIdx.x >> 3;
+    const int bb = (blockIdx.x & 7) + 8 * (kk / per_row), within = kk % per_row;
+    unit = bb * T + within / splits;
+    split = within % splits;
+  } else {
+    unit = blockIdx.x / splits;
+    split = blockIdx.x % splits;
+  }
   const int b = unit / T;
   const int64_t p = positions[unit];
   const int64_t lo64 = p - window + 1;
@@ -1785,11 +1798,11 @@ extern "C" int wptv_sparse_attention(const void* q, const void* k, int64_t k_str
   if (c == 128)
     hipLaunchKernelGGL(sparse_attention_mfma<128>, dim3((unsigned)wgs), dim3(kSparseWaves * 64), 0, stream, qb, kb,
                        k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, rows, K, positions, window, sink, T, H, N,
-                       scale_log2, p.splits, p.per_split, og, ob, lse, part_o, part_lse);
+                       scale_log2, p.splits, p.per_split, B % 8 == 0, og, ob, lse, part_o, part_lse);
   else
     hipLaunchKernelGGL(sparse_attention_mfma<64>, dim3((unsigned)wgs), dim3(kSparseWaves * 64), 0, stream, qb, kb,
                        k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, rows, K, positions, window, sink, T, H, N,
-                       scale_log2, p.splits, p.per_split, og, ob, lse, part_o, part_lse);
+                       scale_log2, p.splits, p.per_split, B % 8 == 0, og, ob, lse, part_o, part_lse);
   st = launched("sparse_attention_mfma");
   if (st != WPTV_OK || p.splits == 1) return st;
   const long long items = (long long)B * T * H * (c / 8);

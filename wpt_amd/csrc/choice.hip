@@ -25,11 +25,15 @@
 //                        v_mfma_f32_16x16x32_bf16 (one key row per lane as
 //                        the A operand), the max over heads through LDS
 //                      otherwise: FP32 dot products on the VALU
-//   choice_select    one workgroup per query: a 4-pass radix select of the
-//                    K-th largest score (order-preserving keys, most
-//                    significant byte first; the scores stay in L2), then one
-//                    pass that compacts the chosen rows in row order with
-//                    wavefront ballots
+//   choice_select_regs  one workgroup per query, tables up to 8192 rows: the
+//                    query's scores in registers, the K-th largest found two
+//                    bits at a time with packed workgroup counts, the chosen
+//                    rows written in row order after one exclusive scan
+//   choice_select    longer tables: a 4-pass radix select of the K-th
+//                    largest score (order-preserving keys, most significant
+//                    byte first; the scores stay in L2), then one pass that
+//                    compacts the chosen rows in row order with wavefront
+//                    ballots
 #include "wptv_common.h"
 
 namespace wptv {
@@ -132,6 +136,78 @@ __global__ __launch_bounds__(kST) void choice_scores_mfma(
   }
   __syncthreads();
   store_scores(xs, blk, pos_b, T, H, N, window, scores, ns);
+}
+
+// 16 heads (each position's heads are one 16-row MFMA block, so the max over
+// the heads is a reduction over the 16 lanes of a lane group): one
+// workgroup per (batch row, 512 table rows), every position of the pass.
+// Each wavefront takes 128 rows in sub-blocks of 16, the keys of four
+// sub-blocks loaded before the first is used, the queries held in
+// registers for the whole range.
+constexpr int kH16Rows = 512;  // table rows per workgroup
+constexpr int kH16Batch = 4;   // 16-row sub-blocks whose keys are in flight together
+
+template <int C, int TT>
+__global__ __launch_bounds__(kST) void choice_scores_h16(
+    const unsigned short* __restrict__ q, const unsigned short* __restrict__ k, int64_t ksb, int64_t ksn,
+    const int64_t* __restrict__ positions, const float* __restrict__ lse, int T, int N, int window, float scale_log2,
+    int nkb, float* __restrict__ scores, int64_t ns) {
+  constexpr int S = C / 32;
+  const int b = blockIdx.x / nkb;
+  const int n0 = (blockIdx.x % nkb) * kH16Rows;
+  const int64_t* pos_b = positions + (int64_t)b * T;
+  int far = 0;
+  for (int t = 0; t < T; ++t) far = max(far, far_rows(pos_b[t], window, N));
+  if (n0 >= far) return;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  bf16x8 qop[TT][S];
+  float l2[TT];
+  int64_t lim[TT];  // row n is a candidate of position t iff n <= lim[t]
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const int tt = t < T ? t : T - 1;
+    const unsigned short* qrow = q + (((int64_t)b * T + tt) * 16 + j) * C;
+#pragma unroll
+    for (int s = 0; s < S; ++s) qop[t][s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g);
+    l2[t] = lse[((int64_t)b * T + tt) * 16 + j] * kLog2e;
+    lim[t] = pos_b[tt] - window;
+  }
+  const int wn0 = n0 + w * (kH16Rows / 4);
+  const unsigned short* kb = k + (int64_t)b * ksb;
+#pragma unroll 1
+  for (int sb0 = 0; sb0 < kH16Rows / 4 / 16; sb0 += kH16Batch) {
+    if (wn0 + 16 * sb0 >= far) break;
+    bf16x8 kop[kH16Batch][S];
+#pragma unroll
+    for (int u = 0; u < kH16Batch; ++u) {
+      int n = wn0 + 16 * (sb0 + u) + j;
+      n = n < N ? n : N - 1;  // clamped rows are not written
+#pragma unroll
+      for (int s = 0; s < S; ++s) kop[u][s] = *reinterpret_cast<const bf16x8*>(kb + (int64_t)n * ksn + 32 * s + 8 * g);
+    }
+#pragma unroll
+    for (int u = 0; u < kH16Batch; ++u) {
+      const int nb = wn0 + 16 * (sb0 + u);  // the sub-block's first row
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        if (t >= T) break;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < S; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[u][s], qop[t][s], acc, 0, 0, 0);
+        // acc[i] = S^T[row nb + 4g + i][head j]; the max over the 16 heads
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = row16_max(fmaf(acc[i], scale_log2, -l2[t]));
+        // lane j < 4 writes row nb + 4g + j: 16 consecutive rows per sub-block
+        const int n = nb + 4 * g + j;
+        if (j < 4 && n < N) {
+          const float v = j == 0 ? x[0] : j == 1 ? x[1] : j == 2 ? x[2] : x[3];
+          scores[((int64_t)b * T + t) * ns + n] = (int64_t)n <= lim[t] ? v : -kInf;
+        }
+      }
+    }
+  }
 }
 
 template <typename E>
@@ -259,6 +335,109 @@ __global__ __launch_bounds__(kST) void choice_select(const float* __restrict__ s
   }
 }
 
+// Sum over the workgroup, one barrier: red holds two buffers of one value per
+// wavefront, used in turn (a wavefront writes a round's buffer only after
+// every wavefront has passed the barrier of the round before, and so has read
+// the buffer of two rounds before).
+__device__ __forceinline__ uint64_t block_sum_u64(uint32_t lo, uint32_t hi, uint64_t (*red)[kST / 64], int round) {
+  const uint64_t x = (uint64_t)wave_sum_u32(lo) | ((uint64_t)wave_sum_u32(hi) << 32);
+  if ((threadIdx.x & 63) == 0) red[round & 1][threadIdx.x >> 6] = x;
+  __syncthreads();
+  uint64_t r = 0;
+#pragma unroll
+  for (int i = 0; i < kST / 64; ++i) r += red[round & 1][i];
+  return r;
+}
+
+// The select for up to kST * ITEMS candidates: thread t holds the keys of
+// rows ITEMS t .. ITEMS t + ITEMS - 1 in registers (one memory round trip);
+// the K-th largest key is found two bits at a time from the top (16 rounds,
+// each counting the keys at or above three candidates in one packed
+// reduction), and the chosen rows are written in row order after one
+// exclusive scan of the threads' counts.
+template <int ITEMS>
+__global__ __launch_bounds__(kST) void choice_select_regs(const float* __restrict__ scores, int64_t ns,
+                                                          const int64_t* __restrict__ positions, int N, int window,
+                                                          int K, int64_t* __restrict__ chosen) {
+  static_assert(ITEMS % 4 == 0 && kST * ITEMS <= 65535, "packed counts hold 16 bits");
+  __shared__ uint64_t red[2][kST / 64];
+  __shared__ int scan_g[kST / 64], scan_e[kST / 64];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t bt = blockIdx.x;
+  const int nf = far_rows(positions[bt], window, N);
+  int64_t* out = chosen + bt * K;
+  if (nf <= K) {  // every candidate, then none
+    for (int i = tid; i < K; i += kST) out[i] = i < nf ? i : -1;
+    return;
+  }
+  const float* s = scores + bt * ns;
+  const int base = tid * ITEMS;
+  uint32_t key[ITEMS];  // 0 (below every score's key) past the candidates
+#pragma unroll
+  for (int v4 = 0; v4 < ITEMS / 4; ++v4) {
+    const int n = base + 4 * v4;
+    const f32x4 x = n < nf ? *reinterpret_cast<const f32x4*>(s + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) key[4 * v4 + e] = n + e < nf ? order_key(x[e]) : 0u;
+  }
+  // the largest t with at least K keys >= t: the K-th largest key
+  uint32_t prefix = 0;
+  for (int shift = 30, round = 0; shift >= 0; shift -= 2, ++round) {
+    const uint32_t c1 = prefix | (1u << shift), c2 = prefix | (2u << shift), c3 = prefix | (3u << shift);
+    uint32_t n12 = 0, n3 = 0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      n12 += (key[i] >= c1 ? 1u : 0u) + (key[i] >= c2 ? 65536u : 0u);
+      n3 += key[i] >= c3 ? 1u : 0u;
+    }
+    const uint64_t sum = block_sum_u64(n12, n3, red, round);
+    const int s1 = (int)(sum & 65535), s2 = (int)((sum >> 16) & 65535), s3 = (int)(sum >> 32);
+    prefix = s3 >= K ? c3 : s2 >= K ? c2 : s1 >= K ? c1 : prefix;
+  }
+  const uint32_t tau = prefix;
+  int cg = 0, ce = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    cg += key[i] > tau ? 1 : 0;
+    ce += key[i] == tau ? 1 : 0;
+  }
+  // exclusive scan of (cg, ce) over the threads in row order
+  int ig = cg, ie = ce;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int og = __shfl_up(ig, o, 64), oe = __shfl_up(ie, o, 64);
+    if (lane >= o) {
+      ig += og;
+      ie += oe;
+    }
+  }
+  if (lane == 63) {
+    scan_g[w] = ig;
+    scan_e[w] = ie;
+  }
+  __syncthreads();
+  int n_gt = 0, pg = ig - cg, pe = ie - ce;
+#pragma unroll
+  for (int i = 0; i < kST / 64; ++i) {
+    n_gt += scan_g[i];
+    if (i < w) {
+      pg += scan_g[i];
+      pe += scan_e[i];
+    }
+  }
+  const int need_eq = K - n_gt;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int n = base + i;
+    if (key[i] > tau) {
+      out[pg++] = n;
+    } else if (key[i] == tau) {
+      if (pe < need_eq) out[n_gt + pe] = n;
+      ++pe;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace wptv
 
@@ -304,7 +483,23 @@ extern "C" int wptv_exact_choice(const void* q, const void* k, int64_t k_stride_
   const float scale_log2 = scale * kLog2e;
   const bool mfma = dtype == WPTV_BF16 && (c == 64 || c == 128) && aligned(q, 16) && aligned(k, 16) &&
                     k_stride_n % 8 == 0 && k_stride_b % 8 == 0;
-  if (mfma) {
+  if (mfma && H == 16 && T <= 8) {
+    const auto* qq = static_cast<const unsigned short*>(q);
+    const auto* kk = static_cast<const unsigned short*>(k);
+    const int nkb16 = (N + kH16Rows - 1) / kH16Rows;
+    const int grid16 = B * nkb16;
+#define WPTV_H16(CC, TT)                                                                                           \
+  choice_scores_h16<CC, TT><<<grid16, kST, 0, stream>>>(qq, kk, k_stride_b, k_stride_n, positions, lse, T, N, window, \
+                                                        scale_log2, nkb16, scores, ns)
+    if (c == 128) {
+      if (T <= 1) WPTV_H16(128, 1); else if (T <= 2) WPTV_H16(128, 2); else if (T <= 4) WPTV_H16(128, 4);
+      else if (T <= 5) WPTV_H16(128, 5); else WPTV_H16(128, 8);
+    } else {
+      if (T <= 1) WPTV_H16(64, 1); else if (T <= 2) WPTV_H16(64, 2); else if (T <= 4) WPTV_H16(64, 4);
+      else if (T <= 5) WPTV_H16(64, 5); else WPTV_H16(64, 8);
+    }
+#undef WPTV_H16
+  } else if (mfma) {
     const auto* qq = static_cast<const unsigned short*>(q);
     const auto* kk = static_cast<const unsigned short*>(k);
     if (c == 128)
@@ -325,6 +520,16 @@ extern "C" int wptv_exact_choice(const void* q, const void* k, int64_t k_stride_
   }
   int status = launched("choice_scores");
   if (status != WPTV_OK) return status;
-  choice_select<<<B * T, kST, 0, stream>>>(scores, ns, positions, N, window, K, chosen);
+  // the candidates of a query are at most N rows: in registers up to 8192
+  if (N <= kST * 4)
+    choice_select_regs<4><<<B * T, kST, 0, stream>>>(scores, ns, positions, N, window, K, chosen);
+  else if (N <= kST * 8)
+    choice_select_regs<8><<<B * T, kST, 0, stream>>>(scores, ns, positions, N, window, K, chosen);
+  else if (N <= kST * 16)
+    choice_select_regs<16><<<B * T, kST, 0, stream>>>(scores, ns, positions, N, window, K, chosen);
+  else if (N <= kST * 32)
+    choice_select_regs<32><<<B * T, kST, 0, stream>>>(scores, ns, positions, N, window, K, chosen);
+  else
+    choice_select<<<B * T, kST, 0, stream>>>(scores, ns, positions, N, window, K, chosen);
   return launched("choice_select");
 }

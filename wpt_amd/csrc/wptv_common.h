@@ -93,6 +93,38 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 
+// ---- lane exchanges without LDS traffic -------------------------------------
+
+// DPP moves within a 16-lane row: lane i takes lane i ^ 1, i ^ 2 (quad
+// permutes), 7 - i within its half-row, 15 - i within its row.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_move(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, false);
+}
+
+// The max over the 16 lanes of a row, in every lane of it.
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, __int_as_float(dpp_move<kDppXor1>(__float_as_int(x))));
+  x = fmaxf(x, __int_as_float(dpp_move<kDppXor2>(__float_as_int(x))));
+  x = fmaxf(x, __int_as_float(dpp_move<kDppHalfMirror>(__float_as_int(x))));
+  return fmaxf(x, __int_as_float(dpp_move<kDppMirror>(__float_as_int(x))));
+}
+
+// The sum over the 64 lanes of a wavefront, in every lane: the rows by DPP,
+// then across the four rows by permlane swaps.
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t x) {
+  x += (uint32_t)dpp_move<kDppXor1>((int)x);
+  x += (uint32_t)dpp_move<kDppXor2>((int)x);
+  x += (uint32_t)dpp_move<kDppHalfMirror>((int)x);
+  x += (uint32_t)dpp_move<kDppMirror>((int)x);
+  const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = a[0] + a[1];
+  const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return b[0] + b[1];
+}
+
 // ---- LDS DMA (global -> LDS without registers) -----------------------------
 
 // s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding).
