@@ -21,9 +21,10 @@ over a graph of 24 back-to-back calls that take six tables in turn (403 MB, so
 the keys and values come from HBM, not the 256 MB Infinity Cache), against
 8 TB/s.  `configs` reports the other
 workloads: the FP32 plumbing decoder's greedy step (checked bit-exact against
-the oracle), sliding-window and tree verification, the step's matrix products
-(MFMA TFLOP/s against the bf16 peak), and the 24-layer step at batch 64 / KV
-2048.  `cpu_baseline` is the oracle (the reference's PyTorch
+the oracle), sliding-window and tree verification, the three attention layers
+of a WPT model at the verify shape (exact with its top-1024 choice, sparse over
+the chosen rows, window over its ring), the step's matrix products (MFMA
+TFLOP/s against the bf16 peak), and the 24-layer step at batch 64 / KV 2048.  `cpu_baseline` is the oracle (the reference's PyTorch
 algorithm restated in FP32 on the CPU) running the headline step for a sample
 of rows on this host's cores.
 """
@@ -250,6 +251,55 @@ def tree_c4(steps, warmup):
             "lm_head_rows": B * M}
 
 
+def wpt_layers(steps, warmup):
+    """The three attention layers of a WPT model at the verify step, at the
+    verify-attention shape (batch 32, 4096 table rows, k+1 = 5 queries, 16
+    heads of 128, bf16): the exact layer with its choice of TOP_K = 1024 rows
+    outside a WINDOW of 128 (attention.py:51-52), the sparse layer over those
+    rows plus its window (sink, output gate), the window layer over its ring
+    (sink, output gate).  Four tables taken in turn (268 MB, more than the
+    Infinity Cache).  Bytes: the exact layer reads every key and value and the
+    keys again for the scores; the sparse layer the 1152 gathered rows of each
+    query (a row two queries chose counts twice); the window layer its 132
+    rows per batch row."""
+    import torch
+
+    from wpt_amd import kernels
+
+    B, T, H, c, N, TOPK, W = 32, 5, 16, 128, 4096, 1024, 128
+    device = torch.device("cuda", 0)
+    generator = torch.Generator(device=device).manual_seed(3)
+    q = torch.randn(B, T, H, c, generator=generator, device=device).to(torch.bfloat16)
+    tables = [torch.randn(B, N, 2 * c, generator=generator, device=device).to(torch.bfloat16) for _ in range(4)]
+    positions = (N - T + torch.arange(T, device=device)).expand(B, T).contiguous()
+    sink = torch.randn(H, generator=generator, device=device)
+    gate = torch.randn(B, T, H * c, generator=generator, device=device).to(torch.bfloat16)
+    rings = [torch.randn(B, 256, 2 * c, generator=generator, device=device).to(torch.bfloat16) for _ in range(4)]
+    chosen = [kernels.exact_attention(q, t[..., :c], t[..., c:], positions, c ** -0.5, TOPK, W)[1] for t in tables]
+    calls = 8
+    io = 2 * B * T * H * c * 2 + B * T * 8
+
+    def per_call(fn):
+        replay = graphed(lambda: [fn(i % 4) for i in range(calls)])
+        return timed(replay, max(1, steps // 4), max(1, warmup // 4)) / calls
+
+    out = {}
+    ms = per_call(lambda i: kernels.exact_attention(q, tables[i][..., :c], tables[i][..., c:], positions, c ** -0.5,
+                                                    TOPK, W))
+    nbytes = attention_bytes(B, T, H, c, N) + B * N * c * 2 + 2 * B * T * N * 4 + B * T * TOPK * 8
+    out["exact_layer_attention_and_choice_top1024"] = {"us": ms * 1e3, "bytes": nbytes,
+                                                       "GBps": nbytes / (ms * 1e-3) / 1e9}
+    ms = per_call(lambda i: kernels.sparse_attention(q, tables[i][..., :c], tables[i][..., c:], sink, chosen[i],
+                                                     positions, c ** -0.5, W, gate=gate))
+    nbytes = B * T * (TOPK + W) * 2 * c * 2 + io + B * T * TOPK * 8 + B * T * H * c * 2
+    out["sparse_layer_1024_chosen_plus_window_128"] = {"us": ms * 1e3, "bytes_gathered": nbytes,
+                                                       "GBps": nbytes / (ms * 1e-3) / 1e9}
+    ms = per_call(lambda i: kernels.ring_attention(q, rings[i], positions, c ** -0.5, W, sink, gate=gate))
+    nbytes = B * (W + T - 1) * 2 * c * 2 + io + B * T * H * c * 2
+    out["window_layer_ring_window_128"] = {"us": ms * 1e3, "bytes": nbytes, "GBps": nbytes / (ms * 1e-3) / 1e9}
+    return out
+
+
 def plumbing_c1():
     """The FP32 plumbing decoder: batch 1, a prompt of 64 tokens, 4 uniform
     drafts, greedy verification on the GPU and in the oracle."""
@@ -439,7 +489,8 @@ def main():
         configs["verify_attention_B32_KV4096"] = attn
         configs["sliding_window_B8_KV32768_W1024"] = attention_c3(args.steps, args.warmup)
         configs["tree_B16_KV8192_31nodes_lm_head"] = tree_c4(args.steps, args.warmup)
-        log("configs c1-c4 done")
+        configs["wpt_attention_layers_B32_KV4096"] = wpt_layers(args.steps, args.warmup)
+        log("configs c1-c4 and the WPT attention layers done")
     pieces = head.pop("_pieces")
     if not args.quick:
         configs["projections_rows160"] = projections(pieces[0], B * (K + 1), args.steps, args.warmup)
