@@ -24,6 +24,9 @@ rejection rule of its speculative-decoding step, restated on the CPU in FP32
                        the child whose token is the argmax (lowest index among
                        equal children), until none is; then the argmax
     cut                _cut (:338-344): up to the first stop, at most limit
+    schedule           DSpark's prefix scheduler (:236-262): pass widths
+                       admitted from the narrowest while the expected tokens
+                       per second grow, the first that does not stopping it
 """
 
 import torch
@@ -179,3 +182,23 @@ def cut(tokens, stops, limit):
             tokens = tokens[:i + 1]
             break
     return tokens[:limit]
+
+
+def schedule(confidences, caps, costs):
+    """How many drafts of each row one pass verifies (:236-262): width w
+    costs costs[w] seconds and adds, for every row whose cap reaches it, the
+    product of that row's confidences up to draft w - 1 to the expected
+    tokens (one per row to start); widths are admitted while tokens / cost
+    grows."""
+    chances = [1.0] * len(caps)
+    expected = float(len(caps))
+    best, admitted = expected / costs[0], 0
+    for width in range(1, max(caps, default=0) + 1):
+        for r, cap in enumerate(caps):
+            if width <= cap:
+                chances[r] *= confidences[r][width - 1]
+                expected += chances[r]
+        if not expected / costs[width] > best:
+            break
+        best, admitted = expected / costs[width], width
+    return [min(admitted, cap) for cap in caps]

@@ -182,6 +182,43 @@ def test_the_writer_s_cache_holds_each_row_s_text(device):
         assert close(scores[row, 0].cpu(), whole.cpu(), 1e-5)
 
 
+class Confident(Uniform):
+    """Uniform drafts with given confidences, for the prefix scheduler."""
+
+    def __init__(self, confidences):
+        self.confidences = confidences
+
+    def draft(self, model, histories, context, count, probabilities, generator):
+        tokens, q, _ = super().draft(model, histories, context, count, probabilities, generator)
+        return tokens, q, torch.tensor(self.confidences[:len(histories)], device=q.device)[:, :count]
+
+
+def test_the_writer_verifies_the_drafts_the_scheduler_admits(device):
+    # the reference's known answer (test_sampling.py:236): passes cost the
+    # same up to 3 tokens per row, then 20 % more; row 0's confident first
+    # drafts are verified, its unlikely ones not, row 1 only to its cap
+    gpu, _ = models(PLUMBING, torch.float32, std=0.05)
+    costs = [1.0, 1.0, 1.0, 1.2, 1.2, 1.2]
+    outcomes = []
+    writer = Writer(gpu, [0, 5, 7], 2, temperature=1.0, top_k=None, costs=costs, outcomes=outcomes,
+                    generator=torch.Generator(device=device).manual_seed(3),
+                    drafter=Confident([[0.9, 0.9, 0.9, 0.1, 0.1], [0.5] * 5]))
+    written = writer.write({}, {0: 100, 1: 2})
+    assert writer.verified == 2 + 1 and [len(c) for c, _ in outcomes] == [2, 1]
+    assert 1 <= len(written[0]) <= 3 and 1 <= len(written[1]) <= 2
+    assert writer.cache.lengths.tolist() == [len(h) - 1 for h in writer.histories]
+
+
+def test_measured_pass_times_feed_the_scheduler(device):
+    from wpt_amd import scheduling
+
+    gpu, _ = models(PLUMBING, torch.float32)
+    costs = scheduling.measure_costs(gpu, rows=2, draft=4, context=32, repeats=2)
+    assert len(costs) == 5 and all(0 < t < 1.0 for t in costs)
+    setup = scheduling.costs_setup(PLUMBING, 2, 4, device)
+    assert scheduling.replayed_costs(scheduling.costs_file(costs, setup), setup) == costs
+
+
 def test_a_writer_without_drafts_samples_one_token_per_call(device):
     gpu, _ = models(PLUMBING, torch.float32)
     writer = Writer(gpu, [1, 2, 3], 2, generator=torch.Generator(device=device).manual_seed(2))

@@ -4,6 +4,8 @@ rule's invariants (the reference's own statistical and self-drafting tests,
 packages/wpt-inference/tests/test_sampling.py:98-137), a lazy run replayed
 through a tape, greedy chains and trees by brute force, and the cut."""
 
+import math
+
 import pytest
 import torch
 
@@ -178,3 +180,37 @@ def test_cut_stops_after_the_first_stop_and_at_the_limit():
     assert sampling.cut([1, 2, 3, 4], {3}, 10) == [1, 2, 3]
     assert sampling.cut([1, 2, 3, 4], set(), 2) == [1, 2]
     assert sampling.cut([5, 3, 3], {3}, 1) == [5]
+
+
+def test_the_scheduler_s_known_answers():
+    # the reference's own known answers (test_sampling.py:230-238): passes
+    # cost the same up to 3 tokens per row, then 20 % more
+    costs = [1.0, 1.0, 1.0, 1.2, 1.2, 1.2]
+    assert sampling.schedule([[0.9, 0.9, 0.9, 0.1, 0.1], [0.5, 0.5, 0.5, 0.5, 0.5]], [5, 1], costs) == [2, 1]
+    assert sampling.schedule([[0.99] * 5, [0.99] * 5], [5, 5], costs) == [5, 5]
+    assert sampling.schedule([[0.9] * 5], [0], costs) == [0]
+
+
+def test_the_scheduler_stops_at_the_first_width_that_does_not_pay():
+    # brute force over the widths: the admitted width is the longest prefix
+    # of widths along which the expected tokens per second rise at every
+    # step, never a later better one (the early stop); flat costs admit
+    # every draft; caps bound every row
+    import random
+
+    rng = random.Random(5)
+    for _ in range(300):
+        rows, draft = rng.randint(1, 4), rng.randint(0, 5)
+        caps = [rng.randint(0, draft) for _ in range(rows)]
+        conf = [[rng.random() for _ in range(draft)] for _ in range(rows)]
+        costs = sorted(rng.uniform(0.5, 2.0) for _ in range(draft + 1))
+        rates = []
+        for width in range(max(caps, default=0) + 1):
+            tokens = rows + sum(math.prod(conf[r][:j + 1]) for r in range(rows) for j in range(min(width, caps[r])))
+            rates.append(tokens / costs[width])
+        width = 0
+        while width + 1 < len(rates) and rates[width + 1] > rates[width]:
+            width += 1
+        assert sampling.schedule(conf, caps, costs) == [min(width, cap) for cap in caps]
+        assert sampling.schedule(conf, caps, [1.0] * (draft + 1)) == caps or any(
+            c == 0.0 for row in conf for c in row)

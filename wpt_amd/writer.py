@@ -13,16 +13,16 @@ What differs from the reference, by design:
                  draws replays it exactly.
     host syncs   one per step (the written tokens), instead of one per draft
                  token (:213, :215, :219, :222).
-    costs        the DSpark prefix scheduler (:236-262) is not built here;
-                 costs raise NotImplementedError rather than be ignored, and
-                 every draft is verified (as the reference does without
-                 costs or confidences).
+With a drafter that gives confidences and a table of pass times (costs), each
+step verifies only the drafts the prefix scheduler admits
+(wpt_amd.scheduling.schedule, the reference's :236-262), as the reference does.
 """
 
 import torch
 import torch.nn.functional as F
 
 from . import sampling
+from .scheduling import schedule
 
 DRAFT = 5  # draft tokens per row and step (the reference's DRAFT, :67)
 
@@ -46,8 +46,6 @@ class Writer:
             raise ValueError("a prompt holds at least one token")
         if costs is not None and len(costs) < draft + 1:
             raise ValueError(f"costs gives {len(costs)} pass times; drafting {draft} tokens needs {draft + 1}")
-        if costs is not None:
-            raise NotImplementedError("the prefix scheduler (costs) is not built in this writer")
         self.model, self.temperature, self.top_k, self.generator = model, temperature, top_k, generator
         self.stops, self.drafter, self.draft, self.costs = set(stops), drafter, draft, costs
         self.outcomes = outcomes
@@ -126,8 +124,9 @@ class Writer:
         drafted, q, confidences = self.drafter.draft(self.model, [self.histories[row] for row in rows], None,
                                                      self.draft, self._probabilities, self.generator)
         drafted, q = drafted.to(self.device), q.to(self.device).float()
-        caps = [min(self.draft, limits[row] - 1) for row in rows]
-        lengths = caps
+        caps = [min(self.draft, limits[row] - 1) for row in rows]  # a row writes at most its drafts and one more
+        scheduled = confidences is not None and self.costs is not None
+        lengths = schedule(confidences.tolist(), caps, self.costs) if scheduled else caps
         scores, _ = self._read(rows, [drafted[i, :n].tolist() for i, n in enumerate(lengths)], undoable=True)
         firsts = [len(self.pending[row]) - 1 for row in rows]
         L = drafted.shape[1]
