@@ -1,0 +1,109 @@
+"""A stub model and drafters for the Writer's golden token streams: small,
+deterministic, CPU-only, with the reference's model protocol (new_cache /
+extend / undo, model.py:451-483) and drafter protocol
+(wpt_inference/__init__.py:17-33).  Shared by make_writer_vectors.py, which
+runs the reference's own Writer on them, and by the test that replays the
+streams through the oracle."""
+
+from types import SimpleNamespace
+
+import torch
+
+
+class Rows:
+    """A cache of lengths only: the stub model's scores do not depend on the
+    text before a token."""
+
+    def __init__(self, rows):
+        self.lengths = torch.zeros(rows, dtype=torch.long)
+        self.before = None
+        self.routes = None
+
+    def select(self, index):
+        copy = Rows(len(index))
+        copy.lengths = self.lengths[torch.as_tensor(index, dtype=torch.long)]
+        return copy
+
+
+class Bigram:
+    """scores of a token = a fixed row of a (V, V) table (times 3, so that
+    the distributions are peaked): the next-token scores depend on the last
+    token only."""
+
+    def __init__(self, vocab=50, seed=0):
+        generator = torch.Generator().manual_seed(seed)
+        self.table = torch.randn(vocab, vocab, generator=generator) * 3
+        self.config = SimpleNamespace(d_model=1, vocab=vocab)
+
+    def parameters(self):
+        return iter([self.table])
+
+    def new_cache(self, rows, routes=False):
+        return Rows(rows)
+
+    def extend(self, ids, cache, counts=None, undoable=False, features=()):
+        B, n = ids.shape
+        counts = torch.full((B,), n) if counts is None else torch.as_tensor(counts)
+        if undoable:
+            cache.before = cache.lengths.clone()
+        cache.lengths = cache.lengths + counts
+        scores = self.table[ids].float()
+        return scores, scores
+
+    def undo(self, cache, kept):
+        cache.lengths = cache.before + torch.as_tensor(kept)
+        cache.before = None
+
+    def __call__(self, ids):
+        return self.table[ids].float()
+
+
+class UniformDrafter:
+    """Drafts uniform over the vocabulary, drawn from the writer's generator."""
+    features, window = (), 0
+
+    def draft(self, model, histories, context, count, probabilities, generator):
+        V = model.config.vocab
+        tokens = torch.randint(V, (len(histories), count), generator=generator)
+        return tokens, torch.full((len(histories), count, V), 1.0 / V), None
+
+
+class SkewedDrafter:
+    """Drafts from the model's own scores plus fixed noise (std 1 against the
+    table's 3), at the writer's temperature and top-k, so that drafts are
+    kept and rejected in a mix; the draws come from the writer's generator,
+    one multinomial per draft."""
+    features, window = (), 0
+
+    def __init__(self, vocab=50, seed=1):
+        self.noise = torch.randn(vocab, vocab, generator=torch.Generator().manual_seed(seed))
+
+    def draft(self, model, histories, context, count, probabilities, generator):
+        tokens, distributions = [], []
+        for history in histories:
+            last = history[-1]
+            row = []
+            for _ in range(count):
+                q = probabilities(model.table[last] + self.noise[last])
+                last = int(torch.multinomial(q, 1, generator=generator))
+                row.append(last)
+                distributions.append(q)
+            tokens.append(row)
+        return torch.tensor(tokens), torch.stack(distributions).view(len(histories), count, -1), None
+
+
+def cases():
+    """The streams: (name, writer arguments, drafter, calls of write)."""
+    return [
+        ("uniform_drafts_top_k_40", dict(rows=3, temperature=0.8, top_k=40, draft=4), "uniform",
+         [{0: 6, 1: 6, 2: 2}] * 4),
+        ("skewed_drafts_no_top_k", dict(rows=3, temperature=1.0, top_k=None, draft=4), "skewed",
+         [{0: 6, 1: 3, 2: 6}] * 5),
+        ("skewed_drafts_top_k_5_t0.7", dict(rows=2, temperature=0.7, top_k=5, draft=5), "skewed",
+         [{0: 7, 1: 7}] * 6),
+        ("no_drafter_top_k_10", dict(rows=2, temperature=0.9, top_k=10, draft=4), None, [{0: 1, 1: 1}] * 5),
+    ]
+
+
+def drafter(kind):
+    return {"uniform": UniformDrafter, "skewed": SkewedDrafter}[kind]() if kind else None
