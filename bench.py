@@ -354,12 +354,12 @@ def projections(model, rows, steps, warmup):
     generator = torch.Generator(device=device).manual_seed(7)
     out = {}
     kinds = [("qkv", cfg.d_model, "build split-K (parts)"), ("out", cfg.heads * cfg.head_dim, "build split-K (parts)"),
-             ("gate_up", cfg.d_model, "hipBLASLt"), ("down", cfg.ffn, "build split-K (parts)")]
+             ("gate_up_tiles", cfg.d_model, "build, SwiGLU in the epilogue"), ("down", cfg.ffn, "build split-K (parts)")]
     for name, K, engine in kinds:
         x = torch.randn(rows, K, generator=generator, device=device).to(torch.bfloat16)
         ws = [model.w[f"layers.{i}.{name}"] for i in range(cfg.layers)]
-        if engine == "hipBLASLt":
-            calls = [lambda w=w: F.linear(x, w) for w in ws]
+        if engine.startswith("build, SwiGLU"):
+            calls = [lambda w=w: layers.linear_swiglu(x, w) for w in ws]
         else:
             calls = [lambda w=w: layers.linear_parts(x, w) for w in ws]
         replay = graphed(lambda: [f() for f in calls])

@@ -268,6 +268,16 @@ int wptv_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int
 int wptv_gemm_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K, int splits,
                     float* parts, size_t parts_bytes, hipStream_t stream);
 
+/* wptv_gemm_swiglu: the feed-forward block's gate/up product with SwiGLU in
+ * its epilogue (layers.py:45-61: silu(gate(x)) * up(x)), one part of K:
+ * out bf16 [M, N / 2] (leading dimension ldo) = silu(g) * u of the product's
+ * bf16-rounded gate g and up u, rounded once (the values wptv_gemm then
+ * wptv_swiglu give).  w holds the gate and up rows interleaved by tiles of
+ * 64: rows 64 t .. 64 t + 31 are the gate rows of features 32 t .. 32 t + 31,
+ * rows 64 t + 32 .. 64 t + 63 their up rows (N a multiple of 64). */
+int wptv_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K, void* out,
+                     int64_t ldo, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Acceptance: the reference's per-row verification loop of
  * Writer._speculate (packages/wpt-inference/src/wpt_inference/__init__.py:

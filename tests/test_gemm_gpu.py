@@ -88,3 +88,20 @@ def test_parts_sum_to_the_product_and_feed_the_norm(device):
     # the same bf16 delta up to the order of the FP32 part sums
     assert (h1.float() - h2.float()).abs().max() <= 2e-2 * h2.float().abs().max()
     assert relative_error(y1.float().cpu(), y2.float().cpu()) < 1e-2
+
+
+@pytest.mark.parametrize("M", [1, 5, 160, 320, 512])
+def test_the_fused_swiglu_product_equals_the_product_then_swiglu(device, M):
+    # the epilogue rounds the gate and up halves to bf16 as the product's
+    # bf16 output holds them, then silu(g) * u rounded once: bit for bit the
+    # product followed by wptv_swiglu
+    from wpt_amd import layers
+
+    generator = torch.Generator().manual_seed(M)
+    F, K = 512, 256
+    x = torch.randn(M, K, generator=generator).to(torch.bfloat16).to(device)
+    w = (torch.randn(2 * F, K, generator=generator) * 0.05).to(torch.bfloat16).to(device)
+    expected = layers.swiglu(layers.linear(x, w, splits=1))
+    got = layers.linear_swiglu(x, layers.interleave_gate_up(w))
+    assert got.shape == (M, F) and got.dtype == torch.bfloat16
+    assert torch.equal(got, expected)

@@ -51,6 +51,7 @@ SIGNATURES = {
     "wptv_swiglu": [_P, _P, _I, _I, _I, _P],
     "wptv_gemm_workspace": [_I, _I, _I, _P, _P],
     "wptv_gemm": [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _I, _I, _P, _SZ, _P],
+    "wptv_gemm_swiglu": [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _P],
     "wptv_gemm_parts": [_P, _I64, _P, _I64, _I, _I, _I, _I, _P, _SZ, _P],
     "wptv_add_rms_norm_parts": [_P, _P, _I, _P, _P, _I, _I, _I, _F, _P],
     "wptv_qkv_post_parts": [_P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I, _I, _F, _P],

@@ -68,12 +68,21 @@ __device__ __forceinline__ void wait_chunks_behind(int behind) {
     wait_vmcnt<0>();
 }
 
-enum GemmOut { kPartF32 = 0, kOutBf16 = 1, kOutF32 = 2 };
+enum GemmOut { kPartF32 = 0, kOutBf16 = 1, kOutF32 = 2, kOutSwiGLU = 3 };
+
+// silu(g) * u of the bf16-rounded halves, rounded once to bf16: what the
+// product rounded to bf16 and then wptv_swiglu give.
+__device__ __forceinline__ unsigned short swiglu_bf16(float g, float u) {
+  const float gb = bf16_to_f32(f32_to_bf16(g)), ub = bf16_to_f32(f32_to_bf16(u));
+  return f32_to_bf16(gb / (1.f + expf(-gb)) * ub);
+}
 
 // grid: (N / 64, splits).  Split z multiplies K chunks [z cps, min((z + 1) cps, K / 64)).
 // OUT: kPartF32 -> part[z][m][n] FP32; kOutBf16 -> out bf16; kOutF32 -> out
 // FP32 holding the bf16-rounded product (the reference's bf16 product cast to
-// FP32).
+// FP32); kOutSwiGLU -> out bf16 [M, N / 2] = silu(gate) * up, the weight's 64
+// rows of a column tile being 32 gate rows then the 32 up rows of the same
+// features (wptv_gemm_swiglu).
 template <int R32, int OUT>
 __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned short* __restrict__ x, int64_t ldx,
                                                                const unsigned short* __restrict__ w, int64_t ldw,
@@ -171,6 +180,18 @@ __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned sh
   for (int ii = 0; ii < MBW; ++ii) {
     const int m = 16 * (mb0 + ii) + j;
     if (ii >= nblk || m >= M) continue;
+    if constexpr (OUT == kOutSwiGLU) {
+      // blocks 0, 1: gate of features n0 / 2 + 16 nb + 4 g .. + 3; blocks 2, 3: their up
+      typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const f32x4 gv = acc[ii][nb], uv = acc[ii][nb + 2];
+        unsigned short* dst = static_cast<unsigned short*>(out) + (int64_t)m * ldo + n0 / 2 + 16 * nb + 4 * g;
+        *reinterpret_cast<u16x4*>(dst) = u16x4{swiglu_bf16(gv[0], uv[0]), swiglu_bf16(gv[1], uv[1]),
+                                               swiglu_bf16(gv[2], uv[2]), swiglu_bf16(gv[3], uv[3])};
+      }
+      continue;
+    }
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int n = n0 + 16 * nb + 4 * g;
@@ -310,6 +331,24 @@ extern "C" int wptv_gemm_parts(const void* x, int64_t ldx, const void* w, int64_
   dim3 grid(N / kTileN, p.splits);
   launch_gemm_rows<kPartF32>(p.r32, grid, stream, static_cast<const unsigned short*>(x), ldx,
                             static_cast<const unsigned short*>(w), ldw, M, N, K, p.cps, parts, 0);
+  return launched("gemm_xwt");
+}
+
+extern "C" int wptv_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K, void* out,
+                                int64_t ldo, hipStream_t stream) {
+  if (!x || !w || !out) return fail(WPTV_E_INVALID, "gemm_swiglu: x, w and out must be given");
+  GemmPlan p;
+  const int st = gemm_plan(M, N, K, 1, &p);  // one part: the epilogue needs the whole sum
+  if (st != WPTV_OK) return st;
+  if (ldx < K || ldw < K || ldo < N / 2)
+    return fail(WPTV_E_INVALID, "gemm_swiglu: a leading dimension below the row width");
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 8) || ldx % 8 || ldw % 8 || ldo % 4)
+    return fail(WPTV_E_INVALID, "gemm_swiglu: x and w 16-byte aligned, leading dimensions of 8 (out: 4) elements");
+  if ((double)N * (double)ldw * 2.0 >= 4.0e9 || (double)M * (double)ldx * 2.0 >= 4.0e9)
+    return fail(WPTV_E_UNSUPPORTED, "gemm_swiglu: operands above 4 GB");
+  dim3 grid(N / kTileN, 1);
+  launch_gemm_rows<kOutSwiGLU>(p.r32, grid, stream, static_cast<const unsigned short*>(x), ldx,
+                               static_cast<const unsigned short*>(w), ldw, M, N, K, p.cps, out, ldo);
   return launched("gemm_xwt");
 }
 

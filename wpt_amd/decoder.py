@@ -22,8 +22,9 @@ On the GPU:
     projections     the matrix products of the dtype on MFMA: wptv_gemm's
                     split-K parts for q/k/v, output and down at up to
                     SPLIT_K_ROWS bf16 rows (summed by qkv_post and the
-                    residual add + norm), hipBLASLt otherwise and for the
-                    gate/up product and the lm_head
+                    residual add + norm), the gate/up product with SwiGLU in
+                    its epilogue (wptv_gemm_swiglu) at up to 512 bf16 rows,
+                    hipBLASLt otherwise and for the lm_head
     window layers   wptv_window_qkv_post (norms, rotary encoding, the ring
                     append), wptv_window_attention over the cache's ring with
                     the sink and the output gate fused
@@ -124,6 +125,9 @@ class MQADecoder:
             self.w[name] = value.to(device=self.device, dtype=torch.float32 if keep_fp32 else dtype).contiguous()
         for i in config.windows:  # one projection for q, k, v and the gate
             self.w[f"layers.{i}.qkvg"] = torch.cat([self.w[f"layers.{i}.qkv"], self.w[f"layers.{i}.gate"]]).contiguous()
+        if dtype == torch.bfloat16:  # the gate/up rows in the order the fused SwiGLU product reads
+            for i in range(config.layers):
+                self.w[f"layers.{i}.gate_up_tiles"] = layers.interleave_gate_up(self.w[f"layers.{i}.gate_up"])
 
     def parameters(self):
         return iter(self.w.values())
@@ -153,7 +157,10 @@ class MQADecoder:
             self._window_attention(i, h, x, cache, positions, counts)
         else:
             self._exact_attention(i, h, x, cache, positions, counts)
-        act = layers.swiglu(F.linear(x, w[f"layers.{i}.gate_up"]))
+        if x.dtype == torch.bfloat16 and B * T <= layers.LINEAR_MAX_ROWS:
+            act = layers.linear_swiglu(x, w[f"layers.{i}.gate_up_tiles"])  # SwiGLU in the product's epilogue
+        else:
+            act = layers.swiglu(F.linear(x, w[f"layers.{i}.gate_up"]))
         down = w[f"layers.{i}.down"]
         if x.dtype == torch.bfloat16 and B * T <= SPLIT_K_ROWS:
             layers.add_rms_norm_parts(h, layers.linear_parts(act, down), next_norm, x)

@@ -155,6 +155,39 @@ def linear(x, w, out_dtype=None, splits=0):
     return out.reshape(*x.shape[:-1], N)
 
 
+def interleave_gate_up(gate_up):
+    """(2F, K) gate rows then up rows -> the tile-interleaved order
+    linear_swiglu reads: for each 32 features, their 32 gate rows then their
+    32 up rows (F a multiple of 32)."""
+    F2, K = gate_up.shape
+    F = F2 // 2
+    if F2 % 2 or F % 32:
+        raise ValueError(f"gate_up must hold 2F rows, F a multiple of 32; got {F2}")
+    gate, up = gate_up[:F].view(F // 32, 32, K), gate_up[F:].view(F // 32, 32, K)
+    return torch.cat([gate, up], 1).reshape(F2, K).contiguous()
+
+
+def linear_swiglu(x, w_interleaved):
+    """silu(x . gate^T) * (x . up^T) of x (..., K) and the interleaved gate/up
+    weight (2F, K) (interleave_gate_up), on the matrix cores with SwiGLU in
+    the product's epilogue: bf16 (..., F).  At most 512 rows."""
+    _gpu(x, w_interleaved)
+    if x.dtype != torch.bfloat16 or w_interleaved.dtype != torch.bfloat16:
+        raise ValueError(f"linear_swiglu takes bf16 operands; got {x.dtype} and {w_interleaved.dtype}")
+    K = x.shape[-1]
+    N = w_interleaved.shape[0]
+    if w_interleaved.dim() != 2 or w_interleaved.shape[1] != K or w_interleaved.stride(1) != 1:
+        raise ValueError(f"w must be (2F, K={K}) with contiguous rows; got {tuple(w_interleaved.shape)}")
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    out = torch.empty(M, N // 2, dtype=torch.bfloat16, device=x.device)
+    check(_lib.lib().wptv_gemm_swiglu(ptr(x2), x2.stride(0), ptr(w_interleaved), w_interleaved.stride(0), M, N, K,
+                                      ptr(out), out.stride(0), _lib.stream(x.device)), "gemm_swiglu")
+    return out.reshape(*x.shape[:-1], N // 2)
+
+
 def linear_parts(x, w, splits=0, max_splits=8):
     """The split-K parts of x (..., K) . w (N, K)^T: FP32 (S, rows, N) whose
     sum over S is the product (wptv_gemm_parts), for a consumer that sums them
