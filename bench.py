@@ -207,7 +207,9 @@ def attention_c3(steps, warmup):
                                                       c ** -0.5, W))
     ms = timed(replay, steps, warmup)
     nbytes = B * (W + T - 1) * 2 * c * 2 + 2 * B * T * H * c * 2 + B * T * 8
-    return {"ms": ms, "bytes": nbytes, "GBps": nbytes / (ms * 1e-3) / 1e9, "query_tokens_per_s": B * T / (ms * 1e-3)}
+    GBps = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": ms, "bytes": nbytes, "GBps": GBps, "frac_hbm_peak": GBps / HBM_PEAK_GBS,
+            "query_tokens_per_s": B * T / (ms * 1e-3), "note": "launch-latency-bound: 4.5 MB"}
 
 
 def tree_c4(steps, warmup):
@@ -283,20 +285,49 @@ def wpt_layers(steps, warmup):
         replay = graphed(lambda: [fn(i % 4) for i in range(calls)])
         return timed(replay, max(1, steps // 4), max(1, warmup // 4)) / calls
 
+    def entry(ms, nbytes, cpu_s):
+        GBps = nbytes / (ms * 1e-3) / 1e9
+        return {"us": ms * 1e3, "bytes": nbytes, "GBps": GBps, "frac_hbm_peak": GBps / HBM_PEAK_GBS,
+                "cpu_oracle_us": cpu_s * 1e6}
+
+    # the oracle (FP32, this host's cores) on 2 of the 32 batch rows, scaled to the batch
+    from oracle import attention as oracle_attention
+
+    rows = 2
+    qc, tc = q[:rows].float().cpu(), tables[0][:rows].float().cpu()
+    pc, sc, gc = positions[:rows].cpu(), sink.cpu(), gate[:rows].float().cpu()
+    ic, rc = chosen[0][:rows].cpu(), rings[0][:rows].float().cpu()
+    ring_table = torch.stack([rc[b, [(int(pc[b, 0]) - W + 1 + j) % 256 for j in range(W - 1 + T)]]
+                              for b in range(rows)])
+
+    def cpu(fn):
+        best = float("inf")
+        for _ in range(2):
+            start = time.perf_counter()
+            fn()
+            best = min(best, time.perf_counter() - start)
+        return best * B / rows
+
     out = {}
     ms = per_call(lambda i: kernels.exact_attention(q, tables[i][..., :c], tables[i][..., c:], positions, c ** -0.5,
                                                     TOPK, W))
     nbytes = attention_bytes(B, T, H, c, N) + B * N * c * 2 + 2 * B * T * N * 4 + B * T * TOPK * 8
-    out["exact_layer_attention_and_choice_top1024"] = {"us": ms * 1e3, "bytes": nbytes,
-                                                       "GBps": nbytes / (ms * 1e-3) / 1e9}
+    out["exact_layer_attention_and_choice_top1024"] = entry(
+        ms, nbytes, cpu(lambda: oracle_attention.exact_attention(qc, tc[..., :c], tc[..., c:], pc, c ** -0.5, TOPK, W)))
     ms = per_call(lambda i: kernels.sparse_attention(q, tables[i][..., :c], tables[i][..., c:], sink, chosen[i],
                                                      positions, c ** -0.5, W, gate=gate))
     nbytes = B * T * (TOPK + W) * 2 * c * 2 + io + B * T * TOPK * 8 + B * T * H * c * 2
-    out["sparse_layer_1024_chosen_plus_window_128"] = {"us": ms * 1e3, "bytes_gathered": nbytes,
-                                                       "GBps": nbytes / (ms * 1e-3) / 1e9}
+    out["sparse_layer_1024_chosen_plus_window_128"] = entry(
+        ms, nbytes, cpu(lambda: oracle_attention.sparse_attention(qc, tc[..., :c], tc[..., c:], sc, ic, pc, c ** -0.5,
+                                                                  W) * torch.sigmoid(gc).view(rows, T, H, c)))
     ms = per_call(lambda i: kernels.ring_attention(q, rings[i], positions, c ** -0.5, W, sink, gate=gate))
     nbytes = B * (W + T - 1) * 2 * c * 2 + io + B * T * H * c * 2
-    out["window_layer_ring_window_128"] = {"us": ms * 1e3, "bytes": nbytes, "GBps": nbytes / (ms * 1e-3) / 1e9}
+    out["window_layer_ring_window_128"] = entry(
+        ms, nbytes, cpu(lambda: oracle_attention.window_attention(qc, ring_table[..., :c], ring_table[..., c:], sc, pc,
+                                                                  c ** -0.5, W) * torch.sigmoid(gc).view(rows, T, H, c)))
+    out["note"] = ("bytes: algorithmic (the sparse layer counts each query's gathered rows); cpu_oracle_us: the "
+                   f"oracle in FP32 on {rows} of the {B} batch rows, scaled to the batch, on "
+                   f"{torch.get_num_threads()} host threads")
     return out
 
 
@@ -464,12 +495,18 @@ def main():
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--quick", action="store_true",
                         help="the headline step and its roofline only (no other configs, no CPU baseline)")
+    parser.add_argument("--wpt-layers", action="store_true",
+                        help="only the WPT attention layers at the verify shape (exact + choice, sparse, window); "
+                             "prints their JSON")
     parser.add_argument("--pmc-workload", action="store_true",
                         help="for a counter pass: five verify-attention calls of the roofline shape, then five "
                              "plain 64 MiB device copies (the counters' calibration); prints no JSON")
     args = parser.parse_args()
     if args.pmc_workload:
         pmc_workload()
+        return
+    if args.wpt_layers:
+        print(json.dumps(wpt_layers(args.steps, args.warmup)), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the verify step here is built and timed on a single MI355X "

@@ -214,7 +214,7 @@ def sparse_attention(q, k, v, sink, idx, positions, scale, window, *, gate=None,
     return _forward_only(out, q, k, v, sink)
 
 
-def _window_call(q, k, v, sink, positions, scale, window, row_base, ring_rows, gate):
+def _window_call(q, k, v, sink, positions, scale, window, row_base, ring_rows, gate, splits=0):
     B, T, H, c = q.shape
     device = q.device
     if not (q.dtype == k.dtype == v.dtype) or k.dim() != 3 or k.shape != v.shape or k.shape[0] != B or \
@@ -236,7 +236,7 @@ def _window_call(q, k, v, sink, positions, scale, window, row_base, ring_rows, g
         gate_stride = gate.stride(1)
     library = _lib.lib()
     dtype = _lib.dtype_code(q.dtype)
-    parts = _lib.ctypes.c_int(0)
+    parts = _lib.ctypes.c_int(int(splits))
     size = _lib.ctypes.c_size_t(0)
     check(library.wptv_window_attention_workspace(B, T, H, c, int(window), dtype, _lib.ctypes.byref(parts),
                                                   _lib.ctypes.byref(size)), "window_attention")
@@ -265,12 +265,13 @@ def window_attention(q, k, v, sink, positions, scale, window=128, gate=None):
     return _window_call(q, k, v, sink, positions, scale, window, row_base, k.shape[1], gate)
 
 
-def ring_attention(q, ring, positions, scale, window, sink, gate=None):
+def ring_attention(q, ring, positions, scale, window, sink, gate=None, splits=0):
     """A window layer's attention over its cache ring (B, R, 2c), R a power
     of 2 of at least window - 1 + T, token n at row n mod R (keys then
     values): window_attention's result from the build's ring cache."""
     c = q.shape[-1]
-    return _window_call(q, ring[..., :c], ring[..., c:], sink, positions, scale, window, None, ring.shape[1], gate)
+    return _window_call(q, ring[..., :c], ring[..., c:], sink, positions, scale, window, None, ring.shape[1], gate,
+                        splits)
 
 
 def tree_ancestors(parents):
