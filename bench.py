@@ -137,7 +137,8 @@ def decoder_step(B, kv, k, steps, warmup, temperature=0.8, top_k=None, seed=0, k
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
     tokens = int(written.sum())
-    params = sum(w.numel() for name, w in model.w.items() if not name.endswith("norm"))
+    params = sum(w.numel() for name, w in model.w.items()  # the matrices a step reads whole
+                 if not name.endswith("norm") and name != "embedding")
     out = {"ms_per_step": ms, "accepted_tokens": tokens, "tokens_per_s": tokens / (steps * ms * 1e-3),
            "tokens_per_row_step": tokens / (steps * B), "weight_bytes": 2 * params,
            "lengths_after": int(cache.lengths.max())}

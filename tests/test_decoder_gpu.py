@@ -219,6 +219,17 @@ def test_measured_pass_times_feed_the_scheduler(device):
     assert scheduling.replayed_costs(scheduling.costs_file(costs, setup), setup) == costs
 
 
+def test_a_wide_bf16_reading_matches_reading_in_pieces(device):
+    # more than 512 rows take the product then SwiGLU of its interleaved
+    # halves, fewer the fused product: the same scores either way
+    gpu, _ = models(SMALL_BF16, torch.bfloat16)
+    ids = torch.randint(SMALL_BF16.vocab, (2, 300), generator=torch.Generator().manual_seed(9)).to(device)
+    whole = gpu(ids)  # 600 rows in one reading
+    cache = gpu.new_cache(2, capacity=300)
+    pieces = torch.cat([gpu.extend(ids[:, a:a + 100], cache)[0] for a in range(0, 300, 100)], 1)  # 200 rows each
+    assert close(pieces.cpu(), whole.cpu(), 2e-2)
+
+
 def test_a_writer_without_drafts_samples_one_token_per_call(device):
     gpu, _ = models(PLUMBING, torch.float32)
     writer = Writer(gpu, [1, 2, 3], 2, generator=torch.Generator(device=device).manual_seed(2))

@@ -125,9 +125,9 @@ class MQADecoder:
             self.w[name] = value.to(device=self.device, dtype=torch.float32 if keep_fp32 else dtype).contiguous()
         for i in config.windows:  # one projection for q, k, v and the gate
             self.w[f"layers.{i}.qkvg"] = torch.cat([self.w[f"layers.{i}.qkv"], self.w[f"layers.{i}.gate"]]).contiguous()
-        if dtype == torch.bfloat16:  # the gate/up rows in the order the fused SwiGLU product reads
+        if dtype == torch.bfloat16:  # the gate/up rows in the order the fused SwiGLU product reads, kept instead
             for i in range(config.layers):
-                self.w[f"layers.{i}.gate_up_tiles"] = layers.interleave_gate_up(self.w[f"layers.{i}.gate_up"])
+                self.w[f"layers.{i}.gate_up_tiles"] = layers.interleave_gate_up(self.w.pop(f"layers.{i}.gate_up"))
 
     def parameters(self):
         return iter(self.w.values())
@@ -157,10 +157,13 @@ class MQADecoder:
             self._window_attention(i, h, x, cache, positions, counts)
         else:
             self._exact_attention(i, h, x, cache, positions, counts)
-        if x.dtype == torch.bfloat16 and B * T <= layers.LINEAR_MAX_ROWS:
-            act = layers.linear_swiglu(x, w[f"layers.{i}.gate_up_tiles"])  # SwiGLU in the product's epilogue
-        else:
+        if x.dtype != torch.bfloat16:
             act = layers.swiglu(F.linear(x, w[f"layers.{i}.gate_up"]))
+        elif B * T <= layers.LINEAR_MAX_ROWS:
+            act = layers.linear_swiglu(x, w[f"layers.{i}.gate_up_tiles"])  # SwiGLU in the product's epilogue
+        else:  # wider readings (a prefill): the product, then SwiGLU of its tile-interleaved halves
+            gu = F.linear(x, w[f"layers.{i}.gate_up_tiles"]).unflatten(-1, (-1, 2, 32))
+            act = (F.silu(gu[..., 0, :].float()) * gu[..., 1, :].float()).flatten(-2).to(x.dtype)
         down = w[f"layers.{i}.down"]
         if x.dtype == torch.bfloat16 and B * T <= SPLIT_K_ROWS:
             layers.add_rms_norm_parts(h, layers.linear_parts(act, down), next_norm, x)
