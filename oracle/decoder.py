@@ -15,7 +15,13 @@ attention.py:109-151): q = rotate(q_norm(q(x))), entries
 [rotate(k_norm(k(x))), v(x)] at the tokens' positions, the window - 1 entries
 carried from before (the cache's tail, cache.py:97-108) joined in front,
 window attention with a sink per head, and the output times sigmoid(gate(x))
-before the output projection.
+before the output projection.  Or the reference's sparse layer
+(SparseAttention, attention.py:190-215): q = q_norm(q(x)), sparse attention
+over the keys and values of the last exact layer's table at the rows that
+layer chose for each query plus each query's last window rows, a sink per
+head, the same gate.  An exact layer chooses (top_k rows) when a sparse layer
+follows it (model.py:134-135); the handoff is the last exact layer's
+(model.py:411-423).
 
 Weights are a dict of tensors (any dtype; used in FP32):
     embedding (V, D); head (V, D); final_norm (D,)
@@ -25,6 +31,7 @@ Weights are a dict of tensors (any dtype; used in FP32):
     layers.{i}.gate_up (2F, D): gate rows, then up rows
     layers.{i}.down (D, F)
     window layers also: layers.{i}.gate (H*c, D), layers.{i}.sink (H,)
+    sparse layers: layers.{i}.q (H*c, D) in place of qkv, no k_norm; gate, sink
 """
 
 import torch
@@ -40,25 +47,41 @@ def rms_norm(x, weight):
 
 
 class Decoder:
-    def __init__(self, weights, layers, heads, head_dim, kinds=(), window=128, rope_dims=64, rope_base=10000.0):
+    def __init__(self, weights, layers, heads, head_dim, kinds=(), window=128, rope_dims=64, rope_base=10000.0,
+                 top_k=1024):
         self.w = {name: value.float() for name, value in weights.items()}
         self.layers, self.heads, self.head_dim = layers, heads, head_dim
         self.kinds = tuple(kinds) or ("exact",) * layers
         self.window, self.rope_dims, self.rope_base = window, rope_dims, rope_base
+        self.top_k = top_k
+        # bf16 scores of two implementations may order near ties of the
+        # choice another way: a test may give a choosing layer's rows
+        # (given[i], (B, T, K) with -1 past a query's rows) for the sparse
+        # layers to read instead of the layer's own, after checking them
+        # against the layer's own choice kept in choices[i] = (chosen, q,
+        # keys, positions) of the last reading
+        self.given, self.choices = {}, {}
 
     def new_cache(self, rows):
         return cache.Rows(rows)
 
-    def _layer(self, i, h, reading):
+    def _layer(self, i, h, reading, handoff):
+        """(h after layer i, the handoff for the layers after it)."""
         w = lambda name: self.w[f"layers.{i}.{name}"]  # noqa: E731
         B, T, _ = h.shape
         H, c = self.heads, self.head_dim
         x = rms_norm(h, w("attn_norm"))
+        positions = reading.positions(T)
+        if self.kinds[i] == "sparse":
+            q = rms_norm((x @ w("q").T).reshape(B, T, H, c), w("q_norm"))
+            keys, values, chosen = handoff
+            o = attention.sparse_attention(q, keys, values, w("sink"), chosen, positions, c ** -0.5, self.window)
+            o = o * torch.sigmoid(x @ w("gate").T).reshape(B, T, H, c)
+            return self._rest(i, h, o), handoff
         qkv = x @ w("qkv").T
         q = rms_norm(qkv[..., :H * c].reshape(B, T, H, c), w("q_norm"))
         k = rms_norm(qkv[..., H * c:H * c + c], w("k_norm"))
         v = qkv[..., H * c + c:]
-        positions = reading.positions(T)
         if self.kinds[i] == "window":
             W = self.window
             q = attention.rotate(q, positions, self.rope_dims, self.rope_base)
@@ -68,7 +91,19 @@ class Decoder:
             o = o * torch.sigmoid(x @ w("gate").T).reshape(B, T, H, c)
         else:
             table = reading.everything(("entries", i), torch.cat([k, v], -1))
-            o, _ = attention.exact_attention(q, table[..., :c], table[..., c:], positions, c ** -0.5, 0, 128)
+            chooses = i + 1 < self.layers and self.kinds[i + 1] == "sparse"
+            o, chosen = attention.exact_attention(q, table[..., :c], table[..., c:], positions, c ** -0.5,
+                                                  self.top_k if chooses else 0, self.window)
+            if chooses:
+                self.choices[i] = (chosen, q, table[..., :c], positions)
+                chosen = self.given.get(i, chosen)
+            handoff = (table[..., :c], table[..., c:], chosen)
+        return self._rest(i, h, o), handoff
+
+    def _rest(self, i, h, o):
+        """The output projection's residual add, then the feed-forward block."""
+        w = lambda name: self.w[f"layers.{i}.{name}"]  # noqa: E731
+        B, T, H, c = o.shape
         h = h + o.reshape(B, T, H * c) @ w("out").T
         x = rms_norm(h, w("ffn_norm"))
         gate, up = (x @ w("gate_up").T).chunk(2, -1)
@@ -81,8 +116,9 @@ class Decoder:
         counts = torch.full((ids.shape[0],), ids.shape[1]) if counts is None else torch.as_tensor(counts)
         reading = rows.reading(counts, undoable)
         h = self.w["embedding"][ids]
+        handoff = None
         for i in range(self.layers):
-            h = self._layer(i, h, reading)
+            h, handoff = self._layer(i, h, reading, handoff)
         scores = rms_norm(h, self.w["final_norm"]) @ self.w["head"].T
         reading.finish()
         return scores, h

@@ -3,8 +3,9 @@ pieces gives the scores of reading it whole (the reference's
 test_cache.py:74-143), rows sharing one prompt go on apart (:173-203), and
 undoing rejected drafts leaves the cache as if only the kept tokens had been
 read (:206-238); tails cut back as carry.last says.  Each holds for the
-exact layers' entries and for the window layers' carried tails (a window of
-8 rows, smaller than the pieces, so that the tails matter)."""
+exact layers' entries, for the window layers' carried tails (a window of
+8 rows, smaller than the pieces, so that the tails matter) and for sparse
+layers reading an exact layer's choice of 4 rows outside that window."""
 
 import pytest
 import torch
@@ -12,7 +13,7 @@ import torch
 from oracle import cache, decoder
 
 PIECES = [37, 1, 1, 5, 100, 1, 155]
-LAYERS, D, H, C, FFN, V = 2, 64, 4, 16, 96, 50
+LAYERS, D, H, C, FFN, V = 3, 64, 4, 16, 96, 50
 
 
 def weights(seed=0):
@@ -30,21 +31,23 @@ def weights(seed=0):
         w[f"layers.{i}.down"] = torch.randn(D, FFN, generator=generator) * 0.1
         w[f"layers.{i}.gate"] = torch.randn(H * C, D, generator=generator) * 0.2
         w[f"layers.{i}.sink"] = torch.randn(H, generator=generator)
+        w[f"layers.{i}.q"] = torch.randn(H * C, D, generator=generator) * 0.2
     return w
 
 
-KINDS = [(), ("window", "exact")]
+KINDS = [(), ("window", "exact", "exact"), ("window", "exact", "sparse")]
+IDS = ["exact", "window+exact", "window+exact+sparse"]
 
 
 def model(kinds=()):
-    return decoder.Decoder(weights(), LAYERS, H, C, kinds=kinds, window=8, rope_dims=8)
+    return decoder.Decoder(weights(), LAYERS, H, C, kinds=kinds, window=8, rope_dims=8, top_k=4)
 
 
 def close(got, expected, share=1e-5):
     return (got - expected).abs().max() <= share * expected.abs().max()
 
 
-@pytest.mark.parametrize("kinds", KINDS, ids=["exact", "window+exact"])
+@pytest.mark.parametrize("kinds", KINDS, ids=IDS)
 def test_reading_in_pieces_gives_the_whole_text_s_scores(kinds):
     m = model(kinds)
     ids = torch.randint(V, (2, sum(PIECES)), generator=torch.Generator().manual_seed(1))
@@ -57,7 +60,7 @@ def test_reading_in_pieces_gives_the_whole_text_s_scores(kinds):
     assert close(torch.cat(got, 1), whole)
 
 
-@pytest.mark.parametrize("kinds", KINDS, ids=["exact", "window+exact"])
+@pytest.mark.parametrize("kinds", KINDS, ids=IDS)
 def test_a_shared_prompt_and_rows_at_different_places(kinds):
     m = model(kinds)
     generator = torch.Generator().manual_seed(2)
@@ -81,7 +84,7 @@ def test_a_shared_prompt_and_rows_at_different_places(kinds):
     assert shared.lengths.tolist() == [len(prompt)]
 
 
-@pytest.mark.parametrize("kinds", KINDS, ids=["exact", "window+exact"])
+@pytest.mark.parametrize("kinds", KINDS, ids=IDS)
 def test_undoing_rejected_drafts_leaves_only_the_kept_tokens(kinds):
     m = model(kinds)
     generator = torch.Generator().manual_seed(3)
@@ -105,7 +108,7 @@ def test_undoing_rejected_drafts_leaves_only_the_kept_tokens(kinds):
         assert close(torch.cat(got[row]), whole[60:])
 
 
-@pytest.mark.parametrize("kinds", KINDS, ids=["exact", "window+exact"])
+@pytest.mark.parametrize("kinds", KINDS, ids=IDS)
 def test_later_tokens_never_change_earlier_scores(kinds):
     m = model(kinds)
     ids = torch.randint(V, (1, 50), generator=torch.Generator().manual_seed(4))

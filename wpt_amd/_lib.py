@@ -48,6 +48,7 @@ SIGNATURES = {
     "wptv_add_rms_norm": [_P, _P, _P, _P, _I, _I, _I, _F, _P],
     "wptv_qkv_post": [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I, _I, _F, _P],
     "wptv_window_qkv_post": [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I, _P, _P, _I, _I, _I, _I, _I, _P, _I, _F, _P],
+    "wptv_heads_rms_norm": [_P, _I64, _P, _P, _I, _I, _I, _I, _F, _P],
     "wptv_swiglu": [_P, _P, _I, _I, _I, _P],
     "wptv_gemm_workspace": [_I, _I, _I, _P, _P],
     "wptv_gemm": [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _I, _I, _P, _SZ, _P],

@@ -13,7 +13,10 @@ with no copy per step, and undo, which only restores the lengths, cuts it
 back as carry.Tail.undo does (rows past a length are written again before
 any query reads them).
 
-Each layer's entries live in one (B, capacity, 2c) table, keys first, token p
+A sparse layer carries nothing (it reads the exact layer's table before it)
+and has no table: its entry in `tables` is None.
+
+Each exact layer's entries live in one (B, capacity, 2c) table, keys first, token p
 of row b at row p.  A reading appends each row's own new entries at its own
 length (wptv_kv_append) and returns nothing to copy: the attention reads the
 table in place up to each query's position.  Undo restores the lengths from
@@ -32,16 +35,18 @@ import torch
 
 class Cache:
     """rings: the layers whose table is a ring of ring_rows rows (window
-    layers); every other layer's table grows with the text."""
+    layers); bare: the layers with no table (sparse layers); every other
+    layer's table grows with the text."""
 
-    def __init__(self, rows, layers, width, dtype, device, capacity=256, rings=(), ring_rows=256):
+    def __init__(self, rows, layers, width, dtype, device, capacity=256, rings=(), ring_rows=256, bare=()):
         if ring_rows <= 0 or ring_rows & (ring_rows - 1):
             raise ValueError(f"a ring holds a power of 2 of rows, not {ring_rows}")
         self.lengths = torch.zeros(rows, dtype=torch.long, device=device)
         self.before = torch.zeros_like(self.lengths)  # the lengths before the last undoable reading
         self.rings = frozenset(rings)
-        self.tables = [torch.zeros(rows, ring_rows if i in self.rings else capacity, width, dtype=dtype,
-                                   device=device) for i in range(layers)]
+        self.tables = [None if i in bare else
+                       torch.zeros(rows, ring_rows if i in self.rings else capacity, width, dtype=dtype, device=device)
+                       for i in range(layers)]
         self.pending = False
         self.bound = 0
         self.routes = None
@@ -52,7 +57,7 @@ class Cache:
 
     @property
     def capacity(self):
-        grown = [t.shape[1] for i, t in enumerate(self.tables) if i not in self.rings]
+        grown = [t.shape[1] for i, t in enumerate(self.tables) if t is not None and i not in self.rings]
         return grown[0] if grown else None
 
     @property
@@ -69,7 +74,7 @@ class Cache:
             raise RuntimeError(f"the cache needs {need} rows but holds {self.capacity}: reserve them before "
                                "capturing a step")
         grown = max(need, 2 * self.capacity)
-        self.tables = [t if i in self.rings else torch.cat([t, t.new_zeros(t.shape[0], grown - t.shape[1],
+        self.tables = [t if t is None or i in self.rings else torch.cat([t, t.new_zeros(t.shape[0], grown - t.shape[1],
                                                                            t.shape[2])], 1)
                        for i, t in enumerate(self.tables)]
 
@@ -113,7 +118,7 @@ class Cache:
         copy = object.__new__(Cache)
         copy.lengths = self.lengths[index]
         copy.before = torch.zeros_like(copy.lengths)
-        copy.tables = [t[index] for t in self.tables]
+        copy.tables = [None if t is None else t[index] for t in self.tables]
         copy.rings = self.rings
         copy.pending, copy.bound, copy.routes = False, self.bound, None
         return copy

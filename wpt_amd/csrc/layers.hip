@@ -279,6 +279,29 @@ __global__ __launch_bounds__(256) void qkv_post(const T* __restrict__ qkv, int64
   Lane<T, EPL>::store(dst + EPL * lane, v);
 }
 
+// RMSNorm of each head of each row: x row r at x + r*row_stride, H heads of
+// C = 64 EPL values; out [rows, H, C].  One wavefront per (row, head).
+template <typename T, int EPL>
+__global__ __launch_bounds__(256) void heads_rms_norm(const T* __restrict__ x, int64_t row_stride,
+                                                      const float* __restrict__ weight, T* __restrict__ out, int rows,
+                                                      int H, float eps) {
+  constexpr int C = 64 * EPL;
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (gw >= rows * H) return;
+  const int row = gw / H, head = gw % H;
+  float v[EPL];
+  Lane<T, EPL>::load(x + (int64_t)row * row_stride + (int64_t)head * C + EPL * lane, v);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) ss += v[e] * v[e];
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / (float)C + eps);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) v[e] = v[e] * inv * weight[EPL * lane + e];
+  Lane<T, EPL>::store(out + ((int64_t)row * H + head) * C + EPL * lane, v);
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
 
 template <typename T>
@@ -512,6 +535,37 @@ extern "C" int wptv_qkv_post_parts(const float* parts, int splits, const float* 
 #undef WPTV_QKVP_S
 #undef WPTV_QKVP
   return launched("qkv_post_parts");
+}
+
+extern "C" int wptv_heads_rms_norm(const void* x, int64_t row_stride, const float* weight, void* out, int rows, int H,
+                                   int c, int dtype, float eps, hipStream_t stream) {
+  if (!x || !weight || !out) return fail(WPTV_E_INVALID, "heads_rms_norm: every pointer must be given");
+  if (rows < 0 || H <= 0) return fail(WPTV_E_INVALID, "heads_rms_norm: bad shape rows=%d H=%d", rows, H);
+  if (c != 64 && c != 128 && c != 256)
+    return fail(WPTV_E_UNSUPPORTED, "heads_rms_norm: head width %d is not 64, 128 or 256", c);
+  if (row_stride < (int64_t)H * c) return fail(WPTV_E_INVALID, "heads_rms_norm: a row stride below H*c");
+  const int epl = c / 64;
+  const int esize = dtype == WPTV_F32 ? 4 : 2;
+  if (row_stride % epl || !aligned(x, epl * esize) || !aligned(out, epl * esize))
+    return fail(WPTV_E_INVALID, "heads_rms_norm: rows must be aligned to %d elements", epl);
+  if (rows == 0) return WPTV_OK;
+  dim3 grid((unsigned)(((int64_t)rows * H + 3) / 4));
+#define WPTV_HN(TT, EE)                                                                                          \
+  hipLaunchKernelGGL((heads_rms_norm<TT, EE>), grid, dim3(256), 0, stream, static_cast<const TT*>(x), row_stride, \
+                     weight, static_cast<TT*>(out), rows, H, eps)
+  if (dtype == WPTV_BF16) {
+    if (epl == 1) WPTV_HN(unsigned short, 1);
+    else if (epl == 2) WPTV_HN(unsigned short, 2);
+    else WPTV_HN(unsigned short, 4);
+  } else if (dtype == WPTV_F32) {
+    if (epl == 1) WPTV_HN(float, 1);
+    else if (epl == 2) WPTV_HN(float, 2);
+    else WPTV_HN(float, 4);
+  } else {
+    return fail(WPTV_E_UNSUPPORTED, "heads_rms_norm: dtype %d is neither fp32 nor bf16", dtype);
+  }
+#undef WPTV_HN
+  return launched("heads_rms_norm");
 }
 
 extern "C" int wptv_swiglu(const void* gate_up, void* out, int M, int F, int dtype, hipStream_t stream) {

@@ -11,7 +11,14 @@ FP32 scores (model.py:471).  One key/value head is shared by every query
 head (MQA).  RMSNorm's eps is the reference's (layers.py:9).  A layer may
 instead be the reference's window layer (WindowAttention, attention.py:
 109-151): rotary encoding of the normed queries and key, a window of the last
-`window` tokens with a sink per head, and the output gated by sigmoid(gate(x)).
+`window` tokens with a sink per head, and the output gated by sigmoid(gate(x)),
+or the reference's sparse layer (SparseAttention, attention.py:190-215): the
+normed queries attend to the rows the exact layer before it chose for each
+query (its top_k rows outside the last `window`, by the largest
+max_h log-softmax weight) and to the last `window` rows of that layer's table,
+with a sink per head and the same output gate.  An exact layer followed by a
+sparse layer makes that choice (model.py:134-135); layer_kinds gives the
+reference's layout of the three kinds (config.py:17-23).
 
 On the GPU:
     KV append       wptv_qkv_post: q/k norms, and the new entries written at
@@ -27,6 +34,10 @@ On the GPU:
                     hipBLASLt otherwise and for the lm_head
     window layers   wptv_window_qkv_post (norms, rotary encoding, the ring
                     append), wptv_window_attention over the cache's ring with
+                    the sink and the output gate fused
+    sparse layers   the exact layer's lse (wptv_verify_attention) and choice
+                    (wptv_exact_choice), wptv_heads_rms_norm for the queries,
+                    wptv_sparse_attention over the exact layer's table with
                     the sink and the output gate fused
     sampling        wpt_amd.sampling (wptv_accept), called by the Writer
 The decoder keeps no state between calls but the cache; a step of fixed
@@ -48,6 +59,17 @@ EPS = 1e-6
 SPLIT_K_ROWS = 256
 
 
+WINDOW, EXACT, SPARSE = "window", "exact", "sparse"
+
+
+def layer_kinds(window_layers, sparse_groups, sparse_layers):
+    """The reference's layout of layer kinds (config.py:17-23): window layers
+    around one exact layer, then groups of one exact layer and the sparse
+    layers that read it."""
+    first = (WINDOW,) * window_layers + (EXACT,) + (WINDOW,) * window_layers
+    return first + ((EXACT,) + (SPARSE,) * sparse_layers) * sparse_groups
+
+
 @dataclass(frozen=True)
 class DecoderConfig:
     layers: int
@@ -56,22 +78,42 @@ class DecoderConfig:
     head_dim: int
     ffn: int
     vocab: int
-    kinds: tuple = ()          # "exact" or "window" per layer; () = every layer exact
-    window: int = 128          # WINDOW, attention.py:51
+    kinds: tuple = ()          # "exact", "window" or "sparse" per layer; () = every layer exact
+    window: int = 128          # WINDOW, attention.py:53
     rope_dims: int = 64        # ROPE_DIMS, attention.py:53
     rope_base: float = 10000.0
+    top_k: int = 1024          # TOP_K, attention.py:54: rows an exact layer chooses for the sparse layers
+
+    def __post_init__(self):
+        if self.kinds:
+            if len(self.kinds) != self.layers or set(self.kinds) - {WINDOW, EXACT, SPARSE}:
+                raise ValueError(f"kinds must name one of {WINDOW!r}, {EXACT!r}, {SPARSE!r} for each of the "
+                                 f"{self.layers} layers; got {self.kinds}")
+            for i, kind in enumerate(self.kinds):
+                if kind == SPARSE and (i == 0 or self.kinds[i - 1] == WINDOW):
+                    raise ValueError(f"sparse layer {i} follows no exact layer or sparse layer: it has no "
+                                     "choice of rows to read")
 
     @property
     def qkv_width(self):
         return self.heads * self.head_dim + 2 * self.head_dim
 
     def kind(self, i):
-        return self.kinds[i] if self.kinds else "exact"
+        return self.kinds[i] if self.kinds else EXACT
 
     @property
     def windows(self):
         """The window layers' indices."""
-        return tuple(i for i in range(self.layers) if self.kind(i) == "window")
+        return tuple(i for i in range(self.layers) if self.kind(i) == WINDOW)
+
+    @property
+    def sparse(self):
+        """The sparse layers' indices."""
+        return tuple(i for i in range(self.layers) if self.kind(i) == SPARSE)
+
+    def chooses(self, i):
+        """Whether exact layer i chooses rows: a sparse layer follows it."""
+        return self.kind(i) == EXACT and i + 1 < self.layers and self.kind(i + 1) == SPARSE
 
 
 # The decoders of the verify-step workloads.
@@ -94,14 +136,18 @@ def random_weights(config, seed=0, std=0.02, dtype=torch.float32, device="cpu"):
     weights = {"embedding": normal(V, D)}
     for i in range(config.layers):
         weights[f"layers.{i}.attn_norm"] = ones(D)
-        weights[f"layers.{i}.qkv"] = normal(config.qkv_width, D)
+        if config.kind(i) == SPARSE:  # queries only: the keys and values are the exact layer's
+            weights[f"layers.{i}.q"] = normal(H * c, D)
+        else:
+            weights[f"layers.{i}.qkv"] = normal(config.qkv_width, D)
         weights[f"layers.{i}.q_norm"] = ones(c)
-        weights[f"layers.{i}.k_norm"] = ones(c)
+        if config.kind(i) != SPARSE:
+            weights[f"layers.{i}.k_norm"] = ones(c)
         weights[f"layers.{i}.out"] = normal(D, H * c)
         weights[f"layers.{i}.ffn_norm"] = ones(D)
         weights[f"layers.{i}.gate_up"] = normal(2 * Fw, D)
         weights[f"layers.{i}.down"] = normal(D, Fw)
-        if config.kind(i) == "window":
+        if config.kind(i) in (WINDOW, SPARSE):
             weights[f"layers.{i}.gate"] = normal(H * c, D)
             # the reference starts its sinks at 0; drawn here so that they matter
             weights[f"layers.{i}.sink"] = torch.randn(H, generator=generator, device=device)
@@ -125,6 +171,8 @@ class MQADecoder:
             self.w[name] = value.to(device=self.device, dtype=torch.float32 if keep_fp32 else dtype).contiguous()
         for i in config.windows:  # one projection for q, k, v and the gate
             self.w[f"layers.{i}.qkvg"] = torch.cat([self.w[f"layers.{i}.qkv"], self.w[f"layers.{i}.gate"]]).contiguous()
+        for i in config.sparse:  # one projection for q and the gate
+            self.w[f"layers.{i}.qg"] = torch.cat([self.w[f"layers.{i}.q"], self.w[f"layers.{i}.gate"]]).contiguous()
         if dtype == torch.bfloat16:  # the gate/up rows in the order the fused SwiGLU product reads, kept instead
             for i in range(config.layers):
                 self.w[f"layers.{i}.gate_up_tiles"] = layers.interleave_gate_up(self.w.pop(f"layers.{i}.gate_up"))
@@ -140,23 +188,29 @@ class MQADecoder:
             raise NotImplementedError("this decoder has no routed experts to record")
         c = self.config.head_dim
         ring = 1 << max(0, (self.config.window - 1 + widest - 1).bit_length())
-        return Cache(rows, self.config.layers, 2 * c, self.dtype, self.device, capacity, self.config.windows, ring)
+        return Cache(rows, self.config.layers, 2 * c, self.dtype, self.device, capacity, self.config.windows, ring,
+                     self.config.sparse)
 
     def widest(self, cache):
         """The most tokens one reading of the cache takes (its rings' size)."""
         ring = cache.ring_rows
         return None if ring is None else ring - self.config.window + 1
 
-    def _layer(self, i, h, x, cache, positions, counts, next_norm):
+    def _layer(self, i, h, x, cache, positions, counts, next_norm, handoff):
         """One layer on the residual stream h (B, T, D), x = RMSNorm(h) with the
         layer's attention norm; leaves h updated and x = RMSNorm(h) with
-        next_norm (the next layer's attention norm, or the final norm)."""
+        next_norm (the next layer's attention norm, or the final norm).
+        handoff: what the last exact layer gave the sparse layers; returns
+        the handoff for the next layer."""
         w = self.w
         B, T, _ = h.shape
-        if self.config.kind(i) == "window":
+        kind = self.config.kind(i)
+        if kind == WINDOW:
             self._window_attention(i, h, x, cache, positions, counts)
+        elif kind == SPARSE:
+            self._sparse_attention(i, h, x, positions, handoff)
         else:
-            self._exact_attention(i, h, x, cache, positions, counts)
+            handoff = self._exact_attention(i, h, x, cache, positions, counts)
         if x.dtype != torch.bfloat16:
             act = layers.swiglu(F.linear(x, w[f"layers.{i}.gate_up"]))
         elif B * T <= layers.LINEAR_MAX_ROWS:
@@ -169,6 +223,17 @@ class MQADecoder:
             layers.add_rms_norm_parts(h, layers.linear_parts(act, down), next_norm, x)
         else:
             layers.add_rms_norm(h, F.linear(act, down), next_norm, x)
+        return handoff
+
+    def _attention_out(self, i, h, x, o):
+        """h += out(o), x = RMSNorm(h) with the feed-forward norm."""
+        B, T, H, c = o.shape
+        out = self.w[f"layers.{i}.out"]
+        if x.dtype == torch.bfloat16 and B * T <= SPLIT_K_ROWS:
+            layers.add_rms_norm_parts(h, layers.linear_parts(o.reshape(B, T, H * c), out),
+                                      self.w[f"layers.{i}.ffn_norm"], x)
+        else:
+            layers.add_rms_norm(h, F.linear(o.reshape(B, T, H * c), out), self.w[f"layers.{i}.ffn_norm"], x)
 
     def _window_attention(self, i, h, x, cache, positions, counts):
         """A window layer's attention block: h += out(o * sigmoid(gate(x))),
@@ -182,16 +247,25 @@ class MQADecoder:
                                    counts, H, cfg.rope_dims, cfg.rope_base)
         o = kernels.ring_attention(q, ring, positions, c ** -0.5, cfg.window, w[f"layers.{i}.sink"],
                                    gate=proj[..., (H + 2) * c:])
-        out = w[f"layers.{i}.out"]
-        if x.dtype == torch.bfloat16 and B * T <= SPLIT_K_ROWS:
-            layers.add_rms_norm_parts(h, layers.linear_parts(o.reshape(B, T, H * c), out), w[f"layers.{i}.ffn_norm"],
-                                      x)
-        else:
-            layers.add_rms_norm(h, F.linear(o.reshape(B, T, H * c), out), w[f"layers.{i}.ffn_norm"], x)
+        self._attention_out(i, h, x, o)
+
+    def _sparse_attention(self, i, h, x, positions, handoff):
+        """A sparse layer's attention block over the exact layer's table and
+        choice (handoff = (keys, values, chosen)): h += out(o * sigmoid(gate(x))),
+        x = RMSNorm(h) with the feed-forward norm."""
+        w, cfg = self.w, self.config
+        H, c = cfg.heads, cfg.head_dim
+        keys, values, chosen = handoff
+        proj = F.linear(x, w[f"layers.{i}.qg"])  # (B, T, 2 H c): q, gate
+        q = layers.heads_rms_norm(proj, w[f"layers.{i}.q_norm"], H)
+        o = kernels.sparse_attention(q, keys, values, w[f"layers.{i}.sink"], chosen, positions, c ** -0.5, cfg.window,
+                                     gate=proj[..., H * c:])
+        self._attention_out(i, h, x, o)
 
     def _exact_attention(self, i, h, x, cache, positions, counts):
         """An exact layer's attention block: h += out(o), x = RMSNorm(h) with
-        the feed-forward norm."""
+        the feed-forward norm.  Returns (keys, values, chosen), the sparse
+        layers' handoff (chosen None when no sparse layer follows)."""
         w, cfg = self.w, self.config
         B, T, _ = h.shape
         H, c = cfg.heads, cfg.head_dim
@@ -207,12 +281,15 @@ class MQADecoder:
             qkv = F.linear(x, w[f"layers.{i}.qkv"])
             q = layers.qkv_post(qkv, w[f"layers.{i}.q_norm"], w[f"layers.{i}.k_norm"], table, cache.lengths, counts,
                                 H)
-        o = kernels.verify_attention(q, table[..., :c], table[..., c:], positions, c ** -0.5, from_positions=True)
-        if few:
-            layers.add_rms_norm_parts(h, layers.linear_parts(o.reshape(B, T, H * c), w[f"layers.{i}.out"]),
-                                      w[f"layers.{i}.ffn_norm"], x)
+        keys, values = table[..., :c], table[..., c:]
+        chosen = None
+        if cfg.chooses(i):  # the top_k rows outside the window by the largest max_h log-softmax weight
+            o, lse = kernels.verify_attention(q, keys, values, positions, c ** -0.5, lse=True, from_positions=True)
+            chosen = kernels.choose_rows(q, keys, positions, lse, c ** -0.5, cfg.top_k, cfg.window)
         else:
-            layers.add_rms_norm(h, F.linear(o.reshape(B, T, H * c), w[f"layers.{i}.out"]), w[f"layers.{i}.ffn_norm"], x)
+            o = kernels.verify_attention(q, keys, values, positions, c ** -0.5, from_positions=True)
+        self._attention_out(i, h, x, o)
+        return keys, values, chosen
 
     @torch.no_grad()
     def extend(self, ids, cache, counts=None, undoable=False, features=()):
@@ -245,10 +322,11 @@ class MQADecoder:
         h = F.embedding(ids, self.w["embedding"])
         x = torch.empty_like(h)
         layers.add_rms_norm(h, None, self.w["layers.0.attn_norm"], x)
+        handoff = None
         for i in range(self.config.layers):
             last = i + 1 == self.config.layers
             next_norm = self.w["final_norm"] if last else self.w[f"layers.{i + 1}.attn_norm"]
-            self._layer(i, h, x, cache, positions, counts_, next_norm)
+            handoff = self._layer(i, h, x, cache, positions, counts_, next_norm, handoff)
         scores = F.linear(x, self.w["head"]).float()
         cache.finish(counts_, undoable, T)
         return scores, h

@@ -116,6 +116,20 @@ def window_qkv_post(proj, q_norm, k_norm, ring, start, counts, heads, rope_dims=
     return q
 
 
+def heads_rms_norm(x, weight, heads, eps=EPS):
+    """x (B, T, >= H*c) (rows one after another) -> (B, T, H, c): RMSNorm of
+    each head of the first H*c columns, times weight (c,) FP32."""
+    _gpu(x, weight)
+    B, T, width = x.shape
+    c = weight.shape[0]
+    if width < heads * c or x.stride(-1) != 1 or x.stride(0) != T * x.stride(1):
+        raise ValueError(f"x must be (B, T, >= H*c) with rows one after another; got {tuple(x.shape)}")
+    out = torch.empty(B, T, heads, c, dtype=x.dtype, device=x.device)
+    check(_lib.lib().wptv_heads_rms_norm(ptr(x), x.stride(1), ptr(weight), ptr(out), B * T, heads, c,
+                                         _lib.dtype_code(x.dtype), float(eps), _lib.stream(x.device)), "heads_rms_norm")
+    return out
+
+
 def swiglu(gate_up):
     """silu(gate) * up of gate_up (..., 2F): (..., F)."""
     _gpu(gate_up)
