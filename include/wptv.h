@@ -239,7 +239,7 @@ int wptv_window_qkv_post(const void* qkv, int64_t qkv_row_stride, const float* q
                          const int64_t* start, const int64_t* counts, int B, int T, int H, int c, int rope_dims,
                          const float* rope_div, int dtype, float eps, hipStream_t stream);
 
-/* wptv_heads_rms_norm: a sparse layer's query norm (attention.py:190-215:
+/* wptv_heads_rms_norm: a sparse layer's query norm (attention.py:191-216:
  *   q_norm(q(x)) per head): out [rows, H, c] = RMSNorm of each head of x
  *   (row r at x + r*row_stride) times weight [c], in FP32. */
 int wptv_heads_rms_norm(const void* x, int64_t row_stride, const float* weight, void* out, int rows, int H, int c,

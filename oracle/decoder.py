@@ -16,7 +16,7 @@ attention.py:109-151): q = rotate(q_norm(q(x))), entries
 carried from before (the cache's tail, cache.py:97-108) joined in front,
 window attention with a sink per head, and the output times sigmoid(gate(x))
 before the output projection.  Or the reference's sparse layer
-(SparseAttention, attention.py:190-215): q = q_norm(q(x)), sparse attention
+(SparseAttention, attention.py:191-216): q = q_norm(q(x)), sparse attention
 over the keys and values of the last exact layer's table at the rows that
 layer chose for each query plus each query's last window rows, a sink per
 head, the same gate.  An exact layer chooses (top_k rows) when a sparse layer

@@ -1,6 +1,6 @@
 """Sparse layers on the GPU against the oracle: the per-head query norm
 (wptv_heads_rms_norm), and decoders whose exact layers choose rows for the
-sparse layers after them (attention.py:157-215, model.py:134-135,411-423)
+sparse layers after them (attention.py:157-216, model.py:134-135,411-423)
 read in pieces, through undone drafts, as the oracle reads them.
 
 The windows (16) and choices (8 rows) are small beside the texts (90 and 200

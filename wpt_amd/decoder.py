@@ -12,7 +12,7 @@ head (MQA).  RMSNorm's eps is the reference's (layers.py:9).  A layer may
 instead be the reference's window layer (WindowAttention, attention.py:
 109-151): rotary encoding of the normed queries and key, a window of the last
 `window` tokens with a sink per head, and the output gated by sigmoid(gate(x)),
-or the reference's sparse layer (SparseAttention, attention.py:190-215): the
+or the reference's sparse layer (SparseAttention, attention.py:191-216): the
 normed queries attend to the rows the exact layer before it chose for each
 query (its top_k rows outside the last `window`, by the largest
 max_h log-softmax weight) and to the last `window` rows of that layer's table,
