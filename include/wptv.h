@@ -40,6 +40,9 @@ enum {
 
 enum { WPTV_F32 = 0, WPTV_BF16 = 1 };
 
+/* index dtypes (counts, kept) */
+enum { WPTV_I64 = 8, WPTV_I32 = 9 };
+
 /* wptv_verify_attention flags */
 enum {
   WPTV_ATTN_FORCE_GENERIC = 1,        /* run the wave-per-query VALU kernel even where the MFMA kernel applies */
@@ -187,6 +190,22 @@ int wptv_kv_append(void* table, int64_t table_stride_b, int64_t table_stride_n, 
                    const int64_t* start, const int64_t* counts, int B, int n, int width, int dtype,
                    hipStream_t stream);
 
+/* wptv_cache_lengths: the cache's lengths (B,) int64 after a reading
+ *   (undo = 0; the reference's Reading.finish, cache.py:130-134: before =
+ *   lengths when before is not NULL, then lengths += counts) or after an undo
+ *   (undo = 1; Rows.undo, cache.py:69-77: lengths = before + counts, counts
+ *   being the kept tokens).  counts (B,) of counts_dtype WPTV_I64 or WPTV_I32.
+ *   Device-side, so that a captured step replays on the cache's state. */
+int wptv_cache_lengths(int64_t* lengths, int64_t* before, const void* counts, int counts_dtype, int B, int undo,
+                       hipStream_t stream);
+
+/* wptv_next_feeds: each row's next pending token after a verify step, the
+ *   last token it wrote (the reference's Writer keeps it pending for the
+ *   next round, __init__.py:196-233): feeds[b * feeds_stride] =
+ *   tokens[b * tokens_stride + clamp(counts[b] - 1, 0, width - 1)]. */
+int wptv_next_feeds(const int64_t* tokens, int64_t tokens_stride, const int* counts, int64_t* feeds,
+                    int64_t feeds_stride, int B, int width, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * The decoder layer's memory-bound steps around its matrix products (the
  * reference's extend runs them as torch operations: model.py:394-436,
@@ -209,6 +228,16 @@ int wptv_add_rms_norm(void* h, const void* delta, const float* weight, void* y, 
 /* wptv_add_rms_norm_parts: as wptv_add_rms_norm with delta = the sum over
  * z < splits of parts[z] (FP32 [splits, M, D], e.g. wptv_gemm_parts' output),
  * rounded to the dtype before the residual add; splits <= 8, D <= 8192. */
+/* wptv_embed_rms_norm: the first layer's input (model.py:394-400: the
+ *   embedding of ids, then the first attention norm): h [M, D] =
+ *   table[ids[m]] (ids clamped into [0, vocab)), y = RMSNorm(h) * weight as
+ *   wptv_add_rms_norm; with positions (not NULL) also positions[m] =
+ *   lengths[m / T] + m % T, each token's place after its row's earlier ones
+ *   (Place.positions, sequence.py:70-73). */
+int wptv_embed_rms_norm(const int64_t* ids, const void* table, int64_t vocab, const float* weight, void* h, void* y,
+                        int M, int D, int dtype, float eps, const int64_t* lengths, int64_t* positions, int T,
+                        hipStream_t stream);
+
 int wptv_add_rms_norm_parts(void* h, const float* parts, int splits, const float* weight, void* y, int M, int D,
                             int dtype, float eps, hipStream_t stream);
 

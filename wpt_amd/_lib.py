@@ -16,6 +16,8 @@ ABI_VERSION = 1
 
 WPTV_F32, WPTV_BF16 = 0, 1
 DTYPES = {torch.float32: WPTV_F32, torch.bfloat16: WPTV_BF16}
+WPTV_I64, WPTV_I32 = 8, 9
+INDEX_DTYPES = {torch.int64: WPTV_I64, torch.int32: WPTV_I32}
 FORCE_GENERIC = 1
 RANGE_FROM_POSITIONS = 2
 KEY_SPLIT = 4
@@ -49,6 +51,9 @@ SIGNATURES = {
     "wptv_qkv_post": [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I, _I, _F, _P],
     "wptv_window_qkv_post": [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I, _P, _P, _I, _I, _I, _I, _I, _P, _I, _F, _P],
     "wptv_heads_rms_norm": [_P, _I64, _P, _P, _I, _I, _I, _I, _F, _P],
+    "wptv_embed_rms_norm": [_P, _P, _I64, _P, _P, _P, _I, _I, _I, _F, _P, _P, _I, _P],
+    "wptv_cache_lengths": [_P, _P, _P, _I, _I, _I, _P],
+    "wptv_next_feeds": [_P, _I64, _P, _P, _I64, _I, _I, _P],
     "wptv_swiglu": [_P, _P, _I, _I, _I, _P],
     "wptv_gemm_workspace": [_I, _I, _I, _P, _P],
     "wptv_gemm": [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _I, _I, _P, _SZ, _P],

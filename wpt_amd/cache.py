@@ -32,6 +32,19 @@ step is captured with the capacity reserved beforehand.
 
 import torch
 
+from . import _lib
+from ._lib import check, ptr
+
+
+def _lengths(lengths, before, counts, undo):
+    """wptv_cache_lengths on the lengths' device: before = lengths (when
+    given), lengths += counts; or, undo, lengths = before + counts."""
+    if counts.device != lengths.device or counts.shape != lengths.shape or counts.dtype not in _lib.INDEX_DTYPES:
+        raise ValueError(f"counts must be ({lengths.shape[0]},) int64 or int32 on {lengths.device}")
+    counts = counts.contiguous()
+    check(_lib.lib().wptv_cache_lengths(ptr(lengths), ptr(before), ptr(counts), _lib.INDEX_DTYPES[counts.dtype],
+                                        lengths.shape[0], int(undo), _lib.stream(lengths.device)), "cache_lengths")
+
 
 class Cache:
     """rings: the layers whose table is a ring of ring_rows rows (window
@@ -96,17 +109,15 @@ class Cache:
         """The rows have read their tokens (the reference's Reading.finish).
         The lengths change in place, so that a captured step replays on the
         cache's current state."""
-        if undoable:
-            self.before.copy_(self.lengths)
+        _lengths(self.lengths, self.before if undoable else None, counts, undo=False)
         self.pending = bool(undoable)
-        self.lengths.add_(counts)
         self.bound += width
 
     def undo(self, kept):
         """Back to the lengths before the last undoable reading, plus kept."""
         if not self.pending:
             raise ValueError("no undoable extend to undo")
-        torch.add(self.before, kept, out=self.lengths)
+        _lengths(self.lengths, self.before, kept, undo=True)
         self.pending = False
 
     def select(self, index):

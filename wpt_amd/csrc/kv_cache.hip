@@ -30,6 +30,36 @@ __global__ __launch_bounds__(256) void kv_append_16(unsigned char* __restrict__ 
   *dst = *src;
 }
 
+// The cache's lengths after a reading (the reference's Reading.finish,
+// cache.py:130-139: before = lengths when the reading can be undone, lengths
+// += counts) or after an undo (Rows.undo, cache.py:69-77: lengths = before +
+// kept); counts / kept int64 or int32.  One thread per batch row.
+template <typename C>
+__global__ __launch_bounds__(64) void cache_lengths(int64_t* __restrict__ lengths, int64_t* __restrict__ before,
+                                                    const C* __restrict__ counts, int B, int undo) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const int64_t n = (int64_t)counts[b];
+  if (undo) {
+    lengths[b] = before[b] + n;
+  } else {
+    const int64_t len = lengths[b];
+    if (before) before[b] = len;
+    lengths[b] = len + n;
+  }
+}
+
+// Each row's next pending token after a verify step: the last token it wrote,
+// tokens[b, max(counts[b] - 1, 0)], into feeds[b, 0].
+__global__ __launch_bounds__(64) void next_feeds(const int64_t* __restrict__ tokens, int64_t tokens_stride,
+                                                 const int* __restrict__ counts, int64_t* __restrict__ feeds,
+                                                 int64_t feeds_stride, int B, int width) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const int last = min(max(counts[b] - 1, 0), width - 1);
+  feeds[(int64_t)b * feeds_stride] = tokens[(int64_t)b * tokens_stride + last];
+}
+
 // Byte-wise form for rows whose size or strides are not multiples of 16 bytes.
 __global__ __launch_bounds__(256) void kv_append_bytes(unsigned char* __restrict__ table, int64_t tsb, int64_t tsn,
                                                        int64_t capacity, const unsigned char* __restrict__ rows,
@@ -84,4 +114,33 @@ extern "C" int wptv_kv_append(void* table, int64_t table_stride_b, int64_t table
   hipLaunchKernelGGL(kv_append_bytes, grid, dim3(threads), 0, stream, static_cast<unsigned char*>(table), tsb, tsn,
                      capacity, static_cast<const unsigned char*>(rows), rsb, rsn, start, counts, n, (int)row_bytes);
   return launched("kv_append_bytes");
+}
+
+extern "C" int wptv_cache_lengths(int64_t* lengths, int64_t* before, const void* counts, int counts_dtype, int B,
+                                  int undo, hipStream_t stream) {
+  if (!lengths || !counts || (undo && !before))
+    return fail(WPTV_E_INVALID, "cache_lengths: lengths and counts (and before, to undo) must be given");
+  if (B < 0) return fail(WPTV_E_INVALID, "cache_lengths: B = %d", B);
+  if (B == 0) return WPTV_OK;
+  dim3 grid((unsigned)((B + 63) / 64));
+  if (counts_dtype == WPTV_I64)
+    hipLaunchKernelGGL(cache_lengths<int64_t>, grid, dim3(64), 0, stream, lengths, before,
+                       static_cast<const int64_t*>(counts), B, undo);
+  else if (counts_dtype == WPTV_I32)
+    hipLaunchKernelGGL(cache_lengths<int>, grid, dim3(64), 0, stream, lengths, before,
+                       static_cast<const int*>(counts), B, undo);
+  else
+    return fail(WPTV_E_UNSUPPORTED, "cache_lengths: counts of dtype %d are neither int64 nor int32", counts_dtype);
+  return launched("cache_lengths");
+}
+
+extern "C" int wptv_next_feeds(const int64_t* tokens, int64_t tokens_stride, const int* counts, int64_t* feeds,
+                               int64_t feeds_stride, int B, int width, hipStream_t stream) {
+  if (!tokens || !counts || !feeds) return fail(WPTV_E_INVALID, "next_feeds: every pointer must be given");
+  if (B < 0 || width <= 0 || tokens_stride < width)
+    return fail(WPTV_E_INVALID, "next_feeds: bad shape B=%d width=%d stride=%lld", B, width, (long long)tokens_stride);
+  if (B == 0) return WPTV_OK;
+  hipLaunchKernelGGL(next_feeds, dim3((unsigned)((B + 63) / 64)), dim3(64), 0, stream, tokens, tokens_stride, counts,
+                     feeds, feeds_stride, B, width);
+  return launched("next_feeds");
 }

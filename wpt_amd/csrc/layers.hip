@@ -102,6 +102,54 @@ __global__ __launch_bounds__(64) void add_rms_norm(T* __restrict__ h, const T* _
   }
 }
 
+// The first layer's input: h = the embedding rows of the tokens (ids
+// outside [0, vocab) read row 0 or vocab - 1; the host checks ids it holds),
+// y = RMSNorm(h) * weight, as add_rms_norm without delta; and, when positions
+// is given, each token's position lengths[b] + t (row b T + t).
+template <typename T, int NCH>
+__global__ __launch_bounds__(64) void embed_rms_norm(const int64_t* __restrict__ ids, const T* __restrict__ table,
+                                                     int64_t vocab, const float* __restrict__ weight,
+                                                     T* __restrict__ h, T* __restrict__ y, int D, float eps,
+                                                     const int64_t* __restrict__ lengths,
+                                                     int64_t* __restrict__ positions, int Tn) {
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  int64_t id = ids[row];
+  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+  const T* src = table + id * D;
+  float x[NCH][8], wt[NCH][8];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int col = min((k * 64 + lane) * 8, D - 8);
+    Vec8<T>::load(src + col, x[k]);
+    Vec8<float>::load(weight + col, wt[k]);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    float part = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part += x[k][e] * x[k][e];
+    ss += (k * 64 + lane) * 8 < D ? part : 0.f;
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / (float)D + eps);
+  T* hrow = h + (int64_t)row * D;
+  T* yrow = y + (int64_t)row * D;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int col = (k * 64 + lane) * 8;
+    if (col < D) {
+      Vec8<T>::store(hrow + col, x[k]);
+      float out[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = x[k][e] * inv * wt[k][e];
+      Vec8<T>::store(yrow + col, out);
+    }
+  }
+  if (positions && lane == 0) positions[row] = lengths[row / Tn] + row % Tn;
+}
+
 // add_rms_norm with delta = the sum of S FP32 parts [S][M][D] (a split-K
 // matrix product's parts, summed in a fixed order): one workgroup of D / 8
 // threads per row, 8 columns a thread; every load -- the parts, h and the
@@ -361,6 +409,39 @@ extern "C" int wptv_add_rms_norm(void* h, const void* delta, const float* weight
 #undef WPTV_ARN_N
 #undef WPTV_ARN
   return launched("add_rms_norm");
+}
+
+extern "C" int wptv_embed_rms_norm(const int64_t* ids, const void* table, int64_t vocab, const float* weight,
+                                   void* h, void* y, int M, int D, int dtype, float eps, const int64_t* lengths,
+                                   int64_t* positions, int T, hipStream_t stream) {
+  if (!ids || !table || !weight || !h || !y) return fail(WPTV_E_INVALID, "embed_rms_norm: a pointer is missing");
+  if (M < 0 || D <= 0 || vocab <= 0) return fail(WPTV_E_INVALID, "embed_rms_norm: bad shape M=%d D=%d", M, D);
+  if (positions && (!lengths || T <= 0 || M % T))
+    return fail(WPTV_E_INVALID, "embed_rms_norm: positions need lengths and M a multiple of T = %d", T);
+  if (D % 8 != 0 || D > 64 * 8 * kChunks)
+    return fail(WPTV_E_UNSUPPORTED, "embed_rms_norm: width %d is not a multiple of 8 up to %d", D, 64 * 8 * kChunks);
+  if (!vec_aligned(table) || !vec_aligned(h) || !vec_aligned(y))
+    return fail(WPTV_E_INVALID, "embed_rms_norm: rows must be 16-byte aligned");
+  if (M == 0) return WPTV_OK;
+  const int nch = (D + 511) / 512;
+#define WPTV_ERN(TT, NN)                                                                                          \
+  hipLaunchKernelGGL((embed_rms_norm<TT, NN>), dim3(M), dim3(64), 0, stream, ids, static_cast<const TT*>(table), \
+                     vocab, weight, static_cast<TT*>(h), static_cast<TT*>(y), D, eps, lengths, positions, T)
+#define WPTV_ERN_N(TT)              \
+  if (nch <= 1) WPTV_ERN(TT, 1);     \
+  else if (nch <= 2) WPTV_ERN(TT, 2); \
+  else if (nch <= 4) WPTV_ERN(TT, 4); \
+  else WPTV_ERN(TT, 8)
+  if (dtype == WPTV_BF16) {
+    WPTV_ERN_N(unsigned short);
+  } else if (dtype == WPTV_F32) {
+    WPTV_ERN_N(float);
+  } else {
+    return fail(WPTV_E_UNSUPPORTED, "embed_rms_norm: dtype %d is neither fp32 nor bf16", dtype);
+  }
+#undef WPTV_ERN_N
+#undef WPTV_ERN
+  return launched("embed_rms_norm");
 }
 
 extern "C" int wptv_add_rms_norm_parts(void* h, const float* parts, int splits, const float* weight, void* y, int M,

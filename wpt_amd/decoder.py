@@ -163,6 +163,7 @@ class MQADecoder:
     def __init__(self, config, weights, dtype=torch.bfloat16, device="cuda"):
         self.config, self.dtype = config, dtype
         self.device = torch.device(device)
+        self._widths = {}
         if self.device.type != "cuda":
             raise kernels.KernelUnavailable(f"the decoder's verify step runs on a GPU, not {self.device}")
         self.w = {}
@@ -299,12 +300,16 @@ class MQADecoder:
         reference's WPT.extend (model.py:456-473)."""
         if features:
             raise NotImplementedError("this decoder gives no intermediate features")
-        ids = ids.to(self.device)
+        if ids.device.type == "cpu" and ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= self.config.vocab):
+            raise IndexError(f"token ids must lie in [0, {self.config.vocab})")
+        ids = ids.to(device=self.device, dtype=torch.long)
         B, T = ids.shape
         if B != cache.rows:
             raise ValueError(f"ids hold {B} rows; the cache {cache.rows}")
-        if counts is None:
-            counts_ = torch.full((B,), T, dtype=torch.long, device=self.device)
+        if counts is None:  # every token of every row: one device tensor per width, made once
+            counts_ = self._widths.get((B, T))
+            if counts_ is None:
+                counts_ = self._widths[(B, T)] = torch.full((B,), T, dtype=torch.long, device=self.device)
         else:
             counts_ = torch.as_tensor(counts, dtype=torch.long).to(self.device)
         widest = self.widest(cache)
@@ -318,10 +323,13 @@ class MQADecoder:
                 pieces.append(part)
             return torch.cat([p[0] for p in pieces], 1), torch.cat([p[1] for p in pieces], 1)
         cache.reserve(cache.bound + T)
-        positions = cache.lengths[:, None] + torch.arange(T, device=self.device)
-        h = F.embedding(ids, self.w["embedding"])
+        D = self.config.d_model
+        h = torch.empty(B, T, D, dtype=self.dtype, device=self.device)
         x = torch.empty_like(h)
-        layers.add_rms_norm(h, None, self.w["layers.0.attn_norm"], x)
+        positions = torch.empty(B, T, dtype=torch.long, device=self.device)
+        # the embedding, the first norm and each token's position in one pass
+        layers.embed_rms_norm(ids.contiguous(), self.w["embedding"], self.w["layers.0.attn_norm"], h, x,
+                              cache.lengths, positions)
         handoff = None
         for i in range(self.config.layers):
             last = i + 1 == self.config.layers
@@ -334,8 +342,11 @@ class MQADecoder:
     @torch.no_grad()
     def undo(self, cache, kept):
         """After an undoable extend: keeps only its first kept[b] tokens of
-        row b (the reference's WPT.undo, model.py:475-483)."""
-        cache.undo(torch.as_tensor(kept, dtype=torch.long).to(self.device))
+        row b (the reference's WPT.undo, model.py:475-483); kept int64 or
+        int32 (a sampler's counts), on the device or the host."""
+        if not (torch.is_tensor(kept) and kept.dtype in (torch.int64, torch.int32)):
+            kept = torch.as_tensor(kept, dtype=torch.long)
+        cache.undo(kept.to(self.device))
 
     @torch.no_grad()
     def __call__(self, ids):

@@ -25,6 +25,26 @@ def _rows(x, name):
     return x
 
 
+def embed_rms_norm(ids, table, weight, h, y, lengths=None, positions=None, eps=EPS):
+    """h = table[ids] (ids (B, T) int64 on the device, clamped into the
+    vocabulary), y = RMSNorm(h) * weight; with lengths (B,) and positions
+    (B, T) int64 also positions = lengths[:, None] + t."""
+    _gpu(table, weight, h, y)
+    B, T = ids.shape
+    V, D = table.shape
+    if h.shape != (B, T, D) or y.shape != h.shape or h.dtype != table.dtype or y.dtype != table.dtype:
+        raise ValueError(f"h and y must be (B={B}, T={T}, D={D}) in the table's dtype")
+    if ids.dtype != torch.int64 or ids.device != h.device or not ids.is_contiguous():
+        raise ValueError("ids must be contiguous int64 on the device")
+    if positions is not None and (lengths is None or positions.shape != (B, T) or positions.dtype != torch.int64
+                                  or lengths.shape != (B,) or lengths.dtype != torch.int64):
+        raise ValueError("positions (B, T) and lengths (B,) must be int64")
+    check(_lib.lib().wptv_embed_rms_norm(ptr(ids), ptr(table), V, ptr(weight), ptr(_rows(h, "h")), ptr(_rows(y, "y")),
+                                         B * T, D, _lib.dtype_code(h.dtype), float(eps), ptr(lengths),
+                                         ptr(positions), T, _lib.stream(h.device)), "embed_rms_norm")
+    return y
+
+
 def add_rms_norm(h, delta, weight, y, eps=EPS):
     """h += delta (None: no add), then y = RMSNorm(h) * weight (FP32 math).
     h, delta, y share shape (..., D) and dtype; weight (D,) FP32."""

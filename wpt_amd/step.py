@@ -16,7 +16,18 @@ device.  The cache's tables must hold every row the replays will write
 
 import torch
 
-from . import sampling
+from . import _lib, sampling
+from ._lib import check, ptr
+
+
+def next_feeds(tokens, counts, feeds):
+    """feeds[:, 0] = each row's last written token, tokens[b, counts[b] - 1]
+    (tokens (B, L + 1) int64, counts (B,) int32), on the device."""
+    B, width = tokens.shape
+    if counts.dtype != torch.int32 or counts.shape != (B,) or feeds.shape[0] != B or feeds.dtype != torch.int64:
+        raise ValueError("tokens (B, L + 1) int64, counts (B,) int32 and feeds (B, n) int64")
+    check(_lib.lib().wptv_next_feeds(ptr(tokens), tokens.stride(0), ptr(counts), ptr(feeds), feeds.stride(0), B, width,
+                                     _lib.stream(tokens.device)), "next_feeds")
 
 
 class VerifyStep:
@@ -40,10 +51,8 @@ class VerifyStep:
             B, V = scores.shape[0], scores.shape[-1]
             u, e = sampling.draws(B, self.k, V, device=scores.device)
             tokens, counts = sampling.accept(scores, self.q, drafts, u, e, self.temperature, self.top_k)
-        self.model.undo(self.cache, counts.long())
-        # the drawn token is each row's next pending token
-        last = (counts.long() - 1).clamp(min=0)[:, None]
-        self.feeds[:, :1].copy_(tokens.gather(1, last))
+        self.model.undo(self.cache, counts)
+        next_feeds(tokens, counts, self.feeds)  # the drawn token is each row's next pending token
         self.tokens, self.counts = tokens, counts
         return tokens, counts
 
