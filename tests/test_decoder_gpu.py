@@ -271,3 +271,21 @@ def test_a_captured_verify_step_replays_as_the_eager_step(device):
         runs.append(out)
     for (te, ce, le), (tg, cg, lg) in zip(*runs):
         assert torch.equal(te, tg) and torch.equal(ce, cg) and torch.equal(le, lg)
+
+
+def test_a_model_folder_loads_the_decoder_it_saved(device, tmp_path):
+    # the reference's model-folder layout (checkpoint.py): the decoder loaded
+    # from it scores as the decoder built from the same weights, bit for bit
+    from wpt_amd import folder
+    from wpt_amd.decoder import layer_kinds
+
+    kinds = layer_kinds(1, 1, 1)
+    config = DecoderConfig(layers=len(kinds), d_model=256, heads=16, head_dim=128, ffn=512, vocab=1024, kinds=kinds,
+                           window=16, rope_dims=64, top_k=8)
+    weights = random_weights(config, seed=3, dtype=torch.bfloat16)
+    folder.save_folder(config, weights, tmp_path, b"{}", "test", max_shard_bytes=1 << 20)
+    folder.save_drafter_record(tmp_path)
+    ids = torch.randint(config.vocab, (2, 40), generator=torch.Generator().manual_seed(4)).to(device)
+    loaded = folder.load_decoder(tmp_path, dtype=torch.bfloat16)
+    built = MQADecoder(config, weights, dtype=torch.bfloat16)
+    assert torch.equal(loaded(ids), built(ids))
