@@ -107,7 +107,7 @@ def dense_attention(q, k, v, sink, visible, scale):
     return torch.einsum("...hqk,...kc->...qhc", (z - lse[..., None]).exp(), v.float())
 
 
-ROPE_DIMS = 64  # attention.py:53-54
+ROPE_DIMS = 64  # attention.py:55-56
 ROPE_BASE = 10000
 
 

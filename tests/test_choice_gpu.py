@@ -49,7 +49,7 @@ def test_the_choice_of_bf16_queries_matches_the_oracle(device, heads, width, T, 
 def test_the_verify_step_choice_of_a_wpt_exact_layer(device):
     # the exact layer of a WPT model at the verify step: 32 rows of 4096
     # tokens, k + 1 = 5 queries of 16 heads, TOP_K 1024 outside a WINDOW of
-    # 128 (attention.py:51-52), keys and values the halves of one table
+    # 128 (attention.py:53-54), keys and values the halves of one table
     B, T, H, c, N, top_k, window = 32, 5, 16, 128, 4096, 1024, 128
     q, _, _, _, positions = inputs(B=B, T=T, H=H, c=c, N=N, dtype=torch.bfloat16)
     table = torch.randn(B, N, 2 * c, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)

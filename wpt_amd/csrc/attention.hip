@@ -183,6 +183,16 @@ struct Tile {
 };
 constexpr int kKeySets = 2;  // wavefront sets that take alternate tiles of the workgroup's key range
 
+// The swizzle of the row-block kernel's row-major tile halves (chunk x of row
+// r at unit (C / 8) r + (x ^ tile_sigma(r))): the 16 rows of a K operand read
+// land on 16 distinct bank groups, and so do the chunk pairs 2cb, 2cb + 1 of
+// rows 0-7 (8-15) that a transposed V read takes.
+template <int C>
+__device__ __forceinline__ int tile_sigma(int r) {
+  if constexpr (C == 128) return 2 * (r & 7) + (r >> 3);
+  else return 2 * ((r >> 1) & 3) + (r >> 3);
+}
+
 // A row's softmax reference maximum is its first finite tile maximum and
 // moves only when a later tile's maximum exceeds it by more than this many
 // powers of two (p then stays below 2^32, far inside the fp32 and bf16
@@ -228,6 +238,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     float* __restrict__ lse_out, unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
   using G = Tile<C>;
   constexpr int kRows = 16 * MB;
+  constexpr int kXC = C / 8;  // 16-byte chunks per key or value row
   constexpr int DMAW = MB >= 4 ? 4 : (MB >= 2 ? 2 : 1);  // wavefronts of a key set that issue its DMA
   constexpr int kCnt = G::kLoads / DMAW;                 // DMA instructions per such wavefront and tile
   constexpr int kRing = G::kSlots * G::kElems;           // elements of one key set's ring
@@ -287,15 +298,15 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   const int niter = (ntiles + kKeySets - 1) / kKeySets;       // workgroup iterations
   const int mine = ntiles > kset ? (ntiles - kset + kKeySets - 1) / kKeySets : 0;  // tiles of this key set
 
-  // DMA: instruction ii of a tile covers 16 rows x 64 bytes of one half
-  // (part = ii / kPerHalf: K rows 0-15, K rows 16-31, V rows 0-15, V rows 16-31).
-  // LDS layout of a half, chunk-major with a swizzle: the 16-byte chunk x of
-  // row r at unit 16x + (r ^ 12 (x & 1)); lane l of the instruction fills
-  // unit 64 (ii % kPerHalf) + l, so it fetches row j ^ 12 (g & 1).  The
-  // swizzle keeps the 16-byte operand reads of K conflict-free and makes the
-  // transposed 8-byte reads of V (rows 4g .. 4g + 3 of chunks x, x + 1)
-  // touch distinct banks (measured: bank-conflict cycles down from 32 % to
-  // 3 % of the LDS's active cycles).
+  // DMA: instruction ii of a tile covers whole rows of one half, 64 / XC
+  // rows of XC = C / 8 16-byte chunks (part = ii / kPerHalf: K rows 0-15,
+  // K rows 16-31, V rows 0-15, V rows 16-31), so each instruction reads
+  // 1 KiB of consecutive rows (measured on the stream alone: 12.4 us for the
+  // 64 MB of batch 32 x 4096 against 14.0 us reading 16 rows x 64 bytes).
+  // LDS layout of a half, row-major with a swizzle: chunk x of row r at
+  // unit XC r + (x ^ tile_sigma(r)); lane l of the instruction fills unit
+  // 64 (ii % kPerHalf) + l, so it fetches the chunk whose swizzled place
+  // that is.
   const i32x4 krs = buffer_resource(k + (int64_t)b * ksb);
   const i32x4 vrs = buffer_resource(v + (int64_t)b * vsb);
   const uint32_t krow_bytes = (uint32_t)ksn * 2u, vrow_bytes = (uint32_t)vsn * 2u;
@@ -309,12 +320,14 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
 #pragma unroll
     for (int c = 0; c < kCnt; ++c) {
       const int ii = mb * kCnt + c;
-      const int part = ii / G::kPerHalf, chunk = ii % G::kPerHalf;
-      int n = s_lo + tile * 32 + 16 * (part & 1) + (j ^ (12 * (g & 1)));
+      const int part = ii / G::kPerHalf, quarter = ii % G::kPerHalf;
+      const int row = quarter * (64 / kXC) + lane / kXC;  // the row of the half this lane fills
+      const int x = (lane % kXC) ^ tile_sigma<C>(row);    // the chunk that belongs there
+      int n = s_lo + tile * 32 + 16 * (part & 1) + row;
       n = n < s_hi ? n : s_hi;  // rows past the split are masked; read a valid one
       const uint32_t phys = (uint32_t)(n - rbase) & rows.mask;
-      const uint32_t off = phys * (part < 2 ? krow_bytes : vrow_bytes) + 64u * chunk + 16u * g;
-      dma_16B(part < 2 ? krs : vrs, off, slot + part * (G::kHalf * 2) + 1024u * chunk);
+      const uint32_t off = phys * (part < 2 ? krow_bytes : vrow_bytes) + 16u * x;
+      dma_16B(part < 2 ? krs : vrs, off, slot + part * (G::kHalf * 2) + 1024u * quarter);
     }
   };
   // The queries go out first (DMA into qlds, each m-block laid out like a
@@ -375,12 +388,15 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
 #pragma unroll
   for (int cb = 0; cb < G::kCBlocks; ++cb) o[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegInf, l_run = 0.f;
-  // per-lane element offset of the transposed V reads: lane 16g + 4rr + qq
-  // addresses row 4g + rr, columns 4qq..4qq+3 of a 16-column block
-  const int tr_off =
-      128 * ((lane & 3) >> 1) + 8 * ((4 * g + ((lane >> 2) & 3)) ^ (12 * ((lane >> 1) & 1))) + 4 * (lane & 1);
-  // the K operand of k-step s: row j, chunk 4s + g, at unit 16 (4s + g) + (j ^ 12 (g & 1))
-  const int k_off = 128 * g + 8 * (j ^ (12 * (g & 1)));
+  // the transposed V reads: lane 16g + 4rr + qq addresses row 4g + rr,
+  // columns 4qq..4qq+3 of the 16-column block cb, i.e. chunk 2cb + (qq >> 1)
+  // (= 2cb ^ (qq >> 1)), element 4 (qq & 1) of it
+  const int tr_row = 4 * g + ((lane >> 2) & 3);
+  const int tr_base = 8 * kXC * tr_row + 4 * (lane & 1);
+  const int tr_y = ((lane & 3) >> 1) ^ tile_sigma<C>(tr_row);
+  // the K operand of k-step s: row j, chunk 4s + g (= 4s ^ g)
+  const int k_base = 8 * kXC * j;
+  const int k_y = g ^ tile_sigma<C>(j);
 
   // Waits for this key set's tile of iteration t (each DMA wavefront for its
   // own loads, at most `later` tiles' loads still in flight behind it), then
@@ -405,8 +421,9 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     s1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < G::kSteps; ++s) {
-      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(st + 512 * s + k_off);
-      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(st + G::kHalf + 512 * s + k_off);
+      const int k_off = k_base + 8 * ((4 * s) ^ k_y);
+      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(st + k_off);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(st + G::kHalf + k_off);
       s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[s], s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[s], s1, 0, 0, 0);
     }
@@ -454,11 +471,12 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     // half (e < 4), key 16 + 4g + e - 4 of the second; the V^T operand holds
     // the same keys at column cb*16 + j, two transposed 4-row reads.
     const bf16x8 pt = pack_bf16x8(p);
-    const unsigned short* vs = st + 2 * G::kHalf + tr_off;
+    const unsigned short* vs = st + 2 * G::kHalf + tr_base;
 #pragma unroll
     for (int cb = 0; cb < G::kCBlocks; ++cb) {
-      const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vs + 256 * cb));
-      const s16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vs + G::kHalf + 256 * cb));
+      const int cofs = 8 * ((2 * cb) ^ tr_y);
+      const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vs + cofs));
+      const s16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vs + G::kHalf + cofs));
       typedef short s16x8 __attribute__((ext_vector_type(8)));
       const s16x8 vt = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
       o[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vt), pt, o[cb], 0, 0, 0);
@@ -573,8 +591,10 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
 // tiles w, w + 4, ... into its own two-tile LDS ring (each lane of an LDS DMA
 // fetches the row its list entry names: the gather costs nothing beyond the
 // DMA) and multiplies them with the H <= 16 heads of the query as one MFMA
-// block (S^T = K . Q^T, O^T += V^T . P^T, as the row-block kernel, with its
-// swizzled tile layout).  A missing row (-1, or past the table) is fetched as
+// block (S^T = K . Q^T, O^T += V^T . P^T, as the row-block kernel).  Its
+// tiles are chunk-major: DMA instruction ii fills 16 rows x 64 bytes, the
+// 16-byte chunk x of row r at unit 16x + (r ^ 12 (x & 1)), so that each
+// lane's row is a list entry.  A missing row (-1, or past the table) is fetched as
 // a valid one and masked.  The four wavefronts merge through LDS; the splits
 // merge in combine_splits.
 

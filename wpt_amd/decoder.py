@@ -21,9 +21,12 @@ sparse layer makes that choice (model.py:134-135); layer_kinds gives the
 reference's layout of the three kinds (config.py:17-23).
 
 On the GPU:
+    the input       wptv_embed_rms_norm: the embedding rows, the first norm
+                    and each token's position in one pass
     KV append       wptv_qkv_post: q/k norms, and the new entries written at
                     each row's own length (no host sync)
     norms, SwiGLU   wptv_add_rms_norm (residual add + RMSNorm), wptv_swiglu
+    the lengths     wptv_cache_lengths after the reading and after an undo
     verify attention wptv_verify_attention, reading only the rows the query
                     positions reach in the cache's table
     projections     the matrix products of the dtype on MFMA: wptv_gemm's
@@ -80,8 +83,8 @@ class DecoderConfig:
     vocab: int
     kinds: tuple = ()          # "exact", "window" or "sparse" per layer; () = every layer exact
     window: int = 128          # WINDOW, attention.py:53
-    rope_dims: int = 64        # ROPE_DIMS, attention.py:53
-    rope_base: float = 10000.0
+    rope_dims: int = 64        # ROPE_DIMS, attention.py:55
+    rope_base: float = 10000.0  # ROPE_BASE, attention.py:56
     top_k: int = 1024          # TOP_K, attention.py:54: rows an exact layer chooses for the sparse layers
 
     def __post_init__(self):
