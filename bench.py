@@ -201,16 +201,22 @@ def attention_c3(steps, warmup):
     lengths = torch.randint(N // 2, N + 1, (B,), generator=generator)
     positions = (lengths[:, None] - T + torch.arange(T)).to(device)
     q = torch.randn(B, T, H, c, generator=generator).to(torch.bfloat16).to(device)
-    table = torch.randn(B, N, 2 * c, generator=generator).to(torch.bfloat16).to(device)
+    tables = [torch.randn(B, N, 2 * c, generator=generator).to(torch.bfloat16).to(device) for _ in range(3)]
     sink = torch.full((H,), float("-inf"), device=device)
     idx = torch.empty(B, T, 0, dtype=torch.long, device=device)
-    replay = graphed(lambda: kernels.sparse_attention(q, table[..., :c], table[..., c:], sink, idx, positions,
-                                                      c ** -0.5, W))
-    ms = timed(replay, steps, warmup)
+    calls = 24  # back-to-back calls per graph replay, so that the graph's own launch is not timed
+
+    def run():
+        for i in range(calls):
+            table = tables[i % len(tables)]
+            kernels.sparse_attention(q, table[..., :c], table[..., c:], sink, idx, positions, c ** -0.5, W)
+
+    ms = timed(graphed(run), max(1, steps // 4), max(1, warmup // 4)) / calls
     nbytes = B * (W + T - 1) * 2 * c * 2 + 2 * B * T * H * c * 2 + B * T * 8
     GBps = nbytes / (ms * 1e-3) / 1e9
     return {"ms": ms, "bytes": nbytes, "GBps": GBps, "frac_hbm_peak": GBps / HBM_PEAK_GBS,
-            "query_tokens_per_s": B * T / (ms * 1e-3), "note": "launch-latency-bound: 4.5 MB"}
+            "query_tokens_per_s": B * T / (ms * 1e-3),
+            "note": "4.5 MB a call: launch-latency-bound; the three tables' windows stay in the Infinity Cache"}
 
 
 def tree_c4(steps, warmup):
@@ -242,8 +248,10 @@ def tree_c4(steps, warmup):
 
     replay = graphed(step)
     ms = timed(replay, steps, warmup)
-    attn = graphed(lambda: kernels.tree_attention(q, table[..., :c], table[..., c:], base, parents, c ** -0.5))
-    attn_ms = timed(attn, steps, warmup)
+    # eight back-to-back calls per graph replay, so that the graph's own launch is not timed
+    attn = graphed(lambda: [kernels.tree_attention(q, table[..., :c], table[..., c:], base, parents, c ** -0.5)
+                            for _ in range(8)])
+    attn_ms = timed(attn, steps, warmup) / 8
     written.zero_()
     replay()
     torch.cuda.synchronize()

@@ -1753,6 +1753,8 @@ int sparse_plan(int B, int T, int H, int c, int K, int window, int N, int dtype,
 extern "C" int wptv_sparse_attention_workspace(int B, int T, int H, int c, int K, int window, int N, int dtype,
                                                int* splits, size_t* bytes) {
   if (!splits || !bytes) return fail(WPTV_E_INVALID, "sparse_attention_workspace: null output pointer");
+  if (K == 0 && window > 0)  // the window alone: the row-block kernel (wptv_sparse_attention routes it there)
+    return wptv_attention_workspace(B, T, H, c, N, window, dtype, WPTV_ATTN_RANGE_FROM_POSITIONS, splits, bytes);
   SparsePlan p;
   const int st = sparse_plan(B, T, H, c, K, window, N, dtype, *splits, &p);
   if (st != WPTV_OK) return st;
@@ -1774,6 +1776,10 @@ extern "C" int wptv_sparse_attention(const void* q, const void* k, int64_t k_str
     return fail(WPTV_E_INVALID, "sparse_attention: a row stride below the head width");
   if (gate && gate_stride < (int64_t)H * c)
     return fail(WPTV_E_INVALID, "sparse_attention: gate row stride %lld below H*c", (long long)gate_stride);
+  if (K == 0 && window > 0)  // no chosen rows: the window attention of the row-block kernel, reading the window only
+    return attend(q, k, k_stride_b, k_stride_n, v, v_stride_b, v_stride_n, dtype, positions, window, nullptr, nullptr,
+                  sink, B, T, H, c, N, scale, splits, WPTV_ATTN_RANGE_FROM_POSITIONS, RowMap{nullptr, 0xffffffffu}, N,
+                  OutGate{gate, gate_stride}, out, lse, workspace, workspace_bytes, stream);
   SparsePlan p;
   int st = sparse_plan(B, T, H, c, K, window, N, dtype, splits, &p);
   if (st != WPTV_OK) return st;
