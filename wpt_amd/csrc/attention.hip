@@ -1426,13 +1426,14 @@ struct Plan {
 int pick_mbw(int R) {
   // Query rows per workgroup: every row of a decode step in one group when
   // it fits five 16-row blocks (k+1 = 5 positions of 16 heads), else groups
-  // of four blocks.
+  // of eight blocks (16 wavefronts, 1024 threads), so that a tree's many
+  // query rows stream the keys and values as few times as a workgroup can.
   const int blocks = (R + 15) / 16;
   if (blocks <= 1) return 1;
   if (blocks <= 2) return 2;
   if (blocks <= 3) return 3;
   if (blocks <= 5) return 5;
-  return 4;
+  return 8;
 }
 
 int plan(int B, int T, int H, int c, int N, int window, int dtype, int flags, int requested, Plan* out) {
@@ -1636,6 +1637,7 @@ int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
         case 2: WPTV_LAUNCH(128, 2); break;
         case 3: WPTV_LAUNCH(128, 3); break;
         case 4: WPTV_LAUNCH(128, 4); break;
+        case 8: WPTV_LAUNCH(128, 8); break;
         default: WPTV_LAUNCH(128, 5); break;
       }
     } else {
@@ -1644,6 +1646,7 @@ int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
         case 2: WPTV_LAUNCH(64, 2); break;
         case 3: WPTV_LAUNCH(64, 3); break;
         case 4: WPTV_LAUNCH(64, 4); break;
+        case 8: WPTV_LAUNCH(64, 8); break;
         default: WPTV_LAUNCH(64, 5); break;
       }
     }
