@@ -98,16 +98,17 @@ def graphed(fn):
 # the verify step of the 24-layer decoder
 # ---------------------------------------------------------------------------
 
-def decoder_step(B, kv, k, steps, warmup, temperature=0.8, top_k=None, seed=0, keep=False):
-    """Builds the decoder, prefills kv - 1 tokens per row, captures the step
-    and times it.  Returns a dict of figures (and the pieces, with keep)."""
+def decoder_step(B, kv, k, steps, warmup, temperature=0.8, top_k=None, seed=0, keep=False, config=None):
+    """Builds the decoder (the 24-layer one unless config is given), prefills
+    kv - 1 tokens per row, captures the step and times it.  Returns a dict of
+    figures (and the pieces, with keep)."""
     import torch
 
     from wpt_amd.decoder import LARGE, MQADecoder, random_weights
     from wpt_amd.step import VerifyStep, prefill
 
     device = torch.device("cuda", 0)
-    config = LARGE
+    config = config or LARGE
     weights = random_weights(config, seed=seed, std=0.02, dtype=torch.bfloat16, device=device)
     model = MQADecoder(config, weights, dtype=torch.bfloat16, device=device)
     generator = torch.Generator(device=device).manual_seed(seed + 1)
@@ -137,13 +138,35 @@ def decoder_step(B, kv, k, steps, warmup, temperature=0.8, top_k=None, seed=0, k
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
     tokens = int(written.sum())
-    params = sum(w.numel() for name, w in model.w.items()  # the matrices a step reads whole
-                 if not name.endswith("norm") and name != "embedding")
+    # the matrices a step reads whole (a window layer's q/k/v and gate as their
+    # one fused matrix, a sparse layer's q and gate too)
+    fused = {f"layers.{i}.{part}" for i in config.windows for part in ("qkv", "gate")}
+    fused |= {f"layers.{i}.{part}" for i in config.sparse for part in ("q", "gate")}
+    params = sum(w.numel() for name, w in model.w.items()
+                 if not name.endswith("norm") and not name.endswith("sink") and name != "embedding"
+                 and name not in fused)
     out = {"ms_per_step": ms, "accepted_tokens": tokens, "tokens_per_s": tokens / (steps * ms * 1e-3),
            "tokens_per_row_step": tokens / (steps * B), "weight_bytes": 2 * params,
            "lengths_after": int(cache.lengths.max())}
     if keep:
         out["_pieces"] = (model, cache, step, weights)
+    return out
+
+
+def wpt_layout_step(B, kv, k, steps, warmup):
+    """The verify step of a decoder in the layout of the reference's largest
+    model recipe (data/recipes/models/interstitial-pecker.json: window layers
+    4, sparse groups 2 of 5 sparse layers, 21 layers; d_model 512, 8 query
+    heads of 128), window 128 and a choice of 1024 rows: all three attention
+    kinds in one step.  A dense SwiGLU block of 1536 (the shared expert's 512
+    plus four routed experts' 256) stands in for the experts; vocab 32768."""
+    from wpt_amd.decoder import DecoderConfig, layer_kinds
+
+    kinds = layer_kinds(4, 2, 5)
+    config = DecoderConfig(layers=len(kinds), d_model=512, heads=8, head_dim=128, ffn=1536, vocab=32768, kinds=kinds,
+                           window=128, top_k=1024)
+    out = decoder_step(B, kv, k, steps, warmup, config=config)
+    out["layers"] = "".join(kind[0] for kind in kinds)  # w window, e exact, s sparse
     return out
 
 
@@ -549,6 +572,8 @@ def main():
             configs[f"decoder_step_B64_KV2048_k4_T0.8_topk{top_k}"] = decoder_step(64, 2048, K, args.steps,
                                                                                   args.warmup, top_k=top_k)
             torch.cuda.empty_cache()
+        configs["wpt_layout_step_B32_KV4096_k4"] = wpt_layout_step(B, KV, K, args.steps, args.warmup)
+        torch.cuda.empty_cache()
     line = {
         "metric": "accepted tok/s (B=32,KV=4096,k=4 bf16); verify-attn % of HBM roofline",
         "value": head["tokens_per_s"], "unit": "accepted tokens/s", "n_gpus": 1, "steps": args.steps,
