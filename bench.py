@@ -24,7 +24,9 @@ workloads: the FP32 plumbing decoder's greedy step (checked bit-exact against
 the oracle), sliding-window and tree verification, the three attention layers
 of a WPT model at the verify shape (exact with its top-1024 choice, sparse over
 the chosen rows, window over its ring), the step's matrix products (MFMA
-TFLOP/s against the bf16 peak), and the 24-layer step at batch 64 / KV 2048.  `cpu_baseline` is the oracle (the reference's PyTorch
+TFLOP/s against the bf16 peak), the 24-layer step at batch 64 / KV 2048, and
+the step of a decoder in the layout of the reference's largest model recipe
+(window, exact and sparse layers).  `cpu_baseline` is the oracle (the reference's PyTorch
 algorithm restated in FP32 on the CPU) running the headline step for a sample
 of rows on this host's cores.
 """
