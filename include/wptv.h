@@ -327,7 +327,8 @@ int wptv_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, int
  *   q        draft distributions, position j (0..L-1) of row b at
  *            q + b*q_stride_b + j*q_stride_t, V contiguous fp32
  *   drafts   [B, L] int64 (row stride drafts_stride_b)
- *   lengths  NULL (every row verifies L drafts) or [B] int32 <= L
+ *   lengths  NULL (every row verifies L drafts) or [B] int32 in 0..L (a
+ *            length outside it is taken as the nearest end)
  *   u        [B, L] fp32 uniforms in [0, 1): draft j of row b is kept iff
  *            u[b, j] * q[b, j, draft] < p[j, draft]
  *   e        [B, V] fp32 Exp(1) draws: the replacement or bonus token is

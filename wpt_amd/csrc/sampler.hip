@@ -4,17 +4,19 @@
 // per-row keep / reject / resample loop (Writer._speculate, :210-229), fused
 // over the vocabulary for every row at once, with the draws read from a tape.
 //
-//   accept_stats   one workgroup per (batch row, position): the row of scores
-//                  divided by the temperature, the top-k threshold (radix
-//                  select of the k-th largest, ties kept), the maximum and the
-//                  softmax denominator, and for a draft position the decision
-//                  u * q[draft] < p[draft]; in greedy mode the first maximal
-//                  index instead, the draft kept iff it is that index
-//   accept_finish  one workgroup per batch row: the first rejected draft, then
-//                  the replacement argmax_v (max(0, p_v - q_v) / S) / e_v, or
-//                  after every draft kept the bonus argmax_v p_v / e_v (one
+//   accept_stats   one workgroup per (batch row, position), the single pass
+//                  over the vocabulary: the row of scores divided by the
+//                  temperature, the top-k threshold (radix select of the k-th
+//                  largest, ties kept), the maximum and the softmax
+//                  denominator, for a draft position the decision
+//                  u * q[draft] < p[draft] and the replacement drawn should it
+//                  be the first rejection, argmax_v (max(0, p_v - q_v) / S) / e_v,
+//                  and after the last draft the bonus argmax_v p_v / e_v (one
 //                  draw from a distribution by the exponential race torch's
-//                  multinomial uses)
+//                  multinomial uses); in greedy mode the first maximal index
+//                  instead, the draft kept iff it is that index
+//   accept_pick    one thread per batch row: the first rejected draft and the
+//                  row's tokens from the per-position results
 //   tree_walk      greedy verification of a draft tree from the per-node argmax
 //
 // Each vocabulary row is read once per pass from HBM with coalesced loads and
@@ -37,6 +39,7 @@ struct Stats {  // per (batch row, position); arrays of B * P in the workspace
   float* thr;   // top-k threshold (entries below it have p = 0), -inf without a cut
   int* best;    // first maximal index of the scores
   int* keep;    // 1 if the draft at this position is kept
+  int* cand;    // the token drawn if this position is the first rejection (the bonus at the last), -1: none
 };
 
 __device__ __forceinline__ float block_max(float x, float* red) {
@@ -90,6 +93,17 @@ __device__ __forceinline__ int block_argmax(float v, int i, float* redv, int* re
   int bi = redi[0];
   for (int w = 1; w < kW; ++w) arg_better(bv, bi, redv[w], redi[w]);
   return bi;
+}
+
+// A row of V floats as a buffer: a load at index v reads row[v], and 0 for
+// v >= V (the buffer's range check), from a 32-bit offset per item rather
+// than a 64-bit address.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_resource(const float* row, int V) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(row), 0, V * 4, 0x00020000);
+}
+
+__device__ __forceinline__ float row_load(__amdgpu_buffer_rsrc_t r, int v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, v * 4, 0, 0));
 }
 
 // The k-th largest of the valid values (radix select over order-preserving
@@ -149,26 +163,31 @@ __device__ float kth_largest(const float (&s)[ITEMS], int V, int k, int* hist, i
 
 template <int ITEMS>
 __global__ __launch_bounds__(kT) void accept_stats(const float* __restrict__ scores, int64_t sb, int64_t st,
-                                                   const int32_t* __restrict__ firsts, const float* __restrict__ q,
+                                                   const int32_t* __restrict__ firsts, const float* q,
                                                    int64_t qb, int64_t qt, const int64_t* __restrict__ drafts,
                                                    int64_t db, const int32_t* __restrict__ lengths,
-                                                   const float* __restrict__ u, float temperature, int top_k,
-                                                   int greedy, int L, int V, Stats stats) {
+                                                   const float* __restrict__ u, const float* e,
+                                                   float temperature, int top_k, int greedy, int L, int V,
+                                                   Stats stats) {
   __shared__ float redv[kW];
   __shared__ int redi[kW];
   __shared__ int hist[256];
   __shared__ int sel[2];
   const int j = blockIdx.x, b = blockIdx.y, P = L + 1;
-  const int n = lengths ? lengths[b] : L;
+  const int n = lengths ? min(max(lengths[b], 0), L) : L;
   if (j > n) return;
   const int64_t first = firsts ? firsts[b] : 0;
   const float* row = scores + b * sb + (first + j) * st;
   const int tid = threadIdx.x;
-  // every load issued before the first use: indices past the row read its
-  // last entry, masked after
+  // every load of a row issued before the first use; indices past the row
+  // read 0, masked after
+  const bool draft_pos = j < n;
+  const float* qrow = (!greedy && draft_pos) ? q + b * qb + j * qt : row;  // row: a valid address, unused
+  const float* erow = greedy ? row : e + (int64_t)b * V;
   float x[ITEMS];
+  const auto rs = row_resource(row, V);
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) x[i] = row[min(tid + i * kT, V - 1)];
+  for (int i = 0; i < ITEMS; ++i) x[i] = row_load(rs, tid + i * kT);
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) x[i] = tid + i * kT < V ? x[i] : kNegInfS;
   // first maximal index of the raw scores
@@ -199,11 +218,48 @@ __global__ __launch_bounds__(kT) void accept_stats(const float* __restrict__ sco
   for (int i = 0; i < ITEMS; ++i)
     if (tid + i * kT < V && x[i] >= thr) part += expf(x[i] - m);
   const float z = block_sum(part, redv);
+  // The draw if this position is the first rejected draft: the residual
+  // max(0, p - q) normalized by its sum, by the exponential race; at the
+  // position after the last draft the bonus draw from p itself (the
+  // reference's multinomial of __init__.py:222-229, as argmax_v w_v / e_v).
+  // The draft row and then the exponentials are read one at a time, so that
+  // no more than two rows are held in registers.
+  const float zinv = 1.f / z;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) x[i] = tid + i * kT < V && x[i] >= thr ? expf(x[i] - m) * zinv : 0.f;
+  float S = 1.f;
+  if (draft_pos) {
+    float qv[ITEMS];
+    const auto rq = row_resource(qrow, V);
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) qv[i] = row_load(rq, tid + i * kT);
+    float rest = 0.f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      x[i] = tid + i * kT < V ? fmaxf(x[i] - qv[i], 0.f) : 0.f;
+      rest += x[i];
+    }
+    S = block_sum(rest, redv);
+  }
+  float ev[ITEMS];
+  const auto re = row_resource(erow, V);
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) ev[i] = row_load(re, tid + i * kT);
+  float cv = kNegInfS;
+  int ci = INT_MAX;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int v = tid + i * kT;
+    if (v < V) arg_better(cv, ci, (draft_pos ? x[i] / S : x[i]) / ev[i], v);
+  }
+  const int drawn = block_argmax(cv, ci, redv, redi);
   if (tid == 0) {
     stats.m[idx] = m;
     stats.z[idx] = z;
     stats.thr[idx] = thr;
     stats.best[idx] = best;
+    // a residual with no mass has no draw (the reference's multinomial raises)
+    stats.cand[idx] = (!(draft_pos && !(S > 0.f)) && drawn >= 0 && drawn < V) ? drawn : -1;
     int keep = 0;
     if (j < n) {
       const int64_t d = drafts[b * db + j];
@@ -217,72 +273,23 @@ __global__ __launch_bounds__(kT) void accept_stats(const float* __restrict__ sco
   }
 }
 
-template <int ITEMS>
-__global__ __launch_bounds__(kT) void accept_finish(const float* __restrict__ scores, int64_t sb, int64_t st,
-                                                    const int32_t* __restrict__ firsts, const float* __restrict__ q,
-                                                    int64_t qb, int64_t qt, const int64_t* __restrict__ drafts,
-                                                    int64_t db, const int32_t* __restrict__ lengths,
-                                                    const float* __restrict__ e, float temperature, int greedy, int L,
-                                                    int V, Stats stats, int64_t* __restrict__ tokens,
-                                                    int32_t* __restrict__ n_tokens) {
-  __shared__ float redv[kW];
-  __shared__ int redi[kW];
-  const int b = blockIdx.x, P = L + 1, tid = threadIdx.x;
-  const int n = lengths ? lengths[b] : L;
+// Each row's tokens from the per-position decisions: the drafts up to the
+// first rejected one, then that position's draw (the argmax in greedy mode),
+// or every draft and the bonus draw (__init__.py:210-229).  One thread per row.
+__global__ __launch_bounds__(64) void accept_pick(const int64_t* __restrict__ drafts, int64_t db,
+                                                  const int32_t* __restrict__ lengths, int greedy, int L, int B,
+                                                  Stats stats, int64_t* __restrict__ tokens,
+                                                  int32_t* __restrict__ n_tokens) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const int P = L + 1;
+  const int n = lengths ? min(max(lengths[b], 0), L) : L;
   int js = 0;  // the first rejected draft, n when every draft is kept
   while (js < n && stats.keep[b * P + js]) ++js;
-  for (int t = tid; t < P; t += kT)
-    if (t != js) tokens[(int64_t)b * P + t] = t < js ? drafts[b * db + t] : -1;  // slot js: thread 0, below
-  const int idx = b * P + js;
-  if (greedy) {
-    if (tid == 0) {
-      tokens[(int64_t)b * P + js] = stats.best[idx];
-      n_tokens[b] = js + 1;
-    }
-    return;
-  }
-  const int64_t first = firsts ? firsts[b] : 0;
-  const float* row = scores + b * sb + (first + js) * st;
-  const float m = stats.m[idx], zinv = 1.f / stats.z[idx], thr = stats.thr[idx];
-  const bool rejected = js < n;
-  const float* qrow = rejected ? q + b * qb + js * qt : row;  // (row: a valid address, unused)
-  const float* erow = e + (int64_t)b * V;
-  // every load issued before the first use: indices past the row read its
-  // last entry, masked after
-  float w[ITEMS], qv[ITEMS], ev[ITEMS];
-#pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    const int vc = min(tid + i * kT, V - 1);
-    w[i] = row[vc];
-    qv[i] = qrow[vc];
-    ev[i] = erow[vc];
-  }
-  float part = 0.f;
-#pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    const float s = w[i] / temperature;
-    float p = s >= thr ? expf(s - m) * zinv : 0.f;
-    if (rejected) p = fmaxf(p - qv[i], 0.f);
-    p = tid + i * kT < V ? p : 0.f;
-    w[i] = p;
-    part += p;
-  }
-  float S = 1.f;
-  if (rejected) S = block_sum(part, redv);
-  float bv = kNegInfS;
-  int bi = INT_MAX;
-#pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    const int v = tid + i * kT;
-    if (v < V) arg_better(bv, bi, (rejected ? w[i] / S : w[i]) / ev[i], v);
-  }
-  const int token = block_argmax(bv, bi, redv, redi);
-  if (tid == 0) {
-    // a residual with no mass has no draw (the reference's multinomial raises)
-    const bool ok = !(rejected && !(S > 0.f)) && token >= 0 && token < V;
-    tokens[(int64_t)b * P + js] = ok ? token : -1;
-    n_tokens[b] = ok ? js + 1 : -1;
-  }
+  for (int t = 0; t < P; ++t) tokens[(int64_t)b * P + t] = t < js ? drafts[b * db + t] : -1;
+  const int drawn = greedy ? stats.best[b * P + js] : stats.cand[b * P + js];
+  tokens[(int64_t)b * P + js] = drawn;
+  n_tokens[b] = drawn >= 0 ? js + 1 : -1;
 }
 
 // Greedy walk down a draft tree: node i's parent parents[i] < i, the root 0.
@@ -326,10 +333,11 @@ Stats carve(void* workspace, int B, int P) {
   s.thr = reinterpret_cast<float*>(p + 2 * n);
   s.best = reinterpret_cast<int*>(p + 3 * n);
   s.keep = reinterpret_cast<int*>(p + 4 * n);
+  s.cand = reinterpret_cast<int*>(p + 5 * n);
   return s;
 }
 
-size_t stats_bytes(int B, int P) { return 5 * align_up((size_t)B * P * 4, 256); }
+size_t stats_bytes(int B, int P) { return 6 * align_up((size_t)B * P * 4, 256); }
 
 int items_for(int V) {
   const int per = (V + kT - 1) / kT;
@@ -382,19 +390,15 @@ extern "C" int wptv_accept(const float* scores, int64_t scores_stride_b, int64_t
   const Stats s = carve(workspace, B, L + 1);
 #define WPTV_STATS(I)                                                                                           \
   hipLaunchKernelGGL(accept_stats<I>, dim3(L + 1, B), dim3(kT), 0, stream, scores, scores_stride_b,             \
-                     scores_stride_t, firsts, q, q_stride_b, q_stride_t, drafts, drafts_stride_b, lengths, u,   \
+                     scores_stride_t, firsts, q, q_stride_b, q_stride_t, drafts, drafts_stride_b, lengths, u, e, \
                      temperature, top_k, greedy, L, V, s)
   WPTV_ITEMS(V, WPTV_STATS)
 #undef WPTV_STATS
   int st = launched("accept_stats");
   if (st != WPTV_OK) return st;
-#define WPTV_FINISH(I)                                                                                          \
-  hipLaunchKernelGGL(accept_finish<I>, dim3(B), dim3(kT), 0, stream, scores, scores_stride_b, scores_stride_t, \
-                     firsts, q, q_stride_b, q_stride_t, drafts, drafts_stride_b, lengths, e, temperature, greedy, \
-                     L, V, s, tokens, n_tokens)
-  WPTV_ITEMS(V, WPTV_FINISH)
-#undef WPTV_FINISH
-  return launched("accept_finish");
+  hipLaunchKernelGGL(accept_pick, dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b, lengths, greedy, L,
+                     B, s, tokens, n_tokens);
+  return launched("accept_pick");
 }
 
 extern "C" int wptv_greedy_tree(const float* scores, int64_t scores_stride_b, int64_t scores_stride_t,
@@ -412,7 +416,7 @@ extern "C" int wptv_greedy_tree(const float* scores, int64_t scores_stride_b, in
   // per-node argmax: the stats pass in greedy mode over M positions with no drafts to judge
 #define WPTV_STATS(I)                                                                                             \
   hipLaunchKernelGGL(accept_stats<I>, dim3(M, B), dim3(kT), 0, stream, scores, scores_stride_b, scores_stride_t, \
-                     nullptr, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, 1.f, 0, 1, M - 1, V, s)
+                     nullptr, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, nullptr, 1.f, 0, 1, M - 1, V, s)
   WPTV_ITEMS(V, WPTV_STATS)
 #undef WPTV_STATS
   int st = launched("accept_stats");
