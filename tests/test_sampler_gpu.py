@@ -37,7 +37,8 @@ def compare(got, expected, gaps):
 
 
 @pytest.mark.parametrize("V, top_k, temperature", [(32768, None, 0.8), (32768, 40, 0.8), (8192, 40, 1.0),
-                                                   (1000, 1, 0.8), (50, None, 1.3)])
+                                                   (1000, 1, 0.8), (50, None, 1.3), (32768, 1024, 0.8),
+                                                   (32768, 1500, 0.8), (2000, 1999, 1.0)])
 def test_accept_matches_the_oracle_on_one_tape(device, V, top_k, temperature):
     B, L = 64, 4
     scores, q, drafts, u, e = step_inputs(B, L, V, seed=V + (top_k or 0))
@@ -50,6 +51,22 @@ def test_accept_matches_the_oracle_on_one_tape(device, V, top_k, temperature):
     assert not near
     kept = [len(t) - 1 for t in expected]
     assert min(kept) < L and (max(kept) > 0 or top_k == 1)  # rows keep and reject
+
+
+@pytest.mark.parametrize("top_k", [5, 40, 1500])
+def test_a_top_k_cut_through_tied_scores_keeps_every_tie(device, top_k):
+    # scores on a few levels, so that the k-th largest ties with dozens to
+    # thousands of entries (28 to 5420 kept per position at these seeds),
+    # every one of them kept as the reference's `scores < v[..., [-1]]` keeps
+    # them
+    B, L, V = 32, 4, 32768
+    scores, q, drafts, u, e = step_inputs(B, L, V, seed=20 + top_k)
+    scores = torch.round(scores / 8)
+    lengths = [L] * B
+    expected = oracle.accept(scores, q, drafts, lengths, 0.8, top_k, [oracle.TapeDraws(u[b], e[b]) for b in range(B)])
+    tokens, counts = sampling.accept(*(x.to(device) for x in (scores, q, drafts, u, e)), 0.8, top_k)
+    near = compare(sampling.written(tokens, counts), expected, oracle.margins(scores, q, drafts, lengths, 0.8, top_k, u))
+    assert not near
 
 
 def test_per_row_lengths_and_first_positions(device):

@@ -106,10 +106,11 @@ __device__ __forceinline__ float row_load(__amdgpu_buffer_rsrc_t r, int v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, v * 4, 0, 0));
 }
 
-// The k-th largest of the valid values (radix select over order-preserving
-// keys, most significant byte first).
-template <int ITEMS>
-__device__ float kth_largest(const float (&s)[ITEMS], int V, int k, int* hist, int* sel) {
+// The k-th largest order key among the entries that count (valid[i] and
+// key[i] >= floor): a radix select, most significant byte first.
+template <int N>
+__device__ uint32_t kth_key(const uint32_t (&key)[N], const bool (&valid)[N], uint32_t floor, int k, int* hist,
+                            int* sel) {
   uint32_t prefix = 0, mask = 0;
   int remaining = k;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -118,13 +119,8 @@ __device__ float kth_largest(const float (&s)[ITEMS], int V, int k, int* hist, i
     if (tid < 256) hist[tid] = 0;
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      const int v = tid + i * kT;
-      if (v < V) {
-        const uint32_t key = order_key(s[i]);
-        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
-      }
-    }
+    for (int i = 0; i < N; ++i)
+      if (valid[i] && key[i] >= floor && (key[i] & mask) == prefix) atomicAdd(&hist[(key[i] >> shift) & 255], 1);
     __syncthreads();
     if (tid < 64) {
       // lane l holds bins 4l .. 4l + 3; above[l] = entries in bins >= 4l + 4
@@ -158,7 +154,36 @@ __device__ float kth_largest(const float (&s)[ITEMS], int V, int k, int* hist, i
     mask |= 255u << shift;
     remaining = sel[1];
   }
-  return key_value(prefix);
+  return prefix;
+}
+
+// The k-th largest of the valid values (v < V), 0 < k < V.  For k up to the
+// number of threads, a floor first: the k-th largest of the threads' own
+// maxima.  The k largest maxima are k distinct entries at or above it, so
+// the k-th largest entry is too, and the full select then counts only the
+// entries at or above the floor (about k of them instead of V, which keeps
+// the histogram's atomics off the few bins that hold most of a row).
+template <int ITEMS>
+__device__ float kth_largest(const float (&s)[ITEMS], int V, int k, int* hist, int* sel) {
+  const int tid = threadIdx.x;
+  uint32_t key[ITEMS];
+  bool valid[ITEMS];
+  uint32_t own = 0;
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    key[i] = order_key(s[i]);
+    valid[i] = tid + i * kT < V;
+    if (valid[i]) own = max(own, key[i]);
+    any |= valid[i];
+  }
+  uint32_t floor = 0;
+  if (k <= kT) {
+    const uint32_t mine[1] = {own};
+    const bool counts[1] = {any};
+    floor = kth_key<1>(mine, counts, 0u, k, hist, sel);
+  }
+  return key_value(kth_key<ITEMS>(key, valid, floor, k, hist, sel));
 }
 
 template <int ITEMS>
