@@ -309,7 +309,8 @@ class MQADecoder:
         B, T = ids.shape
         if B != cache.rows:
             raise ValueError(f"ids hold {B} rows; the cache {cache.rows}")
-        if counts is None:  # every token of every row: one device tensor per width, made once
+        if counts is None:  # every token of every row: one device tensor per width, made once and kept
+            # (a captured step replays the tensor it read, so none is ever dropped)
             counts_ = self._widths.get((B, T))
             if counts_ is None:
                 counts_ = self._widths[(B, T)] = torch.full((B,), T, dtype=torch.long, device=self.device)
