@@ -194,7 +194,8 @@ int wptv_kv_append(void* table, int64_t table_stride_b, int64_t table_stride_n, 
  *   (undo = 0; the reference's Reading.finish, cache.py:130-134: before =
  *   lengths when before is not NULL, then lengths += counts) or after an undo
  *   (undo = 1; Rows.undo, cache.py:69-77: lengths = before + counts, counts
- *   being the kept tokens).  counts (B,) of counts_dtype WPTV_I64 or WPTV_I32.
+ *   being the kept tokens, a count outside 0 .. lengths - before taken as
+ *   the nearest end).  counts (B,) of counts_dtype WPTV_I64 or WPTV_I32.
  *   Device-side, so that a captured step replays on the cache's state. */
 int wptv_cache_lengths(int64_t* lengths, int64_t* before, const void* counts, int counts_dtype, int B, int undo,
                        hipStream_t stream);

@@ -45,8 +45,13 @@ def test_the_lengths_after_a_reading_and_an_undo(device, index):
     assert cache.lengths.tolist() == [9, 4, 19] and cache.before.tolist() == [5, 0, 17]
     cache.undo(torch.tensor([1, 0, 2], dtype=index, device=device))
     assert cache.lengths.tolist() == [6, 0, 19]
+    # a row the sampler could not draw for (-1) keeps nothing, and no row
+    # keeps more than it read
+    cache.finish(torch.tensor([4, 4, 2], dtype=index, device=device), undoable=True, width=4)
+    cache.undo(torch.tensor([-1, 9, 2], dtype=index, device=device))
+    assert cache.lengths.tolist() == [6, 4, 21]
     cache.finish(torch.tensor([3, 1, 0], device=device), undoable=False, width=3)
-    assert cache.lengths.tolist() == [9, 1, 19] and cache.before.tolist() == [5, 0, 17]
+    assert cache.lengths.tolist() == [9, 5, 21] and cache.before.tolist() == [6, 0, 19]
     with pytest.raises(ValueError):
         cache.undo(torch.zeros(3, dtype=torch.long, device=device))
 

@@ -41,7 +41,10 @@ __global__ __launch_bounds__(64) void cache_lengths(int64_t* __restrict__ length
   if (b >= B) return;
   const int64_t n = (int64_t)counts[b];
   if (undo) {
-    lengths[b] = before[b] + n;
+    // kept tokens outside 0 .. the tokens read (a row the sampler could not
+    // draw for writes -1) are taken as the nearest end
+    const int64_t start = before[b], read = lengths[b] - start;
+    lengths[b] = start + min(max(n, (int64_t)0), read);
   } else {
     const int64_t len = lengths[b];
     if (before) before[b] = len;
