@@ -309,8 +309,9 @@ __global__ __launch_bounds__(64) void accept_pick(const int64_t* __restrict__ dr
   if (b >= B) return;
   const int P = L + 1;
   const int n = lengths ? min(max(lengths[b], 0), L) : L;
-  int js = 0;  // the first rejected draft, n when every draft is kept
-  while (js < n && stats.keep[b * P + js]) ++js;
+  int js = n;  // the first rejected draft, n when every draft is kept (independent loads, not a chain)
+  for (int t = n - 1; t >= 0; --t)
+    if (!stats.keep[b * P + t]) js = t;
   for (int t = 0; t < P; ++t) tokens[(int64_t)b * P + t] = t < js ? drafts[b * db + t] : -1;
   const int drawn = greedy ? stats.best[b * P + js] : stats.cand[b * P + js];
   tokens[(int64_t)b * P + js] = drawn;
