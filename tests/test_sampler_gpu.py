@@ -38,7 +38,8 @@ def compare(got, expected, gaps):
 
 @pytest.mark.parametrize("V, top_k, temperature", [(32768, None, 0.8), (32768, 40, 0.8), (8192, 40, 1.0),
                                                    (1000, 1, 0.8), (50, None, 1.3), (32768, 1024, 0.8),
-                                                   (32768, 1500, 0.8), (2000, 1999, 1.0)])
+                                                   (32768, 1500, 0.8), (2000, 1999, 1.0), (65536, 40, 0.8),
+                                                   (65536, None, 1.0)])
 def test_accept_matches_the_oracle_on_one_tape(device, V, top_k, temperature):
     B, L = 64, 4
     scores, q, drafts, u, e = step_inputs(B, L, V, seed=V + (top_k or 0))
