@@ -40,7 +40,11 @@ tests/test_scheduling.py):
                the model's distribution (total variation < 0.05 over 4000
                rows); the scheduler's known answers (test_sampling.py:230-238)
                and a brute force over widths
-Parity unpinned: the exact token stream the reference's Writer draws from a
-seed through its lazy generator order (its tests assert only "same seed, same
-tokens"); the oracle pins the rule, and the tape, not that stream.
+The exact token stream the reference's Writer draws from a seed through its
+lazy generator order (its own tests assert only "same seed, same tokens") is
+pinned by golden streams of the reference's Writer itself
+(tests/golden/writer_vectors.json, written by
+tests/golden/make_writer_vectors.py on the stub model of tests/golden/stubs.py):
+the oracle's lazy replay writes the same tokens and counts
+(tests/test_oracle_writer.py).
 """
