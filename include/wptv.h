@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define WPTV_ABI_VERSION 1
+#define WPTV_ABI_VERSION 2
 
 enum {
   WPTV_OK = 0,
@@ -321,8 +321,11 @@ int wptv_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, int
  * fused over the vocabulary for every row at once.
  *
  *   scores   position j (0..L) of row b at scores + b*scores_stride_b +
- *            (firsts[b] + j)*scores_stride_t, V contiguous fp32: the model's
- *            scores at the pending token and at each draft (the reference's
+ *            (firsts[b] + j)*scores_stride_t (in elements), V contiguous
+ *            values of scores_dtype (WPTV_F32, or WPTV_BF16: the lm_head's
+ *            logits as they come, read as their exact FP32 values, which is
+ *            the reference's scores.float(), :174): the model's scores at the
+ *            pending token and at each draft (the reference's
  *            scores[i, firsts:firsts + L + 1], :210-212)
  *   firsts   NULL (0 for every row) or [B] int32
  *   q        draft distributions, position j (0..L-1) of row b at
@@ -349,8 +352,8 @@ int wptv_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, int
  * ------------------------------------------------------------------------- */
 int wptv_accept_workspace(int B, int L, size_t* bytes);
 
-int wptv_accept(const float* scores, int64_t scores_stride_b, int64_t scores_stride_t, const int32_t* firsts,
-                const float* q, int64_t q_stride_b, int64_t q_stride_t, const int64_t* drafts,
+int wptv_accept(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
+                const int32_t* firsts, const float* q, int64_t q_stride_b, int64_t q_stride_t, const int64_t* drafts,
                 int64_t drafts_stride_b, const int32_t* lengths, const float* u, const float* e, float temperature,
                 int top_k, int greedy, int B, int L, int V, int64_t* tokens, int32_t* n_tokens, void* workspace,
                 size_t workspace_bytes, hipStream_t stream);
@@ -360,7 +363,8 @@ int wptv_accept(const float* scores, int64_t scores_stride_b, int64_t scores_str
  * move to the child whose token equals the argmax (first maximal index) of
  * the current node's scores, the lowest node index among equal children,
  * until none does; then the argmax.  Scores position i = node i (row stride
- * scores_stride_b, node stride scores_stride_t, V contiguous fp32);
+ * scores_stride_b, node stride scores_stride_t, V contiguous values of
+ * scores_dtype, WPTV_F32 or WPTV_BF16);
  * node_tokens [B, M] int64; parents [M] int32.
  *   path     [B, M + 1] int64 out: the accepted node indices from the root
  *            (the root included), -1 after
@@ -368,7 +372,7 @@ int wptv_accept(const float* scores, int64_t scores_stride_b, int64_t scores_str
  *            root, then the argmax; -1 after
  *   n_tokens [B] int32 out: accepted nodes after the root + 1
  *   workspace  wptv_accept_workspace(B, M - 1) bytes */
-int wptv_greedy_tree(const float* scores, int64_t scores_stride_b, int64_t scores_stride_t,
+int wptv_greedy_tree(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
                      const int64_t* node_tokens, const int32_t* parents, int B, int M, int V, int64_t* path,
                      int64_t* tokens, int32_t* n_tokens, void* workspace, size_t workspace_bytes,
                      hipStream_t stream);

@@ -70,6 +70,22 @@ def test_a_top_k_cut_through_tied_scores_keeps_every_tie(device, top_k):
     assert not near
 
 
+@pytest.mark.parametrize("top_k", [None, 40])
+def test_bf16_scores_decide_as_their_fp32_values(device, top_k):
+    # the lm_head's bf16 logits read directly are the reference's
+    # scores.float(): every token and count equal, bit for bit
+    B, L, V = 32, 4, 32768
+    scores, q, drafts, u, e = step_inputs(B, L, V, seed=30)
+    low = scores.to(torch.bfloat16)
+    on = [x.to(device) for x in (q, drafts, u, e)]
+    t16, c16 = sampling.accept(low.to(device), *on, 0.8, top_k)
+    t32, c32 = sampling.accept(low.float().to(device), *on, 0.8, top_k)
+    assert torch.equal(t16, t32) and torch.equal(c16, c32)
+    g16 = sampling.greedy_chain(low.to(device), on[1])
+    g32 = sampling.greedy_chain(low.float().to(device), on[1])
+    assert all(torch.equal(a, b) for a, b in zip(g16, g32))
+
+
 def test_per_row_lengths_and_first_positions(device):
     B, L, V = 16, 4, 4096
     scores, q, drafts, u, e = step_inputs(B, L, V, seed=3)

@@ -98,12 +98,23 @@ __device__ __forceinline__ int block_argmax(float v, int i, float* redv, int* re
 // A row of V floats as a buffer: a load at index v reads row[v], and 0 for
 // v >= V (the buffer's range check), from a 32-bit offset per item rather
 // than a 64-bit address.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_resource(const float* row, int V) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(row), 0, V * 4, 0x00020000);
+template <typename S>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_resource(const S* row, int V) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(row), 0, V * (int)sizeof(S), 0x00020000);
 }
 
 __device__ __forceinline__ float row_load(__amdgpu_buffer_rsrc_t r, int v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, v * 4, 0, 0));
+}
+
+// A scores row of FP32 or bf16 values (the model's logits as they come),
+// read as FP32: a bf16 value converts exactly.
+template <typename S>
+__device__ __forceinline__ float score_load(__amdgpu_buffer_rsrc_t r, int v) {
+  if constexpr (sizeof(S) == 2)
+    return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, v * 2, 0, 0));
+  else
+    return row_load(r, v);
 }
 
 // The k-th largest order key among the entries that count (valid[i] and
@@ -186,8 +197,8 @@ __device__ float kth_largest(const float (&s)[ITEMS], int V, int k, int* hist, i
   return key_value(kth_key<ITEMS>(key, valid, floor, k, hist, sel));
 }
 
-template <int ITEMS>
-__global__ __launch_bounds__(kT) void accept_stats(const float* __restrict__ scores, int64_t sb, int64_t st,
+template <int ITEMS, typename S>
+__global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores, int64_t sb, int64_t st,
                                                    const int32_t* __restrict__ firsts, const float* q,
                                                    int64_t qb, int64_t qt, const int64_t* __restrict__ drafts,
                                                    int64_t db, const int32_t* __restrict__ lengths,
@@ -202,17 +213,17 @@ __global__ __launch_bounds__(kT) void accept_stats(const float* __restrict__ sco
   const int n = lengths ? min(max(lengths[b], 0), L) : L;
   if (j > n) return;
   const int64_t first = firsts ? firsts[b] : 0;
-  const float* row = scores + b * sb + (first + j) * st;
+  const S* row = scores + b * sb + (first + j) * st;
   const int tid = threadIdx.x;
   // every load of a row issued before the first use; indices past the row
   // read 0, masked after
   const bool draft_pos = j < n;
-  const float* qrow = (!greedy && draft_pos) ? q + b * qb + j * qt : row;  // row: a valid address, unused
-  const float* erow = greedy ? row : e + (int64_t)b * V;
+  const float* qrow = (!greedy && draft_pos) ? q + b * qb + j * qt : nullptr;
+  const float* erow = greedy ? nullptr : e + (int64_t)b * V;
   float x[ITEMS];
   const auto rs = row_resource(row, V);
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) x[i] = row_load(rs, tid + i * kT);
+  for (int i = 0; i < ITEMS; ++i) x[i] = score_load<S>(rs, tid + i * kT);
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) x[i] = tid + i * kT < V ? x[i] : kNegInfS;
   // first maximal index of the raw scores
@@ -252,7 +263,7 @@ __global__ __launch_bounds__(kT) void accept_stats(const float* __restrict__ sco
   const float zinv = 1.f / z;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) x[i] = tid + i * kT < V && x[i] >= thr ? expf(x[i] - m) * zinv : 0.f;
-  float S = 1.f;
+  float rest_sum = 1.f;  // the residual's mass (1: the bonus draw from p itself)
   if (draft_pos) {
     float qv[ITEMS];
     const auto rq = row_resource(qrow, V);
@@ -264,7 +275,7 @@ __global__ __launch_bounds__(kT) void accept_stats(const float* __restrict__ sco
       x[i] = tid + i * kT < V ? fmaxf(x[i] - qv[i], 0.f) : 0.f;
       rest += x[i];
     }
-    S = block_sum(rest, redv);
+    rest_sum = block_sum(rest, redv);
   }
   float ev[ITEMS];
   const auto re = row_resource(erow, V);
@@ -275,7 +286,7 @@ __global__ __launch_bounds__(kT) void accept_stats(const float* __restrict__ sco
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const int v = tid + i * kT;
-    if (v < V) arg_better(cv, ci, (draft_pos ? x[i] / S : x[i]) / ev[i], v);
+    if (v < V) arg_better(cv, ci, (draft_pos ? x[i] / rest_sum : x[i]) / ev[i], v);
   }
   const int drawn = block_argmax(cv, ci, redv, redi);
   if (tid == 0) {
@@ -284,12 +295,12 @@ __global__ __launch_bounds__(kT) void accept_stats(const float* __restrict__ sco
     stats.thr[idx] = thr;
     stats.best[idx] = best;
     // a residual with no mass has no draw (the reference's multinomial raises)
-    stats.cand[idx] = (!(draft_pos && !(S > 0.f)) && drawn >= 0 && drawn < V) ? drawn : -1;
+    stats.cand[idx] = (!(draft_pos && !(rest_sum > 0.f)) && drawn >= 0 && drawn < V) ? drawn : -1;
     int keep = 0;
     if (j < n) {
       const int64_t d = drafts[b * db + j];
       if (d >= 0 && d < V) {
-        const float sd = row[d] / temperature;
+        const float sd = load_f32(row + d) / temperature;
         const float pd = sd >= thr ? expf(sd - m) * (1.f / z) : 0.f;
         keep = u[(int64_t)b * L + j] * q[b * qb + j * qt + d] < pd;
       }
@@ -384,6 +395,18 @@ int items_for(int V) {
     default: CALL(64); break;                   \
   }
 
+template <typename S>
+void launch_stats(dim3 grid, hipStream_t stream, const void* scores, int64_t sb, int64_t st, const int32_t* firsts,
+                  const float* q, int64_t qb, int64_t qt, const int64_t* drafts, int64_t db, const int32_t* lengths,
+                  const float* u, const float* e, float temperature, int top_k, int greedy, int L, int V, Stats s) {
+  const S* rows = static_cast<const S*>(scores);
+#define WPTV_STATS(I)                                                                                             \
+  hipLaunchKernelGGL((accept_stats<I, S>), grid, dim3(kT), 0, stream, rows, sb, st, firsts, q, qb, qt, drafts, db, \
+                     lengths, u, e, temperature, top_k, greedy, L, V, s)
+  WPTV_ITEMS(V, WPTV_STATS)
+#undef WPTV_STATS
+}
+
 }  // namespace
 }  // namespace wptv
 
@@ -396,7 +419,7 @@ extern "C" int wptv_accept_workspace(int B, int L, size_t* bytes) {
   return WPTV_OK;
 }
 
-extern "C" int wptv_accept(const float* scores, int64_t scores_stride_b, int64_t scores_stride_t,
+extern "C" int wptv_accept(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
                            const int32_t* firsts, const float* q, int64_t q_stride_b, int64_t q_stride_t,
                            const int64_t* drafts, int64_t drafts_stride_b, const int32_t* lengths, const float* u,
                            const float* e, float temperature, int top_k, int greedy, int B, int L, int V,
@@ -411,15 +434,14 @@ extern "C" int wptv_accept(const float* scores, int64_t scores_stride_b, int64_t
   if (!greedy && !(temperature > 0.f))
     return fail(WPTV_E_INVALID, "accept: temperature must be positive (got %g)", (double)temperature);
   if (items_for(V) == 0) return fail(WPTV_E_UNSUPPORTED, "accept: a vocabulary of %d is above %d", V, 64 * kT);
+  if (scores_dtype != WPTV_F32 && scores_dtype != WPTV_BF16)
+    return fail(WPTV_E_UNSUPPORTED, "accept: scores dtype %d is neither fp32 nor bf16", scores_dtype);
   if (!workspace || workspace_bytes < stats_bytes(B, L + 1))
     return fail(WPTV_E_INVALID, "accept: workspace of %zu bytes, %zu needed", workspace_bytes, stats_bytes(B, L + 1));
   const Stats s = carve(workspace, B, L + 1);
-#define WPTV_STATS(I)                                                                                           \
-  hipLaunchKernelGGL(accept_stats<I>, dim3(L + 1, B), dim3(kT), 0, stream, scores, scores_stride_b,             \
-                     scores_stride_t, firsts, q, q_stride_b, q_stride_t, drafts, drafts_stride_b, lengths, u, e, \
-                     temperature, top_k, greedy, L, V, s)
-  WPTV_ITEMS(V, WPTV_STATS)
-#undef WPTV_STATS
+  (scores_dtype == WPTV_BF16 ? launch_stats<unsigned short> : launch_stats<float>)(
+      dim3(L + 1, B), stream, scores, scores_stride_b, scores_stride_t, firsts, q, q_stride_b, q_stride_t, drafts,
+      drafts_stride_b, lengths, u, e, temperature, top_k, greedy, L, V, s);
   int st = launched("accept_stats");
   if (st != WPTV_OK) return st;
   hipLaunchKernelGGL(accept_pick, dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b, lengths, greedy, L,
@@ -427,24 +449,24 @@ extern "C" int wptv_accept(const float* scores, int64_t scores_stride_b, int64_t
   return launched("accept_pick");
 }
 
-extern "C" int wptv_greedy_tree(const float* scores, int64_t scores_stride_b, int64_t scores_stride_t,
-                                const int64_t* node_tokens, const int32_t* parents, int B, int M, int V,
+extern "C" int wptv_greedy_tree(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t,
+                                int scores_dtype, const int64_t* node_tokens, const int32_t* parents, int B, int M, int V,
                                 int64_t* path, int64_t* tokens, int32_t* n_tokens, void* workspace,
                                 size_t workspace_bytes, hipStream_t stream) {
   if (!scores || !node_tokens || !parents || !path || !tokens || !n_tokens)
     return fail(WPTV_E_INVALID, "greedy_tree: every pointer must be given");
   if (B <= 0 || M <= 0 || V <= 0) return fail(WPTV_E_INVALID, "greedy_tree: bad shape B=%d M=%d V=%d", B, M, V);
   if (items_for(V) == 0) return fail(WPTV_E_UNSUPPORTED, "greedy_tree: a vocabulary of %d is above %d", V, 64 * kT);
+  if (scores_dtype != WPTV_F32 && scores_dtype != WPTV_BF16)
+    return fail(WPTV_E_UNSUPPORTED, "greedy_tree: scores dtype %d is neither fp32 nor bf16", scores_dtype);
   if (!workspace || workspace_bytes < stats_bytes(B, M))
     return fail(WPTV_E_INVALID, "greedy_tree: workspace of %zu bytes, %zu needed", workspace_bytes,
                 stats_bytes(B, M));
   const Stats s = carve(workspace, B, M);
   // per-node argmax: the stats pass in greedy mode over M positions with no drafts to judge
-#define WPTV_STATS(I)                                                                                             \
-  hipLaunchKernelGGL(accept_stats<I>, dim3(M, B), dim3(kT), 0, stream, scores, scores_stride_b, scores_stride_t, \
-                     nullptr, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, nullptr, 1.f, 0, 1, M - 1, V, s)
-  WPTV_ITEMS(V, WPTV_STATS)
-#undef WPTV_STATS
+  (scores_dtype == WPTV_BF16 ? launch_stats<unsigned short> : launch_stats<float>)(
+      dim3(M, B), stream, scores, scores_stride_b, scores_stride_t, nullptr, nullptr, 0, 0, nullptr, 0, nullptr,
+      nullptr, nullptr, 1.f, 0, 1, M - 1, V, s);
   int st = launched("accept_stats");
   if (st != WPTV_OK) return st;
   hipLaunchKernelGGL(tree_walk, dim3((B + 63) / 64), dim3(64), 0, stream, node_tokens, parents, B, M, s, path, tokens,

@@ -296,11 +296,13 @@ class MQADecoder:
         return keys, values, chosen
 
     @torch.no_grad()
-    def extend(self, ids, cache, counts=None, undoable=False, features=()):
+    def extend(self, ids, cache, counts=None, undoable=False, features=(), logits=False):
         """Reads ids (B, n), the next tokens of the cache's B rows: the first
         counts[b] of row b (all n by default), the rest padding.  Returns
         ((B, n, V) FP32 scores, (B, n, D) final hidden states), as the
-        reference's WPT.extend (model.py:456-473)."""
+        reference's WPT.extend (model.py:456-473).  logits=True: the scores
+        in the compute dtype as the head gives them, before the reference's
+        .float() (the sampler reads bf16 scores as those exact FP32 values)."""
         if features:
             raise NotImplementedError("this decoder gives no intermediate features")
         if ids.device.type == "cpu" and ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= self.config.vocab):
@@ -323,7 +325,8 @@ class MQADecoder:
             # in pieces that the window layers' rings hold; every layer is causal
             pieces = []
             for start in range(0, T, widest):
-                part = self.extend(ids[:, start:start + widest], cache, (counts_ - start).clamp(0, widest))
+                part = self.extend(ids[:, start:start + widest], cache, (counts_ - start).clamp(0, widest),
+                                   logits=logits)
                 pieces.append(part)
             return torch.cat([p[0] for p in pieces], 1), torch.cat([p[1] for p in pieces], 1)
         cache.reserve(cache.bound + T)
@@ -339,7 +342,9 @@ class MQADecoder:
             last = i + 1 == self.config.layers
             next_norm = self.w["final_norm"] if last else self.w[f"layers.{i + 1}.attn_norm"]
             handoff = self._layer(i, h, x, cache, positions, counts_, next_norm, handoff)
-        scores = F.linear(x, self.w["head"]).float()
+        scores = F.linear(x, self.w["head"])
+        if not logits:
+            scores = scores.float()
         cache.finish(counts_, undoable, T)
         return scores, h
 

@@ -36,6 +36,18 @@ def _rows_last_contiguous(x, name, dims):
     return x
 
 
+def _scores(x):
+    """The scores as the kernels take them: (B, positions, V), FP32 or bf16
+    (the lm_head's logits, read as their exact FP32 values), rows contiguous."""
+    if x.dim() != 3:
+        raise ValueError(f"scores must have 3 dimensions; got {tuple(x.shape)}")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"scores must be float32 or bfloat16; got {x.dtype}")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    return x
+
+
 def _workspace(device, B, L):
     size = _lib.ctypes.c_size_t(0)
     check(_lib.lib().wptv_accept_workspace(B, L, _lib.ctypes.byref(size)), "accept")
@@ -53,11 +65,11 @@ def accept(scores, q, drafts, u, e, temperature=0.8, top_k=40, lengths=None, fir
     """Each row's written tokens: (tokens (B, L + 1) int64, -1 past a row's
     count; counts (B,) int32 = kept drafts + 1).
 
-    scores (B, >= L + 1, V) FP32: row b's position j is scores[b, firsts[b] + j]
+    scores (B, >= L + 1, V) FP32 or bf16: row b's position j is scores[b, firsts[b] + j]
     (firsts None: 0); q (B, L, V) FP32 the drafts' distributions; drafts (B, L)
     int64; u, e the tape (draws); lengths (B,) the drafts each row verifies
     (None: L).  greedy: keep the drafts equal to the argmax (q, u, e unused)."""
-    scores = _rows_last_contiguous(scores, "scores", 3)
+    scores = _scores(scores)
     B, _, V = scores.shape
     if drafts.dim() != 2 or drafts.shape[0] != B:
         raise ValueError(f"drafts must be (B={B}, L); got {tuple(drafts.shape)}")
@@ -92,7 +104,8 @@ def accept(scores, q, drafts, u, e, temperature=0.8, top_k=40, lengths=None, fir
     tokens = torch.empty(B, L + 1, dtype=torch.long, device=device)
     counts = torch.empty(B, dtype=torch.int32, device=device)
     workspace, size = _workspace(device, B, L)
-    check(_lib.lib().wptv_accept(ptr(scores), scores.stride(0), scores.stride(1), ptr(firsts_), ptr(q),
+    check(_lib.lib().wptv_accept(ptr(scores), scores.stride(0), scores.stride(1), _lib.dtype_code(scores.dtype),
+                                 ptr(firsts_), ptr(q),
                                  q.stride(0) if q is not None else 0, q.stride(1) if q is not None else 0,
                                  ptr(drafts), drafts.stride(0), ptr(lengths_), ptr(u), ptr(e), float(temperature),
                                  0 if top_k is None else int(top_k), 1 if greedy else 0, B, L, V, ptr(tokens),
@@ -107,11 +120,11 @@ def greedy_chain(scores, drafts, lengths=None, firsts=None):
 
 
 def greedy_tree(scores, node_tokens, parents):
-    """Greedy verification of a draft tree: scores (B, M, V) FP32 at the M
+    """Greedy verification of a draft tree: scores (B, M, V) FP32 or bf16 at the M
     nodes, node_tokens (B, M), parents (M,) (parents[0] = -1, parents[i] < i).
     Returns (path (B, M + 1) node indices from the root, tokens (B, M + 1)
     written, counts (B,)); -1 past each row's count."""
-    scores = _rows_last_contiguous(scores, "scores", 3)
+    scores = _scores(scores)
     B, M, V = scores.shape
     device = scores.device
     parents = [int(p) for p in parents]
@@ -129,7 +142,8 @@ def greedy_tree(scores, node_tokens, parents):
     tokens = torch.empty(B, M + 1, dtype=torch.long, device=device)
     counts = torch.empty(B, dtype=torch.int32, device=device)
     workspace, size = _workspace(device, B, M - 1)
-    check(_lib.lib().wptv_greedy_tree(ptr(scores), scores.stride(0), scores.stride(1), ptr(node_tokens),
+    check(_lib.lib().wptv_greedy_tree(ptr(scores), scores.stride(0), scores.stride(1),
+                                      _lib.dtype_code(scores.dtype), ptr(node_tokens),
                                       ptr(parents_), B, M, V, ptr(path), ptr(tokens), ptr(counts), ptr(workspace),
                                       size, _lib.stream(device)), "greedy_tree")
     return path, tokens, counts

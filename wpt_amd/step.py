@@ -43,7 +43,7 @@ class VerifyStep:
 
     def run(self):
         """One eager step; returns (tokens (B, k + 1), counts (B,)) on the device."""
-        scores, _ = self.model.extend(self.feeds, self.cache, undoable=True)
+        scores, _ = self.model.extend(self.feeds, self.cache, undoable=True, logits=True)  # read as they come
         drafts = self.feeds[:, 1:]
         if self.greedy:
             tokens, counts = sampling.greedy_chain(scores, drafts)
