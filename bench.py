@@ -267,7 +267,7 @@ def tree_c4(steps, warmup):
 
     def step():
         o = kernels.tree_attention(q, table[..., :c], table[..., c:], base, parents, c ** -0.5)
-        scores = F.linear(o.reshape(B, M, H * c), head).float()
+        scores = F.linear(o.reshape(B, M, H * c), head)  # bf16 logits, read by the sampler as they come
         _, _, counts = sampling.greedy_tree(scores, node_tokens, parents)
         written.add_(counts.long())
 

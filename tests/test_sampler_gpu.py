@@ -84,6 +84,11 @@ def test_bf16_scores_decide_as_their_fp32_values(device, top_k):
     g16 = sampling.greedy_chain(low.to(device), on[1])
     g32 = sampling.greedy_chain(low.float().to(device), on[1])
     assert all(torch.equal(a, b) for a, b in zip(g16, g32))
+    parents = [-1, 0, 0, 1, 1]
+    nodes = torch.cat([torch.zeros(B, 1, dtype=torch.long), drafts], 1).to(device)
+    w16 = sampling.greedy_tree(low.to(device), nodes, parents)
+    w32 = sampling.greedy_tree(low.float().to(device), nodes, parents)
+    assert all(torch.equal(a, b) for a, b in zip(w16, w32))
 
 
 def test_per_row_lengths_and_first_positions(device):
