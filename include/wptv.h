@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define WPTV_ABI_VERSION 2
+#define WPTV_ABI_VERSION 3
 
 enum {
   WPTV_OK = 0,
@@ -203,9 +203,12 @@ int wptv_cache_lengths(int64_t* lengths, int64_t* before, const void* counts, in
 /* wptv_next_feeds: each row's next pending token after a verify step, the
  *   last token it wrote (the reference's Writer keeps it pending for the
  *   next round, __init__.py:196-233): feeds[b * feeds_stride] =
- *   tokens[b * tokens_stride + clamp(counts[b] - 1, 0, width - 1)]. */
+ *   tokens[b * tokens_stride + min(counts[b], width) - 1].  A row with
+ *   counts[b] < 1 (the sampler had no mass to draw from, where the
+ *   reference's multinomial raises, __init__.py:219) keeps its pending token
+ *   and sets *failed = 1 when failed is not NULL (the caller clears it). */
 int wptv_next_feeds(const int64_t* tokens, int64_t tokens_stride, const int* counts, int64_t* feeds,
-                    int64_t feeds_stride, int B, int width, hipStream_t stream);
+                    int64_t feeds_stride, int B, int width, int* failed, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * The decoder layer's memory-bound steps around its matrix products (the

@@ -23,7 +23,19 @@ head, the same gate.  An exact layer chooses (top_k rows) when a sparse layer
 follows it (model.py:134-135); the handoff is the last exact layer's
 (model.py:411-423).
 
-Weights are a dict of tensors (any dtype; used in FP32):
+autocast=True restates the reference's GPU pass instead, which runs under
+torch.autocast(bfloat16) (model.py:466): every matrix product takes bf16
+inputs, accumulates in FP32 and rounds its output to bf16; RMSNorm of a bf16
+input returns bf16 (nn.RMSNorm with an FP32 weight is not cast by autocast:
+checked against torch on an MI355X); the residual stream and every
+element-wise product stay bf16 (Residuals keeps its sums in the compute dtype,
+residuals.py:106-136); the exact and sparse kernels compute in FP32 and
+return q's dtype (pytorch_kernels.py:98-121); a window layer's dense
+attention takes bf16 scores and bf16 probabilities (attention.py:79-82 under
+autocast); the scores are the head's bf16 output .float().
+
+Weights are a dict of tensors (any dtype; used in FP32, or rounded to bf16
+once under autocast):
     embedding (V, D); head (V, D); final_norm (D,)
     layers.{i}.attn_norm (D,)   layers.{i}.qkv (H*c + 2c, D): q rows, k, v
     layers.{i}.q_norm (c,)      layers.{i}.k_norm (c,)
@@ -46,10 +58,32 @@ def rms_norm(x, weight):
     return F.rms_norm(x.float(), (x.shape[-1],), weight.float(), EPS)
 
 
+def bf16_linear(x, weight):
+    """An autocast bf16 matrix product: bf16 inputs (weight already holds
+    bf16 values), FP32 products and sums, the output rounded to bf16."""
+    return (x.to(torch.bfloat16).float() @ weight.T).to(torch.bfloat16)
+
+
+def bf16_dense_attention(q, k, v, sink, visible, scale):
+    """attention.py:74-82 under autocast: the bf16 product q.k rounded to bf16
+    before .float(), the probabilities rounded to v's dtype (bf16) before the
+    bf16 product with v."""
+    z = torch.einsum("...qhc,...kc->...hqk", q.float(), k.float()).to(torch.bfloat16).float() * scale
+    z = z.masked_fill(~visible[..., None, :, :], float("-inf"))
+    lse = torch.logaddexp(torch.logsumexp(z, -1), sink.float()[:, None])
+    p = (z - lse[..., None]).exp().to(torch.bfloat16)
+    return torch.einsum("...hqk,...kc->...qhc", p.float(), v.float()).to(torch.bfloat16)
+
+
 class Decoder:
     def __init__(self, weights, layers, heads, head_dim, kinds=(), window=128, rope_dims=64, rope_base=10000.0,
-                 top_k=1024):
-        self.w = {name: value.float() for name, value in weights.items()}
+                 top_k=1024, autocast=False):
+        self.autocast = autocast
+        if autocast:  # matrices rounded to bf16 once (held as FP32 values); norm weights and sinks FP32
+            self.w = {name: value.float() if name.endswith("norm") or name.endswith("sink")
+                      else value.to(torch.bfloat16).float() for name, value in weights.items()}
+        else:
+            self.w = {name: value.float() for name, value in weights.items()}
         self.layers, self.heads, self.head_dim = layers, heads, head_dim
         self.kinds = tuple(kinds) or ("exact",) * layers
         self.window, self.rope_dims, self.rope_base = window, rope_dims, rope_base
@@ -65,30 +99,42 @@ class Decoder:
     def new_cache(self, rows):
         return cache.Rows(rows)
 
+    def _linear(self, x, weight):
+        return bf16_linear(x, weight) if self.autocast else x.float() @ weight.T
+
+    def _norm(self, x, weight):
+        if self.autocast:  # torch's RMSNorm on the bf16 input, as the reference's module runs it
+            return F.rms_norm(x.to(torch.bfloat16), (x.shape[-1],), weight.float(), EPS)
+        return rms_norm(x, weight)
+
     def _layer(self, i, h, reading, handoff):
         """(h after layer i, the handoff for the layers after it)."""
         w = lambda name: self.w[f"layers.{i}.{name}"]  # noqa: E731
         B, T, _ = h.shape
         H, c = self.heads, self.head_dim
-        x = rms_norm(h, w("attn_norm"))
+        x = self._norm(h, w("attn_norm"))
         positions = reading.positions(T)
         if self.kinds[i] == "sparse":
-            q = rms_norm((x @ w("q").T).reshape(B, T, H, c), w("q_norm"))
+            q = self._norm(self._linear(x, w("q")).reshape(B, T, H, c), w("q_norm"))
             keys, values, chosen = handoff
             o = attention.sparse_attention(q, keys, values, w("sink"), chosen, positions, c ** -0.5, self.window)
-            o = o * torch.sigmoid(x @ w("gate").T).reshape(B, T, H, c)
+            o = o * torch.sigmoid(self._linear(x, w("gate"))).reshape(B, T, H, c)
             return self._rest(i, h, o), handoff
-        qkv = x @ w("qkv").T
-        q = rms_norm(qkv[..., :H * c].reshape(B, T, H, c), w("q_norm"))
-        k = rms_norm(qkv[..., H * c:H * c + c], w("k_norm"))
+        qkv = self._linear(x, w("qkv"))
+        q = self._norm(qkv[..., :H * c].reshape(B, T, H, c), w("q_norm"))
+        k = self._norm(qkv[..., H * c:H * c + c], w("k_norm"))
         v = qkv[..., H * c + c:]
         if self.kinds[i] == "window":
             W = self.window
             q = attention.rotate(q, positions, self.rope_dims, self.rope_base)
             entries = torch.cat([attention.rotate(k, positions, self.rope_dims, self.rope_base), v], -1)
             table = torch.cat([reading.before(("window", i), W - 1, entries), entries], 1)
-            o = attention.window_attention(q, table[..., :c], table[..., c:], w("sink"), positions, c ** -0.5, W)
-            o = o * torch.sigmoid(x @ w("gate").T).reshape(B, T, H, c)
+            if self.autocast:
+                visible = attention.window_visible(positions.expand(B, T), W, T)
+                o = bf16_dense_attention(q, table[..., :c], table[..., c:], w("sink"), visible, c ** -0.5)
+            else:
+                o = attention.window_attention(q, table[..., :c], table[..., c:], w("sink"), positions, c ** -0.5, W)
+            o = o * torch.sigmoid(self._linear(x, w("gate"))).reshape(B, T, H, c)
         else:
             table = reading.everything(("entries", i), torch.cat([k, v], -1))
             chooses = i + 1 < self.layers and self.kinds[i + 1] == "sparse"
@@ -104,24 +150,55 @@ class Decoder:
         """The output projection's residual add, then the feed-forward block."""
         w = lambda name: self.w[f"layers.{i}.{name}"]  # noqa: E731
         B, T, H, c = o.shape
-        h = h + o.reshape(B, T, H * c) @ w("out").T
-        x = rms_norm(h, w("ffn_norm"))
-        gate, up = (x @ w("gate_up").T).chunk(2, -1)
-        return h + (F.silu(gate) * up) @ w("down").T
+        h = h + self._linear(o.reshape(B, T, H * c), w("out"))
+        x = self._norm(h, w("ffn_norm"))
+        gate, up = self._linear(x, w("gate_up")).chunk(2, -1)
+        return h + self._linear(F.silu(gate) * up, w("down"))
 
-    def extend(self, ids, rows, counts=None, undoable=False):
+    def extend(self, ids, rows, counts=None, undoable=False, features=()):
         """(scores (B, n, V) FP32, hidden (B, n, D)) of ids (B, n), row b's
-        first counts[b] tokens after its earlier ones, the rest padding."""
+        first counts[b] tokens after its earlier ones, the rest padding; with
+        features (layer numbers 0 .. layers), also the residual stream
+        entering each named layer (`layers`: the final hidden states), FP32,
+        side by side in the order named (model.py:406-436, 457-473)."""
         ids = torch.as_tensor(ids, dtype=torch.long)
         counts = torch.full((ids.shape[0],), ids.shape[1]) if counts is None else torch.as_tensor(counts)
         reading = rows.reading(counts, undoable)
         h = self.w["embedding"][ids]
+        if self.autocast:
+            h = h.to(torch.bfloat16)
+        found = {}
         handoff = None
         for i in range(self.layers):
+            if i in features:
+                found[i] = h.float()
             h, handoff = self._layer(i, h, reading, handoff)
-        scores = rms_norm(h, self.w["final_norm"]) @ self.w["head"].T
+        if self.layers in features:
+            found[self.layers] = h.float()
+        scores = self._linear(self._norm(h, self.w["final_norm"]), self.w["head"]).float()
         reading.finish()
+        if features:
+            return scores, h, torch.cat([found[n] for n in features], -1)
         return scores, h
+
+    def forced(self, inputs, rows, counts=None, undoable=True):
+        """Each layer run on another pass's residual streams: inputs[i] (B, n,
+        D) is the stream entering layer i of that pass (its features), for
+        i = 0 .. layers.  Returns (outputs, scores): outputs[i] = layer i's
+        output on inputs[i], which that pass gave as inputs[i + 1], and the
+        head's scores on inputs[layers].  The new tokens' entries come from
+        inputs[i], as that pass wrote them."""
+        B, n, _ = inputs[0].shape
+        counts = torch.full((B,), n) if counts is None else torch.as_tensor(counts)
+        reading = rows.reading(counts, undoable)
+        dtype = torch.bfloat16 if self.autocast else torch.float32
+        outputs, handoff = [], None
+        for i in range(self.layers):
+            h, handoff = self._layer(i, inputs[i].to(dtype), reading, handoff)
+            outputs.append(h)
+        scores = self._linear(self._norm(inputs[self.layers].to(dtype), self.w["final_norm"]), self.w["head"]).float()
+        reading.finish()
+        return outputs, scores
 
     def undo(self, rows, kept):
         rows.undo(kept)

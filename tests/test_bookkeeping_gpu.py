@@ -60,8 +60,13 @@ def test_the_next_pending_token_is_the_last_written(device):
     tokens = torch.tensor([[11, 12, 13, 14], [21, -1, -1, -1], [31, 32, -1, -1]], device=device)
     counts = torch.tensor([4, 1, 2], dtype=torch.int32, device=device)
     feeds = torch.zeros(3, 4, dtype=torch.long, device=device)
-    next_feeds(tokens, counts, feeds)
-    assert feeds[:, 0].tolist() == [14, 21, 32] and not feeds[:, 1:].any()
+    failed = torch.zeros(1, dtype=torch.int32, device=device)
+    next_feeds(tokens, counts, feeds, failed)
+    assert feeds[:, 0].tolist() == [14, 21, 32] and not feeds[:, 1:].any() and int(failed) == 0
+    # a row the sampler could not draw for (-1) keeps its pending token and raises the flag
+    feeds[:, 0] = torch.tensor([7, 8, 9], device=device)
+    next_feeds(tokens, torch.tensor([-1, 1, 0], dtype=torch.int32, device=device), feeds, failed)
+    assert feeds[:, 0].tolist() == [7, 21, 9] and int(failed) == 1
 
 
 def test_host_ids_outside_the_vocabulary_raise(device):

@@ -273,6 +273,29 @@ def test_a_captured_verify_step_replays_as_the_eager_step(device):
         assert torch.equal(te, tg) and torch.equal(ce, cg) and torch.equal(le, lg)
 
 
+def test_a_row_with_nothing_to_draw_from_writes_nothing_and_is_reported(device):
+    # q = 1 for every token (no distribution): every draft is rejected and the
+    # residual max(0, p - q) is 0 everywhere, where the reference's
+    # multinomial raises; the step leaves the rows as they were and check()
+    # raises
+    config = SMALL_BF16
+    model = MQADecoder(config, random_weights(config, seed=2), dtype=torch.bfloat16)
+    B, k = 3, 4
+    cache = model.new_cache(B, capacity=128)
+    ids = torch.randint(config.vocab, (B, 20), generator=torch.Generator().manual_seed(6)).to(device)
+    prefill(model, cache, ids[:, :-1])
+    step = VerifyStep(model, cache, k, temperature=1.0)
+    step.feeds[:, 0] = ids[:, -1]
+    step.feeds[:, 1:] = 7
+    step.q.fill_(1.0)
+    tokens, counts = step.run()
+    assert counts.tolist() == [-1] * B
+    assert cache.lengths.tolist() == [19] * B and step.feeds[:, 0].tolist() == ids[:, -1].tolist()
+    with pytest.raises(RuntimeError, match="no mass"):
+        step.check()
+    step.check()  # cleared
+
+
 def test_a_model_folder_loads_the_decoder_it_saved(device, tmp_path):
     # the reference's model-folder layout (checkpoint.py): the decoder loaded
     # from it scores as the decoder built from the same weights, bit for bit

@@ -133,3 +133,28 @@ def test_a_tail_cut_back_keeps_the_steps_before_the_kept_tokens():
     new = (10 + torch.arange(4.0))[None, :, None].expand(2, 4, 1)
     got = cache.last(torch.cat([before, new], 1), torch.tensor([0, 2]), 3)
     assert got[0, :, 0].tolist() == [0, 1, 2] and got[1, :, 0].tolist() == [2, 10, 11]
+
+
+@pytest.mark.parametrize("kinds", KINDS, ids=IDS)
+@pytest.mark.parametrize("autocast", [False, True], ids=["fp32", "autocast"])
+def test_features_are_the_streams_entering_each_layer(kinds, autocast):
+    # model.py:406-436: feature n is the residual stream entering layer n,
+    # feature `layers` the final hidden states, side by side in the order
+    # named; running each layer on those streams (forced) gives the next one
+    m = decoder.Decoder(weights(), LAYERS, H, C, kinds=kinds, window=8, rope_dims=8, top_k=4, autocast=autocast)
+    ids = torch.randint(V, (2, 40), generator=torch.Generator().manual_seed(11))
+    rows = m.new_cache(2)
+    m.extend(ids[:, :30], rows)
+    copy = rows.select([0, 1])
+    scores, hidden, found = m.extend(ids[:, 30:], rows, undoable=True, features=range(LAYERS + 1))
+    streams = found.split(D, -1)
+    assert found.dtype == torch.float32 and len(streams) == LAYERS + 1
+    assert torch.equal(streams[0], m.w["embedding"][ids[:, 30:]].to(hidden.dtype).float())
+    assert torch.equal(streams[-1], hidden.float())
+    outputs, forced_scores = m.forced(streams, copy)
+    assert all(torch.equal(outputs[i].float(), streams[i + 1]) for i in range(LAYERS))
+    assert torch.equal(forced_scores, scores)
+    again = m.new_cache(2)
+    m.extend(ids[:, :30], again)
+    _, _, pair = m.extend(ids[:, 30:], again, features=(2, 0))
+    assert torch.equal(pair, torch.cat([streams[2], streams[0]], -1))

@@ -300,11 +300,16 @@ class MQADecoder:
         """Reads ids (B, n), the next tokens of the cache's B rows: the first
         counts[b] of row b (all n by default), the rest padding.  Returns
         ((B, n, V) FP32 scores, (B, n, D) final hidden states), as the
-        reference's WPT.extend (model.py:456-473).  logits=True: the scores
-        in the compute dtype as the head gives them, before the reference's
-        .float() (the sampler reads bf16 scores as those exact FP32 values)."""
-        if features:
-            raise NotImplementedError("this decoder gives no intermediate features")
+        reference's WPT.extend (model.py:456-473); with features (layer
+        numbers 0 .. layers), also the residual stream entering each named
+        layer (`layers` naming the final hidden states), FP32, side by side
+        in the order named: (B, n, D * len(features)) (model.py:406-436).
+        logits=True: the scores in the compute dtype as the head gives them,
+        before the reference's .float() (the sampler reads bf16 scores as
+        those exact FP32 values)."""
+        features = tuple(int(n) for n in features)
+        if any(not 0 <= n <= self.config.layers for n in features):
+            raise ValueError(f"features name layers 0 .. {self.config.layers}; got {features}")
         if ids.device.type == "cpu" and ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= self.config.vocab):
             raise IndexError(f"token ids must lie in [0, {self.config.vocab})")
         ids = ids.to(device=self.device, dtype=torch.long)
@@ -326,9 +331,9 @@ class MQADecoder:
             pieces = []
             for start in range(0, T, widest):
                 part = self.extend(ids[:, start:start + widest], cache, (counts_ - start).clamp(0, widest),
-                                   logits=logits)
+                                   features=features, logits=logits)
                 pieces.append(part)
-            return torch.cat([p[0] for p in pieces], 1), torch.cat([p[1] for p in pieces], 1)
+            return tuple(torch.cat([p[i] for p in pieces], 1) for i in range(len(pieces[0])))
         cache.reserve(cache.bound + T)
         D = self.config.d_model
         h = torch.empty(B, T, D, dtype=self.dtype, device=self.device)
@@ -337,15 +342,22 @@ class MQADecoder:
         # the embedding, the first norm and each token's position in one pass
         layers.embed_rms_norm(ids.contiguous(), self.w["embedding"], self.w["layers.0.attn_norm"], h, x,
                               cache.lengths, positions)
+        found = {}
         handoff = None
         for i in range(self.config.layers):
+            if i in features:  # the stream entering layer i (the layers update h in place)
+                found[i] = h.float()
             last = i + 1 == self.config.layers
             next_norm = self.w["final_norm"] if last else self.w[f"layers.{i + 1}.attn_norm"]
             handoff = self._layer(i, h, x, cache, positions, counts_, next_norm, handoff)
+        if self.config.layers in features:
+            found[self.config.layers] = h.float()
         scores = F.linear(x, self.w["head"])
         if not logits:
             scores = scores.float()
         cache.finish(counts_, undoable, T)
+        if features:
+            return scores, h, torch.cat([found[n] for n in features], -1)
         return scores, h
 
     @torch.no_grad()

@@ -10,8 +10,15 @@ The inputs live in static device buffers (`feeds`: the pending token then the
 drafts; `q`: the drafts' distributions), so that a captured graph replays on
 new values: after each step the token it drew becomes each row's pending
 token.  The tape (u, e) is drawn inside the step from torch's generator of the
-device.  The cache's tables must hold every row the replays will write
+device, or read from the static buffers `u`, `e` (`given_tape=True`), which
+the caller fills before each step.  After a step, `scores`, `u` and `e` hold
+what it read.  The cache's tables must hold every row the replays will write
 (reserve), since a graph cannot grow them.
+
+A row whose residual max(0, p - q) has no mass cannot draw; the reference's
+multinomial raises there (__init__.py:219).  Inside a step (and a graph) the
+row writes nothing, keeps its pending token and its cache, and raises a
+device flag; `check()` reads the flag (one synchronization) and raises.
 """
 
 import torch
@@ -20,26 +27,34 @@ from . import _lib, sampling
 from ._lib import check, ptr
 
 
-def next_feeds(tokens, counts, feeds):
+def next_feeds(tokens, counts, feeds, failed=None):
     """feeds[:, 0] = each row's last written token, tokens[b, counts[b] - 1]
-    (tokens (B, L + 1) int64, counts (B,) int32), on the device."""
+    (tokens (B, L + 1) int64, counts (B,) int32), on the device; a row with
+    no token written keeps its feed and sets failed (an int32 device flag,
+    when given) to 1."""
     B, width = tokens.shape
     if counts.dtype != torch.int32 or counts.shape != (B,) or feeds.shape[0] != B or feeds.dtype != torch.int64:
         raise ValueError("tokens (B, L + 1) int64, counts (B,) int32 and feeds (B, n) int64")
+    if failed is not None and (failed.dtype != torch.int32 or failed.numel() < 1):
+        raise ValueError("failed must be an int32 device tensor")
     check(_lib.lib().wptv_next_feeds(ptr(tokens), tokens.stride(0), ptr(counts), ptr(feeds), feeds.stride(0), B, width,
-                                     _lib.stream(tokens.device)), "next_feeds")
+                                     ptr(failed), _lib.stream(tokens.device)), "next_feeds")
 
 
 class VerifyStep:
-    def __init__(self, model, cache, k, temperature=0.8, top_k=None, greedy=False):
+    def __init__(self, model, cache, k, temperature=0.8, top_k=None, greedy=False, given_tape=False):
         self.model, self.cache, self.k = model, cache, k
         self.temperature, self.top_k, self.greedy = temperature, top_k, greedy
+        self.given_tape = given_tape
         B, V = cache.rows, model.config.vocab
         device = model.device
         self.feeds = torch.zeros(B, k + 1, dtype=torch.long, device=device)
         self.q = torch.full((B, k, V), 1.0 / V, device=device)
+        self.u = torch.zeros(B, k, device=device) if given_tape else None
+        self.e = torch.ones(B, V, device=device) if given_tape else None
+        self.failed = torch.zeros(1, dtype=torch.int32, device=device)
         self.graph = None
-        self.tokens = self.counts = None
+        self.tokens = self.counts = self.scores = None
 
     def run(self):
         """One eager step; returns (tokens (B, k + 1), counts (B,)) on the device."""
@@ -48,13 +63,22 @@ class VerifyStep:
         if self.greedy:
             tokens, counts = sampling.greedy_chain(scores, drafts)
         else:
-            B, V = scores.shape[0], scores.shape[-1]
-            u, e = sampling.draws(B, self.k, V, device=scores.device)
-            tokens, counts = sampling.accept(scores, self.q, drafts, u, e, self.temperature, self.top_k)
+            if not self.given_tape:
+                B, V = scores.shape[0], scores.shape[-1]
+                self.u, self.e = sampling.draws(B, self.k, V, device=scores.device)
+            tokens, counts = sampling.accept(scores, self.q, drafts, self.u, self.e, self.temperature, self.top_k)
         self.model.undo(self.cache, counts)
-        next_feeds(tokens, counts, self.feeds)  # the drawn token is each row's next pending token
-        self.tokens, self.counts = tokens, counts
+        next_feeds(tokens, counts, self.feeds, self.failed)  # the drawn token is each row's next pending token
+        self.tokens, self.counts, self.scores = tokens, counts, scores
         return tokens, counts
+
+    def check(self):
+        """Raises if a step since the last check had a row with nothing to
+        draw from (that row wrote nothing and kept its state); clears the flag."""
+        if int(self.failed.item()):
+            self.failed.zero_()
+            raise RuntimeError("a row's residual distribution max(0, p - q) had no mass to draw from: the row "
+                               "wrote nothing")
 
     def capture(self, warmup=2):
         """Captures the step in a HIP graph (after `warmup` eager steps on a
