@@ -98,6 +98,23 @@ int wptv_verify_attention(const void* q, const void* k, int64_t k_stride_b, int6
                           int N, float scale, int splits, int flags, void* out, float* lse,
                           void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* wptv_verify_attention_static: wptv_verify_attention with no workspace
+ *   argument, for callers that cannot allocate device memory (code under HIP
+ *   graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ *   has no counterpart in the reference.  The key-range parts live in a
+ *   static device array of 16 MiB that each device loading the library holds
+ *   until the process ends (enough for every split count the library
+ *   chooses for c <= 128; a request needing more is refused with
+ *   WPTV_E_INVALID and a message).  It calls no allocating routine.  Calls
+ *   that overlap on one device share that array and race; calls ordered on
+ *   one stream do not.  Same kernels and results as wptv_verify_attention. */
+int wptv_verify_attention_static(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
+                                 const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
+                                 const int64_t* positions, int window, const int64_t* tree_base,
+                                 const uint64_t* tree_ancestors, const float* sink, int B, int T, int H, int c,
+                                 int N, float scale, int splits, int flags, void* out, float* lse,
+                                 hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Window attention: each query at position p reads the rows of positions
  * max(0, p - window + 1) .. p, itself included and none before the text, with

@@ -38,6 +38,8 @@ SIGNATURES = {
     "wptv_attention_workspace": [_I, _I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_SZ)],
     "wptv_verify_attention": [_P, _P, _I64, _I64, _P, _I64, _I64, _I, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I,
                               _I, _P, _P, _P, _SZ, _P],
+    "wptv_verify_attention_static": [_P, _P, _I64, _I64, _P, _I64, _I64, _I, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I,
+                                     _F, _I, _I, _P, _P, _P],
     "wptv_sparse_attention_workspace": [_I, _I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_SZ)],
     "wptv_sparse_attention": [_P, _P, _I64, _I64, _P, _I64, _I64, _I, _P, _I, _P, _I, _P, _P, _I64, _I, _I, _I, _I, _I,
                               _F, _I, _P, _P, _P, _SZ, _P],

@@ -34,6 +34,7 @@
 #include "wptv_common.h"
 
 #include <climits>
+#include <mutex>
 #include <type_traits>
 
 namespace wptv {
@@ -1673,6 +1674,76 @@ extern "C" int wptv_verify_attention(const void* q, const void* k, int64_t k_str
   return attend(q, k, k_stride_b, k_stride_n, v, v_stride_b, v_stride_n, dtype, positions, window, tree_base,
                 tree_ancestors, sink, B, T, H, c, N, scale, splits, flags, RowMap{nullptr, 0xffffffffu}, N,
                 OutGate{nullptr, 0}, out, lse, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The allocation-free form of wptv_verify_attention: its parts live in a
+// file-scope device array instead of a caller's workspace.  Each device that
+// loads the library holds one array until the process ends; its address on a
+// device is looked up once (hipGetSymbolAddress, that device current) and
+// kept.  Every call on a device shares that device's array, so calls that
+// overlap on one device (on two streams, or from two threads) race; calls
+// ordered on one stream do not.  The parts need no clearing: every part a
+// merge reads is written by the same call first.
+// ---------------------------------------------------------------------------
+namespace wptv {
+namespace {
+constexpr size_t kScratchBytes = size_t(16) << 20;
+constexpr int kScratchDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_on[kScratchDevices] = {};
+}  // namespace
+}  // namespace wptv
+
+__device__ __align__(256) unsigned char scratch[wptv::kScratchBytes];
+
+namespace wptv {
+namespace {
+// The current device's address of `scratch`, looked up on the first call on that device.
+int scratch_address(void** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return fail(WPTV_E_HIP, "verify_attention_static: hipGetDevice: %s", hipGetErrorString(err));
+  if (device < 0 || device >= kScratchDevices)
+    return fail(WPTV_E_UNSUPPORTED, "verify_attention_static: device %d beyond the %d this library serves", device,
+                kScratchDevices);
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_on[device]) {
+    void* address = nullptr;
+    err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !address)
+      return fail(WPTV_E_HIP, "verify_attention_static: hipGetSymbolAddress(scratch) on device %d: %s", device,
+                  hipGetErrorString(err));
+    scratch_on[device] = address;
+  }
+  *out = scratch_on[device];
+  return WPTV_OK;
+}
+}  // namespace
+}  // namespace wptv
+
+extern "C" int wptv_verify_attention_static(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
+                                            const void* v, int64_t v_stride_b, int64_t v_stride_n, int dtype,
+                                            const int64_t* positions, int window, const int64_t* tree_base,
+                                            const uint64_t* tree_ancestors, const float* sink, int B, int T, int H,
+                                            int c, int N, float scale, int splits, int flags, void* out, float* lse,
+                                            hipStream_t stream) {
+  Plan p;
+  int st = plan(B, T, H, c, N, window, dtype, flags, splits, &p);
+  if (st != WPTV_OK) return st;
+  if (p.bytes > kScratchBytes)
+    return fail(WPTV_E_INVALID,
+                "verify_attention_static: B=%d T=%d H=%d c=%d in %d splits needs %zu bytes of parts, above the %zu "
+                "bytes of its static scratch; call wptv_verify_attention with a workspace",
+                B, T, H, c, p.splits, p.bytes, kScratchBytes);
+  void* ws = nullptr;
+  if (p.bytes > 0) {
+    st = scratch_address(&ws);
+    if (st != WPTV_OK) return st;
+  }
+  return attend(q, k, k_stride_b, k_stride_n, v, v_stride_b, v_stride_n, dtype, positions, window, tree_base,
+                tree_ancestors, sink, B, T, H, c, N, scale, p.splits, flags, RowMap{nullptr, 0xffffffffu}, N,
+                OutGate{nullptr, 0}, out, lse, ws, p.bytes > 0 ? kScratchBytes : 0, stream);
 }
 
 extern "C" int wptv_window_attention_workspace(int B, int T, int H, int c, int window, int dtype, int* splits,

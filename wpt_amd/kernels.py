@@ -80,7 +80,7 @@ def _long(x, device):
 
 
 def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=None, lse=False, splits=0,
-                     generic=False, from_positions=False, key_split=False):
+                     generic=False, from_positions=False, key_split=False, static_scratch=False):
     """MQA attention of q (B, T, H, c) over k, v (B, N, c): query t of row b
     sees rows max(0, p - window + 1) .. min(p, N - 1), p = positions[b, t]
     (window 0: from row 0), and with tree = (tree_base (B,), ancestors (T,)
@@ -91,7 +91,10 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
     the library chooses); generic: the wave-per-query kernel; from_positions:
     read only the rows the positions reach (a cache table with spare rows);
     key_split: where T*H <= 80, the key-parallel MFMA kernel instead of the
-    row-block one."""
+    row-block one; static_scratch: the allocation-free entry point
+    (wptv_verify_attention_static), whose parts live in the library's own
+    device array: no workspace is allocated, and calls overlapping on one
+    device race."""
     B, T, H, c, N = _check_inputs(q, k, v, positions)
     device = q.device
     library = _lib.lib()
@@ -112,9 +115,17 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
     size = _lib.ctypes.c_size_t(0)
     check(library.wptv_attention_workspace(B, T, H, c, N, int(window), dtype, flags, _lib.ctypes.byref(parts),
                                            _lib.ctypes.byref(size)), "verify_attention")
-    workspace = torch.empty(max(1, size.value), dtype=torch.uint8, device=device) if size.value else None
     out = torch.empty_like(q_)
     lse_out = torch.empty(B, T, H, dtype=torch.float32, device=device) if lse else None
+    if static_scratch:
+        check(library.wptv_verify_attention_static(ptr(q_), ptr(k), k.stride(0), k.stride(1), ptr(v), v.stride(0),
+                                                   v.stride(1), dtype, ptr(positions_), int(window), ptr(tree_base),
+                                                   ptr(ancestors), ptr(sink_), B, T, H, c, N, float(scale),
+                                                   int(splits), flags, ptr(out), ptr(lse_out), _lib.stream(device)),
+              "verify_attention_static")
+        out = _forward_only(out, q, k, v, sink)
+        return (out, lse_out) if lse else out
+    workspace = torch.empty(max(1, size.value), dtype=torch.uint8, device=device) if size.value else None
     check(library.wptv_verify_attention(ptr(q_), ptr(k), k.stride(0), k.stride(1), ptr(v), v.stride(0), v.stride(1),
                                         dtype, ptr(positions_), int(window), ptr(tree_base), ptr(ancestors),
                                         ptr(sink_), B, T, H, c, N, float(scale), parts.value, flags, ptr(out),
