@@ -27,6 +27,9 @@ def operands(M, N, K, seed, device):
     (160, 2048, 5632, 0),    # the down projection
     (320, 2048, 2048, 0),    # batch 64
     (496, 1024, 2048, 0),    # the tree's 16 x 31 rows (lm_head shape, fewer columns)
+    (160, 32768, 2048, 0),   # the lm_head at batch 32, k+1 = 5 (128-column tiles)
+    (320, 32768, 2048, 0),   # the lm_head at batch 64
+    (496, 32768, 2048, 0),   # the tree config's lm_head over 16 x 31 node rows
     (17, 192, 320, 3),       # rows that are not a multiple of 16, an uneven K split
     (64, 128, 64, 1),        # one K chunk
 ])
@@ -47,6 +50,14 @@ def test_fp32_output_is_the_bf16_rounded_product(device):
     # the same FP32 sums rounded once: identical to the bf16 output's values
     assert torch.equal(got, bf16.float())
     assert relative_error(got.cpu(), (x.float() @ w.float().T).cpu()) < 1e-2
+
+
+def test_wide_fp32_output_is_the_bf16_rounded_product(device):
+    # the lm_head's 128-column tiles: the FP32 output holds the bf16 output's values
+    M, N, K = 160, 32768, 2048
+    x, w = operands(M, N, K, seed=9, device=device)
+    got = layers.linear(x, w, out_dtype=torch.float32)
+    assert torch.equal(got, layers.linear(x, w).float())
 
 
 def test_splits_agree(device):

@@ -30,7 +30,7 @@ oracle on the CPU.
 * Tree verification at batch 16, 8192 prefix rows, a binary tree of 31 nodes:
   the attention against the oracle (1e-2, the reference's bf16 kernel
   tolerance), then greedy acceptance along the tree on the GPU's bf16
-  lm_head logits against the oracle's walk, with paths planted to depths
+  lm_head logits (the build's product) against the oracle's walk, with paths planted to depths
   0-4 (the tree's five levels) and tied children.
 * The captured stochastic step of the headline workload: graph replays and
   eager steps that read the replays' tapes write the same tokens, counts,
@@ -38,14 +38,12 @@ oracle on the CPU.
 
 import pytest
 import torch
-import torch.nn.functional as F
-
 from oracle import attention as oracle_attention
 from oracle import cache as oracle_cache
 from oracle import decoder as oracle_decoder
 from oracle import sampling as oracle_sampling
 from tests.formulas import relative_error
-from wpt_amd import kernels, sampling
+from wpt_amd import kernels, layers, sampling
 from wpt_amd.decoder import LARGE, MQADecoder, random_weights
 from wpt_amd.step import VerifyStep, prefill
 
@@ -220,7 +218,9 @@ def test_tree_verification_at_its_workload_size(device):
     td = table.to(device)
     o = kernels.tree_attention(q.to(device), td[..., :c], td[..., c:], prefixes.to(device), parents, c ** -0.5)
     assert relative_error(o.cpu(), expected) < 1e-2
-    logits = F.linear(o.reshape(B, M, H * c), head.to(device))  # bf16, read by the sampler as they come
+    # bf16 logits, read by the sampler as they come: the build's product (it
+    # is the step's at up to 320 rows; test_gemm_gpu covers it at these 496)
+    logits = layers.linear(o.reshape(B, M, H * c), head.to(device))
     best = oracle_sampling.first_argmax(logits.float().cpu())
     node_tokens = plant_paths(best, parents, B)
     path, tokens, counts = sampling.greedy_tree(logits, node_tokens.to(device), parents)

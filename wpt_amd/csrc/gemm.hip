@@ -32,21 +32,25 @@ namespace wptv {
 namespace {
 
 constexpr int kGemmWaves = 4;
-constexpr int kTileN = 64;         // output columns per workgroup
+constexpr int kTileN = 64;         // output columns per workgroup (the wide form: 128)
 constexpr int kChunkK = 64;        // K per staged chunk (two k-steps of 32)
 constexpr int kRowBytes = kChunkK * 2;
 
-// R32: the staged X rows, 32 R32 (all M rows, padded to a multiple of 32).
-template <int R32>
+// R32: the staged X rows, 32 R32 (all M rows, padded to a multiple of 32);
+// TN: the workgroup's output columns (64, or 128 where the column tiles
+// outnumber the compute units: half the X re-reads per weight byte).
+template <int R32, int TN = kTileN>
 struct GemmTile {
   static constexpr int kRows = 32 * R32;
   static constexpr int kBlocks = kRows / 16;                        // 16-row blocks
   static constexpr int kMaxPerWave = (kBlocks + kGemmWaves - 1) / kGemmWaves;
-  static constexpr int kWBytes = kTileN * kRowBytes;                // 8 KiB
+  static constexpr int kNBlocks = TN / 16;                          // 16-column blocks
+  static constexpr int kWPieces = TN / 8;                           // 1 KiB W pieces (8 rows) per chunk
+  static constexpr int kWBytes = TN * kRowBytes;                    // 8 or 16 KiB
   static constexpr int kSlotBytes = kWBytes + kRows * kRowBytes;
   static constexpr int kSlots = (160 * 1024) / kSlotBytes < 4 ? (160 * 1024) / kSlotBytes : 4;
   static constexpr int kPieces = kSlotBytes / 1024;                 // 1 KiB DMA instructions per chunk
-  static constexpr int kPerWave = kPieces / kGemmWaves;             // 2 + R32
+  static constexpr int kPerWave = kPieces / kGemmWaves;             // TN / 32 + R32
   static_assert(kPieces % kGemmWaves == 0, "pieces per wave");
   static_assert(kSlots >= 2, "ring");
   static_assert((kSlots - 1) * kPerWave < 64, "vmcnt range");
@@ -83,25 +87,27 @@ __device__ __forceinline__ unsigned short swiglu_bf16(float g, float u) {
 // FP32); kOutSwiGLU -> out bf16 [M, N / 2] = silu(gate) * up, the weight's 64
 // rows of a column tile being 32 gate rows then the 32 up rows of the same
 // features (wptv_gemm_swiglu).
-template <int R32, int OUT>
+template <int R32, int OUT, int TN = kTileN>
 __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned short* __restrict__ x, int64_t ldx,
                                                                const unsigned short* __restrict__ w, int64_t ldw,
                                                                int M, int N, int K, int cps, void* __restrict__ out,
                                                                int64_t ldo) {
-  using G = GemmTile<R32>;
+  using G = GemmTile<R32, TN>;
   constexpr int MBW = G::kMaxPerWave;
+  constexpr int NB = G::kNBlocks;
+  static_assert(OUT != kOutSwiGLU || TN == kTileN, "the SwiGLU epilogue pairs 32 gate and 32 up columns of a 64-column tile");
   __shared__ __attribute__((aligned(16))) unsigned char ring[G::kSlots * G::kSlotBytes];
 
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * kTileN;
+  const int n0 = blockIdx.x * TN;
   const int z = blockIdx.y;
   const int chunks = K / kChunkK;
   const int c0 = z * cps;
   const int nch = max(0, min(chunks, c0 + cps) - c0);
 
-  // DMA: piece p of a chunk is 8 rows x 128 bytes (W rows for p < 8, then X
+  // DMA: piece p of a chunk is 8 rows x 128 bytes (W rows for p < TN / 8, then X
   // rows); lane l fills row rr = l / 8, position pos = l % 8.  The row part of
   // the offset and the chunk's K offset go in the scalar offset.
   const i32x4 wrs = buffer_resource(w);
@@ -118,11 +124,11 @@ __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned sh
 #pragma unroll
     for (int u = 0; u < G::kPerWave; ++u) {
       const int p = wv + kGemmWaves * u;
-      if (p < 8) {
+      if (p < G::kWPieces) {
         const uint32_t sbase = (uint32_t)(n0 + 8 * p) * ldw_b + kb;
         dma_16B_at(wrs, wv_off[p & 1], sbase, slot + 1024u * p);
       } else {
-        const int row = 8 * (p - 8) + rr;
+        const int row = 8 * (p - G::kWPieces) + rr;
         const int src = row < M ? row : M - 1;  // padding rows repeat row M - 1
         dma_16B(xrs, (uint32_t)src * ldx_b + kb + 16u * (uint32_t)(pos ^ gemm_swz(row)), slot + 1024u * p);
       }
@@ -142,11 +148,11 @@ __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned sh
   constexpr int kBase = G::kBlocks / kGemmWaves, kExtra = G::kBlocks % kGemmWaves;
   const int nblk = kBase + (wv < kExtra ? 1 : 0);
   const int mb0 = wv * kBase + min(wv, kExtra);
-  f32x4 acc[MBW][4];
+  f32x4 acc[MBW][NB];
 #pragma unroll
   for (int i = 0; i < MBW; ++i)
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) acc[i][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < NB; ++nb) acc[i][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll 1
   for (int i = 0; i < nch; ++i) {
@@ -159,16 +165,16 @@ __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned sh
     const unsigned char* st = ring + (i % G::kSlots) * G::kSlotBytes;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      bf16x8 wf[4];
+      bf16x8 wf[NB];
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
         wf[nb] = *reinterpret_cast<const bf16x8*>(st + 16 * nb * kRowBytes + op_off[s]);
 #pragma unroll
       for (int ii = 0; ii < MBW; ++ii) {
         if (ii >= nblk || 16 * (mb0 + ii) >= M) break;  // not this wavefront's, or padding rows only
         const bf16x8 xf = *reinterpret_cast<const bf16x8*>(st + G::kWBytes + 16 * (mb0 + ii) * kRowBytes + op_off[s]);
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
           acc[ii][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[nb], xf, acc[ii][nb], 0, 0, 0);
       }
     }
@@ -193,7 +199,7 @@ __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned sh
       continue;
     }
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       const int n = n0 + 16 * nb + 4 * g;
       const f32x4 a = acc[ii][nb];
       if constexpr (OUT == kPartF32) {
@@ -242,6 +248,7 @@ struct GemmPlan {
   int r32;     // staged X rows / 32
   int splits;  // parts of K
   int cps;     // K chunks per split
+  int tn;      // output columns per workgroup
   size_t bytes;
 };
 
@@ -266,21 +273,24 @@ int gemm_plan(int M, int N, int K, int requested, GemmPlan* p) {
   p->r32 = r32;
   p->splits = s;
   p->cps = cps;
+  // one part and at least two 64-column tiles per compute unit (an lm_head):
+  // 128-column tiles, each reading X once for twice the weights
+  p->tn = (s == 1 && N % (2 * kTileN) == 0 && tiles >= 2 * compute_units()) ? 2 * kTileN : kTileN;
   p->bytes = s > 1 ? align_up((size_t)s * M * N * sizeof(float), 256) : 0;
   return WPTV_OK;
 }
 
-template <int R32, int OUT>
+template <int R32, int OUT, int TN>
 void launch_gemm(dim3 grid, hipStream_t stream, const unsigned short* x, int64_t ldx, const unsigned short* w,
                  int64_t ldw, int M, int N, int K, int cps, void* out, int64_t ldo) {
-  hipLaunchKernelGGL((gemm_xwt<R32, OUT>), grid, dim3(kGemmWaves * 64), 0, stream, x, ldx, w, ldw, M, N, K, cps, out,
-                     ldo);
+  hipLaunchKernelGGL((gemm_xwt<R32, OUT, TN>), grid, dim3(kGemmWaves * 64), 0, stream, x, ldx, w, ldw, M, N, K, cps,
+                     out, ldo);
 }
 
-template <int OUT>
+template <int OUT, int TN = kTileN>
 void launch_gemm_rows(int r32, dim3 grid, hipStream_t stream, const unsigned short* x, int64_t ldx,
                       const unsigned short* w, int64_t ldw, int M, int N, int K, int cps, void* out, int64_t ldo) {
-#define WPTV_G(RR) launch_gemm<RR, OUT>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo)
+#define WPTV_G(RR) launch_gemm<RR, OUT, TN>(grid, stream, x, ldx, w, ldw, M, N, K, cps, out, ldo)
   switch (r32) {
     case 1: WPTV_G(1); break;
     case 2: WPTV_G(2); break;
@@ -371,12 +381,18 @@ extern "C" int wptv_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw,
                 p.splits);
   const auto* xb = static_cast<const unsigned short*>(x);
   const auto* wb = static_cast<const unsigned short*>(w);
-  dim3 grid(N / kTileN, p.splits);
+  dim3 grid(N / p.tn, p.splits);
   if (p.splits == 1) {
-    if (out_dtype == WPTV_BF16)
+    if (p.tn != kTileN) {
+      if (out_dtype == WPTV_BF16)
+        launch_gemm_rows<kOutBf16, 2 * kTileN>(p.r32, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, out, ldo);
+      else
+        launch_gemm_rows<kOutF32, 2 * kTileN>(p.r32, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, out, ldo);
+    } else if (out_dtype == WPTV_BF16) {
       launch_gemm_rows<kOutBf16>(p.r32, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, out, ldo);
-    else
+    } else {
       launch_gemm_rows<kOutF32>(p.r32, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, out, ldo);
+    }
     return launched("gemm_xwt");
   }
   launch_gemm_rows<kPartF32>(p.r32, grid, stream, xb, ldx, wb, ldw, M, N, K, p.cps, workspace, 0);

@@ -58,8 +58,8 @@ from .cache import Cache
 EPS = 1e-6
 # Rows up to which the projections run as the build's split-K products: at
 # 160 rows (batch 32, k = 4) the step takes 2.53 ms with them against 2.81 ms
-# with hipBLASLt; at 320 rows the two tie (3.19 vs 3.16 ms).
-SPLIT_K_ROWS = 256
+# with hipBLASLt; at 320 rows (batch 64) the two tie (3.19 vs 3.16 ms).
+SPLIT_K_ROWS = 320
 
 
 WINDOW, EXACT, SPARSE = "window", "exact", "sparse"
@@ -229,6 +229,14 @@ class MQADecoder:
             layers.add_rms_norm(h, F.linear(act, down), next_norm, x)
         return handoff
 
+    @staticmethod
+    def _linear(x, w):
+        """x . w^T in x's dtype: the build's product for bf16 at up to
+        LINEAR_MAX_ROWS rows, torch's otherwise (FP32, or a wide prefill)."""
+        if x.dtype == torch.bfloat16 and x.numel() // x.shape[-1] <= layers.LINEAR_MAX_ROWS:
+            return layers.linear(x, w)
+        return F.linear(x, w)
+
     def _attention_out(self, i, h, x, o):
         """h += out(o), x = RMSNorm(h) with the feed-forward norm."""
         B, T, H, c = o.shape
@@ -246,7 +254,7 @@ class MQADecoder:
         B, T, _ = h.shape
         H, c = cfg.heads, cfg.head_dim
         ring = cache.tables[i]
-        proj = F.linear(x, w[f"layers.{i}.qkvg"])  # (B, T, (2H + 2) c): q, k, v, gate
+        proj = self._linear(x, w[f"layers.{i}.qkvg"])  # (B, T, (2H + 2) c): q, k, v, gate
         q = layers.window_qkv_post(proj, w[f"layers.{i}.q_norm"], w[f"layers.{i}.k_norm"], ring, cache.lengths,
                                    counts, H, cfg.rope_dims, cfg.rope_base)
         o = kernels.ring_attention(q, ring, positions, c ** -0.5, cfg.window, w[f"layers.{i}.sink"],
@@ -260,7 +268,7 @@ class MQADecoder:
         w, cfg = self.w, self.config
         H, c = cfg.heads, cfg.head_dim
         keys, values, chosen = handoff
-        proj = F.linear(x, w[f"layers.{i}.qg"])  # (B, T, 2 H c): q, gate
+        proj = self._linear(x, w[f"layers.{i}.qg"])  # (B, T, 2 H c): q, gate
         q = layers.heads_rms_norm(proj, w[f"layers.{i}.q_norm"], H)
         o = kernels.sparse_attention(q, keys, values, w[f"layers.{i}.sink"], chosen, positions, c ** -0.5, cfg.window,
                                      gate=proj[..., H * c:])
@@ -352,9 +360,13 @@ class MQADecoder:
             handoff = self._layer(i, h, x, cache, positions, counts_, next_norm, handoff)
         if self.config.layers in features:
             found[self.config.layers] = h.float()
-        scores = F.linear(x, self.w["head"])
-        if not logits:
-            scores = scores.float()
+        if x.dtype == torch.bfloat16 and B * T <= layers.HEAD_MAX_ROWS:
+            # the build's product; FP32 output = the bf16 product's values, the reference's .float()
+            scores = layers.linear(x, self.w["head"], out_dtype=torch.bfloat16 if logits else torch.float32)
+        else:
+            scores = F.linear(x, self.w["head"])
+            if not logits:
+                scores = scores.float()
         cache.finish(counts_, undoable, T)
         if features:
             return scores, h, torch.cat([found[n] for n in features], -1)

@@ -11,6 +11,11 @@ from ._lib import KernelUnavailable, check, ptr
 
 EPS = 1e-6
 LINEAR_MAX_ROWS = 512  # rows wptv_gemm takes
+# Rows up to which an lm_head (32768 x 2048) runs on wptv_gemm's 128-column
+# tiles: 46 against hipBLASLt's 43 us at 160 rows, 71 against 53 at 320, 98
+# against 64 at 496 (its X chunks then leave the ring two slots); above it,
+# hipBLASLt.
+HEAD_MAX_ROWS = 320
 
 
 def _gpu(*tensors):
