@@ -24,6 +24,10 @@ rejection rule of its speculative-decoding step, restated on the CPU in FP32
                        the child whose token is the argmax (lowest index among
                        equal children), until none is; then the argmax
     cut                _cut (:338-344): up to the first stop, at most limit
+    remember           the drafter's context after a read (_remember,
+                       :140-152): each row's last `window` feature rows
+                       once the model has read the first counts[b] of its
+                       new tokens (zeros before the text)
     schedule           DSpark's prefix scheduler (:236-262): pass widths
                        admitted from the narrowest while the expected tokens
                        per second grow, the first that does not stopping it
@@ -173,6 +177,17 @@ def greedy_tree(scores, node_tokens, parents):
             tokens.append(int(node_tokens[b, node]))
         out.append((path, tokens))
     return out
+
+
+def remember(context, found, counts, window):
+    """context (B, window, F) or None, found (B, n, F) the features the read
+    gave, counts (B,) ints: the rows that end counts[b] rows into found, for
+    each row b, with the earlier context in front."""
+    found = found.float()
+    if context is None:
+        context = found.new_zeros(found.shape[0], window, found.shape[-1])
+    joined = torch.cat([context, found], 1)
+    return torch.stack([joined[b, int(n):int(n) + window] for b, n in enumerate(counts)])
 
 
 def cut(tokens, stops, limit):

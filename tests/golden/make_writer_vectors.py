@@ -39,6 +39,19 @@ def main():
         out.append({"name": name, "prompt": PROMPT, "rows": rows, **kwargs, "drafter": kind, "seed": 1234,
                     "calls": [{str(k): v for k, v in limits.items()} for limits in calls], "written": written,
                     "rounds": writer.rounds, "verified": writer.verified, "accepted": writer.accepted})
+    for name, prompt, kwargs, calls in stubs.context_cases():
+        model = stubs.Bigram()
+        rows = kwargs.pop("rows")
+        writer = Writer(model, prompt, rows, generator=torch.Generator().manual_seed(1234),
+                        drafter=stubs.drafter("context"), **kwargs)
+        written = []
+        for inputs, limits in calls:
+            got = writer.write(inputs, limits)
+            written.append({str(row): tokens for row, tokens in got.items()})
+        out.append({"name": name, "prompt": prompt, "rows": rows, **kwargs, "drafter": "context", "seed": 1234,
+                    "inputs": [{str(k): v for k, v in inputs.items()} for inputs, _ in calls],
+                    "calls": [{str(k): v for k, v in limits.items()} for _, limits in calls], "written": written,
+                    "rounds": writer.rounds, "verified": writer.verified, "accepted": writer.accepted})
     path = HERE / "writer_vectors.json"
     path.write_text(json.dumps(out, indent=1) + "\n")
     print(f"wrote {path} ({len(out)} streams)")

@@ -193,6 +193,49 @@ class Confident(Uniform):
         return tokens, q, torch.tensor(self.confidences[:len(histories)], device=q.device)[:, :count]
 
 
+class Recording(Uniform):
+    """Uniform drafts; reads layers 0, 2 and 4 (the final hidden states) of
+    the model, keeps every context it is given."""
+    features, window = (0, 2, 4), 5
+
+    def __init__(self):
+        self.seen = []
+
+    def draft(self, model, histories, context, count, probabilities, generator):
+        found, lengths = context
+        self.seen.append((found.clone(), lengths.clone(), [list(h) for h in histories]))
+        return super().draft(model, histories, context, count, probabilities, generator)
+
+
+def test_the_writer_gives_a_feature_drafter_the_last_window_of_features(device):
+    # the reference's _remember / _catch_up (wpt_inference/__init__.py:140-152,
+    # 184-200): before each draft, a row's context is the features of the last
+    # `window` tokens its cache holds (zeros before the text), however the
+    # tokens were read: the prompt, catch-up reads of tool inputs, verified drafts
+    gpu, _ = models(PLUMBING, torch.float32, std=0.05)
+    drafter = Recording()
+    writer = Writer(gpu, [3, 5, 7], 3, temperature=1.0, top_k=None,
+                    generator=torch.Generator(device=device).manual_seed(4), drafter=drafter, draft=3)
+    for call, inputs in enumerate(({}, {1: [11, 12, 13]}, {}, {0: [2], 2: [9, 8]}, {}, {})):
+        writer.write(inputs, {0: 4, 1: 4, 2: 4})
+    assert len(drafter.seen) == 6
+    D = PLUMBING.d_model
+    for found, lengths, histories in drafter.seen:
+        for row, history in enumerate(histories):
+            held = int(lengths[row])
+            assert held == len(history) - 1  # every token but the anchor has been read
+            _, _, whole = gpu.extend(torch.tensor([history[:-1]], device=device), gpu.new_cache(1), features=(0, 2, 4))
+            want = torch.zeros(drafter.window, 3 * D, device=device)
+            last = whole[0, -drafter.window:]
+            want[drafter.window - last.shape[0]:] = last
+            assert close(found[row], want, 1e-5), f"row {row} after {held} tokens"
+    # a one-token prompt starts from zeros
+    first = Recording()
+    Writer(gpu, [3], 2, generator=torch.Generator(device=device).manual_seed(5), drafter=first, draft=2).write(
+        {}, {0: 3, 1: 3})
+    assert not first.seen[0][0].any() and first.seen[0][1].tolist() == [0, 0]
+
+
 def test_the_writer_verifies_the_drafts_the_scheduler_admits(device):
     # the reference's known answer (test_sampling.py:236): passes cost the
     # same up to 3 tokens per row, then 20 % more; row 0's confident first

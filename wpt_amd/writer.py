@@ -16,6 +16,11 @@ What differs from the reference, by design:
 With a drafter that gives confidences and a table of pass times (costs), each
 step verifies only the drafts the prefix scheduler admits
 (wpt_amd.scheduling.schedule, the reference's :236-262), as the reference does.
+A drafter that reads the model's features (drafter.features, the layers whose
+hidden states it reads, and drafter.window, how many of the last read tokens'
+states) gets the context the reference's Writer keeps (:140-152, 184-200):
+each row's last `window` feature rows, updated after every read the model
+makes, with a row's pending tokens but its last read first.
 """
 
 import torch
@@ -54,14 +59,18 @@ class Writer:
         self.histories = [list(prompt) for _ in range(rows)]
         self.pending = [[prompt[-1]] for _ in range(rows)]
         self.features = tuple(drafter.features) if drafter is not None else ()
-        if self.features:
-            raise NotImplementedError("drafters that read the model's features are not supported by this writer")
-        self.cache = None
+        self.cache = self.context = None  # context: the drafter's (rows, window, F)
         if hasattr(model, "new_cache"):
             shared = model.new_cache(1, routes=routes)
             if len(prompt) > 1:
-                model.extend(self._tensor([prompt[:-1]]), shared)
+                read = model.extend(self._tensor([prompt[:-1]]), shared, features=self.features)
+                self._remember(read, [len(prompt) - 1])
             self.cache = shared.select([0] * rows)
+            if self.context is not None:  # the prompt's context, in every row
+                self.context = self.context.expand(rows, -1, -1).clone()
+            elif self.features:  # nothing read yet: zeros before the text
+                self.context = torch.zeros(rows, drafter.window, len(self.features) * model.config.d_model,
+                                           device=self.device)
         elif drafter is not None or routes:
             raise ValueError("drafting and recording routes need a model with a generation cache")
 
@@ -87,12 +96,41 @@ class Writer:
         width = max(len(row) for row in rows)
         return torch.tensor([row + [0] * (width - len(row)) for row in rows], dtype=torch.long, device=self.device)
 
+    def _remember(self, read, counts):
+        """The drafter's context once the model has read (read: extend's
+        result, with features) the first counts[b] of row b's new tokens:
+        each row's last `window` feature rows, older ones first."""
+        if not self.features:
+            return
+        found = read[2].float()
+        window = self.drafter.window
+        if self.context is None:
+            self.context = found.new_zeros(found.shape[0], window, found.shape[-1])
+        joined = torch.cat([self.context, found], 1)
+        starts = torch.as_tensor(counts, dtype=torch.long, device=found.device)
+        places = starts[:, None] + torch.arange(window, device=found.device)
+        self.context = joined.gather(1, places[..., None].expand(-1, -1, found.shape[-1]))
+
     def _read(self, rows, extra=None, undoable=False):
         feeds = [[] for _ in self.pending]
         for i, row in enumerate(rows):
             feeds[row] = self.pending[row] + (extra[i] if extra is not None else [])
-        read = self.model.extend(self._tensor(feeds), self.cache, [len(feed) for feed in feeds], undoable)
+        read = self.model.extend(self._tensor(feeds), self.cache, [len(feed) for feed in feeds], undoable,
+                                 features=self.features)
         return read[0][rows], read
+
+    def _catch_up(self, rows):
+        """The model reads each row's pending tokens but its last (a tool
+        result, the template's), so that the context reaches its anchor."""
+        behind = [row for row in rows if len(self.pending[row]) > 1]
+        if not behind:
+            return
+        feeds = [self.pending[row][:-1] if row in behind else [] for row in range(len(self.pending))]
+        counts = [len(feed) for feed in feeds]
+        read = self.model.extend(self._tensor(feeds), self.cache, counts, features=self.features)
+        self._remember(read, counts)
+        for row in behind:
+            self.pending[row] = self.pending[row][-1:]
 
     def _scores(self, rows):
         if self.cache is None:
@@ -121,13 +159,16 @@ class Writer:
 
     def _speculate(self, rows, limits):
         """One step of speculative decoding for rows (:196-233)."""
-        drafted, q, confidences = self.drafter.draft(self.model, [self.histories[row] for row in rows], None,
+        if self.features:
+            self._catch_up(rows)
+        context = (self.context[rows], self.cache.lengths[rows]) if self.features else None
+        drafted, q, confidences = self.drafter.draft(self.model, [self.histories[row] for row in rows], context,
                                                      self.draft, self._probabilities, self.generator)
         drafted, q = drafted.to(self.device), q.to(self.device).float()
         caps = [min(self.draft, limits[row] - 1) for row in rows]  # a row writes at most its drafts and one more
         scheduled = confidences is not None and self.costs is not None
         lengths = schedule(confidences.tolist(), caps, self.costs) if scheduled else caps
-        scores, _ = self._read(rows, [drafted[i, :n].tolist() for i, n in enumerate(lengths)], undoable=True)
+        scores, read = self._read(rows, [drafted[i, :n].tolist() for i, n in enumerate(lengths)], undoable=True)
         firsts = [len(self.pending[row]) - 1 for row in rows]
         L = drafted.shape[1]
         u, e = sampling.draws(len(rows), L, scores.shape[-1], self.generator, self.device)
@@ -144,4 +185,5 @@ class Writer:
             kept[row] = firsts[i] + len(drawn)
         self.rounds += 1
         self.model.undo(self.cache, kept)
+        self._remember(read, kept)
         return written
