@@ -335,10 +335,11 @@ def wpt_layers(steps, warmup):
         return {"us": ms * 1e3, "bytes": nbytes, "GBps": GBps, "frac_hbm_peak": GBps / HBM_PEAK_GBS,
                 "cpu_oracle_us": cpu_s * 1e6}
 
-    # the oracle (FP32, this host's cores) on 2 of the 32 batch rows, scaled to the batch
+    # the oracle (FP32, this host's cores) on every batch row
     from oracle import attention as oracle_attention
 
-    rows = 2
+    torch.set_num_threads(host_threads()[0])
+    rows = B
     qc, tc = q[:rows].float().cpu(), tables[0][:rows].float().cpu()
     pc, sc, gc = positions[:rows].cpu(), sink.cpu(), gate[:rows].float().cpu()
     ic, rc = chosen[0][:rows].cpu(), rings[0][:rows].float().cpu()
@@ -371,8 +372,7 @@ def wpt_layers(steps, warmup):
         ms, nbytes, cpu(lambda: oracle_attention.window_attention(qc, ring_table[..., :c], ring_table[..., c:], sc, pc,
                                                                   c ** -0.5, W) * torch.sigmoid(gc).view(rows, T, H, c)))
     out["note"] = ("bytes: algorithmic (the sparse layer counts each query's gathered rows); cpu_oracle_us: the "
-                   f"oracle in FP32 on {rows} of the {B} batch rows, scaled to the batch, on "
-                   f"{torch.get_num_threads()} host threads")
+                   f"oracle in FP32 on all {B} batch rows, fastest of 2, on {torch.get_num_threads()} host threads")
     return out
 
 
@@ -460,27 +460,47 @@ def projections(model, rows, steps, warmup):
 # the CPU baseline: the oracle running the headline step for sampled rows
 # ---------------------------------------------------------------------------
 
-def cpu_baseline(pieces, rows=2, budget_s=20.0):
+def host_threads():
+    """(threads to use, the affinity's CPU count, the cgroup's CPU quota or
+    None): the affinity's CPUs, capped by the cgroup quota where one is set
+    (more threads than the quota only time-slice)."""
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        limit, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if limit != "max":
+            quota = max(1, int(int(limit) / int(period)))
+    except (OSError, ValueError):
+        pass
+    return (min(affinity, quota) if quota else affinity), affinity, quota
+
+
+def cpu_baseline(pieces, budget_s=20.0, passes=5):
+    """The oracle (FP32, this host's cores) running the headline step for
+    every row: the same weights, KV cache, pending tokens, drafts and
+    distributions; fastest of up to `passes` passes within the budget, as
+    the reference's measure_costs takes the fastest pass."""
     import torch
 
     from oracle import decoder as oracle_decoder
     from oracle import sampling as oracle_sampling
 
     model, cache, step, weights = pieces
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    threads, affinity, quota = host_threads()
     torch.set_num_threads(threads)
     config = model.config
+    rows = cache.rows
     started = time.perf_counter()
     ora = oracle_decoder.Decoder({name: w.float().cpu() for name, w in weights.items()}, config.layers, config.heads,
                                  config.head_dim)
-    lengths = cache.lengths[:rows].cpu()
-    tables = [t[:rows, :int(lengths.max()) + step.k + 1].float().cpu() for t in cache.tables]
-    feeds = step.feeds[:rows].cpu()
-    q = step.q[:rows].cpu()
-    log(f"oracle set up in {time.perf_counter() - started:.1f} s")
+    lengths = cache.lengths.cpu()
+    tables = [t[:, :int(lengths.max()) + step.k + 1].float().cpu() for t in cache.tables]
+    feeds = step.feeds.cpu()
+    q = step.q.cpu()
+    log(f"oracle set up in {time.perf_counter() - started:.1f} s ({rows} rows, {threads} threads)")
     generator = torch.Generator().manual_seed(0)
-    best, spent, passes, written = float("inf"), 0.0, 0, 0
-    while passes < 1 or (spent < budget_s and passes < 5):
+    best, spent, done, written = float("inf"), 0.0, 0, 0
+    while done < 1 or (spent < budget_s and done < passes):
         state = oracle_decoder.cache.Rows(rows)
         state.lengths = lengths.clone()
         state.values = {("entries", i): t.clone() for i, t in enumerate(tables)}
@@ -490,11 +510,65 @@ def cpu_baseline(pieces, rows=2, budget_s=20.0):
         out = oracle_sampling.accept(scores, q, feeds[:, 1:], [step.k] * rows, step.temperature, step.top_k, draws)
         ora.undo(state, [len(t) for t in out])
         elapsed = time.perf_counter() - start
-        best, spent, passes = min(best, elapsed), spent + elapsed, passes + 1
+        best, spent, done = min(best, elapsed), spent + elapsed, done + 1
         written = sum(len(t) for t in out)
     return {"value": written / best, "unit": "accepted tokens/s", "cores": threads, "kind": "port",
-            "sample": f"the oracle's verify step (24 layers, FP32) for {rows} of the 32 rows at the same KV "
-                      f"length and drafts, fastest of {passes} passes on {cpu_name()}"}
+            "sample": f"the oracle's verify step (24 layers, FP32) for all {rows} rows at the same KV length, "
+                      f"drafts and distributions, drawing lazily as the reference does; fastest of {done} passes "
+                      f"({best:.2f} s) on {threads} threads ({affinity} CPUs in the affinity, cgroup quota "
+                      f"{quota if quota else 'none'}) of {cpu_name()}"}
+
+
+def cpu_attention_c3():
+    """The oracle's sliding-window verify on every row of the C3 workload (FP32, host cores): seconds."""
+    import torch
+
+    from oracle import attention as oracle_attention
+
+    torch.set_num_threads(host_threads()[0])
+    B, T, H, c, N, W = 8, 5, 16, 128, 32768, 1024
+    generator = torch.Generator().manual_seed(0)
+    lengths = torch.randint(N // 2, N + 1, (B,), generator=generator)
+    positions = lengths[:, None] - T + torch.arange(T)
+    q = torch.randn(B, T, H, c, generator=generator).to(torch.bfloat16)
+    table = torch.randn(B, N, 2 * c, generator=generator).to(torch.bfloat16)
+    sink = torch.full((H,), float("-inf"))
+    idx = torch.empty(B, T, 0, dtype=torch.long)
+    best = float("inf")
+    for _ in range(3):
+        start = time.perf_counter()
+        oracle_attention.sparse_attention(q, table[..., :c], table[..., c:], sink, idx, positions, c ** -0.5, W)
+        best = min(best, time.perf_counter() - start)
+    return best
+
+
+def cpu_tree_c4():
+    """The oracle's tree step on every row of the C4 workload (attention, the
+    FP32 lm_head over the 496 node rows, greedy tree acceptance; host
+    cores): (seconds, tokens written)."""
+    import torch
+
+    from oracle import attention as oracle_attention
+    from oracle import sampling as oracle_sampling
+
+    torch.set_num_threads(host_threads()[0])
+    B, M, H, c, prefix, V = 16, 31, 16, 128, 8192, 32768
+    generator = torch.Generator().manual_seed(0)
+    parents = oracle_attention.binary_tree_parents(M)
+    q = torch.randn(B, M, H, c, generator=generator).to(torch.bfloat16)
+    table = torch.randn(B, prefix + M, 2 * c, generator=generator).to(torch.bfloat16)
+    head = (torch.randn(V, H * c, generator=generator) * 0.02).to(torch.bfloat16).float()
+    node_tokens = torch.randint(V, (B, M), generator=generator)
+    prefixes = torch.full((B,), prefix)
+    best, written = float("inf"), 0
+    for _ in range(2):
+        start = time.perf_counter()
+        o = oracle_attention.tree_attention(q, table[..., :c], table[..., c:], prefixes, parents, c ** -0.5)
+        scores = o.float().reshape(B, M, H * c) @ head.T
+        walks = oracle_sampling.greedy_tree(scores, node_tokens, parents)
+        best = min(best, time.perf_counter() - start)
+        written = sum(len(tokens) for _, tokens in walks)
+    return best, written
 
 
 def pmc_workload():
@@ -519,17 +593,54 @@ def pmc_workload():
     log("pmc workload done")
 
 
-def traffic_bytes():
-    """HBM bytes per verify-attention call from the committed counter summary
-    (two rocprofv3 --pmc passes, calibrated by a plain copy), or None."""
-    import re
+COPY_BYTES = 64 * 1024 * 1024  # the plain device copy of --pmc-workload (32 Mi bf16 values), read and written once
 
-    path = ROOT / "profiles" / "verify_attention_B32_KV4096.md"
+
+def counter_pass(counter, timeout=180):
+    """One rocprofv3 --pmc pass of `counter` over this script's
+    --pmc-workload, in a child process: {kernel name: [value per dispatch]}."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    rocprof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    with tempfile.TemporaryDirectory(prefix="wptv_pmc_", dir="/tmp") as where:
+        command = [rocprof, "--pmc", counter, "--output-format", "csv", "-d", where, "-o", "pmc", "--",
+                   sys.executable, str(ROOT / "bench.py"), "--pmc-workload"]
+        subprocess.run(command, cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"}, capture_output=True,
+                       timeout=timeout, check=True)
+        found = {}
+        for path in Path(where).rglob("*counter_collection.csv"):
+            with open(path, newline="") as f:
+                for row in csv.DictReader(f):
+                    if row["Counter_Name"] == counter:
+                        found.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return found
+
+
+def measured_traffic():
+    """HBM bytes per verify-attention call at the roofline shape, measured in
+    this run: FETCH_SIZE and WRITE_SIZE passes (KiB per dispatch) over the
+    five calls of --pmc-workload, each scaled so that the plain 64 MiB copy
+    of the same workload reads (writes) 64 MiB.  (bytes, the two scale
+    factors) or (None, the reason)."""
     try:
-        found = re.search(r"HBM traffic per call: (\d+) bytes", path.read_text())
-    except OSError:
-        return None
-    return int(found.group(1)) if found else None
+        per_call = 0.0
+        factors = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            found = counter_pass(counter)
+            copy = [v for name, values in found.items() if "copy" in name.lower() for v in values[-5:]]
+            attention = [sum(values) for name, values in found.items()
+                         if "verify_attention" in name or "combine_splits" in name]
+            if not copy or not attention:
+                return None, f"{counter}: no copy or attention dispatch in the counter output"
+            factor = COPY_BYTES / (sorted(copy)[len(copy) // 2] * 1024)  # the workload's last copies
+            factors[counter] = factor
+            per_call += sum(attention) / 5 * 1024 * factor  # five calls in the workload
+        return int(per_call), factors
+    except Exception as error:  # the counters are a report, never the run's failure
+        return None, f"{type(error).__name__}: {error}"
 
 
 def main():
@@ -569,7 +680,16 @@ def main():
         configs["plumbing_fp32_greedy_B1"] = plumbing_c1()
         configs["verify_attention_B32_KV4096"] = attn
         configs["sliding_window_B8_KV32768_W1024"] = attention_c3(args.steps, args.warmup)
+        seconds = cpu_attention_c3()
+        configs["sliding_window_B8_KV32768_W1024"]["cpu_baseline"] = {
+            "value": 8 * 5 / seconds, "unit": "query tokens/s", "cores": host_threads()[0], "kind": "port",
+            "sample": f"the oracle's sparse_attention (window only), all 8 rows, fastest of 3: {seconds * 1e3:.1f} ms"}
         configs["tree_B16_KV8192_31nodes_lm_head"] = tree_c4(args.steps, args.warmup)
+        seconds, tokens = cpu_tree_c4()
+        configs["tree_B16_KV8192_31nodes_lm_head"]["cpu_baseline"] = {
+            "value": tokens / seconds, "unit": "accepted tokens/s", "cores": host_threads()[0], "kind": "port",
+            "sample": f"the oracle's tree attention, FP32 lm_head and greedy walk, all 16 rows, fastest of 2: "
+                      f"{seconds * 1e3:.0f} ms"}
         configs["wpt_attention_layers_B32_KV4096"] = wpt_layers(args.steps, args.warmup)
         log("configs c1-c4 and the WPT attention layers done")
     pieces = head.pop("_pieces")
@@ -586,6 +706,11 @@ def main():
             torch.cuda.empty_cache()
         configs["wpt_layout_step_B32_KV4096_k4"] = wpt_layout_step(B, KV, K, args.steps, args.warmup)
         torch.cuda.empty_cache()
+    traffic, traffic_note = (None, "not measured with --quick") if args.quick else measured_traffic()
+    if traffic is not None:
+        traffic_note = (f"rocprofv3 FETCH_SIZE + WRITE_SIZE passes over --pmc-workload in this run, scaled by "
+                        f"{traffic_note['FETCH_SIZE']:.3f} and {traffic_note['WRITE_SIZE']:.3f} (a plain 64 MiB copy "
+                        f"reads and writes 64 MiB); algorithmic bytes {attention_bytes(32, 5, 16, 128, 4096)}")
     line = {
         "metric": "accepted tok/s (B=32,KV=4096,k=4 bf16); verify-attn % of HBM roofline",
         "value": head["tokens_per_s"], "unit": "accepted tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -596,7 +721,8 @@ def main():
                                "rejection sampling T=0.8, HIP graph", "global_batch": B, "seq_len": KV,
                    "draft": K, "tokens_per_row_step": head["tokens_per_row_step"]},
         "roofline": {"bound": "hbm", "achieved": attn["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": attn["GBps"] / HBM_PEAK_GBS, "traffic": traffic_bytes(),
+                     "frac": attn["GBps"] / HBM_PEAK_GBS, "traffic": traffic,
+                     "traffic_note": traffic_note,
                      "kernel": "verify attention, batch 32 x 4096 rows x 5 queries x 16 heads x 128, bf16",
                      "ms": attn["ms"]},
         "cpu_baseline": cpu,

@@ -61,29 +61,41 @@ def _synchronize(device):
         torch.cuda.synchronize(device)
 
 
+def _pass_seconds(run, device):
+    """The seconds one call of run() takes: on a GPU, between two HIP events
+    recorded on the current stream around it (the device's own clock, the
+    launch gaps included); on the CPU, by the host clock."""
+    if device.type == "cuda":
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        run()
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) * 1e-3
+    began = time.perf_counter()
+    run()
+    return time.perf_counter() - began
+
+
 @torch.no_grad()
 def measure_costs(model, rows=1, draft=5, context=256, repeats=3):
     """The seconds of one pass of `model` (with a generation cache) reading n
     tokens per row through a cache of `rows` rows that have read `context`
-    tokens, n = 1 .. draft + 1, each the fastest of `repeats` passes, each
-    undone."""
+    tokens, n = 1 .. draft + 1: for each n the fastest of `repeats` passes,
+    each undone before the next."""
     device = next(model.parameters()).device
     cache = model.new_cache(rows)
     model.extend(torch.zeros(rows, context, dtype=torch.long, device=device), cache)
-    costs = []
-    for n in range(1, draft + 2):
-        ids = torch.zeros(rows, n, dtype=torch.long, device=device)
-        fastest = None
+    _synchronize(device)
+    table = []
+    for width in range(1, draft + 2):
+        ids = torch.zeros(rows, width, dtype=torch.long, device=device)
+        times = []
         for _ in range(repeats):
-            _synchronize(device)
-            start = time.perf_counter()
-            model.extend(ids, cache, undoable=True)
-            _synchronize(device)
-            seconds = time.perf_counter() - start
+            times.append(_pass_seconds(lambda: model.extend(ids, cache, undoable=True), device))
             model.undo(cache, [0] * rows)
-            fastest = seconds if fastest is None else min(fastest, seconds)
-        costs.append(fastest)
-    return costs
+        table.append(min(times))
+    return table
 
 
 def processor_name():
