@@ -26,7 +26,8 @@ of a WPT model at the verify shape (exact with its top-1024 choice, sparse over
 the chosen rows, window over its ring), the step's matrix products (MFMA
 TFLOP/s against the bf16 peak), the 24-layer step at batch 64 / KV 2048, and
 the step of a decoder in the layout of the reference's largest model recipe
-(window, exact and sparse layers).  `cpu_baseline` is the oracle (the reference's PyTorch
+(window, exact and sparse layers), and the Writer's speculative rounds with
+the DSpark-shaped drafter (drafting included).  `cpu_baseline` is the oracle (the reference's PyTorch
 algorithm restated in FP32 on the CPU) running the headline step for a sample
 of rows on this host's cores.
 """
@@ -170,6 +171,53 @@ def wpt_layout_step(B, kv, k, steps, warmup):
     out = decoder_step(B, kv, k, steps, warmup, config=config)
     out["layers"] = "".join(kind[0] for kind in kinds)  # w window, e exact, s sparse
     return out
+
+
+def drafted_writer(model, B, kv, k, rounds=8, warmup=2, seed=0):
+    """Speculative rounds of the Writer (eager, as the reference's runs) with
+    the DSpark-shaped drafter over `model` (24 layers): the drafter reads the
+    residual streams of layers 2, 7, 12, 17 and 22 at the last 128 tokens
+    read, 3 layers, random-init (so nearly every draft is rejected); each
+    round drafts k tokens per row, verifies them in one undoable reading with
+    the features, samples on the GPU and takes back the rejected ones.  B rows
+    share one prompt of kv - 1 random tokens."""
+    import torch
+
+    from wpt_amd import drafter as drafters
+    from wpt_amd.writer import Writer
+
+    device = model.device
+    config = drafters.DrafterConfig.for_model(model.config)
+    drafter = drafters.Drafter(model, config, drafters.random_drafter_weights(model.config, config, seed=seed,
+                                                                              device=device))
+    generator = torch.Generator(device=device).manual_seed(seed + 2)
+    prompt = torch.randint(model.config.vocab, (kv,), generator=generator, device=device).tolist()
+    writer = Writer(model, prompt, B, temperature=0.8, top_k=None, draft=k, generator=generator, drafter=drafter)
+    limits = {row: k + 1 for row in range(B)}
+    for _ in range(warmup):
+        writer.write({}, limits)
+    torch.cuda.synchronize()
+    started, written = time.perf_counter(), 0
+    for _ in range(rounds):
+        written += sum(len(tokens) for tokens in writer.write({}, limits).values())
+    torch.cuda.synchronize()
+    seconds = (time.perf_counter() - started) / rounds
+    context = (writer.context, writer.cache.lengths)
+    histories = writer.histories
+    probabilities = writer._probabilities
+    draft_s = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        drafter.draft(model, histories, context, k, probabilities, generator)
+        torch.cuda.synchronize()
+        draft_s.append(time.perf_counter() - t)
+    return {"ms_per_round": seconds * 1e3, "tokens_per_s": written / rounds / seconds,
+            "tokens_per_row_round": written / rounds / B, "draft_ms": min(draft_s) * 1e3,
+            "drafter": {"features": list(config.features), "layers": config.layers, "block": config.block,
+                        "markov_rank": config.markov_rank},
+            "note": "eager Writer rounds (host lists, one synchronization per round), the reference's protocol; "
+                    "the captured verify step alone is the headline"}
 
 
 def _counting(run, written):
@@ -696,6 +744,8 @@ def main():
     if not args.quick:
         configs["projections_rows160"] = projections(pieces[0], B * (K + 1), args.steps, args.warmup)
         log("projections done")
+        configs["drafted_writer_B32_KV4096_k4"] = drafted_writer(pieces[0], B, KV, K)
+        log(f"drafted writer: {configs['drafted_writer_B32_KV4096_k4']['ms_per_round']:.2f} ms a round")
     cpu = None if args.quick else cpu_baseline(pieces)
     del pieces
     torch.cuda.empty_cache()
