@@ -476,15 +476,25 @@ def projections(model, rows, steps, warmup):
     device = model.device
     generator = torch.Generator(device=device).manual_seed(7)
     out = {}
-    kinds = [("qkv", cfg.d_model, "build split-K (parts)"), ("out", cfg.heads * cfg.head_dim, "build split-K (parts)"),
-             ("gate_up_tiles", cfg.d_model, "build, SwiGLU in the epilogue"), ("down", cfg.ffn, "build split-K (parts)")]
+    fm = model.fm_rows(rows)  # the step's products at these rows: the fm ones, or the row-major split-K ones
+    kinds = [("qkv", cfg.d_model, "split-K (parts)"), ("out", cfg.heads * cfg.head_dim, "split-K (parts)"),
+             ("gate_up_tiles", cfg.d_model, "SwiGLU in the epilogue"), ("down", cfg.ffn, "split-K (parts)")]
     for name, K, engine in kinds:
         x = torch.randn(rows, K, generator=generator, device=device).to(torch.bfloat16)
-        ws = [model.w[f"layers.{i}.{name}"] for i in range(cfg.layers)]
-        if engine.startswith("build, SwiGLU"):
-            calls = [lambda w=w: layers.linear_swiglu(x, w) for w in ws]
+        engine = ("build fm, " if fm else "build, ") + engine
+        if fm:
+            xf = layers.fm_pack(x)
+            ws = [model.fm[f"layers.{i}.{name}"] for i in range(cfg.layers)]
+            if name == "gate_up_tiles":
+                calls = [lambda w=w: layers.linear_fm_swiglu(xf, rows, w) for w in ws]
+            else:
+                calls = [lambda w=w: layers.linear_fm_parts(xf, rows, w) for w in ws]
         else:
-            calls = [lambda w=w: layers.linear_parts(x, w) for w in ws]
+            ws = [model.w[f"layers.{i}.{name}"] for i in range(cfg.layers)]
+            if name == "gate_up_tiles":
+                calls = [lambda w=w: layers.linear_swiglu(x, w) for w in ws]
+            else:
+                calls = [lambda w=w: layers.linear_parts(x, w) for w in ws]
         replay = graphed(lambda: [f() for f in calls])
         ms = timed(replay, max(1, steps // 5), max(1, warmup // 5)) / len(ws)
         N = ws[0].shape[0]

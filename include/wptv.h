@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define WPTV_ABI_VERSION 3
+#define WPTV_ABI_VERSION 4
 
 enum {
   WPTV_OK = 0,
@@ -50,8 +50,11 @@ enum {
                                          past its rows); by default the row-block kernel's single full-causal
                                          query group reads rows 0..N-1 and masks the ones past each query (the
                                          key-parallel kernel always reads only the rows the positions reach) */
-  WPTV_ATTN_KEY_SPLIT = 4             /* where T*H <= 80: the key-parallel MFMA kernel (each wavefront owns key
+  WPTV_ATTN_KEY_SPLIT = 4,            /* where T*H <= 80: the key-parallel MFMA kernel (each wavefront owns key
                                          tiles and holds every query row) instead of the row-block one */
+  WPTV_ATTN_OUT_FM = 8                /* the output as the output projection's operand: [B T, H c] in the
+                                         fragment-major layout (below) with wptv_fm_row_blocks(B T) row blocks;
+                                         bf16 row-block kernel only */
 };
 
 int wptv_abi_version(void);
@@ -248,7 +251,10 @@ int wptv_add_rms_norm(void* h, const void* delta, const float* weight, void* y, 
 
 /* wptv_add_rms_norm_parts: as wptv_add_rms_norm with delta = the sum over
  * z < splits of parts[z] (FP32 [splits, M, D], e.g. wptv_gemm_parts' output),
- * rounded to the dtype before the residual add; splits <= 8, D <= 8192. */
+ * rounded to the dtype before the residual add; splits <= 8, D <= 8192.
+ * y_blocks > 0: y in the fragment-major layout with that many row blocks
+ * (bf16, D a multiple of 32, M <= 16 y_blocks; the operand of
+ * wptv_gemm_fm_*); 0: row-major.  Likewise for wptv_embed_rms_norm. */
 /* wptv_embed_rms_norm: the first layer's input (model.py:394-400: the
  *   embedding of ids, then the first attention norm): h [M, D] =
  *   table[ids[m]] (ids clamped into [0, vocab)), y = RMSNorm(h) * weight as
@@ -256,11 +262,11 @@ int wptv_add_rms_norm(void* h, const void* delta, const float* weight, void* y, 
  *   lengths[m / T] + m % T, each token's place after its row's earlier ones
  *   (Place.positions, sequence.py:70-73). */
 int wptv_embed_rms_norm(const int64_t* ids, const void* table, int64_t vocab, const float* weight, void* h, void* y,
-                        int M, int D, int dtype, float eps, const int64_t* lengths, int64_t* positions, int T,
-                        hipStream_t stream);
+                        int y_blocks, int M, int D, int dtype, float eps, const int64_t* lengths, int64_t* positions,
+                        int T, hipStream_t stream);
 
-int wptv_add_rms_norm_parts(void* h, const float* parts, int splits, const float* weight, void* y, int M, int D,
-                            int dtype, float eps, hipStream_t stream);
+int wptv_add_rms_norm_parts(void* h, const float* parts, int splits, const float* weight, void* y, int y_blocks,
+                            int M, int D, int dtype, float eps, hipStream_t stream);
 
 int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const float* q_norm, const float* k_norm, void* q_out,
                   void* table, int64_t table_stride_b, int64_t table_stride_n, int64_t capacity,
@@ -333,6 +339,46 @@ int wptv_gemm_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, int 
  * rows 64 t + 32 .. 64 t + 63 their up rows (N a multiple of 64). */
 int wptv_gemm_swiglu(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K, void* out,
                      int64_t ldo, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * The same products with fragment-major ("fm") operands, for the verify
+ * step's projections at M <= 160 rows (the reference's nn.Linear under bf16
+ * autocast: attention.py:157-168, layers.py:45-61).  An fm matrix A [R, K]
+ * (bf16, K a multiple of 32) is stored as 1 KiB blocks of 16 rows x 32
+ * columns: block (ks, rb) at element (ks * RB + rb) * 512, RB its row-block
+ * count, and in it element 8 l + e holds A[16 rb + l % 16][32 ks + 8 (l / 16)
+ * + e] (l < 64, e < 8; rows past R are padding): the register order of the
+ * bf16 16x16x32 matrix instruction, so a wavefront reads a block as 1 KiB of
+ * contiguous memory.  Weights are packed once (RB = N / 16); X holds
+ * wptv_fm_row_blocks(M) row blocks and is written in that layout by its
+ * producer (wptv_add_rms_norm_parts, wptv_embed_rms_norm, wptv_verify_attention
+ * with WPTV_ATTN_OUT_FM, wptv_gemm_fm_swiglu).  No counterpart in the
+ * reference: a layout of this build's own.
+ *
+ * wptv_fm_pack: out = a [rows, K] (row-major bf16, leading dimension lda) in
+ *   the fm layout with row_blocks row blocks, padding rows zero.
+ * wptv_fm_row_blocks: the row blocks an fm X of M rows has (2 ceil(M / 32)).
+ * wptv_gemm_fm_plan: the part count of a product (*splits 0: chosen; in: a
+ *   count to check) and the bytes of its FP32 parts; swiglu: the gate/up
+ *   form (one part).  N a multiple of 32 (64 for swiglu), K of 128.
+ * wptv_gemm_fm_parts: parts [splits, M, N] FP32 of x . w^T, each over one
+ *   part of K, for a consumer that sums them (wptv_qkv_post_parts,
+ *   wptv_add_rms_norm_parts).
+ * wptv_gemm_fm_swiglu: the gate/up product (w's rows interleaved by tiles of
+ *   64 as for wptv_gemm_swiglu, then packed) with SwiGLU in its epilogue:
+ *   out_fm [M, N / 2] bf16 in the fm layout with wptv_fm_row_blocks(M) row
+ *   blocks (the down product's X).
+ * ------------------------------------------------------------------------- */
+int wptv_fm_pack(const void* a, int64_t lda, int rows, int K, int row_blocks, void* out, hipStream_t stream);
+
+int wptv_fm_row_blocks(int M);
+
+int wptv_gemm_fm_plan(int M, int N, int K, int swiglu, int* splits, size_t* parts_bytes);
+
+int wptv_gemm_fm_parts(const void* x_fm, const void* w_fm, int M, int N, int K, int splits, float* parts,
+                       size_t parts_bytes, hipStream_t stream);
+
+int wptv_gemm_fm_swiglu(const void* x_fm, const void* w_fm, int M, int N, int K, void* out_fm, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Acceptance: the reference's per-row verification loop of

@@ -12,7 +12,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwptv.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 WPTV_F32, WPTV_BF16 = 0, 1
 DTYPES = {torch.float32: WPTV_F32, torch.bfloat16: WPTV_BF16}
@@ -21,6 +21,7 @@ INDEX_DTYPES = {torch.int64: WPTV_I64, torch.int32: WPTV_I32}
 FORCE_GENERIC = 1
 RANGE_FROM_POSITIONS = 2
 KEY_SPLIT = 4
+OUT_FM = 8
 
 
 class KernelUnavailable(RuntimeError):
@@ -53,7 +54,7 @@ SIGNATURES = {
     "wptv_qkv_post": [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I, _I, _F, _P],
     "wptv_window_qkv_post": [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I, _P, _P, _I, _I, _I, _I, _I, _P, _I, _F, _P],
     "wptv_heads_rms_norm": [_P, _I64, _P, _P, _I, _I, _I, _I, _F, _P],
-    "wptv_embed_rms_norm": [_P, _P, _I64, _P, _P, _P, _I, _I, _I, _F, _P, _P, _I, _P],
+    "wptv_embed_rms_norm": [_P, _P, _I64, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _I, _P],
     "wptv_cache_lengths": [_P, _P, _P, _I, _I, _I, _P],
     "wptv_next_feeds": [_P, _I64, _P, _P, _I64, _I, _I, _P, _P],
     "wptv_swiglu": [_P, _P, _I, _I, _I, _P],
@@ -61,7 +62,12 @@ SIGNATURES = {
     "wptv_gemm": [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _I, _I, _P, _SZ, _P],
     "wptv_gemm_swiglu": [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _P],
     "wptv_gemm_parts": [_P, _I64, _P, _I64, _I, _I, _I, _I, _P, _SZ, _P],
-    "wptv_add_rms_norm_parts": [_P, _P, _I, _P, _P, _I, _I, _I, _F, _P],
+    "wptv_fm_pack": [_P, _I64, _I, _I, _I, _P, _P],
+    "wptv_fm_row_blocks": [_I],
+    "wptv_gemm_fm_plan": [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_SZ)],
+    "wptv_gemm_fm_parts": [_P, _P, _I, _I, _I, _I, _P, _SZ, _P],
+    "wptv_gemm_fm_swiglu": [_P, _P, _I, _I, _I, _P, _P],
+    "wptv_add_rms_norm_parts": [_P, _P, _I, _P, _P, _I, _I, _I, _I, _F, _P],
     "wptv_qkv_post_parts": [_P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I, _I, _F, _P],
     "wptv_accept_workspace": [_I, _I, ctypes.POINTER(_SZ)],
     "wptv_accept": [_P, _I64, _I64, _I, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P, _P,
@@ -117,6 +123,12 @@ def ptr(tensor):
 def stream(device):
     """The current HIP stream of device, as the library takes it."""
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def fm_row_blocks(rows):
+    """The 16-row blocks a fragment-major operand of `rows` rows is stored
+    with (include/wptv.h: 2 ceil(rows / 32))."""
+    return 2 * ((int(rows) + 31) // 32)
 
 
 def dtype_code(dtype):

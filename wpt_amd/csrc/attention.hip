@@ -107,11 +107,11 @@ __device__ __forceinline__ unsigned short gated_bf16(float o, unsigned short g) 
 // eight at a time, every load of a group issued before any is used, with a
 // running maximum across groups.  Writes the 8 outputs and, when lse is
 // given and c8 == 0, the row's natural-log log-sum-exp.  grow: the row's
-// output gate (NULL: none).
+// output gate (NULL: none).  dst8: where the 8 outputs go.
 __device__ __forceinline__ void merge_parts(const unsigned short* __restrict__ part_o,
                                             const float* __restrict__ part_lse, int64_t row0, int64_t stride,
                                             int splits, int C, int c8, float sink_log2,
-                                            unsigned short* __restrict__ orow, float* __restrict__ lse,
+                                            unsigned short* __restrict__ dst8, float* __restrict__ lse,
                                             const unsigned short* __restrict__ grow) {
   constexpr int kGroup = 8;
   float M = kNegInf, L = 0.f;
@@ -164,7 +164,7 @@ __device__ __forceinline__ void merge_parts(const unsigned short* __restrict__ p
 #pragma unroll
     for (int e = 0; e < 8; ++e) res[e] = f32_to_bf16(acc[e] * inv);
   }
-  *reinterpret_cast<u16x8*>(orow + c8) = res;
+  *reinterpret_cast<u16x8*>(dst8) = res;
   if (lse && c8 == 0) *lse = L > 0.f ? (M + log2f(L)) * kLn2 : kNegInf;
 }
 
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
     const float* __restrict__ sink, int T, int H, int N, float scale_log2, int groups, int splits,
     int range_from_positions, int xcd_map, RowMap rows, OutGate gate, unsigned short* __restrict__ out,
-    float* __restrict__ lse_out, unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
+    int out_fm, float* __restrict__ lse_out, unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
   using G = Tile<C>;
   constexpr int kRows = 16 * MB;
   constexpr int kXC = C / 8;  // 16-byte chunks per key or value row
@@ -552,6 +552,8 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
     unsigned short* orow = out + ((int64_t)b * R + r) * C;
     const unsigned short* grow = gate.row<unsigned short>(b, T, r, H, C);
+    // out_fm > 0: the output [B T, H C] in the fm layout with out_fm row blocks
+    const int fm_row = b * T + r / H, fm_col = (r % H) * C;
 #pragma unroll
     for (int cb = 0; cb < G::kCBlocks; ++cb) {
       const f32x4 val = o[cb] * scale_out;
@@ -563,7 +565,9 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
       } else {
         res = u16x4{f32_to_bf16(val[0]), f32_to_bf16(val[1]), f32_to_bf16(val[2]), f32_to_bf16(val[3])};
       }
-      *reinterpret_cast<u16x4*>(orow + cb * 16 + 4 * g) = res;
+      unsigned short* dst = out_fm ? out + fm_offset(fm_row, fm_col + cb * 16 + 4 * g, out_fm)
+                                   : orow + cb * 16 + 4 * g;
+      *reinterpret_cast<u16x4*>(dst) = res;
     }
     if (lse_out && g == 0) lse_out[(int64_t)b * R + r] = lse2 * kLn2;
   } else {
@@ -1295,7 +1299,8 @@ __global__ __launch_bounds__(256) void combine_splits(const unsigned short* __re
                                                       const float* __restrict__ part_lse,
                                                       const float* __restrict__ sink, int B, int T, int H, int C,
                                                       int rows_per_group, int groups, int splits, OutGate gate,
-                                                      unsigned short* __restrict__ out, float* __restrict__ lse_out) {
+                                                      unsigned short* __restrict__ out, int out_fm,
+                                                      float* __restrict__ lse_out) {
   const int R = T * H;
   const int per_row = C / 8;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1307,8 +1312,11 @@ __global__ __launch_bounds__(256) void combine_splits(const unsigned short* __re
   const int grp = r / rows_per_group, rr = r % rows_per_group;
   const int64_t row0 = ((int64_t)(b * groups + grp) * splits) * rows_per_group + rr;  // split 0's part
   const unsigned short* grow = gate.row<unsigned short>(b, T, r, H, C);
-  merge_parts(part_o, part_lse, row0, rows_per_group, splits, C, c8, sink ? sink[r % H] * kLog2e : kNegInf,
-              out + ((int64_t)b * R + r) * C, lse_out ? lse_out + (int64_t)b * R + r : nullptr, grow);
+  // out_fm > 0: the output [B T, H C] in the fm layout with out_fm row blocks
+  unsigned short* dst8 = out_fm ? out + fm_offset(b * T + r / H, (r % H) * C + c8, out_fm)
+                                : out + ((int64_t)b * R + r) * C + c8;
+  merge_parts(part_o, part_lse, row0, rows_per_group, splits, C, c8, sink ? sink[r % H] * kLog2e : kNegInf, dst8,
+              lse_out ? lse_out + (int64_t)b * R + r : nullptr, grow);
 }
 
 // ---------------------------------------------------------------------------
@@ -1513,11 +1521,11 @@ void launch_mfma(dim3 grid, hipStream_t stream, const unsigned short* q, const u
                  int64_t ksn, const unsigned short* v, int64_t vsb, int64_t vsn, const int64_t* positions,
                  int window, const int64_t* tree_base, const uint64_t* ancestors, const float* sink, int T, int H,
                  int N, float scale_log2, int groups, int splits, int range_from_positions, int xcd_map,
-                 RowMap rows, OutGate gate, unsigned short* out, float* lse, unsigned short* part_o,
+                 RowMap rows, OutGate gate, unsigned short* out, int out_fm, float* lse, unsigned short* part_o,
                  float* part_lse) {
   hipLaunchKernelGGL((verify_attention_mfma<C, MBW, TREE>), grid, dim3(kKeySets * MBW * 64), 0, stream, q, k, ksb,
                      ksn, v, vsb, vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, groups,
-                     splits, range_from_positions, xcd_map, rows, gate, out, lse, part_o, part_lse);
+                     splits, range_from_positions, xcd_map, rows, gate, out, out_fm, lse, part_o, part_lse);
 }
 
 }  // namespace
@@ -1563,6 +1571,11 @@ int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
                           (k_stride_n % 8 == 0) && (v_stride_b % 8 == 0) && (v_stride_n % 8 == 0);
     if (!ok_align) p.kind = kGeneric, p.splits = 1, p.bytes = 0;
   }
+  // the output in the fm layout (the output projection's operand): the MFMA row-block kernel only
+  const int out_fm = (flags & WPTV_ATTN_OUT_FM) ? fm_row_blocks(B * T) : 0;
+  if (out_fm && p.kind != kRowBlocks)
+    return fail(WPTV_E_UNSUPPORTED, "verify_attention: the fm output layout needs the bf16 MFMA row-block kernel "
+                                    "(head width 64 or 128, aligned operands, no key split)");
   if (p.kind == kGeneric) {
     dim3 grid(T * H, B);
     if (dtype == WPTV_F32)
@@ -1630,8 +1643,8 @@ int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
 #define WPTV_LAUNCH(CC, MM)                                                                                     \
   (tree_base ? launch_mfma<CC, MM, true> : launch_mfma<CC, MM, false>)(                                         \
       grid, stream, qb, kb, k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, positions, window, tree_base,   \
-      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_map, rows, gate, ob, lse, \
-      po, part_lse)
+      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_map, rows, gate, ob,       \
+      out_fm, lse, po, part_lse)
     if (c == 128) {
       switch (p.mbw) {
         case 1: WPTV_LAUNCH(128, 1); break;
@@ -1660,7 +1673,7 @@ int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
   dim3 cgrid((unsigned)((items + threads - 1) / threads));
   hipLaunchKernelGGL(combine_splits, cgrid, dim3(threads), 0, stream,
                      static_cast<const unsigned short*>(part_o), part_lse, sink, B, T, H, c, rows_per_group, p.groups,
-                     p.splits, gate, ob, lse);
+                     p.splits, gate, ob, out_fm, lse);
   return launched("combine_splits");
 }
 }  // namespace
@@ -1908,6 +1921,6 @@ extern "C" int wptv_sparse_attention(const void* q, const void* k, int64_t k_str
   const long long items = (long long)B * T * H * (c / 8);
   dim3 cgrid((unsigned)((items + 255) / 256));
   hipLaunchKernelGGL(combine_splits, cgrid, dim3(256), 0, stream, part_o, part_lse, sink, B, T, H, c, H, T, p.splits,
-                     og, ob, lse);
+                     og, ob, 0, lse);
   return launched("combine_splits");
 }

@@ -109,8 +109,8 @@ __global__ __launch_bounds__(64) void add_rms_norm(T* __restrict__ h, const T* _
 template <typename T, int NCH>
 __global__ __launch_bounds__(64) void embed_rms_norm(const int64_t* __restrict__ ids, const T* __restrict__ table,
                                                      int64_t vocab, const float* __restrict__ weight,
-                                                     T* __restrict__ h, T* __restrict__ y, int D, float eps,
-                                                     const int64_t* __restrict__ lengths,
+                                                     T* __restrict__ h, T* __restrict__ y, int y_blocks, int D,
+                                                     float eps, const int64_t* __restrict__ lengths,
                                                      int64_t* __restrict__ positions, int Tn) {
   const int row = blockIdx.x;
   const int lane = threadIdx.x;
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(64) void embed_rms_norm(const int64_t* __restrict__
       float out[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) out[e] = x[k][e] * inv * wt[k][e];
-      Vec8<T>::store(yrow + col, out);
+      Vec8<T>::store(y_blocks ? y + fm_offset(row, col, y_blocks) : yrow + col, out);
     }
   }
   if (positions && lane == 0) positions[row] = lengths[row / Tn] + row % Tn;
@@ -156,8 +156,8 @@ __global__ __launch_bounds__(64) void embed_rms_norm(const int64_t* __restrict__
 // norm weight -- issued before the first use.
 template <typename T, int S>
 __global__ __launch_bounds__(1024) void add_rms_norm_parts(T* __restrict__ h, const float* __restrict__ parts,
-                                                           const float* __restrict__ weight, T* __restrict__ y, int M,
-                                                           int D, float eps) {
+                                                           const float* __restrict__ weight, T* __restrict__ y,
+                                                           int y_blocks, int M, int D, float eps) {
   __shared__ float wsum[16];
   const int row = blockIdx.x;
   const int col = threadIdx.x * 8;
@@ -190,7 +190,8 @@ __global__ __launch_bounds__(1024) void add_rms_norm_parts(T* __restrict__ h, co
   float out[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) out[e] = x[e] * inv * wt[e];
-  Vec8<T>::store(y + (int64_t)row * D + col, out);
+  // y_blocks > 0: y in the fm layout (the next product's operand)
+  Vec8<T>::store(y_blocks ? y + fm_offset(row, col, y_blocks) : y + (int64_t)row * D + col, out);
 }
 
 // EPL consecutive elements per lane (a head of 64 EPL values per wavefront).
@@ -411,9 +412,22 @@ extern "C" int wptv_add_rms_norm(void* h, const void* delta, const float* weight
   return launched("add_rms_norm");
 }
 
+namespace wptv {
+namespace {
+// y_blocks > 0: y is an fm operand (bf16, D a multiple of 32, M rows in y_blocks row blocks).
+int check_fm_output(const char* what, int y_blocks, int M, int D, int dtype) {
+  if (y_blocks == 0) return WPTV_OK;
+  if (y_blocks < 0 || dtype != WPTV_BF16 || D % 32 || M > 16 * y_blocks)
+    return fail(WPTV_E_INVALID, "%s: an fm output takes bf16, D a multiple of 32 and M <= 16 row blocks (got %d "
+                                "row blocks, M %d, D %d)", what, y_blocks, M, D);
+  return WPTV_OK;
+}
+}  // namespace
+}  // namespace wptv
+
 extern "C" int wptv_embed_rms_norm(const int64_t* ids, const void* table, int64_t vocab, const float* weight,
-                                   void* h, void* y, int M, int D, int dtype, float eps, const int64_t* lengths,
-                                   int64_t* positions, int T, hipStream_t stream) {
+                                   void* h, void* y, int y_blocks, int M, int D, int dtype, float eps,
+                                   const int64_t* lengths, int64_t* positions, int T, hipStream_t stream) {
   if (!ids || !table || !weight || !h || !y) return fail(WPTV_E_INVALID, "embed_rms_norm: a pointer is missing");
   if (M < 0 || D <= 0 || vocab <= 0) return fail(WPTV_E_INVALID, "embed_rms_norm: bad shape M=%d D=%d", M, D);
   if (positions && (!lengths || T <= 0 || M % T))
@@ -422,11 +436,13 @@ extern "C" int wptv_embed_rms_norm(const int64_t* ids, const void* table, int64_
     return fail(WPTV_E_UNSUPPORTED, "embed_rms_norm: width %d is not a multiple of 8 up to %d", D, 64 * 8 * kChunks);
   if (!vec_aligned(table) || !vec_aligned(h) || !vec_aligned(y))
     return fail(WPTV_E_INVALID, "embed_rms_norm: rows must be 16-byte aligned");
+  if (const int st = check_fm_output("embed_rms_norm", y_blocks, M, D, dtype)) return st;
   if (M == 0) return WPTV_OK;
   const int nch = (D + 511) / 512;
 #define WPTV_ERN(TT, NN)                                                                                          \
   hipLaunchKernelGGL((embed_rms_norm<TT, NN>), dim3(M), dim3(64), 0, stream, ids, static_cast<const TT*>(table), \
-                     vocab, weight, static_cast<TT*>(h), static_cast<TT*>(y), D, eps, lengths, positions, T)
+                     vocab, weight, static_cast<TT*>(h), static_cast<TT*>(y), y_blocks, D, eps, lengths,       \
+                     positions, T)
 #define WPTV_ERN_N(TT)              \
   if (nch <= 1) WPTV_ERN(TT, 1);     \
   else if (nch <= 2) WPTV_ERN(TT, 2); \
@@ -444,8 +460,8 @@ extern "C" int wptv_embed_rms_norm(const int64_t* ids, const void* table, int64_
   return launched("embed_rms_norm");
 }
 
-extern "C" int wptv_add_rms_norm_parts(void* h, const float* parts, int splits, const float* weight, void* y, int M,
-                                       int D, int dtype, float eps, hipStream_t stream) {
+extern "C" int wptv_add_rms_norm_parts(void* h, const float* parts, int splits, const float* weight, void* y,
+                                       int y_blocks, int M, int D, int dtype, float eps, hipStream_t stream) {
   if (!h || !parts || !weight || !y) return fail(WPTV_E_INVALID, "add_rms_norm_parts: every pointer must be given");
   if (M < 0 || D <= 0 || splits <= 0)
     return fail(WPTV_E_INVALID, "add_rms_norm_parts: bad shape M=%d D=%d splits=%d", M, D, splits);
@@ -454,11 +470,12 @@ extern "C" int wptv_add_rms_norm_parts(void* h, const float* parts, int splits, 
   if (splits > 8) return fail(WPTV_E_UNSUPPORTED, "add_rms_norm_parts: %d parts above 8", splits);
   if (!vec_aligned(h) || !vec_aligned(parts) || !vec_aligned(y))
     return fail(WPTV_E_INVALID, "add_rms_norm_parts: rows must be 16-byte aligned");
+  if (const int st = check_fm_output("add_rms_norm_parts", y_blocks, M, D, dtype)) return st;
   if (M == 0) return WPTV_OK;
   dim3 grid(M), block(D / 8);
 #define WPTV_ARNP(TT, SS)                                                                                       \
   hipLaunchKernelGGL((add_rms_norm_parts<TT, SS>), grid, block, 0, stream, static_cast<TT*>(h), parts, weight, \
-                     static_cast<TT*>(y), M, D, eps)
+                     static_cast<TT*>(y), y_blocks, M, D, eps)
 #define WPTV_ARNP_S(TT)             \
   switch (splits) {                 \
     case 1: WPTV_ARNP(TT, 1); break; \

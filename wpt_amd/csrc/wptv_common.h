@@ -125,6 +125,24 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t x) {
   return b[0] + b[1];
 }
 
+// ---- fragment-major ("fm") operands ------------------------------------------
+//
+// A bf16 matrix A [R, K] stored as 1 KiB blocks of 16 rows x 32 columns: block
+// (ks, rb) -- rows 16 rb .. 16 rb + 15, columns 32 ks .. 32 ks + 31 -- at
+// element (ks * RB + rb) * 512, RB the blocks' row count (rows past R are
+// padding); in it lane l = 16 g + j holds row 16 rb + j, columns 32 ks + 8 g
+// .. + 7 (8 elements, 16 bytes).  That is the operand layout of
+// v_mfma_f32_16x16x32_bf16 (A and B alike), so one 16-byte load per lane
+// reads a block, 1 KiB contiguous.  8 consecutive columns from a multiple of
+// 8 (4 from a multiple of 4) are contiguous.
+__device__ __forceinline__ int64_t fm_offset(int r, int k, int rb_count) {
+  return ((int64_t)((k >> 5) * rb_count + (r >> 4)) * 64 + (((k >> 3) & 3) << 4) + (r & 15)) * 8 + (k & 7);
+}
+
+// The row blocks an fm operand of M rows is stored with: an even count,
+// 2 ceil(M / 32), so that a few kernel forms serve every row count.
+__host__ __device__ __forceinline__ int fm_row_blocks(int M) { return 2 * ((M + 31) / 32); }
+
 // ---- LDS DMA (global -> LDS without registers) -----------------------------
 
 // s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding).

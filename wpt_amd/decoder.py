@@ -29,12 +29,16 @@ On the GPU:
     the lengths     wptv_cache_lengths after the reading and after an undo
     verify attention wptv_verify_attention, reading only the rows the query
                     positions reach in the cache's table
-    projections     the matrix products of the dtype on MFMA: wptv_gemm's
-                    split-K parts for q/k/v, output and down at up to
+    projections     the matrix products of the dtype on MFMA: at up to 160
+                    bf16 rows the fragment-major products (wptv_gemm_fm_*:
+                    weights packed once, X written in that layout by the
+                    norms, the attention and the SwiGLU epilogue) for the
+                    exact layers' q/k/v and output and every feed-forward
+                    block; wptv_gemm's split-K parts otherwise up to
                     SPLIT_K_ROWS bf16 rows (summed by qkv_post and the
                     residual add + norm), the gate/up product with SwiGLU in
                     its epilogue (wptv_gemm_swiglu) at up to 512 bf16 rows,
-                    hipBLASLt otherwise and for the lm_head
+                    the lm_head up to 320 rows; hipBLASLt beyond
     window layers   wptv_window_qkv_post (norms, rotary encoding, the ring
                     append), wptv_window_attention over the cache's ring with
                     the sink and the output gate fused
@@ -180,6 +184,15 @@ class MQADecoder:
         if dtype == torch.bfloat16:  # the gate/up rows in the order the fused SwiGLU product reads, kept instead
             for i in range(config.layers):
                 self.w[f"layers.{i}.gate_up_tiles"] = layers.interleave_gate_up(self.w.pop(f"layers.{i}.gate_up"))
+        # the fm products' weights, packed once (beside the row-major ones that wider readings use)
+        self.fm = {}
+        if dtype == torch.bfloat16:
+            for i in range(config.layers):
+                names = ["gate_up_tiles", "down"] + (["qkv", "out"] if config.kind(i) == EXACT else [])
+                for name in names:
+                    key = f"layers.{i}.{name}"
+                    self.fm[key] = layers.FmWeight(self.w[key])
+        self._fm_rows = {}
 
     def parameters(self):
         return iter(self.w.values())
@@ -200,21 +213,47 @@ class MQADecoder:
         ring = cache.ring_rows
         return None if ring is None else ring - self.config.window + 1
 
-    def _layer(self, i, h, x, cache, positions, counts, next_norm, handoff):
+    def fm_rows(self, rows):
+        """Whether a reading of `rows` rows runs the fm products (bf16, at
+        most 160 rows, every layer's shapes taken by a kernel form)."""
+        ok = self._fm_rows.get(rows)
+        if ok is None:
+            ok = self.dtype == torch.bfloat16 and all(
+                layers.fm_plan(rows, w.shape[0], w.shape[1], swiglu=name.endswith("gate_up_tiles")) is not None
+                for name, w in self.fm.items())
+            self._fm_rows[rows] = ok
+        return ok
+
+    def _attn_input_fm(self, i, fm):
+        """Whether layer i's attention block reads its input x in the fm layout."""
+        return fm and i < self.config.layers and self.config.kind(i) == EXACT
+
+    def _layer(self, i, h, x, cache, positions, counts, next_norm, handoff, xf=None):
         """One layer on the residual stream h (B, T, D), x = RMSNorm(h) with the
         layer's attention norm; leaves h updated and x = RMSNorm(h) with
         next_norm (the next layer's attention norm, or the final norm).
         handoff: what the last exact layer gave the sparse layers; returns
-        the handoff for the next layer."""
+        the handoff for the next layer.  xf: a flat fm operand of the rows
+        when the reading runs the fm products: the norms write x there
+        instead of into x when the product that reads it is an fm one (an
+        exact layer's q/k/v, every feed-forward block)."""
         w = self.w
         B, T, _ = h.shape
         kind = self.config.kind(i)
+        fm = xf is not None
+        x_in = xf if self._attn_input_fm(i, fm) else x
         if kind == WINDOW:
-            self._window_attention(i, h, x, cache, positions, counts)
+            self._window_attention(i, h, x_in, cache, positions, counts, xf)
         elif kind == SPARSE:
-            self._sparse_attention(i, h, x, positions, handoff)
+            self._sparse_attention(i, h, x_in, positions, handoff, xf)
         else:
-            handoff = self._exact_attention(i, h, x, cache, positions, counts)
+            handoff = self._exact_attention(i, h, x_in, cache, positions, counts, xf)
+        if fm:
+            act = layers.linear_fm_swiglu(xf, B * T, self.fm[f"layers.{i}.gate_up_tiles"])
+            nxt = self._attn_input_fm(i + 1, fm)
+            layers.add_rms_norm_parts(h, layers.linear_fm_parts(act, B * T, self.fm[f"layers.{i}.down"]), next_norm,
+                                      xf if nxt else x, fm=nxt)
+            return handoff
         if x.dtype != torch.bfloat16:
             act = layers.swiglu(F.linear(x, w[f"layers.{i}.gate_up"]))
         elif B * T <= layers.LINEAR_MAX_ROWS:
@@ -237,8 +276,19 @@ class MQADecoder:
             return layers.linear(x, w)
         return F.linear(x, w)
 
-    def _attention_out(self, i, h, x, o):
-        """h += out(o), x = RMSNorm(h) with the feed-forward norm."""
+    def _attention_out(self, i, h, x, o, xf=None):
+        """h += out(o), x = RMSNorm(h) with the feed-forward norm (into xf,
+        the fm operand, when given).  o (B, T, H, c), or a flat fm operand of
+        the B T rows."""
+        if xf is not None:
+            B, T, D = h.shape
+            rows = B * T
+            if o.dim() == 1:
+                parts = layers.linear_fm_parts(o, rows, self.fm[f"layers.{i}.out"])
+            else:
+                parts = layers.linear_parts(o.reshape(rows, -1), self.w[f"layers.{i}.out"])
+            layers.add_rms_norm_parts(h, parts, self.w[f"layers.{i}.ffn_norm"], xf, fm=True)
+            return
         B, T, H, c = o.shape
         out = self.w[f"layers.{i}.out"]
         if x.dtype == torch.bfloat16 and B * T <= SPLIT_K_ROWS:
@@ -247,7 +297,7 @@ class MQADecoder:
         else:
             layers.add_rms_norm(h, F.linear(o.reshape(B, T, H * c), out), self.w[f"layers.{i}.ffn_norm"], x)
 
-    def _window_attention(self, i, h, x, cache, positions, counts):
+    def _window_attention(self, i, h, x, cache, positions, counts, xf=None):
         """A window layer's attention block: h += out(o * sigmoid(gate(x))),
         x = RMSNorm(h) with the feed-forward norm."""
         w, cfg = self.w, self.config
@@ -259,9 +309,9 @@ class MQADecoder:
                                    counts, H, cfg.rope_dims, cfg.rope_base)
         o = kernels.ring_attention(q, ring, positions, c ** -0.5, cfg.window, w[f"layers.{i}.sink"],
                                    gate=proj[..., (H + 2) * c:])
-        self._attention_out(i, h, x, o)
+        self._attention_out(i, h, x, o, xf)
 
-    def _sparse_attention(self, i, h, x, positions, handoff):
+    def _sparse_attention(self, i, h, x, positions, handoff, xf=None):
         """A sparse layer's attention block over the exact layer's table and
         choice (handoff = (keys, values, chosen)): h += out(o * sigmoid(gate(x))),
         x = RMSNorm(h) with the feed-forward norm."""
@@ -272,21 +322,28 @@ class MQADecoder:
         q = layers.heads_rms_norm(proj, w[f"layers.{i}.q_norm"], H)
         o = kernels.sparse_attention(q, keys, values, w[f"layers.{i}.sink"], chosen, positions, c ** -0.5, cfg.window,
                                      gate=proj[..., H * c:])
-        self._attention_out(i, h, x, o)
+        self._attention_out(i, h, x, o, xf)
 
-    def _exact_attention(self, i, h, x, cache, positions, counts):
+    def _exact_attention(self, i, h, x, cache, positions, counts, xf=None):
         """An exact layer's attention block: h += out(o), x = RMSNorm(h) with
         the feed-forward norm.  Returns (keys, values, chosen), the sparse
-        layers' handoff (chosen None when no sparse layer follows)."""
+        layers' handoff (chosen None when no sparse layer follows).  xf
+        given: x is that fm operand, and the output goes through the fm
+        products."""
         w, cfg = self.w, self.config
         B, T, _ = h.shape
         H, c = cfg.heads, cfg.head_dim
         table = cache.tables[i]
+        fm = xf is not None
         # at the verify step's few bf16 rows, the projections run as the
         # build's split-K MFMA products (each weight read once), their FP32
         # parts summed by the kernel that consumes them; torch's otherwise
-        few = x.dtype == torch.bfloat16 and B * T <= SPLIT_K_ROWS
-        if few:
+        few = h.dtype == torch.bfloat16 and B * T <= SPLIT_K_ROWS
+        if fm:
+            q = layers.qkv_post_parts(layers.linear_fm_parts(xf, B * T, self.fm[f"layers.{i}.qkv"]),
+                                      w[f"layers.{i}.q_norm"], w[f"layers.{i}.k_norm"], table, cache.lengths, counts,
+                                      H, T)
+        elif few:
             q = layers.qkv_post_parts(layers.linear_parts(x, w[f"layers.{i}.qkv"]), w[f"layers.{i}.q_norm"],
                                       w[f"layers.{i}.k_norm"], table, cache.lengths, counts, H, T)
         else:
@@ -296,11 +353,12 @@ class MQADecoder:
         keys, values = table[..., :c], table[..., c:]
         chosen = None
         if cfg.chooses(i):  # the top_k rows outside the window by the largest max_h log-softmax weight
-            o, lse = kernels.verify_attention(q, keys, values, positions, c ** -0.5, lse=True, from_positions=True)
+            o, lse = kernels.verify_attention(q, keys, values, positions, c ** -0.5, lse=True, from_positions=True,
+                                              out_fm=fm)
             chosen = kernels.choose_rows(q, keys, positions, lse, c ** -0.5, cfg.top_k, cfg.window)
         else:
-            o = kernels.verify_attention(q, keys, values, positions, c ** -0.5, from_positions=True)
-        self._attention_out(i, h, x, o)
+            o = kernels.verify_attention(q, keys, values, positions, c ** -0.5, from_positions=True, out_fm=fm)
+        self._attention_out(i, h, x, o, xf)
         return keys, values, chosen
 
     @torch.no_grad()
@@ -347,9 +405,12 @@ class MQADecoder:
         h = torch.empty(B, T, D, dtype=self.dtype, device=self.device)
         x = torch.empty_like(h)
         positions = torch.empty(B, T, dtype=torch.long, device=self.device)
+        # the fm products' operand: x in the fragment-major layout
+        xf = layers.fm_empty(B * T, D, self.device) if self.fm_rows(B * T) else None
+        first_fm = self._attn_input_fm(0, xf is not None)
         # the embedding, the first norm and each token's position in one pass
-        layers.embed_rms_norm(ids.contiguous(), self.w["embedding"], self.w["layers.0.attn_norm"], h, x,
-                              cache.lengths, positions)
+        layers.embed_rms_norm(ids.contiguous(), self.w["embedding"], self.w["layers.0.attn_norm"], h,
+                              xf if first_fm else x, cache.lengths, positions, fm=first_fm)
         found = {}
         handoff = None
         for i in range(self.config.layers):
@@ -357,7 +418,7 @@ class MQADecoder:
                 found[i] = h.float()
             last = i + 1 == self.config.layers
             next_norm = self.w["final_norm"] if last else self.w[f"layers.{i + 1}.attn_norm"]
-            handoff = self._layer(i, h, x, cache, positions, counts_, next_norm, handoff)
+            handoff = self._layer(i, h, x, cache, positions, counts_, next_norm, handoff, xf)
         if self.config.layers in features:
             found[self.config.layers] = h.float()
         if x.dtype == torch.bfloat16 and B * T <= layers.HEAD_MAX_ROWS:

@@ -80,7 +80,7 @@ def _long(x, device):
 
 
 def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=None, lse=False, splits=0,
-                     generic=False, from_positions=False, key_split=False, static_scratch=False):
+                     generic=False, from_positions=False, key_split=False, static_scratch=False, out_fm=False):
     """MQA attention of q (B, T, H, c) over k, v (B, N, c): query t of row b
     sees rows max(0, p - window + 1) .. min(p, N - 1), p = positions[b, t]
     (window 0: from row 0), and with tree = (tree_base (B,), ancestors (T,)
@@ -101,6 +101,8 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
     dtype = _lib.dtype_code(q.dtype)
     q_ = q.contiguous()
     positions_ = _long(positions, device)
+    if out_fm and (static_scratch or q.dtype != torch.bfloat16):
+        raise ValueError("the fm output layout takes bf16 queries and the workspace entry point")
     sink_ = None if sink is None else sink.to(device=device, dtype=torch.float32).contiguous()
     if sink_ is not None and sink_.shape != (H,):
         raise ValueError(f"sink must be (H={H},); got {tuple(sink_.shape)}")
@@ -110,7 +112,7 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
         if tree_base.shape != (B,) or ancestors.shape != (T,):
             raise ValueError(f"tree must be (tree_base (B={B},), ancestors (T={T},))")
     flags = ((_lib.FORCE_GENERIC if generic else 0) | (_lib.RANGE_FROM_POSITIONS if from_positions else 0)
-             | (_lib.KEY_SPLIT if key_split else 0))
+             | (_lib.KEY_SPLIT if key_split else 0) | (_lib.OUT_FM if out_fm else 0))
     parts = _lib.ctypes.c_int(int(splits))
     size = _lib.ctypes.c_size_t(0)
     check(library.wptv_attention_workspace(B, T, H, c, N, int(window), dtype, flags, _lib.ctypes.byref(parts),
@@ -126,12 +128,15 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
         out = _forward_only(out, q, k, v, sink)
         return (out, lse_out) if lse else out
     workspace = torch.empty(max(1, size.value), dtype=torch.uint8, device=device) if size.value else None
+    if out_fm:  # [B T, H c] as the output projection's fm operand (layers.fm_unpack reads it back)
+        out = torch.empty(_lib.fm_row_blocks(B * T) * 16 * H * c, dtype=q.dtype, device=device)
     check(library.wptv_verify_attention(ptr(q_), ptr(k), k.stride(0), k.stride(1), ptr(v), v.stride(0), v.stride(1),
                                         dtype, ptr(positions_), int(window), ptr(tree_base), ptr(ancestors),
                                         ptr(sink_), B, T, H, c, N, float(scale), parts.value, flags, ptr(out),
                                         ptr(lse_out), ptr(workspace), size.value, _lib.stream(device)),
           "verify_attention")
-    out = _forward_only(out, q, k, v, sink)
+    if not out_fm:
+        out = _forward_only(out, q, k, v, sink)
     return (out, lse_out) if lse else out
 
 

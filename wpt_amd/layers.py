@@ -30,22 +30,24 @@ def _rows(x, name):
     return x
 
 
-def embed_rms_norm(ids, table, weight, h, y, lengths=None, positions=None, eps=EPS):
+def embed_rms_norm(ids, table, weight, h, y, lengths=None, positions=None, eps=EPS, fm=False):
     """h = table[ids] (ids (B, T) int64 on the device, clamped into the
     vocabulary), y = RMSNorm(h) * weight; with lengths (B,) and positions
-    (B, T) int64 also positions = lengths[:, None] + t."""
+    (B, T) int64 also positions = lengths[:, None] + t.  fm: y is a flat
+    fragment-major operand of B T rows (fm_empty), not (B, T, D)."""
     _gpu(table, weight, h, y)
     B, T = ids.shape
     V, D = table.shape
-    if h.shape != (B, T, D) or y.shape != h.shape or h.dtype != table.dtype or y.dtype != table.dtype:
-        raise ValueError(f"h and y must be (B={B}, T={T}, D={D}) in the table's dtype")
+    if h.shape != (B, T, D) or h.dtype != table.dtype or y.dtype != table.dtype:
+        raise ValueError(f"h must be (B={B}, T={T}, D={D}) and y in the table's dtype")
+    y_blocks = _fm_output(y, B * T, D) if fm else _same(y, h)
     if ids.dtype != torch.int64 or ids.device != h.device or not ids.is_contiguous():
         raise ValueError("ids must be contiguous int64 on the device")
     if positions is not None and (lengths is None or positions.shape != (B, T) or positions.dtype != torch.int64
                                   or lengths.shape != (B,) or lengths.dtype != torch.int64):
         raise ValueError("positions (B, T) and lengths (B,) must be int64")
     check(_lib.lib().wptv_embed_rms_norm(ptr(ids), ptr(table), V, ptr(weight), ptr(_rows(h, "h")), ptr(_rows(y, "y")),
-                                         B * T, D, _lib.dtype_code(h.dtype), float(eps), ptr(lengths),
+                                         y_blocks, B * T, D, _lib.dtype_code(h.dtype), float(eps), ptr(lengths),
                                          ptr(positions), T, _lib.stream(h.device)), "embed_rms_norm")
     return y
 
@@ -256,17 +258,114 @@ def linear_parts(x, w, splits=0, max_splits=8):
     return out
 
 
-def add_rms_norm_parts(h, parts, weight, y, eps=EPS):
+def add_rms_norm_parts(h, parts, weight, y, eps=EPS, fm=False):
     """add_rms_norm with delta = parts.sum(0) (FP32 (S, rows, D), S <= 8),
-    rounded to h's dtype before the residual add."""
+    rounded to h's dtype before the residual add.  fm: y is a flat
+    fragment-major operand of the rows (fm_empty), not h's shape."""
     _gpu(h, parts, weight, y)
     D = h.shape[-1]
     M = h.numel() // D
     if parts.dim() != 3 or parts.shape[1:] != (M, D) or parts.dtype != torch.float32 or not parts.is_contiguous():
         raise ValueError(f"parts must be contiguous FP32 (S, {M}, {D}); got {tuple(parts.shape)} {parts.dtype}")
-    if y.shape != h.shape or y.dtype != h.dtype or weight.shape != (D,) or weight.dtype != torch.float32:
-        raise ValueError("h and y share shape and dtype; weight is float32 (D,)")
+    if y.dtype != h.dtype or weight.shape != (D,) or weight.dtype != torch.float32:
+        raise ValueError("h and y share a dtype; weight is float32 (D,)")
+    y_blocks = _fm_output(y, M, D) if fm else _same(y, h)
     check(_lib.lib().wptv_add_rms_norm_parts(ptr(_rows(h, "h")), ptr(parts), parts.shape[0], ptr(weight),
-                                             ptr(_rows(y, "y")), M, D, _lib.dtype_code(h.dtype), float(eps),
-                                             _lib.stream(h.device)), "add_rms_norm_parts")
+                                             ptr(_rows(y, "y")), y_blocks, M, D, _lib.dtype_code(h.dtype),
+                                             float(eps), _lib.stream(h.device)), "add_rms_norm_parts")
     return y
+
+
+# ---- fragment-major operands (include/wptv.h) and the products that read them ----
+
+FM_MAX_ROWS = 160  # rows the fm products take
+
+
+def _same(y, h):
+    if y.shape != h.shape:
+        raise ValueError(f"y must have h's shape {tuple(h.shape)}; got {tuple(y.shape)}")
+    return 0
+
+
+def _fm_output(y, rows, width):
+    """The row blocks of y, a flat fm operand of rows x width."""
+    blocks = _lib.fm_row_blocks(rows)
+    if y.dtype != torch.bfloat16 or y.dim() != 1 or y.numel() < blocks * 16 * width or width % 32:
+        raise ValueError(f"an fm operand of {rows} x {width} is a flat bf16 tensor of {blocks * 16 * width} "
+                         f"elements (width a multiple of 32); got {tuple(y.shape)} {y.dtype}")
+    return blocks
+
+
+def fm_empty(rows, width, device, dtype=torch.bfloat16):
+    """An uninitialised flat fm operand of rows x width (padding rows included)."""
+    return torch.empty(_lib.fm_row_blocks(rows) * 16 * width, dtype=dtype, device=device)
+
+
+def fm_pack(a, row_blocks=None):
+    """a (R, K) bf16 in the fm layout, flat, with row_blocks 16-row blocks
+    (default: fm_row_blocks(R)); padding rows zero (wptv_fm_pack)."""
+    _gpu(a)
+    if a.dtype != torch.bfloat16 or a.dim() != 2 or a.stride(1) != 1:
+        raise ValueError(f"fm_pack takes a bf16 (R, K) matrix with contiguous rows; got {tuple(a.shape)} {a.dtype}")
+    R, K = a.shape
+    blocks = _lib.fm_row_blocks(R) if row_blocks is None else int(row_blocks)
+    out = torch.empty(blocks * 16 * K, dtype=a.dtype, device=a.device)
+    check(_lib.lib().wptv_fm_pack(ptr(a), a.stride(0), R, K, blocks, ptr(out), _lib.stream(a.device)), "fm_pack")
+    return out
+
+
+def fm_unpack(packed, rows, width):
+    """The (rows, width) row-major matrix of a flat fm operand (torch
+    reshapes: element 8 l + e of block (ks, rb) is row 16 rb + l % 16,
+    column 32 ks + 8 (l // 16) + e)."""
+    blocks = packed.numel() // (16 * width)
+    a = packed[: blocks * 16 * width].view(width // 32, blocks, 4, 16, 8)  # ks, rb, g, j, e
+    return a.permute(1, 3, 0, 2, 4).reshape(blocks * 16, width)[:rows]
+
+
+class FmWeight:
+    """A weight (N, K) packed once in the fm layout (N / 16 row blocks)."""
+
+    def __init__(self, w):
+        self.shape = tuple(w.shape)
+        self.data = fm_pack(w.contiguous(), w.shape[0] // 16)
+
+
+def fm_plan(M, N, K, swiglu=False):
+    """(parts, parts bytes) of an fm product, or None where no kernel form
+    takes the shape."""
+    if not 0 < M <= FM_MAX_ROWS:
+        return None
+    parts = _lib.ctypes.c_int(1 if swiglu else 0)
+    size = _lib.ctypes.c_size_t(0)
+    status = _lib.lib().wptv_gemm_fm_plan(M, N, K, int(swiglu), _lib.ctypes.byref(parts), _lib.ctypes.byref(size))
+    return (parts.value, size.value) if status == 0 else None
+
+
+def linear_fm_parts(x_fm, rows, w, splits=0):
+    """The split-K parts (S, rows, N) FP32 of x . w^T, x a flat fm operand of
+    rows x K, w an FmWeight (N, K) (wptv_gemm_fm_parts)."""
+    _gpu(x_fm, w.data)
+    N, K = w.shape
+    _fm_output(x_fm, rows, K)
+    library = _lib.lib()
+    parts = _lib.ctypes.c_int(int(splits))
+    size = _lib.ctypes.c_size_t(0)
+    check(library.wptv_gemm_fm_plan(rows, N, K, 0, _lib.ctypes.byref(parts), _lib.ctypes.byref(size)), "gemm_fm")
+    out = torch.empty(parts.value, rows, N, dtype=torch.float32, device=x_fm.device)
+    check(library.wptv_gemm_fm_parts(ptr(x_fm), ptr(w.data), rows, N, K, parts.value, ptr(out), out.numel() * 4,
+                                     _lib.stream(x_fm.device)), "gemm_fm_parts")
+    return out
+
+
+def linear_fm_swiglu(x_fm, rows, w):
+    """silu(gate) * up of x (a flat fm operand of rows x K) and the gate/up
+    FmWeight packed from interleave_gate_up's order: a flat fm operand of
+    rows x N / 2, the down product's X (wptv_gemm_fm_swiglu)."""
+    _gpu(x_fm, w.data)
+    N, K = w.shape
+    _fm_output(x_fm, rows, K)
+    out = fm_empty(rows, N // 2, x_fm.device)
+    check(_lib.lib().wptv_gemm_fm_swiglu(ptr(x_fm), ptr(w.data), rows, N, K, ptr(out), _lib.stream(x_fm.device)),
+          "gemm_fm_swiglu")
+    return out
