@@ -187,7 +187,9 @@ int fm_plan(int M, int N, int K, bool swiglu, int requested, FmPlan* p) {
       return fail(WPTV_E_UNSUPPORTED, "gemm_fm: %d parts of K = %d have no kernel form", requested, K);
     s = requested;
   } else {
-    // the most parts that keep one workgroup per compute unit, else the fewest
+    // the most parts that keep one workgroup per compute unit, else the
+    // fewest (measured in the step at 160 rows: q/k/v 10.0 us in 2 parts of
+    // 144 workgroups, 11.2 us in 4 parts of 288)
     const int cus = compute_units();
     int fewest = 0;
     for (int c = 1; c <= 8; ++c) {
