@@ -209,12 +209,17 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(const float (&p)[8]) {
   return r;
 }
 
+// The larger of two scores: IEEE maximum (NaN propagates), one v_maximum3_f32
+// for up to three operands with no canonicalisation of its inputs (fmaxf
+// would first quiet each input with an extra v_max).
+__device__ __forceinline__ float score_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // max / sum over the four 16-lane groups (lanes j, j+16, j+32, j+48).
 __device__ __forceinline__ float group_max(float x) {
   auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  x = score_max(__uint_as_float(a[0]), __uint_as_float(a[1]));
   auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return score_max(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ float group_sum(float x) {
@@ -450,9 +455,9 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
           x[4 * h + i] = vis ? x[4 * h + i] : kNegInf;
         }
     }
-    const float bm =
-        group_max(fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])))) *
-        scale_log2;
+    const float bm = group_max(score_max(score_max(score_max(x[0], x[1]), score_max(x[2], x[3])),
+                                         score_max(score_max(x[4], x[5]), score_max(x[6], x[7])))) *
+                     scale_log2;
     const bool grow = bm > m_run + kRescaleLog2;
     if (__builtin_amdgcn_ballot_w64(grow && m_run != kNegInf)) {
       const float alpha = (grow && m_run != kNegInf) ? __builtin_amdgcn_exp2f(m_run - bm) : 1.f;
@@ -496,15 +501,20 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   for (int s = 0; s < G::kSteps; ++s)
     qf[s] = *reinterpret_cast<const bf16x8*>(qlds + mb * 16 * C + 512 * s + 8 * lane);
   if (mine > 0) qk(0, s0, s1);
-#pragma unroll 1
-  for (int it = 0; it < niter; ++it) {
+  // Iteration it: the scores of tile it + 1 into (n0, n1), the softmax and PV
+  // of tile it from (c0, c1).  Two iterations per trip, the score registers
+  // taking turns, so that no copy moves them.
+  auto iteration = [&](int it, const f32x4& c0, const f32x4& c1, f32x4& n0, f32x4& n1) {
     arrive(it + 1, min(1, mine - 2 - it));  // every wavefront is done with iteration it - 1
     if (dma_wave && it + G::kSlots - 1 < mine) issue(it + G::kSlots - 1);
-    f32x4 n0v = {0.f, 0.f, 0.f, 0.f}, n1v = {0.f, 0.f, 0.f, 0.f};
-    if (it + 1 < mine) qk(it + 1, n0v, n1v);
-    if (it < mine) accumulate(it, s0, s1);
-    s0 = n0v;
-    s1 = n1v;
+    if (it + 1 < mine) qk(it + 1, n0, n1);
+    if (it < mine) accumulate(it, c0, c1);
+  };
+  f32x4 n0 = {0.f, 0.f, 0.f, 0.f}, n1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int it = 0; it < niter; it += 2) {
+    iteration(it, s0, s1, n0, n1);
+    if (it + 1 < niter) iteration(it + 1, n0, n1, s0, s1);
   }
   wait_vmcnt<0>();
   l_run = group_sum(l_run);
@@ -726,9 +736,9 @@ __global__ __launch_bounds__(kSparseWaves * 64, 1) void sparse_attention_mfma(
       x[4 * h + 2] = le + 2 < cnt && ns.z >= 0 ? sv[2] : kNegInf;
       x[4 * h + 3] = le + 3 < cnt && ns.w >= 0 ? sv[3] : kNegInf;
     }
-    const float bm =
-        group_max(fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])))) *
-        scale_log2;
+    const float bm = group_max(score_max(score_max(score_max(x[0], x[1]), score_max(x[2], x[3])),
+                                         score_max(score_max(x[4], x[5]), score_max(x[6], x[7])))) *
+                     scale_log2;
     const bool grow = bm > m_run + kRescaleLog2;
     if (__builtin_amdgcn_ballot_w64(grow && m_run != kNegInf)) {
       const float alpha = (grow && m_run != kNegInf) ? __builtin_amdgcn_exp2f(m_run - bm) : 1.f;
