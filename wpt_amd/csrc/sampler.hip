@@ -117,6 +117,21 @@ __device__ __forceinline__ float score_load(__amdgpu_buffer_rsrc_t r, int v) {
     return row_load(r, v);
 }
 
+// x / d, correctly rounded, given y = 1 / d correctly rounded (a uniform
+// divisor's reciprocal, computed once): q = x y, then one FMA correction with
+// the exact residual x - q d (Markstein's theorem: the result is the rounded
+// quotient).  The residual loses bits where it falls below the normal range,
+// and the product can overflow: there, and for x = 0's sign, the IEEE division.
+// Checked against the division on the CPU: every finite bf16 value and 2e6
+// random FP32 values a divisor, at 212 divisors in [0.05, 4.05], no mismatch
+// for |x| >= 2^-100 with a finite quotient.
+__device__ __forceinline__ float div_by(float x, float d, float y) {
+  const float q0 = x * y;
+  const float r = fmaf(-q0, d, x);
+  const float q = fmaf(r, y, q0);
+  return (fabsf(x) >= 0x1p-100f && fabsf(q) < 0x1p+126f) ? q : x / d;
+}
+
 // The k-th largest order key among the entries that count (valid[i] and
 // key[i] >= floor): a radix select, most significant byte first.
 template <int N>
@@ -226,33 +241,37 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
   for (int i = 0; i < ITEMS; ++i) x[i] = score_load<S>(rs, tid + i * kT);
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) x[i] = tid + i * kT < V ? x[i] : kNegInfS;
-  // first maximal index of the raw scores
-  float bv = kNegInfS;
-  int bi = INT_MAX;
-#pragma unroll
-  for (int i = 0; i < ITEMS; ++i)
-    if (tid + i * kT < V) arg_better(bv, bi, x[i], tid + i * kT);
-  const int best = block_argmax(bv, bi, redv, redi);
   const int idx = b * P + j;
   if (greedy) {
+    // first maximal index of the raw scores (only greedy decisions read it)
+    float bv = kNegInfS;
+    int bi = INT_MAX;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if (tid + i * kT < V) arg_better(bv, bi, x[i], tid + i * kT);
+    const int best = block_argmax(bv, bi, redv, redi);
     if (tid == 0) {
       stats.best[idx] = best;
       stats.keep[idx] = (j < n && drafts) ? (drafts[b * db + j] == best) : 0;
     }
     return;
   }
+  const float tinv = 1.f / temperature;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) x[i] = x[i] / temperature;
+  for (int i = 0; i < ITEMS; ++i) x[i] = div_by(x[i], temperature, tinv);
   float thr = kNegInfS;
   if (top_k > 0 && top_k < V) thr = kth_largest<ITEMS>(x, V, top_k, hist, sel);
   float mx = kNegInfS;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) mx = fmaxf(mx, x[i]);
   const float m = block_max(mx, redv);
+  // exp(s - m) of the kept entries, 0 elsewhere, kept in x for p
   float part = 0.f;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i)
-    if (tid + i * kT < V && x[i] >= thr) part += expf(x[i] - m);
+  for (int i = 0; i < ITEMS; ++i) {
+    x[i] = tid + i * kT < V && x[i] >= thr ? expf(x[i] - m) : 0.f;
+    part += x[i];
+  }
   const float z = block_sum(part, redv);
   // The draw if this position is the first rejected draft: the residual
   // max(0, p - q) normalized by its sum, by the exponential race; at the
@@ -262,7 +281,7 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
   // no more than two rows are held in registers.
   const float zinv = 1.f / z;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) x[i] = tid + i * kT < V && x[i] >= thr ? expf(x[i] - m) * zinv : 0.f;
+  for (int i = 0; i < ITEMS; ++i) x[i] = x[i] * zinv;
   float rest_sum = 1.f;  // the residual's mass (1: the bonus draw from p itself)
   if (draft_pos) {
     float qv[ITEMS];
@@ -283,17 +302,18 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
   for (int i = 0; i < ITEMS; ++i) ev[i] = row_load(re, tid + i * kT);
   float cv = kNegInfS;
   int ci = INT_MAX;
+  const float rinv = 1.f / rest_sum;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const int v = tid + i * kT;
-    if (v < V) arg_better(cv, ci, (draft_pos ? x[i] / rest_sum : x[i]) / ev[i], v);
+    if (v < V) arg_better(cv, ci, (draft_pos ? div_by(x[i], rest_sum, rinv) : x[i]) / ev[i], v);
   }
   const int drawn = block_argmax(cv, ci, redv, redi);
   if (tid == 0) {
     stats.m[idx] = m;
     stats.z[idx] = z;
     stats.thr[idx] = thr;
-    stats.best[idx] = best;
+    stats.best[idx] = -1;  // the raw argmax: greedy decisions only
     // a residual with no mass has no draw (the reference's multinomial raises)
     stats.cand[idx] = (!(draft_pos && !(rest_sum > 0.f)) && drawn >= 0 && drawn < V) ? drawn : -1;
     int keep = 0;
