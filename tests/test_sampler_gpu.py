@@ -54,6 +54,27 @@ def test_accept_matches_the_oracle_on_one_tape(device, V, top_k, temperature):
     assert min(kept) < L and (max(kept) > 0 or top_k == 1)  # rows keep and reject
 
 
+@pytest.mark.parametrize("V", [32768, 1000])
+def test_draft_rows_copied_into_lds_or_read_in_place_decide_alike(device, V):
+    # contiguous q rows (16-byte aligned: the kernel copies each into LDS) and
+    # the same values as a view whose rows lie V + 1 entries apart (read from
+    # memory entry by entry): the same tokens, bit for bit, and the oracle's
+    B, L = 32, 4
+    scores, q, drafts, u, e = step_inputs(B, L, V, seed=40 + V)
+    wide = torch.zeros(B, L, V + 1)
+    wide[..., :V] = q
+    on = [x.to(device) for x in (scores, drafts, u, e)]
+    spread = wide.to(device)[..., :V]
+    assert spread.stride(1) == V + 1
+    for top_k in (None, 40):
+        t1, c1 = sampling.accept(on[0], q.to(device), on[1], on[2], on[3], 0.8, top_k)
+        t2, c2 = sampling.accept(on[0], spread, on[1], on[2], on[3], 0.8, top_k)
+        assert torch.equal(t1, t2) and torch.equal(c1, c2)
+        expected = oracle.accept(scores, q, drafts, [L] * B, 0.8, top_k,
+                                 [oracle.TapeDraws(u[b], e[b]) for b in range(B)])
+        assert sampling.written(t1, c1) == expected
+
+
 @pytest.mark.parametrize("top_k", [5, 40, 1500])
 def test_a_top_k_cut_through_tied_scores_keeps_every_tie(device, top_k):
     # scores on a few levels, so that the k-th largest ties with dozens to

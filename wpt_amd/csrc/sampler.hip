@@ -95,48 +95,95 @@ __device__ __forceinline__ int block_argmax(float v, int i, float* redv, int* re
   return bi;
 }
 
-// A row of V floats as a buffer: a load at index v reads row[v], and 0 for
-// v >= V (the buffer's range check), from a 32-bit offset per item rather
-// than a 64-bit address.
-template <typename S>
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_resource(const S* row, int V) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(row), 0, V * (int)sizeof(S), 0x00020000);
+// Item i of a thread: entry v = threadIdx.x + i * kT of a row of V values,
+// 0 for v >= V.  Each item loads through a buffer over entries i * kT .. V - 1
+// (its range check giving the 0s), at the thread's byte offset, the same
+// register for every item: no per-item addresses are held.
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t item_resource(const T* row, int V, int i) {
+  const int start = i * kT;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(row) + start, 0, max(V - start, 0) * (int)sizeof(T),
+                                           0x00020000);
 }
 
-__device__ __forceinline__ float row_load(__amdgpu_buffer_rsrc_t r, int v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, v * 4, 0, 0));
+__device__ __forceinline__ float row_item(const float* row, int V, int i) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_raw_buffer_load_b32(item_resource(row, V, i), threadIdx.x * 4, 0, 0));
 }
 
-// A scores row of FP32 or bf16 values (the model's logits as they come),
-// read as FP32: a bf16 value converts exactly.
+// A scores row of FP32 or bf16 values (the model's logits as they come):
+// the entry's bits as loaded, and their FP32 value (a bf16 value converts
+// exactly).  Kept apart so that loads issued after the row's need not wait
+// for it.
 template <typename S>
-__device__ __forceinline__ float score_load(__amdgpu_buffer_rsrc_t r, int v) {
+__device__ __forceinline__ S score_bits(const S* row, int V, int i) {
   if constexpr (sizeof(S) == 2)
-    return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, v * 2, 0, 0));
+    return __builtin_amdgcn_raw_buffer_load_b16(item_resource(row, V, i), threadIdx.x * 2, 0, 0);
   else
-    return row_load(r, v);
+    return row_item(row, V, i);
+}
+
+template <typename S>
+__device__ __forceinline__ float score_value(S bits) {
+  if constexpr (sizeof(S) == 2)
+    return bf16_to_f32(bits);
+  else
+    return bits;
 }
 
 // x / d, correctly rounded, given y = 1 / d correctly rounded (a uniform
 // divisor's reciprocal, computed once): q = x y, then one FMA correction with
 // the exact residual x - q d (Markstein's theorem: the result is the rounded
 // quotient).  The residual loses bits where it falls below the normal range,
-// and the product can overflow: there, and for x = 0's sign, the IEEE division.
-// Checked against the division on the CPU: every finite bf16 value and 2e6
-// random FP32 values a divisor, at 212 divisors in [0.05, 4.05], no mismatch
-// for |x| >= 2^-100 with a finite quotient.
-__device__ __forceinline__ float div_by(float x, float d, float y) {
+// and the product can overflow: quot_exact says where the result is the
+// rounded quotient, x = 0 or |x| >= 2^-100 with |q| < 2^126.  Checked
+// against the division on the CPU: every finite bf16 value and 2e6 random
+// FP32 values a divisor at 212 divisors in [0.05, 4.05], and 2e9 random
+// (x, d) pairs with d over 2^-60 .. 2^60: no mismatch where it holds.
+__device__ __forceinline__ float quot(float x, float d, float y) {
   const float q0 = x * y;
-  const float r = fmaf(-q0, d, x);
-  const float q = fmaf(r, y, q0);
-  return (fabsf(x) >= 0x1p-100f && fabsf(q) < 0x1p+126f) ? q : x / d;
+  return fmaf(fmaf(-q0, d, x), y, q0);
 }
 
-// The k-th largest order key among the entries that count (valid[i] and
-// key[i] >= floor): a radix select, most significant byte first.
-template <int N>
-__device__ uint32_t kth_key(const uint32_t (&key)[N], const bool (&valid)[N], uint32_t floor, int k, int* hist,
-                            int* sel) {
+__device__ __forceinline__ bool quot_exact(float x, float q) {
+  return (x == 0.f) | ((fabsf(x) >= 0x1p-100f) & (fabsf(q) < 0x1p+126f));  // no branches
+}
+
+// x / d correctly rounded: the fast quotient, and the IEEE division only in
+// a wavefront where some lane needs it (a branch every lane takes alike; the
+// empty volatile statement keeps the compiler from computing the division
+// everywhere and selecting).
+__device__ __forceinline__ float div_by(float x, float d, float y) {
+  float q = quot(x, d, y);
+  const bool exact = quot_exact(x, q);
+  if (__builtin_amdgcn_ballot_w64(!exact)) {
+    asm volatile("");
+    if (!exact) q = x / d;
+  }
+  return q;
+}
+
+// e^t for t <= 0 (NaN gives 0): 2^(t log2 e) with the product carried in two
+// parts (its rounding error by an FMA, plus t times the low part of log2 e),
+// split at its nearest integer n, the fraction's power on the hardware's
+// exp2 and scaled by 2^n; below ln 2^-149 the result is 0.  The same steps
+// and constants as the device library's expf, whose overflow branch a
+// non-positive argument never takes.  Contraction off: ph - n must subtract
+// the rounded product, whose rounding error pl carries.
+__device__ __forceinline__ float exp_nonpos(float t) {
+#pragma clang fp contract(off)
+  const float ph = t * kLog2e;
+  const float pl = fmaf(t, 0x1.4ae0bep-26f, fmaf(t, kLog2e, -ph));
+  const float n = __builtin_rintf(ph);
+  const float r = __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f((ph - n) + pl), (int)n);
+  return t >= -0x1.9d1da0p+6f ? r : 0.f;
+}
+
+// The k-th largest order key among the entries that count (key_at(i, key)
+// true and key >= floor): a radix select, most significant byte first.  The
+// keys are formed in each pass rather than held, which keeps N registers free.
+template <int N, typename KeyAt>
+__device__ uint32_t kth_key(KeyAt key_at, uint32_t floor, int k, int* hist, int* sel) {
   uint32_t prefix = 0, mask = 0;
   int remaining = k;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -145,8 +192,10 @@ __device__ uint32_t kth_key(const uint32_t (&key)[N], const bool (&valid)[N], ui
     if (tid < 256) hist[tid] = 0;
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < N; ++i)
-      if (valid[i] && key[i] >= floor && (key[i] & mask) == prefix) atomicAdd(&hist[(key[i] >> shift) & 255], 1);
+    for (int i = 0; i < N; ++i) {
+      uint32_t key;
+      if (key_at(i, key) && key >= floor && (key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
+    }
     __syncthreads();
     if (tid < 64) {
       // lane l holds bins 4l .. 4l + 3; above[l] = entries in bins >= 4l + 4
@@ -183,48 +232,79 @@ __device__ uint32_t kth_key(const uint32_t (&key)[N], const bool (&valid)[N], ui
   return prefix;
 }
 
-// The k-th largest of the valid values (v < V), 0 < k < V.  For k up to the
-// number of threads, a floor first: the k-th largest of the threads' own
-// maxima.  The k largest maxima are k distinct entries at or above it, so
-// the k-th largest entry is too, and the full select then counts only the
-// entries at or above the floor (about k of them instead of V, which keeps
-// the histogram's atomics off the few bins that hold most of a row).
+// The k-th largest of a row's V values, 0 < k < V, the entries past the row
+// (v >= V) holding -inf: they are below or equal to every entry, so with
+// k < V they do not move the k-th largest and are counted like the others.
+// For k up to the number of threads, a floor first: the k-th largest of the
+// threads' own maxima.  The k largest maxima are k distinct entries at or
+// above it, so the k-th largest entry is too, and the full select then
+// counts only the entries at or above the floor (about k of them instead of
+// V, which keeps the histogram's atomics off the few bins that hold most of
+// a row).
+// With a floor, each thread first gathers its entries at or above it (two
+// slots): the radix passes then read those instead of every entry, unless a
+// thread holds more than two (then they read every entry, as without one).
 template <int ITEMS>
-__device__ float kth_largest(const float (&s)[ITEMS], int V, int k, int* hist, int* sel) {
-  const int tid = threadIdx.x;
-  uint32_t key[ITEMS];
-  bool valid[ITEMS];
+__device__ float kth_largest(const float (&s)[ITEMS], int k, int* hist, int* sel, float* red) {
+  const auto entry = [&](int i, uint32_t& key) {
+    key = order_key(s[i]);
+    return true;
+  };
   uint32_t own = 0;
-  bool any = false;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) own = max(own, order_key(s[i]));
+  if (k > kT) return key_value(kth_key<ITEMS>(entry, 0u, k, hist, sel));
+  const uint32_t floor = kth_key<1>(
+      [&](int, uint32_t& key) {
+        key = own;
+        return true;
+      },
+      0u, k, hist, sel);
+  uint32_t c0 = 0, c1 = 0;
+  int count = 0;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    key[i] = order_key(s[i]);
-    valid[i] = tid + i * kT < V;
-    if (valid[i]) own = max(own, key[i]);
-    any |= valid[i];
+    const uint32_t key = order_key(s[i]);
+    const bool at = key >= floor;
+    c1 = at && count == 1 ? key : c1;
+    c0 = at && count == 0 ? key : c0;
+    count += at;
   }
-  uint32_t floor = 0;
-  if (k <= kT) {
-    const uint32_t mine[1] = {own};
-    const bool counts[1] = {any};
-    floor = kth_key<1>(mine, counts, 0u, k, hist, sel);
-  }
-  return key_value(kth_key<ITEMS>(key, valid, floor, k, hist, sel));
+  if (block_max((float)count, red) <= 2.f)
+    return key_value(kth_key<2>(
+        [&](int i, uint32_t& key) {
+          key = i ? c1 : c0;
+          return i < count;
+        },
+        floor, k, hist, sel));
+  return key_value(kth_key<ITEMS>(entry, floor, k, hist, sel));
 }
 
-template <int ITEMS, typename S>
+// QLDS: the draft row is copied into LDS by DMA and the exponentials loaded
+// into registers at the start (after the top-k select when CUT, whose passes
+// need the registers), so that the rows stream in together, and the draft's
+// own p and q come from the thread that holds its score; needs the row in
+// LDS (V <= 32768, a multiple of 4 floats, 16-byte aligned).  CUT: a top-k
+// cut (0 < top_k < V).
+template <int ITEMS, typename S, bool QLDS, bool CUT>
 __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores, int64_t sb, int64_t st,
                                                    const int32_t* __restrict__ firsts, const float* q,
                                                    int64_t qb, int64_t qt, const int64_t* __restrict__ drafts,
                                                    int64_t db, const int32_t* __restrict__ lengths,
                                                    const float* __restrict__ u, const float* e,
-                                                   float temperature, int top_k, int greedy, int L, int V,
-                                                   Stats stats) {
+                                                   float temperature, int top_k, int greedy, int B, int L,
+                                                   int V, Stats stats) {
   __shared__ float redv[kW];
   __shared__ int redi[kW];
   __shared__ int hist[256];
   __shared__ int sel[2];
-  const int j = blockIdx.x, b = blockIdx.y, P = L + 1;
+  __shared__ __attribute__((aligned(16))) float qs[QLDS ? ITEMS * kT : 1];  // QLDS: the draft row, qs[v] = q[v]
+  // A row's P positions on one XCD (workgroups are dealt to the 8 XCDs in
+  // turn, so those whose index agrees mod 8 share one): its exponentials row
+  // is read from HBM once and found in that XCD's L2 by the others.
+  const int P = L + 1, slot = blockIdx.x >> 3;
+  const int b = 8 * (slot / P) + (blockIdx.x & 7), j = slot % P;
+  if (b >= B) return;
   const int n = lengths ? min(max(lengths[b], 0), L) : L;
   if (j > n) return;
   const int64_t first = firsts ? firsts[b] : 0;
@@ -235,15 +315,15 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
   const bool draft_pos = j < n;
   const float* qrow = (!greedy && draft_pos) ? q + b * qb + j * qt : nullptr;
   const float* erow = greedy ? nullptr : e + (int64_t)b * V;
-  float x[ITEMS];
-  const auto rs = row_resource(row, V);
+  S bits[ITEMS];
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) x[i] = score_load<S>(rs, tid + i * kT);
-#pragma unroll
-  for (int i = 0; i < ITEMS; ++i) x[i] = tid + i * kT < V ? x[i] : kNegInfS;
+  for (int i = 0; i < ITEMS; ++i) bits[i] = score_bits<S>(row, V, i);
   const int idx = b * P + j;
+  float x[ITEMS];
   if (greedy) {
     // first maximal index of the raw scores (only greedy decisions read it)
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) x[i] = tid + i * kT < V ? score_value<S>(bits[i]) : kNegInfS;
     float bv = kNegInfS;
     int bi = INT_MAX;
 #pragma unroll
@@ -256,57 +336,124 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
     }
     return;
   }
+  const int64_t d = draft_pos ? drafts[b * db + j] : -1;
+  float ev[ITEMS];
+  if constexpr (QLDS) {
+    // the exponentials, then the draft row by DMA (last: the first wait for
+    // it is before the residual): wave w's instruction c moves floats 4096 c
+    // + 256 w .. + 255 to the same entries of qs (16 bytes a lane); the range
+    // check covers the row's V * 4 bytes
+    if constexpr (!CUT) {
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) ev[i] = row_item(erow, V, i);
+    }
+    if (draft_pos) {
+      i32x4 rq = buffer_resource(qrow);
+      rq[2] = V * 4;
+      const uint32_t lds = lds_address(qs) + 1024u * (uint32_t)__builtin_amdgcn_readfirstlane(tid >> 6);
+#pragma unroll
+      for (int c = 0; c < ITEMS / 4; ++c) dma_16B(rq, 16u * (uint32_t)(c * kT + tid), lds + 16384u * c);
+    }
+  }
+  // The entries past the row (v >= V) are -inf from here on: each later
+  // phase then gives them p = 0, a residual of 0 (the draft row reads 0
+  // there) and a race value of 0 / 0, which never wins.
   const float tinv = 1.f / temperature;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) x[i] = div_by(x[i], temperature, tinv);
+  for (int i = 0; i < ITEMS; ++i) x[i] = div_by(score_value<S>(bits[i]), temperature, tinv);
+  if (V < ITEMS * kT) {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if (tid + i * kT >= V) x[i] = kNegInfS;
+    if constexpr (QLDS) {
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+        if (tid + i * kT >= V) qs[tid + i * kT] = 0.f;  // as the range-checked DMA writes them
+    }
+  }
   float thr = kNegInfS;
-  if (top_k > 0 && top_k < V) thr = kth_largest<ITEMS>(x, V, top_k, hist, sel);
+  if constexpr (CUT) {
+    thr = kth_largest<ITEMS>(x, top_k, hist, sel, redv);
+    if constexpr (QLDS) {
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) ev[i] = row_item(erow, V, i);
+    }
+  }
   float mx = kNegInfS;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) mx = fmaxf(mx, x[i]);
   const float m = block_max(mx, redv);
   // exp(s - m) of the kept entries, 0 elsewhere, kept in x for p
   float part = 0.f;
+  if constexpr (CUT) {
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    x[i] = tid + i * kT < V && x[i] >= thr ? expf(x[i] - m) : 0.f;
-    part += x[i];
+    for (int i = 0; i < ITEMS; ++i) {
+      x[i] = x[i] >= thr ? exp_nonpos(x[i] - m) : 0.f;
+      part += x[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      x[i] = exp_nonpos(x[i] - m);
+      part += x[i];
+    }
   }
   const float z = block_sum(part, redv);
   // The draw if this position is the first rejected draft: the residual
   // max(0, p - q) normalized by its sum, by the exponential race; at the
   // position after the last draft the bonus draw from p itself (the
   // reference's multinomial of __init__.py:222-229, as argmax_v w_v / e_v).
-  // The draft row and then the exponentials are read one at a time, so that
-  // no more than two rows are held in registers.
   const float zinv = 1.f / z;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) x[i] = x[i] * zinv;
+  // QLDS: p of the draft, held by thread d mod kT as item d / kT
+  const bool owner = QLDS && d >= 0 && d < V && (int)(d & (kT - 1)) == tid;
+  float pd = 0.f;
+  if (owner) {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if (i == (int)(d >> 10)) pd = x[i];
+  }
   float rest_sum = 1.f;  // the residual's mass (1: the bonus draw from p itself)
   if (draft_pos) {
-    float qv[ITEMS];
-    const auto rq = row_resource(qrow, V);
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i) qv[i] = row_load(rq, tid + i * kT);
     float rest = 0.f;
+    if constexpr (QLDS) {
+      wait_vmcnt<0>();  // this wavefront's DMA has landed
+      __syncthreads();  // and every other's
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      x[i] = tid + i * kT < V ? fmaxf(x[i] - qv[i], 0.f) : 0.f;
-      rest += x[i];
+      for (int i = 0; i < ITEMS; ++i) {
+        x[i] = fmaxf(x[i] - qs[tid + i * kT], 0.f);
+        rest += x[i];
+      }
+    } else {
+      // the draft row read now, one row in registers at a time
+      float qv[ITEMS];
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) qv[i] = row_item(qrow, V, i);
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) {
+        x[i] = fmaxf(x[i] - qv[i], 0.f);
+        rest += x[i];
+      }
     }
     rest_sum = block_sum(rest, redv);
   }
-  float ev[ITEMS];
-  const auto re = row_resource(erow, V);
+  if constexpr (!QLDS) {
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) ev[i] = row_load(re, tid + i * kT);
+    for (int i = 0; i < ITEMS; ++i) ev[i] = row_item(erow, V, i);
+  }
+  // each thread's entries in index order: the first of its largest values
+  // wins (a NaN never does), as arg_better's order across threads has it
   float cv = kNegInfS;
   int ci = INT_MAX;
   const float rinv = 1.f / rest_sum;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    const int v = tid + i * kT;
-    if (v < V) arg_better(cv, ci, (draft_pos ? div_by(x[i], rest_sum, rinv) : x[i]) / ev[i], v);
+    const float c = (draft_pos ? div_by(x[i], rest_sum, rinv) : x[i]) / ev[i];
+    if (c > cv) {
+      cv = c;
+      ci = tid + i * kT;
+    }
   }
   const int drawn = block_argmax(cv, ci, redv, redi);
   if (tid == 0) {
@@ -316,17 +463,20 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
     stats.best[idx] = -1;  // the raw argmax: greedy decisions only
     // a residual with no mass has no draw (the reference's multinomial raises)
     stats.cand[idx] = (!(draft_pos && !(rest_sum > 0.f)) && drawn >= 0 && drawn < V) ? drawn : -1;
-    int keep = 0;
-    if (j < n) {
-      const int64_t d = drafts[b * db + j];
+    if constexpr (!QLDS) {
+      int keep = 0;
       if (d >= 0 && d < V) {
         const float sd = load_f32(row + d) / temperature;
-        const float pd = sd >= thr ? expf(sd - m) * (1.f / z) : 0.f;
-        keep = u[(int64_t)b * L + j] * q[b * qb + j * qt + d] < pd;
+        const float pdg = sd >= thr ? exp_nonpos(sd - m) * zinv : 0.f;
+        keep = u[(int64_t)b * L + j] * q[b * qb + j * qt + d] < pdg;
       }
+      stats.keep[idx] = keep;
+    } else if (!(d >= 0 && d < V)) {
+      stats.keep[idx] = 0;
     }
-    stats.keep[idx] = keep;
   }
+  // the same p as exp(s_d - m) * (1 / z) of the draft's score: the decision u * q[d] < p[d]
+  if (owner) stats.keep[idx] = u[(int64_t)b * L + j] * qs[d] < pd;
 }
 
 // Each row's tokens from the per-position decisions: the drafts up to the
@@ -339,14 +489,44 @@ __global__ __launch_bounds__(64) void accept_pick(const int64_t* __restrict__ dr
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
   const int P = L + 1;
+  const int* drawn_at = greedy ? stats.best : stats.cand;
+  constexpr int kMaxP = 16;
+  if (P <= kMaxP) {
+    // every load of the row at once (one memory round trip), then the choice in registers
+    int keep[kMaxP], drawn[kMaxP];
+    int64_t draft[kMaxP];
+    const int given = lengths ? lengths[b] : L;
+    // indices clamped into the row: the loads need no branches; entries past
+    // P (or L) are never chosen
+#pragma unroll
+    for (int t = 0; t < kMaxP; ++t) {
+      keep[t] = stats.keep[b * P + min(t, P - 1)];
+      drawn[t] = drawn_at[b * P + min(t, P - 1)];
+      draft[t] = L > 0 ? drafts[b * db + min(t, L - 1)] : -1;
+    }
+    const int n = min(max(given, 0), L);
+    int js = n;  // the first rejected draft, n when every draft is kept
+#pragma unroll
+    for (int t = 0; t < kMaxP; ++t)
+      if (t < n && js == n && !keep[t]) js = t;
+    int pick = -1;
+#pragma unroll
+    for (int t = 0; t < kMaxP; ++t)
+      if (t == js) pick = drawn[t];
+#pragma unroll
+    for (int t = 0; t < kMaxP; ++t)
+      if (t < P) tokens[(int64_t)b * P + t] = t < js ? draft[t] : (t == js ? pick : -1);
+    n_tokens[b] = pick >= 0 ? js + 1 : -1;
+    return;
+  }
   const int n = lengths ? min(max(lengths[b], 0), L) : L;
   int js = n;  // the first rejected draft, n when every draft is kept (independent loads, not a chain)
   for (int t = n - 1; t >= 0; --t)
     if (!stats.keep[b * P + t]) js = t;
   for (int t = 0; t < P; ++t) tokens[(int64_t)b * P + t] = t < js ? drafts[b * db + t] : -1;
-  const int drawn = greedy ? stats.best[b * P + js] : stats.cand[b * P + js];
-  tokens[(int64_t)b * P + js] = drawn;
-  n_tokens[b] = drawn >= 0 ? js + 1 : -1;
+  const int pick = drawn_at[b * P + js];
+  tokens[(int64_t)b * P + js] = pick;
+  n_tokens[b] = pick >= 0 ? js + 1 : -1;
 }
 
 // Greedy walk down a draft tree: node i's parent parents[i] < i, the root 0.
@@ -415,16 +595,37 @@ int items_for(int V) {
     default: CALL(64); break;                   \
   }
 
+// One workgroup per (batch row, position): 8 ceil(B / 8) (L + 1) of them,
+// those past B returning at once.
 template <typename S>
-void launch_stats(dim3 grid, hipStream_t stream, const void* scores, int64_t sb, int64_t st, const int32_t* firsts,
+void launch_stats(int B, hipStream_t stream, const void* scores, int64_t sb, int64_t st, const int32_t* firsts,
                   const float* q, int64_t qb, int64_t qt, const int64_t* drafts, int64_t db, const int32_t* lengths,
                   const float* u, const float* e, float temperature, int top_k, int greedy, int L, int V, Stats s) {
   const S* rows = static_cast<const S*>(scores);
-#define WPTV_STATS(I)                                                                                             \
-  hipLaunchKernelGGL((accept_stats<I, S>), grid, dim3(kT), 0, stream, rows, sb, st, firsts, q, qb, qt, drafts, db, \
-                     lengths, u, e, temperature, top_k, greedy, L, V, s)
+  const dim3 grid(8 * ((B + 7) / 8) * (L + 1));
+  // the draft rows through LDS when every row is 16-byte aligned and fits
+  const bool qlds = !greedy && q && V <= 32 * kT && V % 4 == 0 && aligned(q, 16) && qb % 4 == 0 && qt % 4 == 0;
+  const bool cut = !greedy && top_k > 0 && top_k < V;
+#define WPTV_STATS_Q(I, QL, CU)                                                                                  \
+  hipLaunchKernelGGL((accept_stats<I, S, QL, CU>), grid, dim3(kT), 0, stream, rows, sb, st, firsts, q, qb, qt,     \
+                     drafts, db, lengths, u, e, temperature, top_k, greedy, B, L, V, s)
+#define WPTV_STATS_C(I, QL)            \
+  if (cut) WPTV_STATS_Q(I, QL, true);  \
+  else WPTV_STATS_Q(I, QL, false);
+#define WPTV_STATS(I)                  \
+  if constexpr (I <= 32) {             \
+    if (qlds) {                        \
+      WPTV_STATS_C(I, true)            \
+    } else {                           \
+      WPTV_STATS_C(I, false)           \
+    }                                  \
+  } else {                             \
+    WPTV_STATS_C(I, false)             \
+  }
   WPTV_ITEMS(V, WPTV_STATS)
 #undef WPTV_STATS
+#undef WPTV_STATS_C
+#undef WPTV_STATS_Q
 }
 
 }  // namespace
@@ -460,7 +661,7 @@ extern "C" int wptv_accept(const void* scores, int64_t scores_stride_b, int64_t 
     return fail(WPTV_E_INVALID, "accept: workspace of %zu bytes, %zu needed", workspace_bytes, stats_bytes(B, L + 1));
   const Stats s = carve(workspace, B, L + 1);
   (scores_dtype == WPTV_BF16 ? launch_stats<unsigned short> : launch_stats<float>)(
-      dim3(L + 1, B), stream, scores, scores_stride_b, scores_stride_t, firsts, q, q_stride_b, q_stride_t, drafts,
+      B, stream, scores, scores_stride_b, scores_stride_t, firsts, q, q_stride_b, q_stride_t, drafts,
       drafts_stride_b, lengths, u, e, temperature, top_k, greedy, L, V, s);
   int st = launched("accept_stats");
   if (st != WPTV_OK) return st;
@@ -485,7 +686,7 @@ extern "C" int wptv_greedy_tree(const void* scores, int64_t scores_stride_b, int
   const Stats s = carve(workspace, B, M);
   // per-node argmax: the stats pass in greedy mode over M positions with no drafts to judge
   (scores_dtype == WPTV_BF16 ? launch_stats<unsigned short> : launch_stats<float>)(
-      dim3(M, B), stream, scores, scores_stride_b, scores_stride_t, nullptr, nullptr, 0, 0, nullptr, 0, nullptr,
+      B, stream, scores, scores_stride_b, scores_stride_t, nullptr, nullptr, 0, 0, nullptr, 0, nullptr,
       nullptr, nullptr, 1.f, 0, 1, M - 1, V, s);
   int st = launched("accept_stats");
   if (st != WPTV_OK) return st;
