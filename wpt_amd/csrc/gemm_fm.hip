@@ -12,10 +12,14 @@
 // contiguous memory, straight into registers: no LDS staging, no barrier in
 // the main loop.
 //
-// One workgroup of four wavefronts per 16 NB output columns and one part of
-// K ("split"); its wavefronts share out the part's 32-wide k-steps (wave w
-// takes k-steps w, w + 4, ...), each multiplying all M rows (MB 16-row
-// blocks) by the NB column blocks:
+// One workgroup of four wavefronts per 16 NB output columns, one part of K
+// ("split") and one group of MB row blocks (all of them, or at 160 rows each
+// half: 80 rows by twice the columns, which moves less of X and W through
+// each compute unit for the same workgroup count: measured on the MI355X with
+// cold weights, q/k/v 6.4 against 7.2 us, output 5.7 against 5.9, down 10.9
+// against 12.2, gate/up 18.9 against 20.0); its wavefronts share out the
+// part's 32-wide k-steps (wave w takes k-steps w, w + 4, ...), each
+// multiplying the group's rows by the NB column blocks:
 //
 //   C^T[n, m] += W[n, k] . X^T[k, m]    W as the A operand, so lane (j, g)
 //                                      ends with columns 4g .. 4g + 3 of row j
@@ -60,24 +64,25 @@ __device__ __forceinline__ unsigned short fm_swiglu_bf16(float g, float u) {
   return f32_to_bf16(gb / (1.f + expf(-gb)) * ub);
 }
 
-// grid (N / (16 NB), splits); split z takes k-steps [4 STEPS z, 4 STEPS (z + 1)).
-// x: MB row blocks; w: NBT = N / 16 row blocks.  OUT kFmParts: part[z][m][n]
-// FP32; kFmSwiGLU (NB = 4, one split): blocks 0, 1 of a column tile are the
-// gate rows of features 32 tile .. + 31, blocks 2, 3 their up rows; out holds
-// silu(g) * u [M, N / 2] in the fm layout with MB row blocks.
+// grid (N / (16 NB), splits, RBT / MB); split z takes k-steps [4 STEPS z, 4
+// STEPS (z + 1)), row group rg the row blocks [MB rg, MB (rg + 1)).  x: RBT
+// row blocks; w: NBT = N / 16 row blocks.  OUT kFmParts: part[z][m][n] FP32;
+// kFmSwiGLU (NB a multiple of 4, one split): each 4 blocks of a column tile
+// are the gate rows of 32 features (2 blocks) then their up rows (2 blocks);
+// out holds silu(g) * u [M, N / 2] in the fm layout with RBT row blocks.
 template <int MB, int NB, int STEPS, int OUT>
 __global__ __launch_bounds__(kFmWaves * 64, 1) void gemm_fm(const u32x4* __restrict__ x, const u32x4* __restrict__ w,
-                                                            int NBT, int M, int N, void* __restrict__ out) {
-  static_assert(OUT != kFmSwiGLU || NB == 4, "the SwiGLU epilogue pairs two gate and two up blocks");
+                                                            int NBT, int RBT, int M, int N, void* __restrict__ out) {
+  static_assert(OUT != kFmSwiGLU || NB % 4 == 0, "the SwiGLU epilogue pairs two gate and two up blocks");
   constexpr int R = MB * NB * 4;  // accumulator registers per lane
   __shared__ float red[kFmWaves * R * 64];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = blockIdx.x, z = blockIdx.y;
+  const int tile = blockIdx.x, z = blockIdx.y, rb0 = blockIdx.z * MB;
   const int ks0 = z * kFmWaves * STEPS + wv;
   const u32x4* wp = w + ((int64_t)ks0 * NBT + tile * NB) * 64 + lane;
-  const u32x4* xp = x + (int64_t)ks0 * MB * 64 + lane;
-  const int64_t wstep = (int64_t)kFmWaves * NBT * 64, xstep = (int64_t)kFmWaves * MB * 64;
+  const u32x4* xp = x + ((int64_t)ks0 * RBT + rb0) * 64 + lane;
+  const int64_t wstep = (int64_t)kFmWaves * NBT * 64, xstep = (int64_t)kFmWaves * RBT * 64;
 
   f32x4 acc[MB][NB];
 #pragma unroll
@@ -129,7 +134,7 @@ __global__ __launch_bounds__(kFmWaves * 64, 1) void gemm_fm(const u32x4* __restr
   if constexpr (OUT == kFmParts) {
     for (int p = wv; p < MB * NB; p += kFmWaves) {
       const int rb = p / NB, nb = p % NB;
-      const int m = rb * 16 + j;
+      const int m = (rb0 + rb) * 16 + j;
       if (m >= M) continue;
       const f32x4 v = {summed(p, 0), summed(p, 1), summed(p, 2), summed(p, 3)};
       *reinterpret_cast<f32x4*>(static_cast<float*>(out) + ((int64_t)z * M + m) * N + tile * NB * 16 + nb * 16 +
@@ -137,15 +142,18 @@ __global__ __launch_bounds__(kFmWaves * 64, 1) void gemm_fm(const u32x4* __restr
     }
   } else {
     typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
-    for (int p = wv; p < MB * 2; p += kFmWaves) {
-      const int rb = p >> 1, nb = p & 1;
-      const int m = rb * 16 + j;
+    // output block p: row block rb, gate block gb (of the tile's NB / 2), feature column 16 gb + 4 g
+    constexpr int kOutBlocks = NB / 2;
+    for (int p = wv; p < MB * kOutBlocks; p += kFmWaves) {
+      const int rb = p / kOutBlocks, gb = p % kOutBlocks;
+      const int m = (rb0 + rb) * 16 + j;
       if (m >= M) continue;
+      const int nb = 4 * (gb >> 1) + (gb & 1);  // the gate block; its up block is nb + 2
       const int pg = rb * NB + nb, pu = pg + 2;
       u16x4 res;
 #pragma unroll
       for (int i = 0; i < 4; ++i) res[i] = fm_swiglu_bf16(summed(pg, i), summed(pu, i));
-      *reinterpret_cast<u16x4*>(static_cast<unsigned short*>(out) + fm_offset(m, tile * 32 + nb * 16 + 4 * g, MB)) =
+      *reinterpret_cast<u16x4*>(static_cast<unsigned short*>(out) + fm_offset(m, tile * 8 * NB + gb * 16 + 4 * g, RBT)) =
           res;
     }
   }
@@ -162,6 +170,7 @@ bool fm_steps_built(int s) {
 
 struct FmPlan {
   int mb, nb, splits, steps;
+  int groups;  // row groups: 2 (80 rows by 2 nb column blocks each) at 160 rows, else 1
   size_t bytes;
 };
 
@@ -202,6 +211,12 @@ int fm_plan(int M, int N, int K, bool swiglu, int requested, FmPlan* p) {
   }
   p->mb = fm_row_blocks(M);
   p->nb = nb;
+  p->groups = 1;
+  if (p->mb == 10 && N % (32 * nb) == 0) {  // the same workgroups, squarer tiles
+    p->mb = 5;
+    p->nb = 2 * nb;
+    p->groups = 2;
+  }
   p->splits = s;
   p->steps = quarter / s;
   p->bytes = swiglu ? 0 : align_up((size_t)s * M * N * sizeof(float), 256);
@@ -209,12 +224,13 @@ int fm_plan(int M, int N, int K, bool swiglu, int requested, FmPlan* p) {
 }
 
 template <int MB, int NB, int OUT>
-int launch_fm_steps(int steps, dim3 grid, hipStream_t stream, const void* x, const void* w, int NBT, int M, int N,
-                    void* out) {
+int launch_fm_steps(int steps, dim3 grid, hipStream_t stream, const void* x, const void* w, int NBT, int RBT, int M,
+                    int N, void* out) {
   const auto* xv = static_cast<const u32x4*>(x);
   const auto* wv = static_cast<const u32x4*>(w);
-#define WPTV_FM(SS) \
-  hipLaunchKernelGGL((gemm_fm<MB, NB, SS, OUT>), grid, dim3(kFmWaves * 64), 0, stream, xv, wv, NBT, M, N, out)
+#define WPTV_FM(SS)                                                                                                \
+  hipLaunchKernelGGL((gemm_fm<MB, NB, SS, OUT>), grid, dim3(kFmWaves * 64), 0, stream, xv, wv, NBT, RBT, M, N, \
+                     out)
   switch (steps) {
     case 2: WPTV_FM(2); break;
     case 4: WPTV_FM(4); break;
@@ -229,14 +245,18 @@ int launch_fm_steps(int steps, dim3 grid, hipStream_t stream, const void* x, con
 
 template <int NB, int OUT>
 int launch_fm(const FmPlan& p, hipStream_t stream, const void* x, const void* w, int M, int N, void* out) {
-  dim3 grid(N / (16 * NB), p.splits);
-  const int NBT = N / 16;
+  const int NBT = N / 16, RBT = fm_row_blocks(M);
+  if (p.groups == 2) {  // two groups of 5 row blocks, 2 NB column blocks a tile
+    const dim3 grid(N / (32 * NB), p.splits, 2);
+    return launch_fm_steps<5, 2 * NB, OUT>(p.steps, grid, stream, x, w, NBT, RBT, M, N, out);
+  }
+  const dim3 grid(N / (16 * NB), p.splits, 1);
   switch (p.mb) {
-    case 2: return launch_fm_steps<2, NB, OUT>(p.steps, grid, stream, x, w, NBT, M, N, out);
-    case 4: return launch_fm_steps<4, NB, OUT>(p.steps, grid, stream, x, w, NBT, M, N, out);
-    case 6: return launch_fm_steps<6, NB, OUT>(p.steps, grid, stream, x, w, NBT, M, N, out);
-    case 8: return launch_fm_steps<8, NB, OUT>(p.steps, grid, stream, x, w, NBT, M, N, out);
-    default: return launch_fm_steps<10, NB, OUT>(p.steps, grid, stream, x, w, NBT, M, N, out);
+    case 2: return launch_fm_steps<2, NB, OUT>(p.steps, grid, stream, x, w, NBT, RBT, M, N, out);
+    case 4: return launch_fm_steps<4, NB, OUT>(p.steps, grid, stream, x, w, NBT, RBT, M, N, out);
+    case 6: return launch_fm_steps<6, NB, OUT>(p.steps, grid, stream, x, w, NBT, RBT, M, N, out);
+    case 8: return launch_fm_steps<8, NB, OUT>(p.steps, grid, stream, x, w, NBT, RBT, M, N, out);
+    default: return launch_fm_steps<10, NB, OUT>(p.steps, grid, stream, x, w, NBT, RBT, M, N, out);
   }
 }
 
