@@ -76,7 +76,8 @@ const char* wptv_last_error(void);
  *   positions  [B, T] int64: query t of row b sees table rows
  *              max(0, p - window + 1) .. min(p, N - 1), p = positions[b, t]
  *              (window <= 0: from row 0).  A padding query past the table
- *              reads up to its last row.
+ *              reads up to its last row.  NULL with a tree: query t of row
+ *              b is node t, at position tree_base[b] + t.
  *   tree_base, tree_ancestors  NULL, or [B] int64 and [T] uint64: rows
  *              r >= tree_base[b] are draft-tree nodes, and query t sees node
  *              r - tree_base[b] only where that bit of tree_ancestors[t] is

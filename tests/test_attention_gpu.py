@@ -128,6 +128,13 @@ def test_a_small_tree_on_both_mfma_kernels(device):
     masks = kernels.tree_ancestors(parents).to(device)
     got = kernels.verify_attention(qd, kd, vd, positions, c ** -0.5, tree=(bd, masks), key_split=True)
     assert relative_error(got.cpu(), expected) < 1e-2
+    # the positions given, or formed by the kernel as tree_base + node: the same bits on every kernel
+    for form in ({}, {"key_split": True}, {"generic": True}):
+        given = kernels.verify_attention(qd, kd, vd, positions, c ** -0.5, tree=(bd, masks), **form)
+        formed = kernels.verify_attention(qd, kd, vd, None, c ** -0.5, tree=(bd, masks), **form)
+        assert torch.equal(given, formed)
+    with pytest.raises(ValueError):
+        kernels.verify_attention(qd, kd, vd, None, c ** -0.5)  # no positions and no tree
 
 
 @pytest.mark.parametrize("with_sink", [False, True])

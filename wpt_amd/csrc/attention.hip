@@ -49,8 +49,20 @@ struct Bounds {
 };
 
 // The key rows query position t of batch row b sees, before the tree mask.
-__device__ __forceinline__ Bounds query_bounds(const int64_t* __restrict__ pos_b, int t, int window, int N) {
-  const int64_t p = pos_b[t];
+// A batch row's query positions: p[t], or (a draft tree given without
+// positions) node t at base + t.
+struct QueryPos {
+  const int64_t* p;
+  int64_t base;
+  __device__ __forceinline__ int64_t at(int t) const { return p ? p[t] : base + t; }
+};
+
+__device__ __forceinline__ QueryPos query_pos(const int64_t* positions, const int64_t* tree_base, int b, int T) {
+  return positions ? QueryPos{positions + (int64_t)b * T, 0} : QueryPos{nullptr, tree_base[b]};
+}
+
+__device__ __forceinline__ Bounds query_bounds(const QueryPos& pos_b, int t, int window, int N) {
+  const int64_t p = pos_b.at(t);
   int64_t hi = p < (int64_t)N - 1 ? p : (int64_t)N - 1;
   int64_t lo = window > 0 ? p - window + 1 : 0;
   if (lo < 0) lo = 0;
@@ -276,7 +288,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   const int grp = unit % groups;
   const int R = T * H;
   const int r_base = grp * kRows;
-  const int64_t* pos_b = positions + (int64_t)b * T;
+  const QueryPos pos_b = query_pos(positions, tree_base, b, T);
 
   // The key rows this workgroup's queries can see.
   int u_lo = 0, u_hi = N - 1;
@@ -931,7 +943,7 @@ __global__ __launch_bounds__(kKeyWaves * 64, 1) void verify_attention_keys(
     }
   }
   const int R = T * H;
-  const int64_t* pos_b = positions + (int64_t)b * T;
+  const QueryPos pos_b = query_pos(positions, tree_base, b, T);
   // DMA lane roles: lane l fills row rr of a piece (kRowsPerLoad whole rows), 16-byte position p.
   const int rr = lane / G::kChunks, p = lane % G::kChunks;
 
@@ -1348,7 +1360,7 @@ __global__ __launch_bounds__(64) void attention_generic(
   const int b = blockIdx.y;
   const int64_t row = ((int64_t)b * T_ + t) * H + h;
   const T* qrow = q + row * C;
-  const int64_t* pos_b = positions + (int64_t)b * T_;
+  const QueryPos pos_b = query_pos(positions, tree_base, b, T_);
 
   // Rows visited: the chosen rows idx[b, t, :] (K of them, -1 = none), then
   // the rows max(0, p - window + 1) .. min(p, N - 1) (the sparse form's
@@ -1562,8 +1574,8 @@ int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
            const uint64_t* tree_ancestors, const float* sink, int B, int T, int H, int c, int N, float scale,
            int splits, int flags, RowMap rows, int64_t phys_rows, OutGate gate, void* out, float* lse,
            void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  if (!q || !k || !v || !positions || !out)
-    return fail(WPTV_E_INVALID, "verify_attention: q, k, v, positions and out must be given");
+  if (!q || !k || !v || !out || !(positions || tree_base))
+    return fail(WPTV_E_INVALID, "verify_attention: q, k, v, out and positions (or a tree) must be given");
   if ((tree_base == nullptr) != (tree_ancestors == nullptr))
     return fail(WPTV_E_INVALID, "verify_attention: tree_base and tree_ancestors go together");
   if (k_stride_n < c || v_stride_n < c)

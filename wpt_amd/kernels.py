@@ -68,7 +68,7 @@ def _check_inputs(q, k, v, positions):
         raise KernelUnavailable(f"the HIP attention runs on a GPU; q is on {q.device}")
     if k.stride(2) != 1 or v.stride(2) != 1:
         raise ValueError("each row of k and v must be contiguous")
-    if tuple(positions.shape) != (B, T):
+    if positions is not None and tuple(positions.shape) != (B, T):
         raise ValueError(f"positions must be (B={B}, T={T}); got {tuple(positions.shape)}")
     if k.shape[1] == 0:
         raise ValueError("the table is empty")
@@ -85,7 +85,8 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
     sees rows max(0, p - window + 1) .. min(p, N - 1), p = positions[b, t]
     (window 0: from row 0), and with tree = (tree_base (B,), ancestors (T,)
     int64 bit masks) a row r >= tree_base[b] only where bit r - tree_base[b]
-    of ancestors[t] is set; sink (H,) joins each head's softmax denominator.
+    of ancestors[t] is set (positions None with a tree: query t is node t, at
+    tree_base[b] + t); sink (H,) joins each head's softmax denominator.
     Returns the output (B, T, H, c) in q's dtype, and with lse=True also the
     (B, T, H) FP32 log-sum-exp.  splits: key-range parts per batch row (0:
     the library chooses); generic: the wave-per-query kernel; from_positions:
@@ -100,7 +101,9 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
     library = _lib.lib()
     dtype = _lib.dtype_code(q.dtype)
     q_ = q.contiguous()
-    positions_ = _long(positions, device)
+    if positions is None and tree is None:
+        raise ValueError("positions are needed unless a tree gives them")
+    positions_ = None if positions is None else _long(positions, device)
     if out_fm and (static_scratch or q.dtype != torch.bfloat16):
         raise ValueError("the fm output layout takes bf16 queries and the workspace entry point")
     sink_ = None if sink is None else sink.to(device=device, dtype=torch.float32).contiguous()
@@ -309,14 +312,13 @@ def tree_attention(q, k, v, tree_base, parents, scale, sink=None):
     row tree_base[b] + i) over the prefix rows before tree_base[b] and over
     the node's ancestors and itself: the reference's dense_attention
     (attention.py:74-82) with the mask "prefix plus ancestors-or-self"."""
-    B, M = q.shape[:2]
     base = tree_base.to(device=q.device, dtype=torch.long)
-    positions = base[:, None] + torch.arange(M, device=q.device)
     key = (tuple(int(p) for p in parents), q.device)
     masks = _TREES.get(key)
     if masks is None:  # made once per tree and device, outside any graph capture
         masks = _TREES[key] = tree_ancestors(parents).to(q.device)
-    return verify_attention(q, k, v, positions, scale, sink=sink, tree=(base, masks))
+    # node i's position, tree_base[b] + i, is formed by the kernel
+    return verify_attention(q, k, v, None, scale, sink=sink, tree=(base, masks))
 
 
 _TREES = {}  # (parents, device) -> the ancestors-or-self masks on the device
