@@ -126,12 +126,11 @@ def decoder_step(B, kv, k, steps, warmup, temperature=0.8, top_k=None, seed=0, k
     logits = torch.randn(B, k, config.vocab, generator=generator, device=device)
     step.q.copy_(torch.softmax(logits, -1))
     step.feeds[:, 1:] = torch.multinomial(step.q.reshape(-1, config.vocab), 1, generator=generator).reshape(B, k)
-    written = torch.zeros(B, dtype=torch.long, device=device)
-    step.run = _counting(step.run, written)
     step.capture(warmup=1)
     for _ in range(warmup):
         step.replay()
     torch.cuda.synchronize()
+    written = step.written  # the step's own running counts (kept by its next_feeds kernel)
     written.zero_()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
@@ -218,15 +217,6 @@ def drafted_writer(model, B, kv, k, rounds=8, warmup=2, seed=0):
                         "markov_rank": config.markov_rank},
             "note": "eager Writer rounds (host lists, one synchronization per round), the reference's protocol; "
                     "the captured verify step alone is the headline"}
-
-
-def _counting(run, written):
-    def counted():
-        tokens, counts = run()
-        written.add_(counts.long())
-        return tokens, counts
-
-    return counted
 
 
 # ---------------------------------------------------------------------------
@@ -324,20 +314,22 @@ def tree_c4(steps, warmup):
     base = torch.full((B,), prefix, device=device)
     written = torch.zeros(B, dtype=torch.long, device=device)
 
-    def step():
+    def step(count=False):
         o = kernels.tree_attention(q, table[..., :c], table[..., c:], base, parents, c ** -0.5)
         scores = head_product(o.reshape(B, M, H * c), head)  # bf16 logits, read by the sampler as they come
         _, _, counts = sampling.greedy_tree(scores, node_tokens, parents)
-        written.add_(counts.long())
+        if count:  # counted in a graph of its own, outside the timed one
+            written.add_(counts.long())
 
     replay = graphed(step)
     ms = timed(replay, steps, warmup)
+    counted = graphed(lambda: step(count=True))
     # eight back-to-back calls per graph replay, so that the graph's own launch is not timed
     attn = graphed(lambda: [kernels.tree_attention(q, table[..., :c], table[..., c:], base, parents, c ** -0.5)
                             for _ in range(8)])
     attn_ms = timed(attn, steps, warmup) / 8
     written.zero_()
-    replay()
+    counted()
     torch.cuda.synchronize()
     per_step = int(written.sum())
     attn_flops = 4 * B * M * H * c * (prefix + M)

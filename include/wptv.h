@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define WPTV_ABI_VERSION 4
+#define WPTV_ABI_VERSION 5
 
 enum {
   WPTV_OK = 0,
@@ -227,9 +227,12 @@ int wptv_cache_lengths(int64_t* lengths, int64_t* before, const void* counts, in
  *   tokens[b * tokens_stride + min(counts[b], width) - 1].  A row with
  *   counts[b] < 1 (the sampler had no mass to draw from, where the
  *   reference's multinomial raises, __init__.py:219) keeps its pending token
- *   and sets *failed = 1 when failed is not NULL (the caller clears it). */
+ *   and sets *failed = 1 when failed is not NULL (the caller clears it).
+ *   written: NULL, or [B] int64 running counts: written[b] += counts[b] for
+ *   a row that wrote (the accepted tokens a serving loop reports, counted
+ *   without a kernel of its own). */
 int wptv_next_feeds(const int64_t* tokens, int64_t tokens_stride, const int* counts, int64_t* feeds,
-                    int64_t feeds_stride, int B, int width, int* failed, hipStream_t stream);
+                    int64_t feeds_stride, int B, int width, int* failed, int64_t* written, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * The decoder layer's memory-bound steps around its matrix products (the

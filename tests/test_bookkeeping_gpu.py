@@ -61,12 +61,14 @@ def test_the_next_pending_token_is_the_last_written(device):
     counts = torch.tensor([4, 1, 2], dtype=torch.int32, device=device)
     feeds = torch.zeros(3, 4, dtype=torch.long, device=device)
     failed = torch.zeros(1, dtype=torch.int32, device=device)
-    next_feeds(tokens, counts, feeds, failed)
+    written = torch.tensor([5, 0, 2], device=device)
+    next_feeds(tokens, counts, feeds, failed, written)
     assert feeds[:, 0].tolist() == [14, 21, 32] and not feeds[:, 1:].any() and int(failed) == 0
+    assert written.tolist() == [9, 1, 4]
     # a row the sampler could not draw for (-1) keeps its pending token and raises the flag
     feeds[:, 0] = torch.tensor([7, 8, 9], device=device)
-    next_feeds(tokens, torch.tensor([-1, 1, 0], dtype=torch.int32, device=device), feeds, failed)
-    assert feeds[:, 0].tolist() == [7, 21, 9] and int(failed) == 1
+    next_feeds(tokens, torch.tensor([-1, 1, 0], dtype=torch.int32, device=device), feeds, failed, written)
+    assert feeds[:, 0].tolist() == [7, 21, 9] and int(failed) == 1 and written.tolist() == [9, 2, 4]
 
 
 def test_host_ids_outside_the_vocabulary_raise(device):

@@ -58,7 +58,8 @@ __global__ __launch_bounds__(64) void cache_lengths(int64_t* __restrict__ length
 // token and raises *failed (when given) for the host to report.
 __global__ __launch_bounds__(64) void next_feeds(const int64_t* __restrict__ tokens, int64_t tokens_stride,
                                                  const int* __restrict__ counts, int64_t* __restrict__ feeds,
-                                                 int64_t feeds_stride, int B, int width, int* __restrict__ failed) {
+                                                 int64_t feeds_stride, int B, int width, int* __restrict__ failed,
+                                                 int64_t* __restrict__ written) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
   const int n = counts[b];
@@ -67,6 +68,7 @@ __global__ __launch_bounds__(64) void next_feeds(const int64_t* __restrict__ tok
     return;
   }
   feeds[(int64_t)b * feeds_stride] = tokens[(int64_t)b * tokens_stride + min(n, width) - 1];
+  if (written) written[b] += n;
 }
 
 // Byte-wise form for rows whose size or strides are not multiples of 16 bytes.
@@ -144,12 +146,13 @@ extern "C" int wptv_cache_lengths(int64_t* lengths, int64_t* before, const void*
 }
 
 extern "C" int wptv_next_feeds(const int64_t* tokens, int64_t tokens_stride, const int* counts, int64_t* feeds,
-                               int64_t feeds_stride, int B, int width, int* failed, hipStream_t stream) {
+                               int64_t feeds_stride, int B, int width, int* failed, int64_t* written,
+                               hipStream_t stream) {
   if (!tokens || !counts || !feeds) return fail(WPTV_E_INVALID, "next_feeds: every pointer must be given");
   if (B < 0 || width <= 0 || tokens_stride < width)
     return fail(WPTV_E_INVALID, "next_feeds: bad shape B=%d width=%d stride=%lld", B, width, (long long)tokens_stride);
   if (B == 0) return WPTV_OK;
   hipLaunchKernelGGL(next_feeds, dim3((unsigned)((B + 63) / 64)), dim3(64), 0, stream, tokens, tokens_stride, counts,
-                     feeds, feeds_stride, B, width, failed);
+                     feeds, feeds_stride, B, width, failed, written);
   return launched("next_feeds");
 }

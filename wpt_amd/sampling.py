@@ -75,7 +75,9 @@ def accept(scores, q, drafts, u, e, temperature=0.8, top_k=40, lengths=None, fir
         raise ValueError(f"drafts must be (B={B}, L); got {tuple(drafts.shape)}")
     L = drafts.shape[1]
     device = scores.device
-    drafts = drafts.to(device=device, dtype=torch.long).contiguous()
+    drafts = drafts.to(device=device, dtype=torch.long)
+    if drafts.stride(1) != 1:  # rows of drafts are read with their own stride
+        drafts = drafts.contiguous()
     if not greedy:
         q = _rows_last_contiguous(q, "q", 3)
         if q.shape != (B, L, V):

@@ -27,18 +27,21 @@ from . import _lib, sampling
 from ._lib import check, ptr
 
 
-def next_feeds(tokens, counts, feeds, failed=None):
+def next_feeds(tokens, counts, feeds, failed=None, written=None):
     """feeds[:, 0] = each row's last written token, tokens[b, counts[b] - 1]
     (tokens (B, L + 1) int64, counts (B,) int32), on the device; a row with
     no token written keeps its feed and sets failed (an int32 device flag,
-    when given) to 1."""
+    when given) to 1.  written (B,) int64, when given: written[b] +=
+    counts[b] for each row that wrote."""
     B, width = tokens.shape
     if counts.dtype != torch.int32 or counts.shape != (B,) or feeds.shape[0] != B or feeds.dtype != torch.int64:
         raise ValueError("tokens (B, L + 1) int64, counts (B,) int32 and feeds (B, n) int64")
     if failed is not None and (failed.dtype != torch.int32 or failed.numel() < 1):
         raise ValueError("failed must be an int32 device tensor")
+    if written is not None and (written.dtype != torch.int64 or written.shape != (B,) or not written.is_contiguous()):
+        raise ValueError("written must be a contiguous (B,) int64 device tensor")
     check(_lib.lib().wptv_next_feeds(ptr(tokens), tokens.stride(0), ptr(counts), ptr(feeds), feeds.stride(0), B, width,
-                                     ptr(failed), _lib.stream(tokens.device)), "next_feeds")
+                                     ptr(failed), ptr(written), _lib.stream(tokens.device)), "next_feeds")
 
 
 class VerifyStep:
@@ -53,6 +56,7 @@ class VerifyStep:
         self.u = torch.zeros(B, k, device=device) if given_tape else None
         self.e = torch.ones(B, V, device=device) if given_tape else None
         self.failed = torch.zeros(1, dtype=torch.int32, device=device)
+        self.written = torch.zeros(B, dtype=torch.long, device=device)  # tokens each row has written, running
         self.graph = None
         self.tokens = self.counts = self.scores = None
 
@@ -68,7 +72,8 @@ class VerifyStep:
                 self.u, self.e = sampling.draws(B, self.k, V, device=scores.device)
             tokens, counts = sampling.accept(scores, self.q, drafts, self.u, self.e, self.temperature, self.top_k)
         self.model.undo(self.cache, counts)
-        next_feeds(tokens, counts, self.feeds, self.failed)  # the drawn token is each row's next pending token
+        # the drawn token is each row's next pending token; the running counts grow
+        next_feeds(tokens, counts, self.feeds, self.failed, self.written)
         self.tokens, self.counts, self.scores = tokens, counts, scores
         return tokens, counts
 
