@@ -703,6 +703,9 @@ def main():
     parser.add_argument("--wpt-layers", action="store_true",
                         help="only the WPT attention layers at the verify shape (exact + choice, sparse, window); "
                              "prints their JSON")
+    parser.add_argument("--tree", action="store_true",
+                        help="only the tree workload (batch 16, 8192 prefix rows, 31 nodes, lm_head, greedy walk); "
+                             "prints its JSON")
     parser.add_argument("--pmc-workload", action="store_true",
                         help="for a counter pass: five verify-attention calls of the roofline shape, then five "
                              "plain 64 MiB device copies (the counters' calibration); prints no JSON")
@@ -712,6 +715,9 @@ def main():
         return
     if args.wpt_layers:
         print(json.dumps(wpt_layers(args.steps, args.warmup)), flush=True)
+        return
+    if args.tree:
+        print(json.dumps(tree_c4(args.steps, args.warmup)), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the verify step here is built and timed on a single MI355X "
