@@ -126,6 +126,7 @@ def decoder_step(B, kv, k, steps, warmup, temperature=0.8, top_k=None, seed=0, k
     logits = torch.randn(B, k, config.vocab, generator=generator, device=device)
     step.q.copy_(torch.softmax(logits, -1))
     step.feeds[:, 1:] = torch.multinomial(step.q.reshape(-1, config.vocab), 1, generator=generator).reshape(B, k)
+    torch.cuda.manual_seed(seed + 2)  # the tape's draws come from the device's default generator: seeded
     step.capture(warmup=1)
     for _ in range(warmup):
         step.replay()
