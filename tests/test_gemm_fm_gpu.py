@@ -50,6 +50,9 @@ def test_fm_pack_reads_back_as_the_matrix(device, R, K, blocks):
     (160, 2304, 2048),   # the exact layer's q/k/v at batch 32, k+1 = 5
     (160, 2048, 2048),   # the output projection
     (160, 2048, 5632),   # the down projection
+    (320, 2304, 2048),   # batch 64: q/k/v in row quarters
+    (320, 2048, 5632),   # batch 64: the down projection
+    (300, 2048, 2048),   # rows in the last row group only partly real
     (37, 384, 512),      # rows that are not a multiple of 16
     (5, 64, 256),        # one verify step of one row
 ])
@@ -74,7 +77,7 @@ def test_fm_parts_take_a_given_part_count(device):
         layers.linear_fm_parts(xf, M, wf, splits=3)  # 16 k-steps a wave do not split in 3
 
 
-@pytest.mark.parametrize("M, F, K", [(160, 5632, 2048), (37, 384, 256), (5, 64, 512)])
+@pytest.mark.parametrize("M, F, K", [(160, 5632, 2048), (320, 5632, 2048), (37, 384, 256), (5, 64, 512)])
 def test_fm_swiglu_is_silu_gate_times_up(device, M, F, K):
     x, w = operands(M, 2 * F, K, seed=M + F, device=device)
     tiles = layers.interleave_gate_up(w)
@@ -90,15 +93,23 @@ def test_fm_swiglu_is_silu_gate_times_up(device, M, F, K):
     assert close.float().mean() > 0.99
 
 
-def test_fm_swiglu_feeds_the_down_product(device):
+@pytest.mark.parametrize("M", [160, 320])
+def test_fm_swiglu_feeds_the_down_product(device, M):
     # the down product reads the SwiGLU output in place: parts of act . down^T
-    M, F, D = 160, 5632, 2048
+    F, D = 5632, 2048
     x, w = operands(M, 2 * F, D, seed=11, device=device)
     _, down = operands(M, D, F, seed=12, device=device)
     act = layers.linear_fm_swiglu(layers.fm_pack(x), M, layers.FmWeight(layers.interleave_gate_up(w)))
     parts = layers.linear_fm_parts(act, M, layers.FmWeight(down))
     expected = layers.fm_unpack(act, M, F).float() @ down.float().T
     assert relative_error(parts.sum(0).cpu(), expected.cpu()) < 1e-5
+
+
+def test_rows_without_a_kernel_form_have_no_plan():
+    # 161 to 288 rows (11 to 18 row blocks) and above 320: the decoder reads them on the row-major products
+    assert layers.fm_plan(200, 2048, 2048) is None and layers.fm_plan(288, 2048, 2048) is None
+    assert layers.fm_plan(321, 2048, 2048) is None
+    assert layers.fm_plan(289, 2048, 2048) is not None and layers.fm_plan(160, 2048, 2048) is not None
 
 
 def test_the_norms_write_the_same_bits_in_the_fm_layout(device):

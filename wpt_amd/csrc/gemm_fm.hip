@@ -13,13 +13,14 @@
 // the main loop.
 //
 // One workgroup of four wavefronts per 16 NB output columns, one part of K
-// ("split") and one group of MB row blocks (all of them, or at 160 rows each
-// half: 80 rows by twice the columns, which moves less of X and W through
-// each compute unit for the same workgroup count: measured on the MI355X with
-// cold weights, q/k/v 6.4 against 7.2 us, output 5.7 against 5.9, down 10.9
-// against 12.2, gate/up 18.9 against 20.0); its wavefronts share out the
-// part's 32-wide k-steps (wave w takes k-steps w, w + 4, ...), each
-// multiplying the group's rows by the NB column blocks:
+// ("split") and one group of MB row blocks (all of them up to 128 rows; at
+// 160 rows each half, 80 rows by twice the columns, which moves less of X and
+// W through each compute unit for the same workgroup count: measured on the
+// MI355X with cold weights, q/k/v 6.4 against 7.2 us, output 5.7 against 5.9,
+// down 10.9 against 12.2, gate/up 18.9 against 20.0; at 320 rows each
+// quarter, 80 rows by 128 columns, and 80 by 64 for gate/up); its wavefronts
+// share out the part's 32-wide k-steps (wave w takes k-steps w, w + 4, ...),
+// each multiplying the group's rows by the NB column blocks:
 //
 //   C^T[n, m] += W[n, k] . X^T[k, m]    W as the A operand, so lane (j, g)
 //                                      ends with columns 4g .. 4g + 3 of row j
@@ -42,7 +43,7 @@ namespace {
 
 constexpr int kFmWaves = 4;
 constexpr int kFmDepth = 2;  // k-steps a wavefront has loaded ahead while it multiplies one
-constexpr int kFmMaxRows = 160;
+constexpr int kFmMaxRows = 320;
 enum FmOut { kFmParts = 0, kFmSwiGLU = 1 };
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -170,7 +171,7 @@ bool fm_steps_built(int s) {
 
 struct FmPlan {
   int mb, nb, splits, steps;
-  int groups;  // row groups: 2 (80 rows by 2 nb column blocks each) at 160 rows, else 1
+  int groups;  // row groups of mb row blocks: 2 at 160 rows, 4 at 320, else 1
   size_t bytes;
 };
 
@@ -209,13 +210,21 @@ int fm_plan(int M, int N, int K, bool swiglu, int requested, FmPlan* p) {
     if (!s) s = fewest;
     if (!s) return fail(WPTV_E_UNSUPPORTED, "gemm_fm: no part count of K = %d has a kernel form", K);
   }
-  p->mb = fm_row_blocks(M);
+  // row groups: the same workgroups as all rows by nb blocks, squarer tiles
+  const int rb = fm_row_blocks(M);
+  p->mb = rb;
   p->nb = nb;
   p->groups = 1;
-  if (p->mb == 10 && N % (32 * nb) == 0) {  // the same workgroups, squarer tiles
+  if (rb == 10 && N % (32 * nb) == 0) {  // 160 rows: halves by 2 nb blocks
     p->mb = 5;
     p->nb = 2 * nb;
     p->groups = 2;
+  } else if (rb == 20 && N % (64 * nb) == 0) {  // 320 rows: quarters by 4 nb blocks (gate/up: by nb, two per CU)
+    p->mb = 5;
+    p->nb = swiglu ? nb : 4 * nb;
+    p->groups = 4;
+  } else if (rb > 10) {
+    return fail(WPTV_E_UNSUPPORTED, "gemm_fm: %d rows have no kernel form (up to 160, or 289 to 320)", M);
   }
   p->splits = s;
   p->steps = quarter / s;
@@ -246,11 +255,11 @@ int launch_fm_steps(int steps, dim3 grid, hipStream_t stream, const void* x, con
 template <int NB, int OUT>
 int launch_fm(const FmPlan& p, hipStream_t stream, const void* x, const void* w, int M, int N, void* out) {
   const int NBT = N / 16, RBT = fm_row_blocks(M);
-  if (p.groups == 2) {  // two groups of 5 row blocks, 2 NB column blocks a tile
-    const dim3 grid(N / (32 * NB), p.splits, 2);
-    return launch_fm_steps<5, 2 * NB, OUT>(p.steps, grid, stream, x, w, NBT, RBT, M, N, out);
+  const dim3 grid(N / (16 * p.nb), p.splits, p.groups);
+  if (p.groups > 1) {  // groups of 5 row blocks by 4 or 8 column blocks
+    if (p.nb == 4) return launch_fm_steps<5, 4, OUT>(p.steps, grid, stream, x, w, NBT, RBT, M, N, out);
+    return launch_fm_steps<5, 8, OUT>(p.steps, grid, stream, x, w, NBT, RBT, M, N, out);
   }
-  const dim3 grid(N / (16 * NB), p.splits, 1);
   switch (p.mb) {
     case 2: return launch_fm_steps<2, NB, OUT>(p.steps, grid, stream, x, w, NBT, RBT, M, N, out);
     case 4: return launch_fm_steps<4, NB, OUT>(p.steps, grid, stream, x, w, NBT, RBT, M, N, out);

@@ -214,8 +214,8 @@ class MQADecoder:
         return None if ring is None else ring - self.config.window + 1
 
     def fm_rows(self, rows):
-        """Whether a reading of `rows` rows runs the fm products (bf16, at
-        most 160 rows, every layer's shapes taken by a kernel form)."""
+        """Whether a reading of `rows` rows runs the fm products (bf16, up to
+        160 rows or 289 to 320, every layer's shapes taken by a kernel form)."""
         ok = self._fm_rows.get(rows)
         if ok is None:
             ok = self.dtype == torch.bfloat16 and all(

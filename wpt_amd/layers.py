@@ -278,7 +278,7 @@ def add_rms_norm_parts(h, parts, weight, y, eps=EPS, fm=False):
 
 # ---- fragment-major operands (include/wptv.h) and the products that read them ----
 
-FM_MAX_ROWS = 160  # rows the fm products take
+FM_MAX_ROWS = 320  # rows the fm products take (up to 160, or 289 to 320)
 
 
 def _same(y, h):
