@@ -52,9 +52,12 @@ enum {
                                          key-parallel kernel always reads only the rows the positions reach) */
   WPTV_ATTN_KEY_SPLIT = 4,            /* where T*H <= 80: the key-parallel MFMA kernel (each wavefront owns key
                                          tiles and holds every query row) instead of the row-block one */
-  WPTV_ATTN_OUT_FM = 8                /* the output as the output projection's operand: [B T, H c] in the
+  WPTV_ATTN_OUT_FM = 8,               /* the output as the output projection's operand: [B T, H c] in the
                                          fragment-major layout (below) with wptv_fm_row_blocks(B T) row blocks;
-                                         bf16 row-block kernel only */
+                                         bf16 row-block kernels only */
+  WPTV_ATTN_ROWS32 = 16               /* head width 128: the row-block kernel on 32-row blocks (each wavefront
+                                         holds 32 query rows, v_mfma_f32_32x32x16_bf16), which is the default
+                                         above 128 query rows (T*H) a batch row */
 };
 
 int wptv_abi_version(void);

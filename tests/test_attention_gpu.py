@@ -8,7 +8,7 @@ import torch
 
 from oracle import attention as oracle
 from tests.formulas import relative_error
-from wpt_amd import kernels
+from wpt_amd import kernels, layers
 
 pytestmark = pytest.mark.gpu
 
@@ -28,6 +28,10 @@ def on(device, *tensors):
     return [t.to(device) for t in tensors]
 
 
+# the MFMA kernel forms: 16-row blocks, key-parallel, 32-row blocks
+FORMS = {"row-blocks": {}, "key-parallel": {"key_split": True}, "rows32": {"rows32": True}}
+
+
 @pytest.mark.parametrize("B, T, H, c, N, splits", [
     (32, 5, 16, 128, 4096, 0),   # the verify-attention workload: 16 query heads, 1 KV head, k+1 = 5
     (32, 5, 16, 128, 4096, 1),   # one part per batch row: no combine
@@ -38,8 +42,8 @@ def on(device, *tensors):
     (1, 1, 4, 64, 1, 0),         # a single row
     (64, 5, 16, 128, 2048, 0),   # the end-to-end step's layer shape
 ])
-@pytest.mark.parametrize("key_split", [False, True], ids=["row-blocks", "key-parallel"])
-def test_exact_attention_matches_the_oracle(device, B, T, H, c, N, splits, key_split):
+@pytest.mark.parametrize("form", list(FORMS))
+def test_exact_attention_matches_the_oracle(device, B, T, H, c, N, splits, form):
     q = draw(B, T, H, c, seed=1)
     _, k, v = entries_table(B, N, c, seed=2)
     positions = (N - T + torch.arange(T)).clamp(min=0).expand(B, T).contiguous()
@@ -48,7 +52,7 @@ def test_exact_attention_matches_the_oracle(device, B, T, H, c, N, splits, key_s
     # the strided halves of the device table, as the model's cache gives them
     table = torch.cat([kd, vd], -1)
     got = kernels.verify_attention(qd, table[..., :c], table[..., c:], pd, c ** -0.5, splits=splits,
-                                   key_split=key_split)
+                                   **FORMS[form])
     assert got.dtype == torch.bfloat16 and got.shape == (B, T, H, c)
     assert relative_error(got.cpu(), expected) < 1e-2
 
@@ -84,13 +88,13 @@ def test_the_generic_and_mfma_kernels_agree(device):
     positions = (N - T + torch.arange(T)).expand(B, T).contiguous()
     args = on(device, q, k, v, positions)
     generic = kernels.verify_attention(*args, c ** -0.5, generic=True).cpu().float()
-    for key_split in (False, True):
-        mfma = kernels.verify_attention(*args, c ** -0.5, key_split=key_split)
+    for form in FORMS.values():
+        mfma = kernels.verify_attention(*args, c ** -0.5, **form)
         assert relative_error(mfma.cpu(), generic) < 1e-2
 
 
-@pytest.mark.parametrize("key_split", [False, True], ids=["row-blocks", "key-parallel"])
-def test_scores_growing_along_the_keys(device, key_split):
+@pytest.mark.parametrize("form", list(FORMS))
+def test_scores_growing_along_the_keys(device, form):
     # every query along one direction u, key n = f_n u with f_n rising over
     # the rows: each row's maximum grows by far more than 2^32 across the
     # tiles, so the running maximum moves and the partial sums are rescaled
@@ -107,7 +111,7 @@ def test_scores_growing_along_the_keys(device, key_split):
     expected, _ = oracle.exact_attention(q, k, v, positions, c ** -0.5, 0, 128)
     for splits in (1, 0):
         got = kernels.verify_attention(*on(device, q, k, v, positions), c ** -0.5, splits=splits,
-                                       key_split=key_split)
+                                       **FORMS[form])
         assert relative_error(got.cpu(), expected) < 1e-2
 
 
@@ -129,7 +133,7 @@ def test_a_small_tree_on_both_mfma_kernels(device):
     got = kernels.verify_attention(qd, kd, vd, positions, c ** -0.5, tree=(bd, masks), key_split=True)
     assert relative_error(got.cpu(), expected) < 1e-2
     # the positions given, or formed by the kernel as tree_base + node: the same bits on every kernel
-    for form in ({}, {"key_split": True}, {"generic": True}):
+    for form in ({}, {"key_split": True}, {"rows32": True}, {"generic": True}):
         given = kernels.verify_attention(qd, kd, vd, positions, c ** -0.5, tree=(bd, masks), **form)
         formed = kernels.verify_attention(qd, kd, vd, None, c ** -0.5, tree=(bd, masks), **form)
         assert torch.equal(given, formed)
@@ -203,7 +207,8 @@ def test_the_sparse_gather_kernel_matches_the_oracle(device, B, T, H, c, N, W, K
 
 def test_tree_attention_matches_the_oracle(device):
     # the tree workload's shape at a smaller prefix: a binary draft tree of 31
-    # nodes (depth 5) after the prefix, ancestor-only mask
+    # nodes (depth 5) after the prefix, ancestor-only mask (496 query rows: the
+    # 32-row kernel by default, the key-parallel form below)
     B, M, H, c, prefix = 4, 31, 16, 128, 1000
     parents = oracle.binary_tree_parents(M)
     q = draw(B, M, H, c, seed=15)
@@ -226,8 +231,10 @@ def test_lse_is_the_log_sum_exp(device):
     z = torch.einsum("bthc,bnc->bthn", q.float(), k.float()) * c ** -0.5
     z = z.masked_fill(torch.arange(N) > positions[..., None, None], float("-inf"))
     for splits in (1, 4):
-        _, lse = kernels.verify_attention(*on(device, q, k, v, positions), c ** -0.5, lse=True, splits=splits)
-        assert (lse.cpu() - z.logsumexp(-1)).abs().max() < 2e-2
+        for form in FORMS.values():
+            _, lse = kernels.verify_attention(*on(device, q, k, v, positions), c ** -0.5, lse=True, splits=splits,
+                                              **form)
+            assert (lse.cpu() - z.logsumexp(-1)).abs().max() < 2e-2
 
 
 def test_bad_shapes_raise_value_error(device):
@@ -238,3 +245,37 @@ def test_bad_shapes_raise_value_error(device):
         kernels.verify_attention(q, k, k, positions, 0.1)
     with pytest.raises(ValueError):
         kernels.verify_attention(q, k.float(), k.float(), positions[:, :1].expand(2, 5), 0.1)
+
+
+@pytest.mark.parametrize("rows", [160, 240])
+def test_the_32_row_kernel_with_window_sink_gate_and_fm_output(device, rows):
+    # more than 128 query rows a batch row (the 32-row kernel's default
+    # range): a window, a sink and the output gate against the oracle, the
+    # log-sum-exps, and the fm output bit for bit the row-major one
+    B, H, c, N, W = 3, 16, 128, 900, 256
+    T = rows // H
+    q = draw(B, T, H, c, seed=41)
+    _, k, v = entries_table(B, N, c, seed=42)
+    sink = draw(H, seed=43, dtype=torch.float32)
+    gate = draw(B, T, H * c, seed=44)
+    positions = torch.stack([torch.arange(N - T, N), torch.arange(300, 300 + T), torch.arange(N - 2 * T, N - T)])
+    idx = torch.empty(B, T, 0, dtype=torch.long)
+    expected = oracle.sparse_attention(q, k, v, sink, idx, positions, c ** -0.5, W)
+    gated = expected.float() * torch.sigmoid(gate.float()).reshape(B, T, H, c)
+    qd, kd, vd, pd, sd, gd = on(device, q, k, v, positions, sink, gate)
+    for splits in (1, 0):
+        got = kernels.verify_attention(qd, kd, vd, pd, c ** -0.5, window=W, sink=sd, splits=splits)
+        assert relative_error(got.cpu(), expected) < 1e-2
+    got, lse = kernels.verify_attention(qd, kd, vd, pd, c ** -0.5, window=W, lse=True)
+    z = torch.einsum("bthc,bnc->bthn", q.float(), k.float()) * c ** -0.5
+    n = torch.arange(N)
+    seen = (n <= positions[..., None]) & (n > positions[..., None] - W)
+    z = z.masked_fill(~seen[:, :, None, :], float("-inf"))
+    assert (lse.cpu() - z.logsumexp(-1)).abs().max() < 2e-2
+    out = kernels.verify_attention(qd, kd, vd, pd, c ** -0.5, window=W)
+    out_fm = kernels.verify_attention(qd, kd, vd, pd, c ** -0.5, window=W, out_fm=True)
+    assert torch.equal(layers.fm_unpack(out_fm, B * T, H * c), out.reshape(B * T, H * c))
+    # the window-only sparse form runs the same kernel, here with the output gate
+    id_ = idx.to(device)
+    got = kernels.sparse_attention(qd, kd, vd, sd, id_, pd, c ** -0.5, W, gate=gd)
+    assert relative_error(got.cpu().float(), gated) < 2e-2

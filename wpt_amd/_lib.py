@@ -22,6 +22,7 @@ FORCE_GENERIC = 1
 RANGE_FROM_POSITIONS = 2
 KEY_SPLIT = 4
 OUT_FM = 8
+ROWS32 = 16
 
 
 class KernelUnavailable(RuntimeError):

@@ -607,6 +607,385 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
 }
 
 // ---------------------------------------------------------------------------
+// Row-block kernel on 32-row blocks (v_mfma_f32_32x32x16_bf16)
+// ---------------------------------------------------------------------------
+//
+// The same workgroup, key split, DMA ring and tile layout as
+// verify_attention_mfma, with each wavefront holding 32 query rows instead
+// of 16: per 32-key tile a wavefront reads the tile once from LDS for twice
+// the rows, and the per-tile VALU work (the maximum across lanes, the
+// rescale test, addresses, loop control) is paid once per 32 rows.  The
+// instruction's layouts (checked on the MI355X): A and B, lane l holds row /
+// column l % 32, k-elements 8 (l / 32) .. + 7; the FP32 result, lane l
+// register i holds row 8 (i / 4) + 4 (l / 32) + i % 4 of column l % 32.
+//
+//   S^T[key, q] = K . Q^T       A = K (lane l: key l % 32, columns 16 s + 8 (l / 32) .. of k-step s)
+//                               B = Q^T (lane l: query row l % 32, the same columns)
+//   so lane l holds the scores of query l % 32 against keys
+//   {8 a + 4 h + m} (h = l / 32, register i = 4 a + m): the maximum of a
+//   query is an in-lane maximum of 16 and one exchange with lane l ^ 32.
+//   O^T[c, q] += V^T . P^T      per 16-key step kk, B = P^T is registers
+//                               8 kk .. 8 kk + 7 of the scores' layout:
+//                               k-element 8 h + e is key 16 kk + 4 h + e
+//                               (e < 4) or 16 kk + 8 + 4 h + e - 4; A =
+//                               V^T, lane l column 32 cb + l % 32 at those
+//                               keys, two transposed 4-row reads
+template <int C, int MB, bool TREE>
+__global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
+    const unsigned short* __restrict__ q, const unsigned short* __restrict__ k, int64_t ksb, int64_t ksn,
+    const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn, const int64_t* __restrict__ positions,
+    int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
+    const float* __restrict__ sink, int T, int H, int N, float scale_log2, int groups, int splits,
+    int range_from_positions, int xcd_map, RowMap rows, OutGate gate, unsigned short* __restrict__ out,
+    int out_fm, float* __restrict__ lse_out, unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
+  static_assert(C == 128, "the 32-row kernel is built for head width 128");
+  using G = Tile<C>;
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  constexpr int kRows = 32 * MB;
+  constexpr int kXC = C / 8;
+  constexpr int kQSteps = C / 16;  // k-steps of the QK^T product (32x32x16)
+  constexpr int kCB = C / 32;      // 32-wide column blocks of O
+  constexpr int DMAW = MB >= 4 ? 4 : (MB >= 2 ? 2 : 1);
+  constexpr int kCnt = G::kLoads / DMAW;
+  constexpr int kRing = G::kSlots * G::kElems;
+  constexpr int kPitch = C + 4;
+  static_assert(G::kLoads % DMAW == 0, "DMA split");
+  static_assert(MB * (32 * kPitch + 64) * 4 <= kKeySets * kRing * 2, "the merge buffer reuses the rings");
+  __shared__ __attribute__((aligned(16))) unsigned short lds[kKeySets * kRing];
+  __shared__ __attribute__((aligned(16))) unsigned short qlds[MB * 32 * C];  // each m-block's Q^T operands
+
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kset = wid / MB, mb = wid % MB;
+  const int j = lane & 31;  // this lane's query row (S^T, O^T columns) or key row (K operand)
+  const int h = lane >> 5;  // lane half
+
+  int unit, split;
+  {
+    const int L = blockIdx.x;
+    if (xcd_map) {
+      const int kk = L >> 3;
+      unit = (L & 7) + 8 * (kk / splits);
+      split = kk % splits;
+    } else {
+      unit = L / splits;
+      split = L % splits;
+    }
+  }
+  const int b = unit / groups;
+  const int grp = unit % groups;
+  const int R = T * H;
+  const int r_base = grp * kRows;
+  const QueryPos pos_b = query_pos(positions, tree_base, b, T);
+
+  int u_lo = 0, u_hi = N - 1;
+  if (range_from_positions) {
+    u_lo = INT_MAX;
+    u_hi = -1;
+    const int t_first = r_base / H, t_last = (min(r_base + kRows, R) - 1) / H;
+    for (int t = t_first; t <= t_last; ++t) {
+      const Bounds bt = query_bounds(pos_b, t, window, N);
+      if (bt.hi >= bt.lo) {
+        u_lo = min(u_lo, bt.lo);
+        u_hi = max(u_hi, bt.hi);
+      }
+    }
+  }
+  int s_lo = 0, s_hi = -1;
+  if (u_hi >= u_lo) {
+    const int U = u_hi - u_lo + 1;
+    int per = (U + splits - 1) / splits;
+    per = (per + 32 * kKeySets - 1) / (32 * kKeySets) * (32 * kKeySets);
+    s_lo = u_lo + split * per;
+    s_hi = min(s_lo + per - 1, u_hi);
+  }
+  const int ntiles = s_hi >= s_lo ? (s_hi - s_lo + 1 + 31) / 32 : 0;
+  const int niter = (ntiles + kKeySets - 1) / kKeySets;
+  const int mine = ntiles > kset ? (ntiles - kset + kKeySets - 1) / kKeySets : 0;
+
+  // DMA of the key/value tiles: as verify_attention_mfma (whole rows per
+  // instruction into the swizzled row-major halves).
+  const i32x4 krs = buffer_resource(k + (int64_t)b * ksb);
+  const i32x4 vrs = buffer_resource(v + (int64_t)b * vsb);
+  const uint32_t krow_bytes = (uint32_t)ksn * 2u, vrow_bytes = (uint32_t)vsn * 2u;
+  unsigned short* const ring = lds + kset * kRing;
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_address(ring));
+  const bool dma_wave = mb < DMAW;
+  const int rbase = row_base(rows, b);
+  auto issue = [&](int it) {
+    const int tile = kset + it * kKeySets;
+    const uint32_t slot = ring_lds + (uint32_t)(it % G::kSlots) * (G::kElems * 2);
+#pragma unroll
+    for (int c = 0; c < kCnt; ++c) {
+      const int ii = mb * kCnt + c;
+      const int part = ii / G::kPerHalf, quarter = ii % G::kPerHalf;
+      const int row = quarter * (64 / kXC) + lane / kXC;
+      const int x = (lane % kXC) ^ tile_sigma<C>(row);
+      int n = s_lo + tile * 32 + 16 * (part & 1) + row;
+      n = n < s_hi ? n : s_hi;
+      const uint32_t phys = (uint32_t)(n - rbase) & rows.mask;
+      const uint32_t off = phys * (part < 2 ? krow_bytes : vrow_bytes) + 16u * x;
+      dma_16B(part < 2 ? krs : vrs, off, slot + part * (G::kHalf * 2) + 1024u * quarter);
+    }
+  };
+  // The queries first (each m-block's Q^T operand of k-step s at units
+  // 64 s + lane: query row l % 32, columns 16 s + 8 (l / 32) .. + 7), by
+  // the first key set; then the first tiles.
+  const int r = r_base + 32 * mb + j;
+  const bool real = r < R;
+  if (kset == 0) {
+    const i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
+    const uint32_t qoff = (uint32_t)(real ? r : R - 1) * (uint32_t)(C * 2) + 16u * h;
+    const uint32_t qdst = __builtin_amdgcn_readfirstlane(lds_address(qlds + mb * 32 * C));
+#pragma unroll
+    for (int s = 0; s < kQSteps; ++s) dma_16B(qrs, qoff + 32u * s, qdst + 1024u * s);
+  }
+  if (dma_wave) {
+#pragma unroll
+    for (int it = 0; it < G::kSlots - 1; ++it)
+      if (it < mine) issue(it);
+  }
+  int lo = 0, hi = -1;
+  uint64_t anc = 0;
+  int f_lo = 0, f_hi = INT_MAX;
+  const int64_t tbase = TREE ? tree_base[b] : (int64_t)INT_MAX;
+  {
+    const int w_first = r_base + 32 * mb;
+    if (w_first < R) {
+      const int t_first = w_first / H, t_last = (min(w_first + 32, R) - 1) / H;
+      const int my_t = real ? r / H : -1;
+      for (int t = t_first; t <= t_last; ++t) {
+        const Bounds bt = query_bounds(pos_b, t, window, N);
+        f_lo = max(f_lo, bt.lo);
+        f_hi = min(f_hi, bt.hi);
+        if (my_t == t) {
+          lo = bt.lo;
+          hi = min(bt.hi, s_hi);
+        }
+        if constexpr (TREE) {
+          const uint64_t a = ancestors[t];
+          if (my_t == t) anc = a;
+        }
+      }
+    } else {
+      f_hi = -1;
+    }
+    if (TREE && tbase <= (int64_t)f_hi) f_hi = (int)tbase - 1;
+    f_hi = min(f_hi, s_hi);
+  }
+
+  bf16x8 qf[kQSteps];
+  f32x16 o[kCB];
+#pragma unroll
+  for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[cb][i] = 0.f;
+  float m_run = kNegInf, l_run = 0.f;
+  // K operand of k-step s: key row j (half j / 16, row j % 16), chunk 2 s + h
+  const int k_base = (j >> 4) * G::kHalf + 8 * kXC * (j & 15);
+  const int k_y = h ^ tile_sigma<C>(j & 15);
+  // V^T operand of step kk, column block cb: lane group gq = lane / 16 reads
+  // the 4 x 16 block at rows 4 (gq / 2) + rr (+ 8: the second read) of V
+  // half 2 + kk, columns 32 cb + 16 (gq % 2) + 4 qq, rr = (lane / 4) % 4, qq = lane % 4
+  const int gq = lane >> 4, rr = (lane >> 2) & 3, qq = lane & 3;
+  const int va_row = 4 * (gq >> 1) + rr;
+  const int va_base = 8 * kXC * va_row + 4 * (qq & 1);
+  const int va_y = ((2 * (gq & 1)) | (qq >> 1)) ^ tile_sigma<C>(va_row);
+  const int vb_base = 8 * kXC * (va_row + 8) + 4 * (qq & 1);
+  const int vb_y = ((2 * (gq & 1)) | (qq >> 1)) ^ tile_sigma<C>(va_row + 8);
+
+  auto arrive = [&](int t, int later) {
+    if (dma_wave && t < mine) {
+      if (later >= 2)
+        wait_vmcnt<2 * kCnt>();
+      else if (later == 1)
+        wait_vmcnt<kCnt>();
+      else
+        wait_vmcnt<0>();
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  auto qk = [&](int t, f32x16& sc) {
+    const unsigned short* st = ring + (t % G::kSlots) * G::kElems;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sc[i] = 0.f;
+#pragma unroll
+    for (int s = 0; s < kQSteps; ++s) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(st + k_base + 8 * ((2 * s) ^ k_y));
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sc, 0, 0, 0);
+    }
+  };
+  auto accumulate = [&](int t, const f32x16& sc) {
+    const unsigned short* st = ring + (t % G::kSlots) * G::kElems;
+    const int n0 = s_lo + (kset + t * kKeySets) * 32;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = sc[i];
+    if (!(n0 >= f_lo && n0 + 31 <= f_hi)) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int n = n0 + 8 * (i >> 2) + 4 * h + (i & 3);
+        bool vis = n >= lo && n <= hi;
+        if constexpr (TREE) vis = vis && tree_visible(n, tbase, anc);
+        x[i] = vis ? x[i] : kNegInf;
+      }
+    }
+    float mx = score_max(score_max(score_max(x[0], x[1]), score_max(x[2], x[3])),
+                         score_max(score_max(x[4], x[5]), score_max(x[6], x[7])));
+    mx = score_max(mx, score_max(score_max(score_max(x[8], x[9]), score_max(x[10], x[11])),
+                                 score_max(score_max(x[12], x[13]), score_max(x[14], x[15]))));
+    {
+      auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = score_max(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    const float bm = mx * scale_log2;
+    const bool grow = bm > m_run + kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(grow && m_run != kNegInf)) {
+      const float alpha = (grow && m_run != kNegInf) ? __builtin_amdgcn_exp2f(m_run - bm) : 1.f;
+      l_run *= alpha;
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) o[cb] *= alpha;
+    }
+    m_run = grow ? bm : m_run;
+    const float neg_m = m_run == kNegInf ? 0.f : -m_run;
+    float p[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(x[i], scale_log2, neg_m));
+    l_run += (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]))) +
+             (((p[8] + p[9]) + (p[10] + p[11])) + ((p[12] + p[13]) + (p[14] + p[15])));
+    bf16x8 pt[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pt[kk][e] = static_cast<__bf16>(p[8 * kk + e]);
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const unsigned short* vh = st + (2 + kk) * G::kHalf;
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) {
+        const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vh + va_base + 8 * ((4 * cb) ^ va_y)));
+        const s16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vh + vb_base + 8 * ((4 * cb) ^ vb_y)));
+        const s16x8 vt = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+        o[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vt), pt[kk], o[cb], 0, 0, 0);
+      }
+    }
+  };
+
+  f32x16 s0, sn;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s0[i] = sn[i] = 0.f;
+  if (kset == 0 && !(dma_wave && mine > 0)) wait_vmcnt<0>();
+  arrive(0, min(G::kSlots - 2, mine - 1));  // tile 0 and every m-block's queries are in LDS
+#pragma unroll
+  for (int s = 0; s < kQSteps; ++s)
+    qf[s] = *reinterpret_cast<const bf16x8*>(qlds + mb * 32 * C + 512 * s + 8 * lane);
+  if (mine > 0) qk(0, s0);
+  auto iteration = [&](int it, const f32x16& cur, f32x16& nxt) {
+    arrive(it + 1, min(1, mine - 2 - it));
+    if (dma_wave && it + G::kSlots - 1 < mine) issue(it + G::kSlots - 1);
+    if (it + 1 < mine) qk(it + 1, nxt);
+    if (it < mine) accumulate(it, cur);
+  };
+#pragma unroll 1
+  for (int it = 0; it < niter; it += 2) {
+    iteration(it, s0, sn);
+    if (it + 1 < niter) iteration(it + 1, sn, s0);
+  }
+  wait_vmcnt<0>();
+  {
+    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+    l_run = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+
+  // ---- merge the key sets (the merge buffer reuses the rings) ----
+  __syncthreads();
+  float* mbuf = reinterpret_cast<float*>(lds) + mb * (32 * kPitch + 64);  // this m-block's O (row q: 32 cb + c), m, l
+  if (kset == 1) {
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+        *reinterpret_cast<f32x4*>(mbuf + j * kPitch + 32 * cb + 8 * a + 4 * h) =
+            f32x4{o[cb][4 * a], o[cb][4 * a + 1], o[cb][4 * a + 2], o[cb][4 * a + 3]};
+    if (h == 0) {
+      mbuf[32 * kPitch + j] = m_run;
+      mbuf[32 * kPitch + 32 + j] = l_run;
+    }
+  }
+  __syncthreads();
+  if (kset != 0) return;
+  {
+    const float m1 = mbuf[32 * kPitch + j], l1 = mbuf[32 * kPitch + 32 + j];
+    const float M = fmaxf(m_run, m1);
+    const float a0 = m_run == kNegInf ? 0.f : exp2f(m_run - M);
+    const float a1 = m1 == kNegInf ? 0.f : exp2f(m1 - M);
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const f32x4 w = *reinterpret_cast<const f32x4*>(mbuf + j * kPitch + 32 * cb + 8 * a + 4 * h);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) o[cb][4 * a + m] = o[cb][4 * a + m] * a0 + w[m] * a1;
+      }
+    l_run = l_run * a0 + l1 * a1;
+    m_run = M;
+  }
+  if (!real) return;
+
+  float M = m_run, L = l_run, f = 1.f;
+  if (splits == 1 && sink) {
+    const float sl = sink[r % H] * kLog2e;
+    const float M2 = fmaxf(M, sl);
+    f = (M == kNegInf) ? 0.f : exp2f(M - M2);
+    L = L * f + exp2f(sl - M2);
+    M = M2;
+  }
+  const float scale_out = L > 0.f ? f / L : 0.f;
+  const float lse2 = L > 0.f ? M + log2f(L) : kNegInf;
+  typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+  if (splits == 1) {
+    unsigned short* orow = out + ((int64_t)b * R + r) * C;
+    const unsigned short* grow = gate.row<unsigned short>(b, T, r, H, C);
+    const int fm_row = b * T + r / H, fm_col = (r % H) * C;
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int c0 = 32 * cb + 8 * a + 4 * h;
+        u16x4 res;
+        if (grow) {
+          const u16x4 gv = *reinterpret_cast<const u16x4*>(grow + c0);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) res[m] = gated_bf16(o[cb][4 * a + m] * scale_out, gv[m]);
+        } else {
+#pragma unroll
+          for (int m = 0; m < 4; ++m) res[m] = f32_to_bf16(o[cb][4 * a + m] * scale_out);
+        }
+        unsigned short* dst = out_fm ? out + fm_offset(fm_row, fm_col + c0, out_fm) : orow + c0;
+        *reinterpret_cast<u16x4*>(dst) = res;
+      }
+    if (lse_out && h == 0) lse_out[(int64_t)b * R + r] = lse2 * kLn2;
+  } else {
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    const int64_t prow = ((int64_t)unit * splits + split) * kRows + 32 * mb + j;
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int c0 = 32 * cb + 8 * a + 4 * h;
+        *reinterpret_cast<bf16x4*>(part_o + prow * C + c0) =
+            bf16x4{static_cast<__bf16>(o[cb][4 * a] * scale_out), static_cast<__bf16>(o[cb][4 * a + 1] * scale_out),
+                   static_cast<__bf16>(o[cb][4 * a + 2] * scale_out),
+                   static_cast<__bf16>(o[cb][4 * a + 3] * scale_out)};
+      }
+    if (h == 0) part_lse[prow] = lse2;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Sparse MFMA kernel: chosen rows plus the window (at most 16 heads)
 // ---------------------------------------------------------------------------
 //
@@ -1444,11 +1823,11 @@ __global__ __launch_bounds__(64) void attention_generic(
 // Host side
 // ---------------------------------------------------------------------------
 
-enum Kind { kGeneric = 0, kRowBlocks = 1, kKeySplit = 2 };
+enum Kind { kGeneric = 0, kRowBlocks = 1, kKeySplit = 2, kRowBlocks32 = 3 };
 
 struct Plan {
   Kind kind;
-  int mbw;      // m-blocks per workgroup (row-block kernel) or per wavefront (key-parallel kernel)
+  int mbw;      // 16-row m-blocks per workgroup (row-block kernels) or per wavefront (key-parallel kernel)
   int groups;   // query-row groups per batch row
   int splits;   // key-range parts per batch row
   size_t bytes; // workspace
@@ -1489,9 +1868,21 @@ int plan(int B, int T, int H, int c, int N, int window, int dtype, int flags, in
   const int R = T * H;
   const int blocks = (R + 15) / 16;
   p.kind = (blocks <= 5 && (flags & WPTV_ATTN_KEY_SPLIT)) ? kKeySplit : kRowBlocks;
+  // Head width 128 and more than 128 query rows a batch row (a draft tree,
+  // a wide reading): the 32-row blocks (measured on the MI355X at batch 16,
+  // 8192 prefix rows and 31 nodes of 16 heads: 54 against 61 us); up to 128
+  // rows (a verify step's 80) the 16-row blocks (23.7 against 24.6 us at
+  // batch 32, 4096 rows).
+  if (c == 128 && !(flags & WPTV_ATTN_KEY_SPLIT) && ((flags & WPTV_ATTN_ROWS32) || R > 128)) p.kind = kRowBlocks32;
   if (p.kind == kKeySplit) {
     p.mbw = blocks;
     p.groups = 1;
+  } else if (p.kind == kRowBlocks32) {
+    // up to four 32-row blocks per key set (eight wavefronts)
+    const int b32 = (R + 31) / 32;
+    const int m32 = b32 < 4 ? b32 : 4;
+    p.mbw = 2 * m32;
+    p.groups = (R + 32 * m32 - 1) / (32 * m32);
   } else {
     p.mbw = pick_mbw(R);
     p.groups = (R + 16 * p.mbw - 1) / (16 * p.mbw);
@@ -1550,6 +1941,17 @@ void launch_mfma(dim3 grid, hipStream_t stream, const unsigned short* q, const u
                      splits, range_from_positions, xcd_map, rows, gate, out, out_fm, lse, part_o, part_lse);
 }
 
+template <int MB, bool TREE>
+void launch_m32(dim3 grid, hipStream_t stream, const unsigned short* q, const unsigned short* k, int64_t ksb,
+                int64_t ksn, const unsigned short* v, int64_t vsb, int64_t vsn, const int64_t* positions, int window,
+                const int64_t* tree_base, const uint64_t* ancestors, const float* sink, int T, int H, int N,
+                float scale_log2, int groups, int splits, int range_from_positions, int xcd_map, RowMap rows,
+                OutGate gate, unsigned short* out, int out_fm, float* lse, unsigned short* part_o, float* part_lse) {
+  hipLaunchKernelGGL((verify_attention_m32<128, MB, TREE>), grid, dim3(kKeySets * MB * 64), 0, stream, q, k, ksb,
+                     ksn, v, vsb, vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, groups,
+                     splits, range_from_positions, xcd_map, rows, gate, out, out_fm, lse, part_o, part_lse);
+}
+
 }  // namespace
 }  // namespace wptv
 
@@ -1595,7 +1997,7 @@ int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
   }
   // the output in the fm layout (the output projection's operand): the MFMA row-block kernel only
   const int out_fm = (flags & WPTV_ATTN_OUT_FM) ? fm_row_blocks(B * T) : 0;
-  if (out_fm && p.kind != kRowBlocks)
+  if (out_fm && p.kind != kRowBlocks && p.kind != kRowBlocks32)
     return fail(WPTV_E_UNSUPPORTED, "verify_attention: the fm output layout needs the bf16 MFMA row-block kernel "
                                     "(head width 64 or 128, aligned operands, no key split)");
   if (p.kind == kGeneric) {
@@ -1657,6 +2059,22 @@ int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
     }
 #undef WPTV_LAUNCH
     st = launched("verify_attention_keys");
+  } else if (p.kind == kRowBlocks32) {
+    const int from_positions = (window > 0 || p.groups > 1 || (flags & WPTV_ATTN_RANGE_FROM_POSITIONS)) ? 1 : 0;
+    auto* po = static_cast<unsigned short*>(part_o);
+#define WPTV_LAUNCH(MM)                                                                                         \
+  (tree_base ? launch_m32<MM, true> : launch_m32<MM, false>)(                                                   \
+      grid, stream, qb, kb, k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, positions, window, tree_base,   \
+      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_map, rows, gate, ob,       \
+      out_fm, lse, po, part_lse)
+    switch (p.mbw / 2) {
+      case 1: WPTV_LAUNCH(1); break;
+      case 2: WPTV_LAUNCH(2); break;
+      case 3: WPTV_LAUNCH(3); break;
+      default: WPTV_LAUNCH(4); break;
+    }
+#undef WPTV_LAUNCH
+    st = launched("verify_attention_m32");
   } else {
     // Full causal attention of a single query group reads the whole table; any
     // other case takes its key range from the positions.

@@ -80,7 +80,8 @@ def _long(x, device):
 
 
 def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=None, lse=False, splits=0,
-                     generic=False, from_positions=False, key_split=False, static_scratch=False, out_fm=False):
+                     generic=False, from_positions=False, key_split=False, static_scratch=False, out_fm=False,
+                     rows32=False):
     """MQA attention of q (B, T, H, c) over k, v (B, N, c): query t of row b
     sees rows max(0, p - window + 1) .. min(p, N - 1), p = positions[b, t]
     (window 0: from row 0), and with tree = (tree_base (B,), ancestors (T,)
@@ -92,7 +93,8 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
     the library chooses); generic: the wave-per-query kernel; from_positions:
     read only the rows the positions reach (a cache table with spare rows);
     key_split: where T*H <= 80, the key-parallel MFMA kernel instead of the
-    row-block one; static_scratch: the allocation-free entry point
+    row-block one; rows32: at head width 128, the row-block kernel on 32-row
+    blocks (v_mfma_f32_32x32x16_bf16); static_scratch: the allocation-free entry point
     (wptv_verify_attention_static), whose parts live in the library's own
     device array: no workspace is allocated, and calls overlapping on one
     device race."""
@@ -115,7 +117,8 @@ def verify_attention(q, k, v, positions, scale, *, window=0, sink=None, tree=Non
         if tree_base.shape != (B,) or ancestors.shape != (T,):
             raise ValueError(f"tree must be (tree_base (B={B},), ancestors (T={T},))")
     flags = ((_lib.FORCE_GENERIC if generic else 0) | (_lib.RANGE_FROM_POSITIONS if from_positions else 0)
-             | (_lib.KEY_SPLIT if key_split else 0) | (_lib.OUT_FM if out_fm else 0))
+             | (_lib.KEY_SPLIT if key_split else 0) | (_lib.OUT_FM if out_fm else 0)
+             | (_lib.ROWS32 if rows32 else 0))
     parts = _lib.ctypes.c_int(int(splits))
     size = _lib.ctypes.c_size_t(0)
     check(library.wptv_attention_workspace(B, T, H, c, N, int(window), dtype, flags, _lib.ctypes.byref(parts),
