@@ -595,6 +595,80 @@ int items_for(int V) {
     default: CALL(64); break;                   \
   }
 
+// Greedy decisions alone (no drafts' distributions to form): each (batch
+// row, position)'s first maximal index of the raw scores, by one workgroup of
+// kGT threads reading the row 16 bytes a lane, every load of a thread issued
+// before the first comparison; the same order as arg_better's (larger value,
+// then lower index; a NaN never wins), so the index does not depend on how the
+// row is shared out.  Rows 16-byte aligned, V a multiple of 16 / sizeof(S).
+constexpr int kGT = 256;
+constexpr int kGLoads = 16;  // 16-byte loads a thread has in flight
+
+template <typename S>
+__global__ __launch_bounds__(kGT) void greedy_argmax(const S* __restrict__ scores, int64_t sb, int64_t st,
+                                                     const int32_t* __restrict__ firsts,
+                                                     const int64_t* __restrict__ drafts, int64_t db,
+                                                     const int32_t* __restrict__ lengths, int B, int L, int V,
+                                                     Stats stats) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int kPer = 16 / (int)sizeof(S);  // values a 16-byte load holds
+  __shared__ float redv[kGT / 64];
+  __shared__ int redi[kGT / 64];
+  const int P = L + 1;
+  const int b = blockIdx.x / P, j = blockIdx.x % P;
+  if (b >= B) return;
+  const int n = lengths ? min(max(lengths[b], 0), L) : L;
+  if (j > n) return;
+  const int64_t first = firsts ? firsts[b] : 0;
+  const u32x4* row = reinterpret_cast<const u32x4*>(scores + b * sb + (first + j) * st);
+  const int chunks = V / kPer, tid = threadIdx.x;
+  float bv = kNegInfS;
+  int bi = INT_MAX;
+  for (int c0 = 0; c0 < chunks; c0 += kGT * kGLoads) {
+    u32x4 w[kGLoads];
+#pragma unroll
+    for (int u = 0; u < kGLoads; ++u) {
+      const int c = c0 + tid + u * kGT;
+      w[u] = c < chunks ? row[c] : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kGLoads; ++u) {
+      const int c = c0 + tid + u * kGT;
+      if (c >= chunks) continue;
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        float x;
+        if constexpr (sizeof(S) == 2)
+          x = __uint_as_float(e & 1 ? (w[u][e >> 1] & 0xffff0000u) : (w[u][e >> 1] << 16));
+        else
+          x = __uint_as_float(w[u][e]);
+        arg_better(bv, bi, x, c * kPer + e);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(bv, o, 64);
+    const int i2 = __shfl_xor(bi, o, 64);
+    arg_better(bv, bi, v2, i2);
+  }
+  const int wave = tid >> 6, lane = tid & 63;
+  if (lane == 0) {
+    redv[wave] = bv;
+    redi[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float v = redv[0];
+    int i = redi[0];
+#pragma unroll
+    for (int w = 1; w < kGT / 64; ++w) arg_better(v, i, redv[w], redi[w]);
+    const int idx = b * P + j;
+    stats.best[idx] = i;
+    stats.keep[idx] = (j < n && drafts) ? (drafts[b * db + j] == i) : 0;
+  }
+}
+
 // One workgroup per (batch row, position): 8 ceil(B / 8) (L + 1) of them,
 // those past B returning at once.
 template <typename S>
@@ -602,6 +676,12 @@ void launch_stats(int B, hipStream_t stream, const void* scores, int64_t sb, int
                   const float* q, int64_t qb, int64_t qt, const int64_t* drafts, int64_t db, const int32_t* lengths,
                   const float* u, const float* e, float temperature, int top_k, int greedy, int L, int V, Stats s) {
   const S* rows = static_cast<const S*>(scores);
+  constexpr int kPer = 16 / (int)sizeof(S);
+  if (greedy && V % kPer == 0 && sb % kPer == 0 && st % kPer == 0 && aligned(scores, 16)) {
+    hipLaunchKernelGGL(greedy_argmax<S>, dim3(B * (L + 1)), dim3(kGT), 0, stream, rows, sb, st, firsts, drafts, db,
+                       lengths, B, L, V, s);
+    return;
+  }
   const dim3 grid(8 * ((B + 7) / 8) * (L + 1));
   // the draft rows through LDS when every row is 16-byte aligned and fits
   const bool qlds = !greedy && q && V <= 32 * kT && V % 4 == 0 && aligned(q, 16) && qb % 4 == 0 && qt % 4 == 0;
