@@ -595,14 +595,16 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   } else {
     typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
     const int64_t prow = ((int64_t)unit * splits + split) * kRows + 16 * mb + j;
+    // the parts are read once, by another kernel: written non-temporally
 #pragma unroll
     for (int cb = 0; cb < G::kCBlocks; ++cb) {
       const f32x4 val = o[cb] * scale_out;
-      *reinterpret_cast<bf16x4*>(part_o + prow * C + cb * 16 + 4 * g) =
-          bf16x4{static_cast<__bf16>(val[0]), static_cast<__bf16>(val[1]), static_cast<__bf16>(val[2]),
-                 static_cast<__bf16>(val[3])};
+      const bf16x4 pv = bf16x4{static_cast<__bf16>(val[0]), static_cast<__bf16>(val[1]),
+                               static_cast<__bf16>(val[2]), static_cast<__bf16>(val[3])};
+      __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, pv),
+                                  reinterpret_cast<uint64_t*>(part_o + prow * C + cb * 16 + 4 * g));
     }
-    if (g == 0) part_lse[prow] = lse2;
+    if (g == 0) __builtin_nontemporal_store(lse2, part_lse + prow);
   }
 }
 
@@ -809,17 +811,31 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
   };
   auto qk = [&](int t, f32x16& sc) {
     const unsigned short* st = ring + (t % G::kSlots) * G::kElems;
+    // every K fragment requested before the first product
+    bf16x8 kf[kQSteps];
+#pragma unroll
+    for (int s = 0; s < kQSteps; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(st + k_base + 8 * ((2 * s) ^ k_y));
 #pragma unroll
     for (int i = 0; i < 16; ++i) sc[i] = 0.f;
 #pragma unroll
-    for (int s = 0; s < kQSteps; ++s) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(st + k_base + 8 * ((2 * s) ^ k_y));
-      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sc, 0, 0, 0);
-    }
+    for (int s = 0; s < kQSteps; ++s) sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s], qf[s], sc, 0, 0, 0);
   };
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
   auto accumulate = [&](int t, const f32x16& sc) {
     const unsigned short* st = ring + (t % G::kSlots) * G::kElems;
     const int n0 = s_lo + (kset + t * kKeySets) * 32;
+    // the V^T operands requested before the softmax, whose arithmetic covers their latency
+    s16x8 vt[2][kCB];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const unsigned short* vh = st + (2 + kk) * G::kHalf;
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) {
+        const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vh + va_base + 8 * ((4 * cb) ^ va_y)));
+        const s16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vh + vb_base + 8 * ((4 * cb) ^ vb_y)));
+        vt[kk][cb] = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    }
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = sc[i];
@@ -860,18 +876,12 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int e = 0; e < 8; ++e) pt[kk][e] = static_cast<__bf16>(p[8 * kk + e]);
-    typedef short s16x8 __attribute__((ext_vector_type(8)));
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const unsigned short* vh = st + (2 + kk) * G::kHalf;
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int cb = 0; cb < kCB; ++cb) {
-        const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vh + va_base + 8 * ((4 * cb) ^ va_y)));
-        const s16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vh + vb_base + 8 * ((4 * cb) ^ vb_y)));
-        const s16x8 vt = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
-        o[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vt), pt[kk], o[cb], 0, 0, 0);
-      }
-    }
+      for (int cb = 0; cb < kCB; ++cb)
+        o[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vt[kk][cb]), pt[kk], o[cb], 0, 0,
+                                                        0);
   };
 
   f32x16 s0, sn;

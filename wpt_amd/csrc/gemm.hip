@@ -202,14 +202,16 @@ __global__ __launch_bounds__(kGemmWaves * 64, 1) void gemm_xwt(const unsigned sh
     for (int nb = 0; nb < NB; ++nb) {
       const int n = n0 + 16 * nb + 4 * g;
       const f32x4 a = acc[ii][nb];
+      // parts and bf16 outputs (the lm_head's logits) are read once, by another kernel: written non-temporally
       if constexpr (OUT == kPartF32) {
         float* dst = static_cast<float*>(out) + ((int64_t)z * M + m) * N + n;
-        *reinterpret_cast<f32x4*>(dst) = a;
+        __builtin_nontemporal_store(a, reinterpret_cast<f32x4*>(dst));
       } else if constexpr (OUT == kOutBf16) {
         typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
         unsigned short* dst = static_cast<unsigned short*>(out) + (int64_t)m * ldo + n;
-        *reinterpret_cast<bf16x4*>(dst) = bf16x4{static_cast<__bf16>(a[0]), static_cast<__bf16>(a[1]),
-                                                 static_cast<__bf16>(a[2]), static_cast<__bf16>(a[3])};
+        const bf16x4 r = bf16x4{static_cast<__bf16>(a[0]), static_cast<__bf16>(a[1]), static_cast<__bf16>(a[2]),
+                                static_cast<__bf16>(a[3])};
+        __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, r), reinterpret_cast<uint64_t*>(dst));
       } else {
         float* dst = static_cast<float*>(out) + (int64_t)m * ldo + n;
         *reinterpret_cast<f32x4*>(dst) =

@@ -138,8 +138,9 @@ __global__ __launch_bounds__(kFmWaves * 64, 1) void gemm_fm(const u32x4* __restr
       const int m = (rb0 + rb) * 16 + j;
       if (m >= M) continue;
       const f32x4 v = {summed(p, 0), summed(p, 1), summed(p, 2), summed(p, 3)};
-      *reinterpret_cast<f32x4*>(static_cast<float*>(out) + ((int64_t)z * M + m) * N + tile * NB * 16 + nb * 16 +
-                                4 * g) = v;
+      // the parts are read once, by the consumer kernel: written non-temporally
+      __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(static_cast<float*>(out) + ((int64_t)z * M + m) * N +
+                                                              tile * NB * 16 + nb * 16 + 4 * g));
     }
   } else {
     typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));

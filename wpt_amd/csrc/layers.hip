@@ -34,6 +34,13 @@ struct Vec8<unsigned short> {  // 8 bf16
     for (int e = 0; e < 8; ++e) v[e] = f32_to_bf16(x[e]);
     *reinterpret_cast<raw*>(p) = v;
   }
+  // for an output one later kernel reads once: written non-temporally
+  static __device__ __forceinline__ void store_nt(unsigned short* p, const float (&x)[8]) {
+    raw v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = f32_to_bf16(x[e]);
+    __builtin_nontemporal_store(v, reinterpret_cast<raw*>(p));
+  }
 };
 template <>
 struct Vec8<float> {
@@ -45,6 +52,10 @@ struct Vec8<float> {
   static __device__ __forceinline__ void store(float* p, const float (&x)[8]) {
     *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
     *reinterpret_cast<f32x4*>(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
+  }
+  static __device__ __forceinline__ void store_nt(float* p, const float (&x)[8]) {
+    __builtin_nontemporal_store(f32x4{x[0], x[1], x[2], x[3]}, reinterpret_cast<f32x4*>(p));
+    __builtin_nontemporal_store(f32x4{x[4], x[5], x[6], x[7]}, reinterpret_cast<f32x4*>(p + 4));
   }
 };
 
@@ -186,7 +197,7 @@ __global__ __launch_bounds__(1024) void add_rms_norm_parts(T* __restrict__ h, co
   const int waves = (blockDim.x + 63) / 64;
   for (int u = 0; u < waves; ++u) total += wsum[u];
   const float inv = rsqrtf(total / (float)D + eps);
-  Vec8<T>::store(hrow + col, x);
+  Vec8<T>::store_nt(hrow + col, x);  // the residual stream: read once, by the next residual add
   float out[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) out[e] = x[e] * inv * wt[e];
