@@ -345,7 +345,15 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
       n = n < s_hi ? n : s_hi;  // rows past the split are masked; read a valid one
       const uint32_t phys = (uint32_t)(n - rbase) & rows.mask;
       const uint32_t off = phys * (part < 2 ? krow_bytes : vrow_bytes) + 16u * x;
-      dma_16B(part < 2 ? krs : vrs, off, slot + part * (G::kHalf * 2) + 1024u * quarter);
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(slot + part * (G::kHalf * 2) + 1024u * quarter);
+      i32x4 rs;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rs[e] = __builtin_amdgcn_readfirstlane(part < 2 ? krs[e] : vrs[e]);
+      // read by this query group only: non-temporal (several groups share them through the caches)
+      if (groups == 1)
+        dma_16B_nt(rs, off, dst);
+      else
+        dma_16B(rs, off, dst);
     }
   };
   // The queries go out first (DMA into qlds, each m-block laid out like a
@@ -727,7 +735,15 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
       n = n < s_hi ? n : s_hi;
       const uint32_t phys = (uint32_t)(n - rbase) & rows.mask;
       const uint32_t off = phys * (part < 2 ? krow_bytes : vrow_bytes) + 16u * x;
-      dma_16B(part < 2 ? krs : vrs, off, slot + part * (G::kHalf * 2) + 1024u * quarter);
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(slot + part * (G::kHalf * 2) + 1024u * quarter);
+      i32x4 rs;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rs[e] = __builtin_amdgcn_readfirstlane(part < 2 ? krs[e] : vrs[e]);
+      // read by this query group only: non-temporal (several groups share them through the caches)
+      if (groups == 1)
+        dma_16B_nt(rs, off, dst);
+      else
+        dma_16B(rs, off, dst);
     }
   };
   // The queries first (each m-block's Q^T operand of k-step s at units

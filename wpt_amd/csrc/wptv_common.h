@@ -186,6 +186,17 @@ __device__ __forceinline__ void dma_16B(i32x4 rsrc, uint32_t voffset, uint32_t l
 }
 #pragma clang diagnostic pop
 
+// The same for data read once (non-temporal: no cache line kept for reuse).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_16B_nt(i32x4 rsrc, uint32_t voffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // Global -> LDS copy of 16 bytes per lane at base + soffset + voffset
 // (soffset uniform): lane l's bytes land at LDS byte address `lds` + 16 l.
 #pragma clang diagnostic push
