@@ -349,8 +349,9 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
       i32x4 rs;
 #pragma unroll
       for (int e = 0; e < 4; ++e) rs[e] = __builtin_amdgcn_readfirstlane(part < 2 ? krs[e] : vrs[e]);
-      // read by this query group only: non-temporal (several groups share them through the caches)
-      if (groups == 1)
+      // a full-context table read by this query group only: non-temporal (several groups, or the
+      // next step's reading of a sliding window, reuse them through the caches)
+      if (groups == 1 && window == 0)
         dma_16B_nt(rs, off, dst);
       else
         dma_16B(rs, off, dst);
@@ -739,8 +740,9 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
       i32x4 rs;
 #pragma unroll
       for (int e = 0; e < 4; ++e) rs[e] = __builtin_amdgcn_readfirstlane(part < 2 ? krs[e] : vrs[e]);
-      // read by this query group only: non-temporal (several groups share them through the caches)
-      if (groups == 1)
+      // a full-context table read by this query group only: non-temporal (several groups, or the
+      // next step's reading of a sliding window, reuse them through the caches)
+      if (groups == 1 && window == 0)
         dma_16B_nt(rs, off, dst);
       else
         dma_16B(rs, off, dst);
