@@ -272,13 +272,17 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   const int j = lane & 15;  // this lane's column: query row (S^T, O^T) or key row (K operand)
   const int g = lane >> 4;  // lane group 0..3
 
+  // Workgroups are dealt to the 8 XCDs in turn: every group and split of a
+  // batch row share one XCD (its L2), where several groups read the same
+  // keys and values
   int unit, split;
   {
     const int L = blockIdx.x;
     if (xcd_map) {
-      const int kk = L >> 3;
-      unit = (L & 7) + 8 * (kk / splits);
-      split = kk % splits;
+      const int slot = L >> 3, per_row = groups * splits;
+      const int bb = (L & 7) + 8 * (slot / per_row), rem = slot % per_row;
+      unit = bb * groups + rem / splits;
+      split = rem % splits;
     } else {
       unit = L / splits;
       split = L % splits;
@@ -671,13 +675,17 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
   const int j = lane & 31;  // this lane's query row (S^T, O^T columns) or key row (K operand)
   const int h = lane >> 5;  // lane half
 
+  // Workgroups are dealt to the 8 XCDs in turn: every group and split of a
+  // batch row share one XCD (its L2), where several groups read the same
+  // keys and values
   int unit, split;
   {
     const int L = blockIdx.x;
     if (xcd_map) {
-      const int kk = L >> 3;
-      unit = (L & 7) + 8 * (kk / splits);
-      split = kk % splits;
+      const int slot = L >> 3, per_row = groups * splits;
+      const int bb = (L & 7) + 8 * (slot / per_row), rem = slot % per_row;
+      unit = bb * groups + rem / splits;
+      split = rem % splits;
     } else {
       unit = L / splits;
       split = L % splits;
@@ -2089,11 +2097,13 @@ int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
     st = launched("verify_attention_keys");
   } else if (p.kind == kRowBlocks32) {
     const int from_positions = (window > 0 || p.groups > 1 || (flags & WPTV_ATTN_RANGE_FROM_POSITIONS)) ? 1 : 0;
+    // the kernel's XCD numbering puts batch row b on XCD b mod 8: a batch count that 8 divides
+    const int xcd_rows = B % 8 == 0 ? 1 : 0;
     auto* po = static_cast<unsigned short*>(part_o);
 #define WPTV_LAUNCH(MM)                                                                                         \
   (tree_base ? launch_m32<MM, true> : launch_m32<MM, false>)(                                                   \
       grid, stream, qb, kb, k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, positions, window, tree_base,   \
-      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_map, rows, gate, ob,       \
+      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_rows, rows, gate, ob,      \
       out_fm, lse, po, part_lse)
     switch (p.mbw / 2) {
       case 1: WPTV_LAUNCH(1); break;
@@ -2107,11 +2117,13 @@ int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
     // Full causal attention of a single query group reads the whole table; any
     // other case takes its key range from the positions.
     const int from_positions = (window > 0 || p.groups > 1 || (flags & WPTV_ATTN_RANGE_FROM_POSITIONS)) ? 1 : 0;
+    // the kernel's XCD numbering puts batch row b on XCD b mod 8: a batch count that 8 divides
+    const int xcd_rows = B % 8 == 0 ? 1 : 0;
     auto* po = static_cast<unsigned short*>(part_o);
 #define WPTV_LAUNCH(CC, MM)                                                                                     \
   (tree_base ? launch_mfma<CC, MM, true> : launch_mfma<CC, MM, false>)(                                         \
       grid, stream, qb, kb, k_stride_b, k_stride_n, vb, v_stride_b, v_stride_n, positions, window, tree_base,   \
-      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_map, rows, gate, ob,       \
+      tree_ancestors, sink, T, H, N, scale_log2, p.groups, p.splits, from_positions, xcd_rows, rows, gate, ob,      \
       out_fm, lse, po, part_lse)
     if (c == 128) {
       switch (p.mbw) {
