@@ -180,6 +180,20 @@ __device__ __forceinline__ void merge_parts(const unsigned short* __restrict__ p
   if (lse && c8 == 0) *lse = L > 0.f ? (M + log2f(L)) * kLn2 : kNegInf;
 }
 
+// The key rows [u_lo, u_hi] in `splits` parts of whole 32-row tiles, as even
+// as they go (the first full % splits parts one tile more); the rows past the
+// last whole tile join the last part as a partial tile, whose DMA re-reads
+// its last row for the rest.  An empty part has s_hi < s_lo.
+__device__ __forceinline__ void split_range(int u_lo, int u_hi, int splits, int split, int& s_lo, int& s_hi) {
+  const int U = u_hi - u_lo + 1;
+  const int full = U / 32, rem = U % 32;
+  const int q = full / splits, r = full % splits;
+  const int first = split * q + min(split, r);
+  const int tiles = q + (split < r ? 1 : 0);
+  s_lo = u_lo + 32 * first;
+  s_hi = s_lo + 32 * tiles - 1 + (split == splits - 1 ? rem : 0);
+}
+
 // ---------------------------------------------------------------------------
 // MFMA kernel
 // ---------------------------------------------------------------------------
@@ -309,13 +323,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
     }
   }
   int s_lo = 0, s_hi = -1;
-  if (u_hi >= u_lo) {
-    const int U = u_hi - u_lo + 1;
-    int per = (U + splits - 1) / splits;
-    per = (per + 32 * kKeySets - 1) / (32 * kKeySets) * (32 * kKeySets);
-    s_lo = u_lo + split * per;
-    s_hi = min(s_lo + per - 1, u_hi);
-  }
+  if (u_hi >= u_lo) split_range(u_lo, u_hi, splits, split, s_lo, s_hi);
   const int ntiles = s_hi >= s_lo ? (s_hi - s_lo + 1 + 31) / 32 : 0;
   const int niter = (ntiles + kKeySets - 1) / kKeySets;       // workgroup iterations
   const int mine = ntiles > kset ? (ntiles - kset + kKeySets - 1) / kKeySets : 0;  // tiles of this key set
@@ -711,13 +719,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
     }
   }
   int s_lo = 0, s_hi = -1;
-  if (u_hi >= u_lo) {
-    const int U = u_hi - u_lo + 1;
-    int per = (U + splits - 1) / splits;
-    per = (per + 32 * kKeySets - 1) / (32 * kKeySets) * (32 * kKeySets);
-    s_lo = u_lo + split * per;
-    s_hi = min(s_lo + per - 1, u_hi);
-  }
+  if (u_hi >= u_lo) split_range(u_lo, u_hi, splits, split, s_lo, s_hi);
   const int ntiles = s_hi >= s_lo ? (s_hi - s_lo + 1 + 31) / 32 : 0;
   const int niter = (ntiles + kKeySets - 1) / kKeySets;
   const int mine = ntiles > kset ? (ntiles - kset + kKeySets - 1) / kKeySets : 0;
