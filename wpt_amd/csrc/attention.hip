@@ -849,7 +849,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
     for (int s = 0; s < kQSteps; ++s) sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s], qf[s], sc, 0, 0, 0);
   };
   typedef short s16x8 __attribute__((ext_vector_type(8)));
-  auto accumulate = [&](int t, const f32x16& sc) {
+  auto accumulate = [&](int t, f32x16& sc) {  // the scores masked in place (no copy)
     const unsigned short* st = ring + (t % G::kSlots) * G::kElems;
     const int n0 = s_lo + (kset + t * kKeySets) * 32;
     // the V^T operands requested before the softmax, whose arithmetic covers their latency
@@ -864,18 +864,16 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
         vt[kk][cb] = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
       }
     }
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = sc[i];
     if (!(n0 >= f_lo && n0 + 31 <= f_hi)) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int n = n0 + 8 * (i >> 2) + 4 * h + (i & 3);
         bool vis = n >= lo && n <= hi;
         if constexpr (TREE) vis = vis && tree_visible(n, tbase, anc);
-        x[i] = vis ? x[i] : kNegInf;
+        sc[i] = vis ? sc[i] : kNegInf;
       }
     }
+    const f32x16& x = sc;
     float mx = score_max(score_max(score_max(x[0], x[1]), score_max(x[2], x[3])),
                          score_max(score_max(x[4], x[5]), score_max(x[6], x[7])));
     mx = score_max(mx, score_max(score_max(score_max(x[8], x[9]), score_max(x[10], x[11])),
@@ -921,7 +919,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
   for (int s = 0; s < kQSteps; ++s)
     qf[s] = *reinterpret_cast<const bf16x8*>(qlds + mb * 32 * C + 512 * s + 8 * lane);
   if (mine > 0) qk(0, s0);
-  auto iteration = [&](int it, const f32x16& cur, f32x16& nxt) {
+  auto iteration = [&](int it, f32x16& cur, f32x16& nxt) {
     arrive(it + 1, min(1, mine - 2 - it));
     if (dma_wave && it + G::kSlots - 1 < mine) issue(it + G::kSlots - 1);
     if (it + 1 < mine) qk(it + 1, nxt);
