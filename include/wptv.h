@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define WPTV_ABI_VERSION 5
+#define WPTV_ABI_VERSION 6
 
 enum {
   WPTV_OK = 0,
@@ -430,6 +430,26 @@ int wptv_accept(const void* scores, int64_t scores_stride_b, int64_t scores_stri
                 int64_t drafts_stride_b, const int32_t* lengths, const float* u, const float* e, float temperature,
                 int top_k, int greedy, int B, int L, int V, int64_t* tokens, int32_t* n_tokens, void* workspace,
                 size_t workspace_bytes, hipStream_t stream);
+
+/* wptv_accept_commit: wptv_accept, and in the same launch as the pick, what
+ *   the verify step does next with each row's count n = n_tokens[b] (the
+ *   reference's Writer._speculate, __init__.py:196-233, after the sampler):
+ *   the cache takes back the rejected drafts (WPT.undo / Rows.undo,
+ *   model.py:475-483, cache.py:69-77): cache_lengths[b] = cache_before[b] +
+ *   n, n taken into 0 .. cache_lengths[b] - cache_before[b]; then, as
+ *   wptv_next_feeds with tokens and n_tokens, the last written token becomes
+ *   feeds[b * feeds_stride], a row with n < 1 keeps its pending token and
+ *   sets *failed = 1 (failed may be NULL), and written[b] += n (written may
+ *   be NULL).  The same results as wptv_accept, wptv_cache_lengths (undo) and
+ *   wptv_next_feeds in turn, in two launches instead of four.
+ *   cache_lengths, cache_before [B] int64; feeds int64. */
+int wptv_accept_commit(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
+                       const int32_t* firsts, const float* q, int64_t q_stride_b, int64_t q_stride_t,
+                       const int64_t* drafts, int64_t drafts_stride_b, const int32_t* lengths, const float* u,
+                       const float* e, float temperature, int top_k, int greedy, int B, int L, int V, int64_t* tokens,
+                       int32_t* n_tokens, void* workspace, size_t workspace_bytes, int64_t* cache_lengths,
+                       const int64_t* cache_before, int64_t* feeds, int64_t feeds_stride, int32_t* failed,
+                       int64_t* written, hipStream_t stream);
 
 /* Greedy verification of a draft tree of M nodes per row (node 0 the root,
  * the token already written; parents[i] < i, parents[0] = -1): from the root,

@@ -230,3 +230,40 @@ def test_bad_shapes_raise_value_error(device):
     with pytest.raises(ValueError):
         sampling.accept(scores, q, torch.zeros(2, 4, dtype=torch.long, device=device), torch.zeros(2, 4, device=device),
                         torch.ones(2, 100, device=device), temperature=0.0)
+
+
+@pytest.mark.parametrize("greedy, top_k", [(False, None), (False, 40), (True, None)])
+def test_the_fused_commit_equals_accept_undo_and_next_feeds(device, greedy, top_k):
+    # wptv_accept_commit against wptv_accept, wptv_cache_lengths (undo) and
+    # wptv_next_feeds in turn, on the same inputs: every output bit for bit;
+    # row 0 has a residual with no mass (count -1: it keeps its pending token,
+    # its cache drops the reading and the flag is raised unless greedy)
+    from wpt_amd.cache import _lengths
+    from wpt_amd.step import next_feeds
+    B, L, V = 48, 4, 4096
+    scores, q, drafts, u, e = step_inputs(B, L, V, seed=77)
+    scores[0] = 0.0
+    q[0] = torch.softmax(scores[0, :L], -1)
+    u[0] = 1.0
+    on = [x.to(device) for x in (scores, q, drafts, u, e)]
+    generator = torch.Generator().manual_seed(5)
+    before = torch.randint(0, 1000, (B,), generator=generator)
+    lengths = before + L + 1
+    lengths[1] = before[1] + 2  # a row that read fewer tokens than it may keep
+    feeds = torch.randint(0, V, (B, L + 1), generator=generator)
+    written = torch.randint(0, 50, (B,), generator=generator)
+    state = [x.to(device) for x in (lengths, before, feeds, written)] + [torch.zeros(1, dtype=torch.int32,
+                                                                                    device=device)]
+    fused = [x.clone() for x in state]
+    t1, c1 = sampling.accept(*on, 0.8, top_k, greedy=greedy)
+    _lengths(state[0], state[1], c1, undo=True)
+    next_feeds(t1, c1, state[2], state[4], state[3])
+    t2, c2 = sampling.accept(*on, 0.8, top_k, greedy=greedy,
+                             commit=(fused[0], fused[1], fused[2], fused[4], fused[3]))
+    assert torch.equal(t1, t2) and torch.equal(c1, c2)
+    for a, b in zip(state, fused):
+        assert torch.equal(a, b)
+    if not greedy:
+        assert int(c2[0]) == -1 and int(fused[4]) == 1
+        assert int(fused[0][0]) == int(before[0]) and torch.equal(fused[2][0].cpu(), feeds[0])
+    assert int(fused[0][1]) <= int(before[1]) + 2

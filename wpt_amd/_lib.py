@@ -12,7 +12,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwptv.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 WPTV_F32, WPTV_BF16 = 0, 1
 DTYPES = {torch.float32: WPTV_F32, torch.bfloat16: WPTV_BF16}
@@ -73,6 +73,8 @@ SIGNATURES = {
     "wptv_accept_workspace": [_I, _I, ctypes.POINTER(_SZ)],
     "wptv_accept": [_P, _I64, _I64, _I, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P, _P,
                     _P, _SZ, _P],
+    "wptv_accept_commit": [_P, _I64, _I64, _I, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P,
+                           _P, _P, _SZ, _P, _P, _P, _I64, _P, _P, _P],
     "wptv_greedy_tree": [_P, _I64, _I64, _I, _P, _P, _I, _I, _I, _P, _P, _P, _P, _SZ, _P],
 }
 

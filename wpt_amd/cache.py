@@ -120,6 +120,15 @@ class Cache:
         _lengths(self.lengths, self.before, kept, undo=True)
         self.pending = False
 
+    def undo_on_device(self):
+        """The lengths and the lengths before the last undoable reading, for a
+        kernel that applies the undo itself (the sampler's commit); the
+        reading counts as undone from here on."""
+        if not self.pending:
+            raise ValueError("no undoable extend to undo")
+        self.pending = False
+        return self.lengths, self.before
+
     def select(self, index):
         """A new cache of the rows index names (a row may come several times),
         copied (the reference's Cache.select, cache.py:157-166)."""

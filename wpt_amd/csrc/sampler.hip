@@ -479,13 +479,40 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
   if (owner) stats.keep[idx] = u[(int64_t)b * L + j] * qs[d] < pd;
 }
 
+// What a verify step does with a row's count once it is known, in the pick's
+// own thread (COMMIT): the cache takes back the rejected drafts (the
+// reference's Rows.undo, cache.py:69-77: lengths = before + kept, kept outside
+// 0 .. the tokens read taken as the nearest end) and the last written token
+// becomes the row's pending token; a row that wrote nothing keeps its pending
+// token and raises *failed.
+struct Commit {
+  int64_t* lengths;
+  const int64_t* before;
+  int64_t* feeds;
+  int64_t feeds_stride;
+  int* failed;
+  int64_t* written;
+};
+
+__device__ inline void commit_row(const Commit& c, int b, int n, int64_t last) {
+  const int64_t start = c.before[b], read = c.lengths[b] - start;
+  c.lengths[b] = start + min(max((int64_t)n, (int64_t)0), read);
+  if (n < 1) {
+    if (c.failed) *c.failed = 1;
+    return;
+  }
+  c.feeds[(int64_t)b * c.feeds_stride] = last;
+  if (c.written) c.written[b] += n;
+}
+
 // Each row's tokens from the per-position decisions: the drafts up to the
 // first rejected one, then that position's draw (the argmax in greedy mode),
 // or every draft and the bonus draw (__init__.py:210-229).  One thread per row.
+template <bool COMMIT>
 __global__ __launch_bounds__(64) void accept_pick(const int64_t* __restrict__ drafts, int64_t db,
                                                   const int32_t* __restrict__ lengths, int greedy, int L, int B,
                                                   Stats stats, int64_t* __restrict__ tokens,
-                                                  int32_t* __restrict__ n_tokens) {
+                                                  int32_t* __restrict__ n_tokens, Commit commit) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
   const int P = L + 1;
@@ -517,6 +544,7 @@ __global__ __launch_bounds__(64) void accept_pick(const int64_t* __restrict__ dr
     for (int t = 0; t < kMaxP; ++t)
       if (t < P) tokens[(int64_t)b * P + t] = t < js ? draft[t] : (t == js ? pick : -1);
     n_tokens[b] = pick >= 0 ? js + 1 : -1;
+    if constexpr (COMMIT) commit_row(commit, b, pick >= 0 ? js + 1 : -1, pick);
     return;
   }
   const int n = lengths ? min(max(lengths[b], 0), L) : L;
@@ -527,6 +555,7 @@ __global__ __launch_bounds__(64) void accept_pick(const int64_t* __restrict__ dr
   const int pick = drawn_at[b * P + js];
   tokens[(int64_t)b * P + js] = pick;
   n_tokens[b] = pick >= 0 ? js + 1 : -1;
+  if constexpr (COMMIT) commit_row(commit, b, pick >= 0 ? js + 1 : -1, pick);
 }
 
 // Greedy walk down a draft tree: node i's parent parents[i] < i, the root 0.
@@ -720,12 +749,13 @@ extern "C" int wptv_accept_workspace(int B, int L, size_t* bytes) {
   return WPTV_OK;
 }
 
-extern "C" int wptv_accept(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
-                           const int32_t* firsts, const float* q, int64_t q_stride_b, int64_t q_stride_t,
-                           const int64_t* drafts, int64_t drafts_stride_b, const int32_t* lengths, const float* u,
-                           const float* e, float temperature, int top_k, int greedy, int B, int L, int V,
-                           int64_t* tokens, int32_t* n_tokens, void* workspace, size_t workspace_bytes,
-                           hipStream_t stream) {
+namespace {
+
+int accept_impl(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
+                const int32_t* firsts, const float* q, int64_t q_stride_b, int64_t q_stride_t, const int64_t* drafts,
+                int64_t drafts_stride_b, const int32_t* lengths, const float* u, const float* e, float temperature,
+                int top_k, int greedy, int B, int L, int V, int64_t* tokens, int32_t* n_tokens, void* workspace,
+                size_t workspace_bytes, const Commit* commit, hipStream_t stream) {
   if (!scores || !tokens || !n_tokens || (L > 0 && !drafts))
     return fail(WPTV_E_INVALID, "accept: scores, tokens, n_tokens (and drafts when L > 0) must be given");
   if (!greedy && (!e || (L > 0 && (!q || !u))))
@@ -745,9 +775,42 @@ extern "C" int wptv_accept(const void* scores, int64_t scores_stride_b, int64_t 
       drafts_stride_b, lengths, u, e, temperature, top_k, greedy, L, V, s);
   int st = launched("accept_stats");
   if (st != WPTV_OK) return st;
-  hipLaunchKernelGGL(accept_pick, dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b, lengths, greedy, L,
-                     B, s, tokens, n_tokens);
+  if (commit)
+    hipLaunchKernelGGL(accept_pick<true>, dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b, lengths,
+                       greedy, L, B, s, tokens, n_tokens, *commit);
+  else
+    hipLaunchKernelGGL(accept_pick<false>, dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b, lengths,
+                       greedy, L, B, s, tokens, n_tokens, Commit{});
   return launched("accept_pick");
+}
+
+}  // namespace
+
+extern "C" int wptv_accept(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
+                           const int32_t* firsts, const float* q, int64_t q_stride_b, int64_t q_stride_t,
+                           const int64_t* drafts, int64_t drafts_stride_b, const int32_t* lengths, const float* u,
+                           const float* e, float temperature, int top_k, int greedy, int B, int L, int V,
+                           int64_t* tokens, int32_t* n_tokens, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream) {
+  return accept_impl(scores, scores_stride_b, scores_stride_t, scores_dtype, firsts, q, q_stride_b, q_stride_t, drafts,
+                     drafts_stride_b, lengths, u, e, temperature, top_k, greedy, B, L, V, tokens, n_tokens, workspace,
+                     workspace_bytes, nullptr, stream);
+}
+
+extern "C" int wptv_accept_commit(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t,
+                                  int scores_dtype, const int32_t* firsts, const float* q, int64_t q_stride_b,
+                                  int64_t q_stride_t, const int64_t* drafts, int64_t drafts_stride_b,
+                                  const int32_t* lengths, const float* u, const float* e, float temperature, int top_k,
+                                  int greedy, int B, int L, int V, int64_t* tokens, int32_t* n_tokens,
+                                  void* workspace, size_t workspace_bytes, int64_t* cache_lengths,
+                                  const int64_t* cache_before, int64_t* feeds, int64_t feeds_stride, int32_t* failed,
+                                  int64_t* written, hipStream_t stream) {
+  if (!cache_lengths || !cache_before || !feeds)
+    return fail(WPTV_E_INVALID, "accept_commit: cache_lengths, cache_before and feeds must be given");
+  const Commit c{cache_lengths, cache_before, feeds, feeds_stride, failed, written};
+  return accept_impl(scores, scores_stride_b, scores_stride_t, scores_dtype, firsts, q, q_stride_b, q_stride_t, drafts,
+                     drafts_stride_b, lengths, u, e, temperature, top_k, greedy, B, L, V, tokens, n_tokens, workspace,
+                     workspace_bytes, &c, stream);
 }
 
 extern "C" int wptv_greedy_tree(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t,

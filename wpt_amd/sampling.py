@@ -61,14 +61,21 @@ def draws(B, L, V, generator=None, device="cuda"):
     return u, e
 
 
-def accept(scores, q, drafts, u, e, temperature=0.8, top_k=40, lengths=None, firsts=None, greedy=False):
+def accept(scores, q, drafts, u, e, temperature=0.8, top_k=40, lengths=None, firsts=None, greedy=False,
+           commit=None):
     """Each row's written tokens: (tokens (B, L + 1) int64, -1 past a row's
     count; counts (B,) int32 = kept drafts + 1).
 
     scores (B, >= L + 1, V) FP32 or bf16: row b's position j is scores[b, firsts[b] + j]
     (firsts None: 0); q (B, L, V) FP32 the drafts' distributions; drafts (B, L)
     int64; u, e the tape (draws); lengths (B,) the drafts each row verifies
-    (None: L).  greedy: keep the drafts equal to the argmax (q, u, e unused)."""
+    (None: L).  greedy: keep the drafts equal to the argmax (q, u, e unused).
+
+    commit (cache_lengths, cache_before, feeds, failed, written): the verify
+    step's next moves in the same launch as the pick (wptv_accept_commit):
+    cache_lengths = cache_before + counts (the undo), feeds[:, 0] = each
+    row's last written token (a row with none keeps it and sets failed),
+    written += counts; failed and written may be None."""
     scores = _scores(scores)
     B, _, V = scores.shape
     if drafts.dim() != 2 or drafts.shape[0] != B:
@@ -106,12 +113,26 @@ def accept(scores, q, drafts, u, e, temperature=0.8, top_k=40, lengths=None, fir
     tokens = torch.empty(B, L + 1, dtype=torch.long, device=device)
     counts = torch.empty(B, dtype=torch.int32, device=device)
     workspace, size = _workspace(device, B, L)
-    check(_lib.lib().wptv_accept(ptr(scores), scores.stride(0), scores.stride(1), _lib.dtype_code(scores.dtype),
-                                 ptr(firsts_), ptr(q),
-                                 q.stride(0) if q is not None else 0, q.stride(1) if q is not None else 0,
-                                 ptr(drafts), drafts.stride(0), ptr(lengths_), ptr(u), ptr(e), float(temperature),
-                                 0 if top_k is None else int(top_k), 1 if greedy else 0, B, L, V, ptr(tokens),
-                                 ptr(counts), ptr(workspace), size, _lib.stream(device)), "accept")
+    args = (ptr(scores), scores.stride(0), scores.stride(1), _lib.dtype_code(scores.dtype), ptr(firsts_), ptr(q),
+            q.stride(0) if q is not None else 0, q.stride(1) if q is not None else 0, ptr(drafts), drafts.stride(0),
+            ptr(lengths_), ptr(u), ptr(e), float(temperature), 0 if top_k is None else int(top_k),
+            1 if greedy else 0, B, L, V, ptr(tokens), ptr(counts), ptr(workspace), size)
+    if commit is None:
+        check(_lib.lib().wptv_accept(*args, _lib.stream(device)), "accept")
+        return tokens, counts
+    cache_lengths, cache_before, feeds, failed, written = commit
+    for name, t in (("cache_lengths", cache_lengths), ("cache_before", cache_before)):
+        if t.dtype != torch.int64 or t.shape != (B,) or not t.is_contiguous() or t.device != device:
+            raise ValueError(f"{name} must be a contiguous ({B},) int64 tensor on {device}")
+    if feeds.dtype != torch.int64 or feeds.shape[0] != B or feeds.device != device:
+        raise ValueError(f"feeds must be ({B}, n) int64 on {device}")
+    if failed is not None and (failed.dtype != torch.int32 or failed.numel() < 1 or failed.device != device):
+        raise ValueError("failed must be an int32 device tensor")
+    if written is not None and (written.dtype != torch.int64 or written.shape != (B,) or not written.is_contiguous()
+                                or written.device != device):
+        raise ValueError(f"written must be a contiguous ({B},) int64 tensor on {device}")
+    check(_lib.lib().wptv_accept_commit(*args, ptr(cache_lengths), ptr(cache_before), ptr(feeds), feeds.stride(0),
+                                        ptr(failed), ptr(written), _lib.stream(device)), "accept_commit")
     return tokens, counts
 
 

@@ -25,6 +25,8 @@ import torch
 
 from . import _lib, sampling
 from ._lib import check, ptr
+from .cache import Cache
+from .decoder import MQADecoder
 
 
 def next_feeds(tokens, counts, feeds, failed=None, written=None):
@@ -64,16 +66,22 @@ class VerifyStep:
         """One eager step; returns (tokens (B, k + 1), counts (B,)) on the device."""
         scores, _ = self.model.extend(self.feeds, self.cache, undoable=True, logits=True)  # read as they come
         drafts = self.feeds[:, 1:]
-        if self.greedy:
-            tokens, counts = sampling.greedy_chain(scores, drafts)
+        if not (self.greedy or self.given_tape):
+            B, V = scores.shape[0], scores.shape[-1]
+            self.u, self.e = sampling.draws(B, self.k, V, device=scores.device)
+        # the pick's kernel also takes back the rejected drafts (the model's
+        # undo, which for this cache is its lengths alone), makes the drawn
+        # token each row's next pending token and grows the running counts
+        if isinstance(self.cache, Cache) and type(self.model).undo is MQADecoder.undo:
+            lengths, before = self.cache.undo_on_device()
+            commit = (lengths, before, self.feeds, self.failed, self.written)
         else:
-            if not self.given_tape:
-                B, V = scores.shape[0], scores.shape[-1]
-                self.u, self.e = sampling.draws(B, self.k, V, device=scores.device)
-            tokens, counts = sampling.accept(scores, self.q, drafts, self.u, self.e, self.temperature, self.top_k)
-        self.model.undo(self.cache, counts)
-        # the drawn token is each row's next pending token; the running counts grow
-        next_feeds(tokens, counts, self.feeds, self.failed, self.written)
+            commit = None
+        tokens, counts = sampling.accept(scores, self.q, drafts, self.u, self.e, self.temperature, self.top_k,
+                                         greedy=self.greedy, commit=commit)
+        if commit is None:
+            self.model.undo(self.cache, counts)
+            next_feeds(tokens, counts, self.feeds, self.failed, self.written)
         self.tokens, self.counts, self.scores = tokens, counts, scores
         return tokens, counts
 
