@@ -283,16 +283,6 @@ def attention_c3(steps, warmup):
             "note": "4.5 MB a call: launch-latency-bound; the three tables' windows stay in the Infinity Cache"}
 
 
-def head_product(x, head):
-    """An lm_head's bf16 logits as the decoder computes them: the build's
-    product up to HEAD_MAX_ROWS rows, hipBLASLt (torch) above."""
-    import torch.nn.functional as F
-
-    from wpt_amd import layers
-
-    if x.numel() // x.shape[-1] <= layers.HEAD_MAX_ROWS:
-        return layers.linear(x, head)
-    return F.linear(x, head)
 
 
 def tree_c4(steps, warmup):
@@ -311,13 +301,16 @@ def tree_c4(steps, warmup):
     q = torch.randn(B, M, H, c, generator=generator, device=device).to(torch.bfloat16)
     table = torch.randn(B, prefix + M, 2 * c, generator=generator, device=device).to(torch.bfloat16)
     head = (torch.randn(V, H * c, generator=generator, device=device) * 0.02).to(torch.bfloat16)
+    head_fm = layers.FmWeight(head)  # packed once, as a model's weights are
     node_tokens = torch.randint(V, (B, M), generator=generator, device=device)
     base = torch.full((B,), prefix, device=device)
     written = torch.zeros(B, dtype=torch.long, device=device)
 
     def step(count=False):
-        o = kernels.tree_attention(q, table[..., :c], table[..., c:], base, parents, c ** -0.5)
-        scores = head_product(o.reshape(B, M, H * c), head)  # bf16 logits, read by the sampler as they come
+        # the nodes' attention output written as the lm_head's fm operand, the
+        # head on the 256 x 256 tiles: bf16 logits, read by the walk as they come
+        o = kernels.tree_attention(q, table[..., :c], table[..., c:], base, parents, c ** -0.5, out_fm=True)
+        scores = layers.linear_fm_wide(o, B * M, head_fm).view(B, M, V)
         _, _, counts = sampling.greedy_tree(scores, node_tokens, parents)
         if count:  # counted in a graph of its own, outside the timed one
             written.add_(counts.long())

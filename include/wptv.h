@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define WPTV_ABI_VERSION 6
+#define WPTV_ABI_VERSION 7
 
 enum {
   WPTV_OK = 0,
@@ -311,11 +311,13 @@ int wptv_heads_rms_norm(const void* x, int64_t row_stride, const float* weight, 
 int wptv_swiglu(const void* gate_up, void* out, int M, int F, int dtype, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
- * Skinny matrix products on the matrix cores: out[M, N] = x[M, K] . w[N, K]^T
- * in bf16 with FP32 accumulation -- the reference's nn.Linear projections and
+ * Matrix products on the matrix cores: out[M, N] = x[M, K] . w[N, K]^T in
+ * bf16 with FP32 accumulation -- the reference's nn.Linear projections and
  * lm_head under bf16 autocast (packages/wpt-model/src/wpt_model/
- * attention.py:113-124,157-168, layers.py:45-61, model.py:267,471), at the
- * verify step's few rows (M <= 512; N a multiple of 64, K of 64).
+ * attention.py:113-124,157-168, layers.py:45-61, model.py:267,471): the
+ * skinny products at the verify step's few rows (M <= 512; N a multiple of
+ * 64, K of 64), and with splits 0 above 320 rows the 256 x 256 tiles (any
+ * M; N a multiple of 256, K of 32; no workspace).
  *
  *   x, w       row-major bf16 with leading dimensions ldx, ldw (elements)
  *   out        [M, N] with leading dimension ldo: bf16 (out_dtype
@@ -386,6 +388,19 @@ int wptv_gemm_fm_parts(const void* x_fm, const void* w_fm, int M, int N, int K, 
                        size_t parts_bytes, hipStream_t stream);
 
 int wptv_gemm_fm_swiglu(const void* x_fm, const void* w_fm, int M, int N, int K, void* out_fm, hipStream_t stream);
+
+/* wptv_gemm_fm_wide: out [M, N] = x . w^T over many rows -- the lm_head of a
+ *   reading wider than the skinny products serve (model.py:471 under bf16
+ *   autocast: the tree verification's 16 x 31 = 496 node rows against the
+ *   [32768 x 2048] head) -- on 256 x 256 output tiles, one workgroup of eight
+ *   wavefronts each.  x_fm: fm with x_blocks >= wptv_fm_row_blocks(M) row
+ *   blocks; w_fm: fm with N / 16 row blocks (wptv_fm_pack); N a multiple of
+ *   256, K of 32.  out: bf16 (out_dtype WPTV_BF16) or FP32 holding the
+ *   bf16-rounded product (WPTV_F32, the reference's .float() of the bf16
+ *   logits), leading dimension ldo (a multiple of 8, >= N).  One pass, no
+ *   workspace. */
+int wptv_gemm_fm_wide(const void* x_fm, int x_blocks, const void* w_fm, int M, int N, int K, void* out, int64_t ldo,
+                      int out_dtype, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Acceptance: the reference's per-row verification loop of

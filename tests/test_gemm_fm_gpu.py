@@ -152,3 +152,43 @@ def test_verify_attention_writes_the_same_bits_in_the_fm_layout(device, B, N, sp
     out = kernels.verify_attention(q, k, v, positions, c ** -0.5, splits=splits)
     out_fm = kernels.verify_attention(q, k, v, positions, c ** -0.5, splits=splits, out_fm=True)
     assert torch.equal(layers.fm_unpack(out_fm, B * T, H * c), out.reshape(B * T, H * c))
+
+
+@pytest.mark.parametrize("M, N, K", [
+    (496, 32768, 2048),   # the tree verification's lm_head (16 x 31 node rows)
+    (600, 512, 256),      # three row tiles, the last partial; two column tiles
+    (321, 768, 64),       # the fewest rows of the wide tiles; two K chunks
+    (1100, 2048, 2048),   # five row tiles by eight column tiles
+    (40, 256, 32),        # one row tile, one K chunk, rows not a multiple of 16
+])
+def test_the_wide_fm_product_is_the_row_major_wide_product(device, M, N, K):
+    # the same 256 x 256 tiles and 32x32x16 products on fm operands: the same
+    # bits as the row-major form (which runs above 320 rows), within one bf16
+    # rounding of an FP32 product
+    x, w = operands(M, N, K, seed=M + K, device=device)
+    got = layers.linear_fm_wide(layers.fm_pack(x), M, layers.FmWeight(w))
+    assert got.shape == (M, N) and got.dtype == torch.bfloat16
+    if M >= layers.WIDE_MIN_ROWS:
+        assert torch.equal(got, layers.linear(x, w))
+    assert relative_error(got.float().cpu(), (x.float() @ w.float().T).cpu()) < 1e-2
+    wide32 = layers.linear_fm_wide(layers.fm_pack(x), M, layers.FmWeight(w), out_dtype=torch.float32)
+    assert torch.equal(wide32, got.float())
+
+
+def test_the_wide_fm_product_reads_x_with_more_row_blocks(device):
+    # an fm operand holding more row blocks than its rows need (a producer's
+    # padding): the rows past M are never read into the output
+    M, N, K = 300, 512, 128
+    x, w = operands(M, N, K, seed=3, device=device)
+    padded = layers.fm_pack(x, 40)  # 640 rows of storage for 300
+    assert torch.equal(layers.linear_fm_wide(padded, M, layers.FmWeight(w)),
+                       layers.linear_fm_wide(layers.fm_pack(x), M, layers.FmWeight(w)))
+
+
+def test_the_wide_fm_product_refuses_bad_shapes(device):
+    x, w = operands(64, 320, 64, seed=4, device=device)
+    with pytest.raises(ValueError):
+        layers.linear_fm_wide(layers.fm_pack(x), 64, layers.FmWeight(w))  # N not a multiple of 256
+    x2, w2 = operands(64, 256, 64, seed=4, device=device)
+    with pytest.raises(ValueError):
+        layers.linear_fm_wide(layers.fm_pack(x2)[: 2 * 16 * 64], 64, layers.FmWeight(w2))  # too few row blocks

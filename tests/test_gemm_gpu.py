@@ -32,6 +32,11 @@ def operands(M, N, K, seed, device):
     (496, 32768, 2048, 0),   # the tree config's lm_head over 16 x 31 node rows
     (17, 192, 320, 3),       # rows that are not a multiple of 16, an uneven K split
     (64, 128, 64, 1),        # one K chunk
+    # the wide 256 x 256 tiles (above 320 rows, N a multiple of 256, K of 32)
+    (321, 256, 64, 0),       # the fewest rows they take; two K chunks, fewer than the ring's lead
+    (600, 512, 256, 0),      # three row tiles, the last one partial; two column tiles (no XCD grouping)
+    (1100, 2048, 2048, 0),   # five row tiles by 8 column tiles (the XCD grouping)
+    (512, 768, 32, 0),       # one K chunk
 ])
 def test_linear_matches_the_fp32_product(device, M, N, K, splits):
     x, w = operands(M, N, K, seed=M + N + K, device=device)
@@ -60,6 +65,33 @@ def test_wide_fp32_output_is_the_bf16_rounded_product(device):
     assert torch.equal(got, layers.linear(x, w).float())
 
 
+def test_wide_tiles_fp32_output_is_the_bf16_rounded_product(device):
+    # the wide tiles' FP32 output holds the bf16 output's values (the
+    # reference's .float() of the autocast product), rows past the last whole tile included
+    M, N, K = 496, 4096, 2048
+    x, w = operands(M, N, K, seed=11, device=device)
+    got = layers.linear(x, w, out_dtype=torch.float32)
+    assert got.dtype == torch.float32 and got.shape == (M, N)
+    assert torch.equal(got, layers.linear(x, w).float())
+    assert relative_error(got.cpu(), (x.float() @ w.float().T).cpu()) < 1e-2
+
+
+def test_wide_tiles_write_no_row_past_the_output(device):
+    # a 330-row output inside a larger buffer: the rows after it stay untouched
+    M, N, K = 330, 512, 128
+    x, w = operands(M, N, K, seed=12, device=device)
+    buffer = torch.full((M + 40, N), 7.0, dtype=torch.bfloat16, device=device)
+    from wpt_amd import _lib
+
+    check = _lib.check
+    library = _lib.lib()
+    check(library.wptv_gemm(x.data_ptr(), K, w.data_ptr(), K, M, N, K, buffer.data_ptr(), N,
+                            _lib.dtype_code(torch.bfloat16), 0, None, 0, _lib.stream(device)), "gemm")
+    torch.cuda.synchronize()
+    assert torch.all(buffer[M:] == 7.0)
+    assert relative_error(buffer[:M].float().cpu(), (x.float() @ w.float().T).cpu()) < 1e-2
+
+
 def test_splits_agree(device):
     M, N, K = 160, 512, 2048
     x, w = operands(M, N, K, seed=6, device=device)
@@ -76,7 +108,8 @@ def test_batched_rows_and_bad_shapes(device):
     with pytest.raises(NotImplementedError):
         layers.linear(x, w[:100])            # N not a multiple of 64
     with pytest.raises(NotImplementedError):
-        layers.linear(torch.zeros(600, 128, dtype=torch.bfloat16, device=device), w)  # above 512 rows
+        # above 512 rows only the wide tiles serve, and they need N a multiple of 256
+        layers.linear(torch.zeros(600, 128, dtype=torch.bfloat16, device=device), w[:192])
     with pytest.raises(ValueError):
         layers.linear(x.float(), w)
 

@@ -218,9 +218,15 @@ def test_tree_verification_at_its_workload_size(device):
     td = table.to(device)
     o = kernels.tree_attention(q.to(device), td[..., :c], td[..., c:], prefixes.to(device), parents, c ** -0.5)
     assert relative_error(o.cpu(), expected) < 1e-2
-    # bf16 logits, read by the sampler as they come: the build's product (it
-    # is the step's at up to 320 rows; test_gemm_gpu covers it at these 496)
-    logits = layers.linear(o.reshape(B, M, H * c), head.to(device))
+    # the benchmark's path: the attention output as the lm_head's fm operand
+    # (the same bits), the head on the wide tiles, bf16 logits read by the walk
+    o_fm = kernels.tree_attention(q.to(device), td[..., :c], td[..., c:], prefixes.to(device), parents, c ** -0.5,
+                                  out_fm=True)
+    assert torch.equal(layers.fm_unpack(o_fm, B * M, H * c), o.reshape(B * M, H * c))
+    head_d = head.to(device)
+    logits = layers.linear_fm_wide(o_fm, B * M, layers.FmWeight(head_d)).view(B, M, V)
+    expected_logits = o.reshape(B * M, H * c).float().cpu() @ head.float().T
+    assert relative_error(logits.reshape(B * M, V).float().cpu(), expected_logits) < 1e-2
     best = oracle_sampling.first_argmax(logits.float().cpu())
     node_tokens = plant_paths(best, parents, B)
     path, tokens, counts = sampling.greedy_tree(logits, node_tokens.to(device), parents)

@@ -245,6 +245,10 @@ __global__ __launch_bounds__(256) void gemm_reduce(const float* __restrict__ par
 }
 
 constexpr int kMaxGemmRows = 512;  // 8 row blocks per wavefront
+// Above this many rows an unsplit product runs on the wide tiles (gemm_wide.hip):
+// measured on the MI355X at the lm_head's 32768 x 2048, the skinny product
+// reaches hipBLASLt's time up to 320 rows only.
+constexpr int kWideMinRows = 321;
 
 struct GemmPlan {
   int r32;     // staged X rows / 32
@@ -252,11 +256,22 @@ struct GemmPlan {
   int cps;     // K chunks per split
   int tn;      // output columns per workgroup
   size_t bytes;
+  bool wide;   // the 256 x 256 tiles of gemm_wide
 };
 
-int gemm_plan(int M, int N, int K, int requested, GemmPlan* p) {
+int gemm_plan(int M, int N, int K, int requested, GemmPlan* p, bool allow_wide = false) {
   if (M <= 0 || N <= 0 || K <= 0)
     return fail(WPTV_E_INVALID, "gemm: M, N and K must be positive (got %d, %d, %d)", M, N, K);
+  p->wide = false;
+  if (allow_wide && M >= kWideMinRows && requested <= 0 && gemm_wide_fits(M, N, K)) {
+    p->wide = true;
+    p->r32 = 0;
+    p->splits = 1;
+    p->cps = K / kChunkK;
+    p->tn = 256;
+    p->bytes = 0;
+    return WPTV_OK;
+  }
   if (M > kMaxGemmRows) return fail(WPTV_E_UNSUPPORTED, "gemm: M = %d above %d rows", M, kMaxGemmRows);
   if (N % kTileN || K % kChunkK)
     return fail(WPTV_E_UNSUPPORTED, "gemm: N (%d) must be a multiple of %d and K (%d) of %d", N, kTileN, K, kChunkK);
@@ -316,7 +331,7 @@ using namespace wptv;
 extern "C" int wptv_gemm_workspace(int M, int N, int K, int* splits, size_t* bytes) {
   if (!splits || !bytes) return fail(WPTV_E_INVALID, "gemm_workspace: null output pointer");
   GemmPlan p;
-  const int st = gemm_plan(M, N, K, *splits, &p);
+  const int st = gemm_plan(M, N, K, *splits, &p, true);
   if (st != WPTV_OK) return st;
   *splits = p.splits;
   *bytes = p.bytes;
@@ -371,7 +386,7 @@ extern "C" int wptv_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw,
   if (out_dtype != WPTV_BF16 && out_dtype != WPTV_F32)
     return fail(WPTV_E_UNSUPPORTED, "gemm: output dtype %d is neither bf16 nor fp32", out_dtype);
   GemmPlan p;
-  int st = gemm_plan(M, N, K, splits, &p);
+  int st = gemm_plan(M, N, K, splits, &p, true);
   if (st != WPTV_OK) return st;
   if (ldx < K || ldw < K || ldo < N) return fail(WPTV_E_INVALID, "gemm: a leading dimension below the row width");
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16) || ldx % 8 || ldw % 8 || ldo % 4)
@@ -381,6 +396,7 @@ extern "C" int wptv_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw,
   if (p.splits > 1 && (!workspace || workspace_bytes < p.bytes))
     return fail(WPTV_E_INVALID, "gemm: workspace of %zu bytes, %zu needed for %d splits", workspace_bytes, p.bytes,
                 p.splits);
+  if (p.wide) return gemm_wide(x, ldx, w, ldw, M, N, K, out, ldo, out_dtype, stream);
   const auto* xb = static_cast<const unsigned short*>(x);
   const auto* wb = static_cast<const unsigned short*>(w);
   dim3 grid(N / p.tn, p.splits);

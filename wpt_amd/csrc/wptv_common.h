@@ -21,6 +21,12 @@ int launched(const char* kernel);
 // Compute units of the current device (cached per device).
 int compute_units();
 
+// The wide-tile product (gemm_wide.hip): out[M, N] = x . w^T on 256 x 256
+// tiles, for readings of more rows than the skinny products take.
+bool gemm_wide_fits(int M, int N, int K);
+int gemm_wide(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K, void* out, int64_t ldo,
+              int out_dtype, hipStream_t stream);
+
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }

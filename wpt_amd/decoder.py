@@ -37,8 +37,10 @@ On the GPU:
                     block; wptv_gemm's split-K parts otherwise up to
                     SPLIT_K_ROWS bf16 rows (summed by qkv_post and the
                     residual add + norm), the gate/up product with SwiGLU in
-                    its epilogue (wptv_gemm_swiglu) at up to 512 bf16 rows,
-                    the lm_head up to 320 rows; hipBLASLt beyond
+                    its epilogue (wptv_gemm_swiglu) at up to 512 bf16 rows;
+                    the lm_head on wptv_gemm (the skinny products up to 320
+                    rows, the 256 x 256 tiles above); hipBLASLt only for a
+                    prefill's wider layer products
     window layers   wptv_window_qkv_post (norms, rotary encoding, the ring
                     append), wptv_window_attention over the cache's ring with
                     the sink and the output gate fused
@@ -421,11 +423,14 @@ class MQADecoder:
             handoff = self._layer(i, h, x, cache, positions, counts_, next_norm, handoff, xf)
         if self.config.layers in features:
             found[self.config.layers] = h.float()
-        if x.dtype == torch.bfloat16 and B * T <= layers.HEAD_MAX_ROWS:
-            # the build's product; FP32 output = the bf16 product's values, the reference's .float()
-            scores = layers.linear(x, self.w["head"], out_dtype=torch.bfloat16 if logits else torch.float32)
+        head = self.w["head"]
+        if x.dtype == torch.bfloat16 and (B * T <= layers.LINEAR_MAX_ROWS
+                                          or layers.wide_tiles(B * T, head.shape[0], head.shape[1])):
+            # the build's product (the skinny products up to 320 rows, the wide tiles
+            # above); FP32 output = the bf16 product's values, the reference's .float()
+            scores = layers.linear(x, head, out_dtype=torch.bfloat16 if logits else torch.float32)
         else:
-            scores = F.linear(x, self.w["head"])
+            scores = F.linear(x, head)
             if not logits:
                 scores = scores.float()
         cache.finish(counts_, undoable, T)

@@ -310,18 +310,20 @@ def tree_ancestors(parents):
     return torch.tensor([m - (1 << 64) if m >= 1 << 63 else m for m in masks], dtype=torch.long)
 
 
-def tree_attention(q, k, v, tree_base, parents, scale, sink=None):
+def tree_attention(q, k, v, tree_base, parents, scale, sink=None, out_fm=False):
     """Attention of the M draft-tree nodes (q (B, M, H, c), node i at table
     row tree_base[b] + i) over the prefix rows before tree_base[b] and over
     the node's ancestors and itself: the reference's dense_attention
-    (attention.py:74-82) with the mask "prefix plus ancestors-or-self"."""
+    (attention.py:74-82) with the mask "prefix plus ancestors-or-self".
+    out_fm: the output as a flat fm operand of B M rows x H c (the lm_head's
+    X, layers.linear_fm_wide)."""
     base = tree_base.to(device=q.device, dtype=torch.long)
     key = (tuple(int(p) for p in parents), q.device)
     masks = _TREES.get(key)
     if masks is None:  # made once per tree and device, outside any graph capture
         masks = _TREES[key] = tree_ancestors(parents).to(q.device)
     # node i's position, tree_base[b] + i, is formed by the kernel
-    return verify_attention(q, k, v, None, scale, sink=sink, tree=(base, masks))
+    return verify_attention(q, k, v, None, scale, sink=sink, tree=(base, masks), out_fm=out_fm)
 
 
 _TREES = {}  # (parents, device) -> the ancestors-or-self masks on the device

@@ -10,12 +10,8 @@ from . import _lib
 from ._lib import KernelUnavailable, check, ptr
 
 EPS = 1e-6
-LINEAR_MAX_ROWS = 512  # rows wptv_gemm takes
-# Rows up to which an lm_head (32768 x 2048) runs on wptv_gemm's 128-column
-# tiles: 46 against hipBLASLt's 43 us at 160 rows, 71 against 53 at 320, 98
-# against 64 at 496 (its X chunks then leave the ring two slots); above it,
-# hipBLASLt.
-HEAD_MAX_ROWS = 320
+LINEAR_MAX_ROWS = 512  # rows wptv_gemm's skinny products take
+WIDE_MIN_ROWS = 321   # from here an unsplit wptv_gemm runs on the 256 x 256 tiles
 
 
 def _gpu(*tensors):
@@ -167,11 +163,19 @@ def swiglu(gate_up):
     return out
 
 
+def wide_tiles(M, N, K):
+    """Whether wptv_gemm runs an unsplit product of M rows on its 256 x 256
+    tiles (gemm_wide.hip): above 320 rows, N a multiple of 256, K of 32."""
+    return M >= WIDE_MIN_ROWS and N % 256 == 0 and K % 32 == 0
+
+
 def linear(x, w, out_dtype=None, splits=0):
     """x (..., K) . w (N, K)^T on the matrix cores (the projections' and the
     lm_head's nn.Linear under bf16 autocast): bf16 operands, FP32
     accumulation; out_dtype bfloat16 (default) or float32 (the bf16-rounded
-    product as FP32).  At most 512 rows; N and K multiples of 64."""
+    product as FP32).  Up to 512 rows on the skinny products (N and K
+    multiples of 64); with splits 0, above 320 rows, any number of rows on the
+    wide tiles (N a multiple of 256, K of 32)."""
     _gpu(x, w)
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
         raise ValueError(f"linear takes bf16 operands; got {x.dtype} and {w.dtype}")
@@ -188,7 +192,8 @@ def linear(x, w, out_dtype=None, splits=0):
     library = _lib.lib()
     parts = _lib.ctypes.c_int(int(splits))
     size = _lib.ctypes.c_size_t(0)
-    check(library.wptv_gemm_workspace(M, N, K, _lib.ctypes.byref(parts), _lib.ctypes.byref(size)), "gemm")
+    if not (splits == 0 and wide_tiles(M, N, K)):  # the wide tiles need no split count and no workspace
+        check(library.wptv_gemm_workspace(M, N, K, _lib.ctypes.byref(parts), _lib.ctypes.byref(size)), "gemm")
     workspace = torch.empty(size.value, dtype=torch.uint8, device=x.device) if size.value else None
     out = torch.empty(M, N, dtype=out_dtype, device=x.device)
     check(library.wptv_gemm(ptr(x2), x2.stride(0), ptr(w), w.stride(0), M, N, K, ptr(out), out.stride(0), code,
@@ -355,6 +360,21 @@ def linear_fm_parts(x_fm, rows, w, splits=0):
     out = torch.empty(parts.value, rows, N, dtype=torch.float32, device=x_fm.device)
     check(library.wptv_gemm_fm_parts(ptr(x_fm), ptr(w.data), rows, N, K, parts.value, ptr(out), out.numel() * 4,
                                      _lib.stream(x_fm.device)), "gemm_fm_parts")
+    return out
+
+
+def linear_fm_wide(x_fm, rows, w, out_dtype=torch.bfloat16):
+    """x . w^T on the 256 x 256 tiles: x a flat fm operand of rows x K, w an
+    FmWeight (N, K), N a multiple of 256 (wptv_gemm_fm_wide; the lm_head of a
+    reading of many rows).  Returns (rows, N) bf16, or FP32 holding the
+    bf16-rounded product."""
+    _gpu(x_fm, w.data)
+    N, K = w.shape
+    _fm_output(x_fm, rows, K)
+    blocks = x_fm.numel() // (16 * K)  # every row block the operand holds
+    out = torch.empty(rows, N, dtype=out_dtype, device=x_fm.device)
+    check(_lib.lib().wptv_gemm_fm_wide(ptr(x_fm), blocks, ptr(w.data), rows, N, K, ptr(out), out.stride(0),
+                                       _lib.dtype_code(out_dtype), _lib.stream(x_fm.device)), "gemm_fm_wide")
     return out
 
 
