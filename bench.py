@@ -216,8 +216,8 @@ def drafted_writer(model, B, kv, k, rounds=8, warmup=2, seed=0):
             "tokens_per_row_round": written / rounds / B, "draft_ms": min(draft_s) * 1e3,
             "drafter": {"features": list(config.features), "layers": config.layers, "block": config.block,
                         "markov_rank": config.markov_rank},
-            "note": "eager Writer rounds (host lists, one synchronization per round), the reference's protocol; "
-                    "the captured verify step alone is the headline"}
+            "note": "eager Writer rounds (the drafts laid into the feed on the device, one synchronization per "
+                    "round), the reference's protocol; the captured verify step alone is the headline"}
 
 
 # ---------------------------------------------------------------------------
@@ -700,6 +700,9 @@ def main():
     parser.add_argument("--tree", action="store_true",
                         help="only the tree workload (batch 16, 8192 prefix rows, 31 nodes, lm_head, greedy walk); "
                              "prints its JSON")
+    parser.add_argument("--writer", action="store_true",
+                        help="only the drafted Writer rounds over the 24-layer decoder (batch 32, KV 4096, k 4); "
+                             "prints their JSON")
     parser.add_argument("--pmc-workload", action="store_true",
                         help="for a counter pass: five verify-attention calls of the roofline shape, then five "
                              "plain 64 MiB device copies (the counters' calibration); prints no JSON")
@@ -712,6 +715,10 @@ def main():
         return
     if args.tree:
         print(json.dumps(tree_c4(args.steps, args.warmup)), flush=True)
+        return
+    if args.writer:
+        model = decoder_step(32, 4096, 4, 2, 1, keep=True)["_pieces"][0]
+        print(json.dumps(drafted_writer(model, 32, 4096, 4)), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the verify step here is built and timed on a single MI355X "

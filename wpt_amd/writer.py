@@ -1,49 +1,76 @@
-"""Speculative writing with the verify step on the GPU: the reference's Writer
-(packages/wpt-inference/src/wpt_inference/__init__.py:71-233) with the same
-signature, protocol and counters, its acceptance loop replaced by the fused
-HIP sampler (wpt_amd.sampling).
+"""Speculative writing around the GPU verify step: the reference's Writer
+interface (packages/wpt-inference/src/wpt_inference/__init__.py:71-233:
+constructor arguments, `write`, the rounds/verified/accepted counters and the
+drafter protocol), built on this package's device-resident pieces.
 
-What differs from the reference, by design:
-    the draws    the reference draws lazily from `generator` (torch.rand per
-                 draft it looks at, torch.multinomial per row, :214-222);
-                 here each step draws one tape up front from the same
-                 generator (sampling.draws: u (rows, drafts), e (rows, V)),
-                 and every row is decided on the GPU at once.  The tokens
-                 follow the same distribution; a tape made from a lazy run's
-                 draws replays it exactly.
-    host syncs   one per step (the written tokens), instead of one per draft
-                 token (:213, :215, :219, :222).
-With a drafter that gives confidences and a table of pass times (costs), each
-step verifies only the drafts the prefix scheduler admits
-(wpt_amd.scheduling.schedule, the reference's :236-262), as the reference does.
-A drafter that reads the model's features (drafter.features, the layers whose
-hidden states it reads, and drafter.window, how many of the last read tokens'
-states) gets the context the reference's Writer keeps (:140-152, 184-200):
-each row's last `window` feature rows, updated after every read the model
-makes, with a row's pending tokens but its last read first.
+How a round runs here:
+    drafting    the drafter drafts for the rows being written (with the
+                features context when it reads the model's features);
+    the feed    each row's unread tokens and the drafts it verifies are laid
+                into one (rows, width) id tensor on the device -- the drafts
+                never travel to the host;
+    verify      one undoable `extend` reads every row, the fused sampler
+                (wpt_amd.sampling.accept) decides all rows at once on the
+                logits as the lm_head wrote them;
+    the host    one synchronization brings the written tokens back (plus one
+                for the confidences when the prefix scheduler runs); the
+                cache then keeps what each row wrote, and the features
+                context follows.
+
+The draws come from a tape per round (sampling.draws: the uniforms of the
+drafts, then one row of Exp(1) per row) drawn from `generator`; the reference
+draws lazily in its row loop, so a seeded Writer here writes another stream
+of the same distribution.  A tape recovered from a lazy run replays that run
+exactly (tests/test_writer_golden_gpu.py).
 """
+
+from dataclasses import dataclass, field
 
 import torch
 import torch.nn.functional as F
 
 from . import sampling
+from .decoder import MQADecoder
 from .scheduling import schedule
 
-DRAFT = 5  # draft tokens per row and step (the reference's DRAFT, :67)
+DRAFT = 5  # draft tokens a row may verify per round (the reference's default, __init__.py:67)
 
 
 def cut(tokens, stops, limit):
-    """tokens up to the first stop token, at most limit of them (:338-344)."""
-    for i, token in enumerate(tokens):
-        if token in stops:
-            tokens = tokens[:i + 1]
-            break
-    return tokens[:limit]
+    """The tokens through the first one in `stops`, and no more than `limit`
+    of them (the reference's _cut, __init__.py:338-344)."""
+    end = next((i + 1 for i, token in enumerate(tokens) if token in stops), len(tokens))
+    return tokens[:min(end, limit)]
+
+
+@dataclass
+class _Row:
+    """One row being written: its whole text, and the tail of it the model
+    has not read yet (at least its last token, which the next draft follows)."""
+    text: list
+    unread: list = field(default_factory=list)
+
+
+def sampling_distribution(scores, temperature, top_k):
+    """The reference's Writer._probabilities (__init__.py:173-179): FP32
+    scores over the temperature, every score below the top_k-th at -inf (ties
+    with it kept), softmax.  Handed to drafters as `probabilities`."""
+    scaled = scores.float() / temperature
+    if top_k is not None:
+        kth = torch.topk(scaled, min(top_k, scaled.shape[-1])).values[..., -1:]
+        scaled = torch.where(scaled < kth, torch.full_like(scaled, float("-inf")), scaled)
+    return F.softmax(scaled, dim=-1)
 
 
 class Writer:
-    """Writes for `rows` rows that all start from prompt (a list of ints, at
-    least one); the arguments are the reference's (:71-116)."""
+    """Writes for `rows` rows that all start from `prompt` (a list of ints,
+    at least one token).  Arguments as the reference's Writer: temperature,
+    top_k (None: the whole vocabulary), generator (on the model's device;
+    None: torch's default), stops (tokens after which a row's call returns),
+    drafter / draft / costs / outcomes (speculative decoding: the drafts per
+    round, the pass-time table the prefix scheduler reads, a list collecting
+    (confidences, kept drafts) per verified row), routes (passed to the
+    model's cache)."""
 
     def __init__(self, model, prompt, rows=1, *, temperature=0.8, top_k=40, generator=None, stops=(), drafter=None,
                  draft=DRAFT, costs=None, outcomes=None, routes=False):
@@ -51,139 +78,185 @@ class Writer:
             raise ValueError("a prompt holds at least one token")
         if costs is not None and len(costs) < draft + 1:
             raise ValueError(f"costs gives {len(costs)} pass times; drafting {draft} tokens needs {draft + 1}")
-        self.model, self.temperature, self.top_k, self.generator = model, temperature, top_k, generator
-        self.stops, self.drafter, self.draft, self.costs = set(stops), drafter, draft, costs
-        self.outcomes = outcomes
+        cached = hasattr(model, "new_cache")
+        if not cached and (drafter is not None or routes):
+            raise ValueError("drafting and recording routes need a model with a generation cache")
+        self.model, self.drafter, self.draft, self.costs, self.outcomes = model, drafter, draft, costs, outcomes
+        self.temperature, self.top_k, self.generator, self.stops = temperature, top_k, generator, frozenset(stops)
         self.rounds = self.verified = self.accepted = 0
         self.device = next(model.parameters()).device
-        self.histories = [list(prompt) for _ in range(rows)]
-        self.pending = [[prompt[-1]] for _ in range(rows)]
-        self.features = tuple(drafter.features) if drafter is not None else ()
-        self.cache = self.context = None  # context: the drafter's (rows, window, F)
-        if hasattr(model, "new_cache"):
-            shared = model.new_cache(1, routes=routes)
-            if len(prompt) > 1:
-                read = model.extend(self._tensor([prompt[:-1]]), shared, features=self.features)
-                self._remember(read, [len(prompt) - 1])
-            self.cache = shared.select([0] * rows)
-            if self.context is not None:  # the prompt's context, in every row
-                self.context = self.context.expand(rows, -1, -1).clone()
-            elif self.features:  # nothing read yet: zeros before the text
-                self.context = torch.zeros(rows, drafter.window, len(self.features) * model.config.d_model,
+        self._rows = [_Row(list(prompt), [prompt[-1]]) for _ in range(rows)]
+        self.features = tuple(getattr(drafter, "features", ())) if drafter is not None else ()
+        self.cache = None
+        self.context = None  # a feature-reading drafter's context: (rows, window, features x d_model) FP32
+        if not cached:
+            return
+        # the prompt but its last token is read once, into a one-row cache copied to every row
+        one = model.new_cache(1, routes=routes)
+        if len(prompt) > 1:
+            read = model.extend(torch.tensor([prompt[:-1]], dtype=torch.long, device=self.device), one,
+                                features=self.features)
+            self._follow(read, [len(prompt) - 1])
+        self.cache = one.select([0] * rows)
+        if self.features:
+            if self.context is None:  # nothing read: the window holds zeros before the text
+                self.context = torch.zeros(1, drafter.window, len(self.features) * model.config.d_model,
                                            device=self.device)
-        elif drafter is not None or routes:
-            raise ValueError("drafting and recording routes need a model with a generation cache")
+            self.context = self.context.expand(rows, -1, -1).clone()
+
+    @property
+    def histories(self):
+        """Each row's whole text: the prompt, its inputs and what it wrote."""
+        return [row.text for row in self._rows]
+
+    @property
+    def routes(self):
+        """Each row's recorded routes, from the model's cache (None without one)."""
+        return self.cache.routes if self.cache is not None else None
+
+    @property
+    def pending(self):
+        """Each row's tokens the model has not read yet (the last is the anchor)."""
+        return [row.unread for row in self._rows]
+
+    def _probabilities(self, scores):
+        return sampling_distribution(scores, self.temperature, self.top_k)
 
     @torch.no_grad()
     def write(self, inputs, limits):
-        """inputs: {row: tokens it reads before writing}; limits: {row: the
-        most tokens it may write now, at least 1}.  Returns {row: the tokens
-        it wrote}: at least one, at most its limit, ending at the first stop."""
-        rows = sorted(limits)
-        for row in rows:
-            self.pending[row] += inputs.get(row, [])
-            self.histories[row] += inputs.get(row, [])
-        if self.drafter is not None:
-            written = self._speculate(rows, limits)
+        """inputs: {row: tokens it reads before writing (possibly none)};
+        limits: {row: the most tokens it may write now, at least 1}.  Returns
+        {row: the tokens it wrote}: at least one, at most its limit, through
+        its first stop token."""
+        order = sorted(limits)
+        for r in order:
+            extra = list(inputs.get(r, ()))
+            self._rows[r].text.extend(extra)
+            self._rows[r].unread.extend(extra)
+        if self.drafter is None:
+            out = dict(zip(order, ([t] for t in self._plain(order))))
         else:
-            written = {row: [token] for row, token in zip(rows, self._sample(self._scores(rows)))}
-        for row, tokens in written.items():
-            self.histories[row] += tokens
-            self.pending[row] = [tokens[-1]]
-        return written
+            out = self._round(order, limits)
+        for r, tokens in out.items():
+            self._rows[r].text.extend(tokens)
+            self._rows[r].unread = [tokens[-1]]
+        return out
 
-    def _tensor(self, rows):
-        width = max(len(row) for row in rows)
-        return torch.tensor([row + [0] * (width - len(row)) for row in rows], dtype=torch.long, device=self.device)
+    # ---- reading ---------------------------------------------------------
 
-    def _remember(self, read, counts):
-        """The drafter's context once the model has read (read: extend's
-        result, with features) the first counts[b] of row b's new tokens:
-        each row's last `window` feature rows, older ones first."""
+    def _ids(self, feeds, spare=0):
+        """feeds: a token list per cache row -> (ids (rows, width + spare)
+        int64 on the device, zero-padded; the counts); width is the longest
+        feed (at least 1)."""
+        counts = [len(f) for f in feeds]
+        width = max(1, max(counts))
+        ids = torch.zeros(len(feeds), width + spare, dtype=torch.long)
+        for r, f in enumerate(feeds):
+            if f:
+                ids[r, :len(f)] = torch.tensor(f, dtype=torch.long)
+        return ids.to(self.device, non_blocking=True), counts
+
+    def _follow(self, read, counts):
+        """Moves the drafter's features context past the first counts[b] of
+        the tokens the model just read (read: extend's result with features):
+        each row keeps the features of its last `window` read tokens."""
         if not self.features:
             return
-        found = read[2].float()
+        fresh = read[2].float()
         window = self.drafter.window
-        if self.context is None:
-            self.context = found.new_zeros(found.shape[0], window, found.shape[-1])
-        joined = torch.cat([self.context, found], 1)
-        starts = torch.as_tensor(counts, dtype=torch.long, device=found.device)
-        places = starts[:, None] + torch.arange(window, device=found.device)
-        self.context = joined.gather(1, places[..., None].expand(-1, -1, found.shape[-1]))
+        held = self.context if self.context is not None else fresh.new_zeros(fresh.shape[0], window, fresh.shape[-1])
+        both = torch.cat([held, fresh], 1)
+        take = torch.as_tensor(counts, dtype=torch.long, device=fresh.device)[:, None] + torch.arange(
+            window, device=fresh.device)
+        self.context = torch.take_along_dim(both, take[..., None], 1)
 
-    def _read(self, rows, extra=None, undoable=False):
-        feeds = [[] for _ in self.pending]
-        for i, row in enumerate(rows):
-            feeds[row] = self.pending[row] + (extra[i] if extra is not None else [])
-        read = self.model.extend(self._tensor(feeds), self.cache, [len(feed) for feed in feeds], undoable,
-                                 features=self.features)
-        return read[0][rows], read
-
-    def _catch_up(self, rows):
-        """The model reads each row's pending tokens but its last (a tool
-        result, the template's), so that the context reaches its anchor."""
-        behind = [row for row in rows if len(self.pending[row]) > 1]
-        if not behind:
+    def _read_up_to_anchor(self, order):
+        """Reads each row's unread tokens but its anchor (inputs given with a
+        call), so that the features context ends at the anchor."""
+        feeds = [row.unread[:-1] if (r in order and len(row.unread) > 1) else [] for r, row in enumerate(self._rows)]
+        if not any(feeds):
             return
-        feeds = [self.pending[row][:-1] if row in behind else [] for row in range(len(self.pending))]
-        counts = [len(feed) for feed in feeds]
-        read = self.model.extend(self._tensor(feeds), self.cache, counts, features=self.features)
-        self._remember(read, counts)
-        for row in behind:
-            self.pending[row] = self.pending[row][-1:]
+        ids, counts = self._ids(feeds)
+        self._follow(self.model.extend(ids, self.cache, counts, features=self.features), counts)
+        for r, f in enumerate(feeds):
+            if f:
+                self._rows[r].unread = self._rows[r].unread[-1:]
 
-    def _scores(self, rows):
-        if self.cache is None:
-            return torch.cat([self.model(self._tensor([self.histories[row]]))[:, -1] for row in rows])
-        scores, _ = self._read(rows)
-        ends = torch.tensor([len(self.pending[row]) - 1 for row in rows], device=self.device)
-        return scores[torch.arange(len(rows), device=self.device), ends]
+    # ---- a call without a drafter: one sampled token per row ---------------
 
-    def _probabilities(self, scores):
-        """The reference's sampling distribution (:173-179), for drafters."""
-        scores = scores.float() / self.temperature
-        if self.top_k is not None:
-            k = min(self.top_k, scores.size(-1))
-            v, _ = torch.topk(scores, k)
-            scores = scores.masked_fill(scores < v[..., [-1]], float("-inf"))
-        return F.softmax(scores, dim=-1)
-
-    def _sample(self, scores):
-        """One token per row from the distribution of its scores (R, V)."""
-        R, V = scores.shape
-        u, e = sampling.draws(R, 0, V, self.generator, self.device)
-        tokens, counts = sampling.accept(scores[:, None].float(), scores.new_empty(R, 0, V, dtype=torch.float32),
-                                         torch.empty(R, 0, dtype=torch.long, device=self.device), u, e,
+    def _plain(self, order):
+        if self.cache is None:  # a model without a cache reads each row's whole text
+            last = torch.cat([self.model(torch.tensor([self._rows[r].text], dtype=torch.long, device=self.device))[:, -1]
+                              for r in order])
+        else:
+            feeds = [row.unread if r in order else [] for r, row in enumerate(self._rows)]
+            ids, counts = self._ids(feeds)
+            scores = self.model.extend(ids, self.cache, counts)[0]
+            pick = torch.tensor(order, dtype=torch.long, device=self.device)
+            at = torch.tensor([counts[r] - 1 for r in order], dtype=torch.long, device=self.device)
+            last = scores[pick, at]
+        n, V = last.shape
+        u, e = sampling.draws(n, 0, V, self.generator, self.device)
+        tokens, counts = sampling.accept(last[:, None].float(), last.new_empty(n, 0, V, dtype=torch.float32),
+                                         torch.empty(n, 0, dtype=torch.long, device=self.device), u, e,
                                          self.temperature, self.top_k)
-        return [row[0] for row in sampling.written(tokens, counts)]
+        return [drawn[0] for drawn in sampling.written(tokens, counts)]
 
-    def _speculate(self, rows, limits):
-        """One step of speculative decoding for rows (:196-233)."""
+    # ---- a speculative round ------------------------------------------------
+
+    def _round(self, order, limits):
         if self.features:
-            self._catch_up(rows)
-        context = (self.context[rows], self.cache.lengths[rows]) if self.features else None
-        drafted, q, confidences = self.drafter.draft(self.model, [self.histories[row] for row in rows], context,
-                                                     self.draft, self._probabilities, self.generator)
-        drafted, q = drafted.to(self.device), q.to(self.device).float()
-        caps = [min(self.draft, limits[row] - 1) for row in rows]  # a row writes at most its drafts and one more
-        scheduled = confidences is not None and self.costs is not None
-        lengths = schedule(confidences.tolist(), caps, self.costs) if scheduled else caps
-        scores, read = self._read(rows, [drafted[i, :n].tolist() for i, n in enumerate(lengths)], undoable=True)
-        firsts = [len(self.pending[row]) - 1 for row in rows]
-        L = drafted.shape[1]
-        u, e = sampling.draws(len(rows), L, scores.shape[-1], self.generator, self.device)
-        tokens, counts = sampling.accept(scores, q, drafted, u, e, self.temperature, self.top_k, lengths=lengths,
-                                         firsts=firsts)
-        written, kept = {}, [0] * len(self.pending)
-        for i, (row, drawn) in enumerate(zip(rows, sampling.written(tokens, counts))):
-            self.verified += lengths[i]
-            self.accepted += len(drawn) - 1
-            if self.outcomes is not None and confidences is not None:
-                self.outcomes.append((confidences[i, :lengths[i]].tolist(), min(len(drawn) - 1, lengths[i])))
-            drawn = cut(drawn, self.stops, limits[row])
-            written[row] = drawn
-            kept[row] = firsts[i] + len(drawn)
+            self._read_up_to_anchor(order)
+        context = (self.context[order], self.cache.lengths[order]) if self.features else None
+        drafts, q, confidence = self.drafter.draft(self.model, [self._rows[r].text for r in order], context,
+                                                   self.draft, self._probabilities, self.generator)
+        drafts = drafts.to(self.device, torch.long)
+        q = q.to(self.device, torch.float32)
+        L = drafts.shape[1]
+        # a row writes at most its verified drafts and one token more
+        caps = [min(self.draft, limits[r] - 1) for r in order]
+        if confidence is not None and self.costs is not None:
+            verify = schedule(confidence.tolist(), caps, self.costs)
+        else:
+            verify = caps
+        # the feed of row r: its unread tokens, then the first verify[i] drafts;
+        # the first token each row writes is scored at its last unread token
+        firsts = [len(self._rows[r].unread) - 1 for r in order]
+        feeds = [[] for _ in self._rows]
+        for i, r in enumerate(order):
+            feeds[r] = self._rows[r].unread + [0] * verify[i]
+        ids, counts = self._ids(feeds, spare=1)
+        width = ids.shape[1] - 1
+        pick = torch.tensor(order, dtype=torch.long, device=self.device)
+        if L:
+            # the drafts laid in on the device (no trip to the host): draft j of
+            # row order[i] at column firsts[i] + 1 + j when j < verify[i], the
+            # others into the spare last column, which is then cut off
+            j = torch.arange(L, device=self.device)[None]
+            start = torch.tensor(firsts, dtype=torch.long, device=self.device)[:, None] + 1
+            wanted = j < torch.tensor(verify, dtype=torch.long, device=self.device)[:, None]
+            cols = torch.where(wanted, start + j, torch.full_like(start + j, width))
+            ids[pick[:, None].expand(-1, L), cols] = drafts
+        ids = ids[:, :width].contiguous()
+        if isinstance(self.model, MQADecoder):  # the logits as the head writes them, read by the sampler as FP32
+            read = self.model.extend(ids, self.cache, counts, True, features=self.features, logits=True)
+        else:
+            read = self.model.extend(ids, self.cache, counts, True, features=self.features)
+        scores = read[0] if order == list(range(len(self._rows))) else read[0][pick]
+        u, e = sampling.draws(len(order), L, scores.shape[-1], self.generator, self.device)
+        tokens, ncounts = sampling.accept(scores, q, drafts, u, e, self.temperature, self.top_k,
+                                          lengths=verify, firsts=firsts)
+        drawn = sampling.written(tokens, ncounts)  # the round's synchronization
+        out, keep = {}, [0] * len(self._rows)
+        for i, r in enumerate(order):
+            self.verified += verify[i]
+            self.accepted += len(drawn[i]) - 1
+            if self.outcomes is not None and confidence is not None:
+                self.outcomes.append((confidence[i, :verify[i]].tolist(), min(len(drawn[i]) - 1, verify[i])))
+            out[r] = cut(drawn[i], self.stops, limits[r])
+            # the cache keeps the row's unread tokens and what it wrote but the last (the next anchor)
+            keep[r] = firsts[i] + len(out[r])
         self.rounds += 1
-        self.model.undo(self.cache, kept)
-        self._remember(read, kept)
-        return written
+        self.model.undo(self.cache, keep)
+        self._follow(read, keep)
+        return out
