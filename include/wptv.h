@@ -4,10 +4,12 @@
  * entry point is stream-ordered and asynchronous: it validates its arguments
  * on the host, enqueues kernels on `stream` and returns.  Device pointers are
  * on the current HIP device; the caller owns every buffer, the workspaces
- * included, and the library allocates nothing.  The library keeps no state
- * between calls apart from a per-device cache of the compute-unit count, so
- * it is re-entrant across host threads (calls that share a workspace on one
- * stream are ordered by that stream).
+ * included, and the library allocates nothing at run time.  Its state: a
+ * per-device cache of the compute-unit count, and one file-scope device array
+ * (16 MiB, present on every device the library runs on from load to exit)
+ * that only wptv_verify_attention_static uses, with its address resolved once
+ * per device.  Every other entry point is re-entrant across host threads
+ * (calls that share a workspace on one stream are ordered by that stream).
  *
  * Status codes: WPTV_OK, or a negative WPTV_E_* value; wptv_last_error()
  * then holds a thread-local message naming the argument or the HIP error.

@@ -221,6 +221,26 @@ def test_a_residual_with_no_mass_raises(device):
         sampling.written(tokens, counts)
 
 
+def test_a_greedy_row_of_nan_scores_writes_nothing(device):
+    # no maximum to take: the row writes no token (the failed-row path), the
+    # other rows decide as usual, in the chain and in the tree
+    B, L, V = 3, 2, 64
+    generator = torch.Generator().manual_seed(13)
+    scores = torch.randn(B, L + 1, V, generator=generator)
+    scores[1] = float("nan")
+    drafts = scores.argmax(-1)[:, :L].clone()
+    tokens, counts = sampling.greedy_chain(scores.to(device), drafts.to(device))
+    assert counts.tolist() == [L + 1, -1, L + 1]
+    with pytest.raises(RuntimeError, match="no maximum"):
+        sampling.written(tokens, counts)
+    parents = [-1, 0, 0]
+    tree_scores = torch.randn(B, 3, V, generator=generator)
+    tree_scores[2, 0] = float("nan")
+    _, _, tree_counts = sampling.greedy_tree(tree_scores.to(device), torch.zeros(B, 3, dtype=torch.long).to(device),
+                                             parents)
+    assert tree_counts[2] == -1 and (tree_counts[:2] >= 1).all()
+
+
 def test_bad_shapes_raise_value_error(device):
     scores = torch.zeros(2, 5, 100, device=device)
     q = torch.zeros(2, 4, 100, device=device)

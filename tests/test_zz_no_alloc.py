@@ -56,3 +56,18 @@ def test_a_request_beyond_the_static_scratch_is_refused(device):
     with pytest.raises(ValueError, match="static scratch"):
         kernels.verify_attention(q, table[..., :128], table[..., 128:], positions, 128 ** -0.5, splits=64,
                                  static_scratch=True)
+
+
+def test_the_library_s_own_split_count_steps_down_to_fit(device):
+    # 255 batch rows of 128 query rows: the library's choice for the workspace
+    # entry point is 2 splits, whose parts (17 MB) do not fit the static array;
+    # the allocation-free entry point takes one split instead, the same bits as
+    # the workspace entry point asked for one split
+    B, T, H, c, N = 255, 8, 16, 128, 300
+    print(f"static scratch step-down: B={B} T={T} H={H} c={c} N={N}", flush=True)
+    q, table, positions = (x.to(device) for x in inputs(B, T, H, c, N, seed=11))
+    k, v = table[..., :c], table[..., c:]
+    got = kernels.verify_attention(q, k, v, positions, c ** -0.5, static_scratch=True)
+    expected = kernels.verify_attention(q, k, v, positions, c ** -0.5, splits=1)
+    torch.cuda.synchronize()
+    assert torch.equal(got, expected)

@@ -2224,6 +2224,12 @@ extern "C" int wptv_verify_attention_static(const void* q, const void* k, int64_
   Plan p;
   int st = plan(B, T, H, c, N, window, dtype, flags, splits, &p);
   if (st != WPTV_OK) return st;
+  // a split count of the library's choosing steps down until its parts fit
+  // the static array (one split needs none)
+  while (splits <= 0 && p.bytes > kScratchBytes && p.splits > 1) {
+    st = plan(B, T, H, c, N, window, dtype, flags, p.splits - 1, &p);
+    if (st != WPTV_OK) return st;
+  }
   if (p.bytes > kScratchBytes)
     return fail(WPTV_E_INVALID,
                 "verify_attention_static: B=%d T=%d H=%d c=%d in %d splits needs %zu bytes of parts, above the %zu "

@@ -329,10 +329,12 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i)
       if (tid + i * kT < V) arg_better(bv, bi, x[i], tid + i * kT);
-    const int best = block_argmax(bv, bi, redv, redi);
+    // a row of NaN has no maximum: no index (the pick then writes nothing and flags the row)
+    const int found = block_argmax(bv, bi, redv, redi);
+    const int best = found >= 0 && found < V ? found : -1;
     if (tid == 0) {
       stats.best[idx] = best;
-      stats.keep[idx] = (j < n && drafts) ? (drafts[b * db + j] == best) : 0;
+      stats.keep[idx] = (j < n && drafts && best >= 0) ? (drafts[b * db + j] == best) : 0;
     }
     return;
   }
@@ -587,7 +589,8 @@ __global__ void tree_walk(const int64_t* __restrict__ node_tokens, const int32_t
     ++depth;
     pa[depth] = node;
   }
-  n_tokens[b] = depth + 1;
+  // a node whose scores are all NaN has no maximum: the row writes nothing (-1)
+  n_tokens[b] = tk[depth] >= 0 ? depth + 1 : -1;
 }
 
 Stats carve(void* workspace, int B, int P) {
@@ -693,8 +696,9 @@ __global__ __launch_bounds__(kGT) void greedy_argmax(const S* __restrict__ score
 #pragma unroll
     for (int w = 1; w < kGT / 64; ++w) arg_better(v, i, redv[w], redi[w]);
     const int idx = b * P + j;
-    stats.best[idx] = i;
-    stats.keep[idx] = (j < n && drafts) ? (drafts[b * db + j] == i) : 0;
+    const int best = i >= 0 && i < V ? i : -1;  // a row of NaN has no maximum
+    stats.best[idx] = best;
+    stats.keep[idx] = (j < n && drafts && best >= 0) ? (drafts[b * db + j] == best) : 0;
   }
 }
 

@@ -20,7 +20,7 @@ written, not yet read):
     Markov    q_k = probabilities(U_k + markov_out(markov_in[x_{k-1}])), the
               writer's distribution (temperature, top-k); x_0 the anchor;
               x_k drawn from q_k with the writer's generator (drafter.py:215-234)
-    confidence c_k = sigmoid(w . [h_k ; markov_in[x_{k-1}]] + b) / T_k)
+    confidence c_k = sigmoid((w . [h_k ; markov_in[x_{k-1}]] + b) / T_k)
 
 What differs from the reference, by design: the feed-forward block is a dense
 SwiGLU block in place of the routed experts, and the sublayers are linked by

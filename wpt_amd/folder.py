@@ -19,17 +19,20 @@ Parts are filled in the weights' own order and a new part starts when the
 next tensor would push the current one past the limit (a tensor larger than
 the limit sits alone).
 
-Design: a `ModelFolder` object owns one directory.  Writing stages every file
-under a temporary name and renames config.json into place last, so a folder
-whose write stopped part-way has no config.json and does not load.  Reading
+Design: a `ModelFolder` object owns one directory.  Writing puts the weight
+shards and tokenizer.json in place first and config.json last (the JSON files
+each written under a temporary name and renamed into place), so a folder whose
+write stopped part-way has no config.json and does not load.  Reading
 checks the two pairings the format encodes before any weight is used: the
 drafter/ record must name the folder's weight files by their current sha256
 (else `DrafterMismatch`), and tokenizer.json must hash to what every weight
 header names (else `TokenizerMismatch`).  Only safetensors and JSON are read,
 so loading executes nothing from the files.
 
-The weights are this decoder's (wpt_amd.decoder.random_weights' names).  The
-build has no drafter network, so drafter/ is checked and not loaded;
+The weights are this decoder's (wpt_amd.decoder.random_weights' names).  A
+reference drafter/ folder holds DSpark weights with routed experts and
+Attention Residuals, which this build's drafter (wpt_amd.drafter, a dense
+stand-in) cannot take, so drafter/ is checked and not loaded;
 `record_drafter` writes the two files the check reads.
 """
 

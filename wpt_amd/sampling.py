@@ -183,6 +183,7 @@ def written(tokens, counts):
     out = []
     for b, n in enumerate(counts):
         if n < 0:
-            raise RuntimeError(f"row {b}: the residual distribution max(0, p - q) has no mass to draw from")
+            raise RuntimeError(f"row {b}: no token to write: the residual distribution max(0, p - q) has no mass to "
+                               f"draw from, or the scores have no maximum (all NaN)")
         out.append(rows[b][:n])
     return out
