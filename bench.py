@@ -307,11 +307,12 @@ def tree_c4(steps, warmup):
     written = torch.zeros(B, dtype=torch.long, device=device)
 
     def step(count=False):
-        # the nodes' attention output written as the lm_head's fm operand, the
-        # head on the 256 x 256 tiles: bf16 logits, read by the walk as they come
+        # the nodes' attention output written as the lm_head's fm operand; the
+        # head on the 256 x 256 tiles keeps each node's first maximal index of
+        # its bf16 logits (the greedy walk's only use of them), then the walk
         o = kernels.tree_attention(q, table[..., :c], table[..., c:], base, parents, c ** -0.5, out_fm=True)
-        scores = layers.linear_fm_wide(o, B * M, head_fm).view(B, M, V)
-        _, _, counts = sampling.greedy_tree(scores, node_tokens, parents)
+        best = layers.head_argmax_fm_wide(o, B * M, head_fm).view(B, M)
+        _, _, counts = sampling.greedy_tree_from_argmax(best, node_tokens, parents)
         if count:  # counted in a graph of its own, outside the timed one
             written.add_(counts.long())
 

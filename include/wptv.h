@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define WPTV_ABI_VERSION 7
+#define WPTV_ABI_VERSION 8
 
 enum {
   WPTV_OK = 0,
@@ -404,6 +404,20 @@ int wptv_gemm_fm_swiglu(const void* x_fm, const void* w_fm, int M, int N, int K,
 int wptv_gemm_fm_wide(const void* x_fm, int x_blocks, const void* w_fm, int M, int N, int K, void* out, int64_t ldo,
                       int out_dtype, hipStream_t stream);
 
+/* wptv_gemm_fm_wide_argmax: the greedy decisions' per-row argmax of that
+ *   product without storing it: best[m] = the first index of the largest
+ *   bf16-rounded value of row m of x . w^T (torch.argmax of the reference's
+ *   bf16 logits, model.py:471, as its greedy verification reads them:
+ *   packages/wpt-worker/src/wpt_worker/evaluation.py:74-81), -1 for a row
+ *   whose values are all NaN.  The 256 x 256 tiles' epilogue keeps each
+ *   row's (maximum, index) over its columns in the workspace
+ *   (wptv_gemm_fm_wide_argmax_workspace bytes: 8 (N / 256) M), a second
+ *   kernel reduces them in column order.  Shapes as wptv_gemm_fm_wide. */
+int wptv_gemm_fm_wide_argmax_workspace(int M, int N, size_t* bytes);
+
+int wptv_gemm_fm_wide_argmax(const void* x_fm, int x_blocks, const void* w_fm, int M, int N, int K, int32_t* best,
+                             void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Acceptance: the reference's per-row verification loop of
  * Writer._speculate (packages/wpt-inference/src/wpt_inference/__init__.py:
@@ -480,12 +494,19 @@ int wptv_accept_commit(const void* scores, int64_t scores_stride_b, int64_t scor
  *            (the root included), -1 after
  *   tokens   [B, M + 1] int64 out: the accepted nodes' tokens after the
  *            root, then the argmax; -1 after
- *   n_tokens [B] int32 out: accepted nodes after the root + 1
+ *   n_tokens [B] int32 out: accepted nodes after the root + 1 (-1: a node
+ *            on the walk had no maximum, every score NaN)
  *   workspace  wptv_accept_workspace(B, M - 1) bytes */
 int wptv_greedy_tree(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
                      const int64_t* node_tokens, const int32_t* parents, int B, int M, int V, int64_t* path,
                      int64_t* tokens, int32_t* n_tokens, void* workspace, size_t workspace_bytes,
                      hipStream_t stream);
+
+/* wptv_greedy_tree_best: the same walk from each node's argmax already
+ *   found (best [B, M] int32, -1 for a node with no maximum: for instance
+ *   wptv_gemm_fm_wide_argmax of the nodes' lm_head rows). */
+int wptv_greedy_tree_best(const int32_t* best, const int64_t* node_tokens, const int32_t* parents, int B, int M,
+                          int64_t* path, int64_t* tokens, int32_t* n_tokens, hipStream_t stream);
 
 #ifdef __cplusplus
 }

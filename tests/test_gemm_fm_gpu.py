@@ -192,3 +192,27 @@ def test_the_wide_fm_product_refuses_bad_shapes(device):
     x2, w2 = operands(64, 256, 64, seed=4, device=device)
     with pytest.raises(ValueError):
         layers.linear_fm_wide(layers.fm_pack(x2)[: 2 * 16 * 64], 64, layers.FmWeight(w2))  # too few row blocks
+
+
+@pytest.mark.parametrize("M, N, K", [(496, 32768, 2048), (300, 1024, 128), (40, 512, 64)])
+def test_the_fused_head_argmax_is_the_argmax_of_the_bf16_logits(device, M, N, K):
+    # the first maximal index of each row's bf16 logits, without storing them:
+    # ties planted within a column tile (5, 6) and across tiles (N - 100), a
+    # row of NaN (no maximum: -1)
+    generator = torch.Generator().manual_seed(M + N)
+    x = torch.randn(M, K, generator=generator).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=generator) * 0.02).to(torch.bfloat16)
+    rows_tied = torch.arange(0, M, 3)
+    favourite = torch.full((K,), 0.05).to(torch.bfloat16)
+    w[[5, 6, N - 100]] = favourite  # the same column three times (the last in another column tile)
+    x[1] = float("nan")
+    x, w = x.to(device), w.to(device)
+    x[rows_tied] = x[rows_tied].abs() + 0.5  # these rows prefer the planted columns
+    x_fm, w_fm = layers.fm_pack(x), layers.FmWeight(w)
+    best = layers.head_argmax_fm_wide(x_fm, M, w_fm)
+    logits = layers.linear_fm_wide(x_fm, M, w_fm).float()
+    expected = logits.argmax(-1).to(torch.int32)
+    expected[1] = -1  # torch takes the NaN as the maximum; a greedy row of NaN has none
+    assert best.dtype == torch.int32 and best.shape == (M,)
+    assert torch.equal(best, expected)
+    assert (best[rows_tied[rows_tied != 1]] == 5).all()

@@ -209,6 +209,25 @@ def test_greedy_tree_matches_the_oracle(device):
         assert path[b, :len(p)].tolist() == p and written[b, :len(w)].tolist() == w
 
 
+def test_the_walk_from_given_argmaxes_is_the_walk_from_the_scores(device):
+    B, V = 16, 4096
+    parents = [-1] + [(i - 1) // 2 for i in range(1, 31)]
+    generator = torch.Generator().manual_seed(14)
+    scores = torch.randn(B, 31, V, generator=generator)
+    best = scores.argmax(-1)
+    tokens = torch.randint(V, (B, 31), generator=generator)
+    for b in range(B):
+        node = 0
+        for _ in range(int(torch.randint(0, 5, (), generator=generator))):
+            child = 2 * node + 1 + int(torch.randint(0, 2, (), generator=generator))
+            tokens[b, child] = best[b, node]
+            node = child
+    want = sampling.greedy_tree(scores.to(device), tokens.to(device), parents)
+    got = sampling.greedy_tree_from_argmax(best.to(torch.int32).to(device), tokens.to(device), parents)
+    for a, b in zip(want, got):
+        assert torch.equal(a, b)
+
+
 def test_a_residual_with_no_mass_raises(device):
     V = 16
     scores = torch.zeros(1, 2, V)

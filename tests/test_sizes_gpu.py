@@ -229,7 +229,10 @@ def test_tree_verification_at_its_workload_size(device):
     assert relative_error(logits.reshape(B * M, V).float().cpu(), expected_logits) < 1e-2
     best = oracle_sampling.first_argmax(logits.float().cpu())
     node_tokens = plant_paths(best, parents, B)
-    path, tokens, counts = sampling.greedy_tree(logits, node_tokens.to(device), parents)
+    # the benchmark's walk: each node's argmax from the head's epilogue, no logits stored
+    fused = layers.head_argmax_fm_wide(o_fm, B * M, layers.FmWeight(head_d)).view(B, M)
+    assert torch.equal(fused.long().cpu(), best)
+    path, tokens, counts = sampling.greedy_tree_from_argmax(fused, node_tokens.to(device), parents)
     walks = oracle_sampling.greedy_tree(logits.float().cpu(), node_tokens, parents)
     counts = counts.cpu().tolist()
     for b, (want_path, want_tokens) in enumerate(walks):

@@ -12,7 +12,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwptv.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 WPTV_F32, WPTV_BF16 = 0, 1
 DTYPES = {torch.float32: WPTV_F32, torch.bfloat16: WPTV_BF16}
@@ -69,6 +69,8 @@ SIGNATURES = {
     "wptv_gemm_fm_parts": [_P, _P, _I, _I, _I, _I, _P, _SZ, _P],
     "wptv_gemm_fm_swiglu": [_P, _P, _I, _I, _I, _P, _P],
     "wptv_gemm_fm_wide": [_P, _I, _P, _I, _I, _I, _P, _I64, _I, _P],
+    "wptv_gemm_fm_wide_argmax_workspace": [_I, _I, _P],
+    "wptv_gemm_fm_wide_argmax": [_P, _I, _P, _I, _I, _I, _P, _P, _SZ, _P],
     "wptv_add_rms_norm_parts": [_P, _P, _I, _P, _P, _I, _I, _I, _I, _F, _P],
     "wptv_qkv_post_parts": [_P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I, _I, _F, _P],
     "wptv_accept_workspace": [_I, _I, ctypes.POINTER(_SZ)],
@@ -77,6 +79,7 @@ SIGNATURES = {
     "wptv_accept_commit": [_P, _I64, _I64, _I, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P,
                            _P, _P, _SZ, _P, _P, _P, _I64, _P, _P, _P],
     "wptv_greedy_tree": [_P, _I64, _I64, _I, _P, _P, _I, _I, _I, _P, _P, _P, _P, _SZ, _P],
+    "wptv_greedy_tree_best": [_P, _P, _P, _I, _I, _P, _P, _P, _P],
 }
 
 _handle = None

@@ -40,6 +40,8 @@
 // from that XCD's L2 for the other row tiles.
 #include "wptv_common.h"
 
+#include <climits>
+
 namespace wptv {
 namespace {
 
@@ -52,6 +54,7 @@ constexpr int kWideStage = 2 * kWideHalf;        // 32 KiB: X then W
 constexpr int kWideStages = 4;
 constexpr int kWidePerWave = kWideStage / 1024 / kWideWaves;  // 1 KiB DMA pieces a wavefront issues per chunk
 constexpr int kWideSlices = kWideChunk / 16;                  // k-slices of the 32x32x16 products per chunk
+constexpr float kNegInfW = -__builtin_inff();
 static_assert(kWideStages * kWideStage >= kWideTile * kWideTile * 2, "the output tile is staged in the ring");
 static_assert(kWidePerWave == 4, "two X and two W pieces a wavefront");
 
@@ -80,7 +83,20 @@ __device__ __forceinline__ void wait_lgkm0() {
 // kWideF32.  FM false: x and w row-major with leading dimensions ldx, ldw;
 // FM true: both in the fm layout (wptv_common.h), x with ldx row blocks (at
 // least 2 ceil(M / 32)), w with ldw = N / 16.
-enum WideOut { kWideBf16 = 0, kWideF32 = 1 };
+// kWideArgmax: no product stored; each row's largest bf16-rounded value over
+// the tile's 256 columns and its first index, as a (value, index) pair at
+// out[column tile * M + row] (the greedy decisions' first maximal index,
+// reduced over the column tiles by wide_argmax_reduce).
+enum WideOut { kWideBf16 = 0, kWideF32 = 1, kWideArgmax = 2 };
+
+// The larger value, the lower index on a tie; a NaN never wins (the first
+// maximal index torch.argmax gives, over the non-NaN values).
+__device__ __forceinline__ void wide_better(float& v, int& i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
 
 template <int OUT, bool FM>
 __global__ __launch_bounds__(kWideWaves * 64, 1) void gemm_wide(const unsigned short* __restrict__ x, int64_t ldx,
@@ -236,6 +252,47 @@ __global__ __launch_bounds__(kWideWaves * 64, 1) void gemm_wide(const unsigned s
     }
   }
 
+  if constexpr (OUT == kWideArgmax) {
+    // lane l holds, of row 128 wm + 32 i + l % 32, the columns 64 wn + 32 j +
+    // 8 g + 4 (l / 32) + e of the tile: its first maximum in column order,
+    // then the other half-wave's (lane l ^ 32), then the four wavefronts of
+    // the row's half through LDS, in column order
+    __syncthreads();  // the ring is free
+    float* rv = reinterpret_cast<float*>(ring);                // [wm][wn][128]
+    int* ri = reinterpret_cast<int*>(ring + 2 * 4 * 128 * 4);  // the same layout
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float bv = kNegInfW;
+      int bi = INT_MAX;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          wide_better(bv, bi, bf16_to_f32(f32_to_bf16(acc[j][i][e])),
+                      n0 + 64 * wn + 32 * j + 8 * (e >> 2) + 4 * hl + (e & 3));
+      const float ov = __shfl_xor(bv, 32, 64);
+      const int oi = __shfl_xor(bi, 32, 64);
+      wide_better(bv, bi, ov, oi);
+      if (hl == 0) {
+        rv[(wm * 4 + wn) * 128 + 32 * i + rl] = bv;
+        ri[(wm * 4 + wn) * 128 + 32 * i + rl] = bi;
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < kWideTile) {
+      const int ml = threadIdx.x, half = ml >> 7, r = ml & 127;
+      float bv = kNegInfW;
+      int bi = INT_MAX;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) wide_better(bv, bi, rv[(half * 4 + u) * 128 + r], ri[(half * 4 + u) * 128 + r]);
+      if (m0 + ml < M) {
+        float2* part = static_cast<float2*>(out) + (int64_t)ct * M + m0 + ml;
+        *part = float2{bv, __int_as_float(bi)};
+      }
+    }
+    return;
+  }
+
   // every wavefront is done with the ring: stage the tile as bf16 [m][n]
   __syncthreads();
   typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
@@ -271,6 +328,27 @@ __global__ __launch_bounds__(kWideWaves * 64, 1) void gemm_wide(const unsigned s
   }
 }
 
+// Each row's first maximal index over the column tiles' (value, index) pairs,
+// -1 for a row with no maximum (every value NaN): one wavefront per row.
+__global__ __launch_bounds__(256) void wide_argmax_reduce(const float2* __restrict__ parts, int col_tiles, int M,
+                                                          int32_t* __restrict__ best) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  float bv = kNegInfW;
+  int bi = INT_MAX;
+  for (int t = lane; t < col_tiles; t += 64) {
+    const float2 p = parts[(int64_t)t * M + row];
+    wide_better(bv, bi, p.x, __float_as_int(p.y));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    wide_better(bv, bi, ov, oi);
+  }
+  if (lane == 0) best[row] = bi == INT_MAX ? -1 : bi;
+}
+
 }  // namespace
 
 bool gemm_wide_fits(int M, int N, int K) { return M > 0 && N > 0 && K > 0 && N % kWideTile == 0 && K % kWideChunk == 0; }
@@ -278,6 +356,8 @@ bool gemm_wide_fits(int M, int N, int K) { return M > 0 && N > 0 && K > 0 && N %
 // Host checks are the caller's (wptv_gemm): operands 16-byte aligned, leading
 // dimensions multiples of 8, operands under 4 GB.
 namespace {
+
+constexpr int kWideArgmaxOut = -100;  // launch_wide's out_dtype for the argmax epilogue
 
 template <bool FM>
 int launch_wide(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K, void* out, int64_t ldo,
@@ -287,7 +367,10 @@ int launch_wide(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, i
   if (groups > 0x7fffffffLL) return fail(WPTV_E_UNSUPPORTED, "gemm: %lld output tiles", groups);
   const auto* xb = static_cast<const unsigned short*>(x);
   const auto* wb = static_cast<const unsigned short*>(w);
-  if (out_dtype == WPTV_BF16)
+  if (out_dtype == kWideArgmaxOut)
+    hipLaunchKernelGGL((gemm_wide<kWideArgmax, FM>), dim3((unsigned)groups), dim3(kWideWaves * 64), 0, stream, xb,
+                       ldx, wb, ldw, M, N, K, row_tiles, out, ldo);
+  else if (out_dtype == WPTV_BF16)
     hipLaunchKernelGGL((gemm_wide<kWideBf16, FM>), dim3((unsigned)groups), dim3(kWideWaves * 64), 0, stream, xb, ldx,
                        wb, ldw, M, N, K, row_tiles, out, ldo);
   else
@@ -328,4 +411,36 @@ extern "C" int wptv_gemm_fm_wide(const void* x_fm, int x_blocks, const void* w_f
   if ((double)N * (double)K * 2.0 >= 4.0e9 || (double)x_blocks * 16.0 * (double)K * 2.0 >= 4.0e9)
     return fail(WPTV_E_UNSUPPORTED, "gemm_fm_wide: operands above 4 GB");
   return launch_wide<true>(x_fm, x_blocks, w_fm, N / 16, M, N, K, out, ldo, out_dtype, stream);
+}
+
+extern "C" int wptv_gemm_fm_wide_argmax_workspace(int M, int N, size_t* bytes) {
+  if (!bytes) return fail(WPTV_E_INVALID, "gemm_fm_wide_argmax_workspace: null output pointer");
+  if (M <= 0 || N <= 0 || N % kWideTile)
+    return fail(WPTV_E_INVALID, "gemm_fm_wide_argmax_workspace: M > 0 and N a multiple of %d (got %d, %d)", kWideTile,
+                M, N);
+  *bytes = (size_t)(N / kWideTile) * M * sizeof(float2);
+  return WPTV_OK;
+}
+
+extern "C" int wptv_gemm_fm_wide_argmax(const void* x_fm, int x_blocks, const void* w_fm, int M, int N, int K,
+                                        int32_t* best, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!x_fm || !w_fm || !best || !workspace)
+    return fail(WPTV_E_INVALID, "gemm_fm_wide_argmax: x_fm, w_fm, best and workspace must be given");
+  if (M <= 0 || N <= 0 || K <= 0 || N % kWideTile || K % kWideChunk)
+    return fail(WPTV_E_INVALID, "gemm_fm_wide_argmax: M > 0, N a multiple of %d and K of %d (got %d, %d, %d)",
+                kWideTile, kWideChunk, M, N, K);
+  if (x_blocks < fm_row_blocks(M))
+    return fail(WPTV_E_INVALID, "gemm_fm_wide_argmax: %d row blocks of x hold fewer than M = %d rows", x_blocks, M);
+  const size_t need = (size_t)(N / kWideTile) * M * sizeof(float2);
+  if (workspace_bytes < need)
+    return fail(WPTV_E_INVALID, "gemm_fm_wide_argmax: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  if (!aligned(x_fm, 16) || !aligned(w_fm, 16) || !aligned(workspace, 16) || !aligned(best, 4))
+    return fail(WPTV_E_INVALID, "gemm_fm_wide_argmax: x_fm, w_fm and workspace 16-byte aligned");
+  if ((double)N * (double)K * 2.0 >= 4.0e9 || (double)x_blocks * 16.0 * (double)K * 2.0 >= 4.0e9)
+    return fail(WPTV_E_UNSUPPORTED, "gemm_fm_wide_argmax: operands above 4 GB");
+  int st = launch_wide<true>(x_fm, x_blocks, w_fm, N / 16, M, N, K, workspace, 0, kWideArgmaxOut, stream);
+  if (st != WPTV_OK) return st;
+  hipLaunchKernelGGL(wide_argmax_reduce, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream,
+                     static_cast<const float2*>(workspace), N / kWideTile, M, best);
+  return launched("wide_argmax_reduce");
 }

@@ -841,3 +841,15 @@ extern "C" int wptv_greedy_tree(const void* scores, int64_t scores_stride_b, int
                      n_tokens);
   return launched("tree_walk");
 }
+
+extern "C" int wptv_greedy_tree_best(const int32_t* best, const int64_t* node_tokens, const int32_t* parents, int B,
+                                     int M, int64_t* path, int64_t* tokens, int32_t* n_tokens, hipStream_t stream) {
+  if (!best || !node_tokens || !parents || !path || !tokens || !n_tokens)
+    return fail(WPTV_E_INVALID, "greedy_tree_best: every pointer must be given");
+  if (B <= 0 || M <= 0) return fail(WPTV_E_INVALID, "greedy_tree_best: bad shape B=%d M=%d", B, M);
+  Stats s{};
+  s.best = const_cast<int32_t*>(best);  // the walk only reads it
+  hipLaunchKernelGGL(tree_walk, dim3((B + 63) / 64), dim3(64), 0, stream, node_tokens, parents, B, M, s, path, tokens,
+                     n_tokens);
+  return launched("tree_walk");
+}

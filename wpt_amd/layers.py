@@ -378,6 +378,25 @@ def linear_fm_wide(x_fm, rows, w, out_dtype=torch.bfloat16):
     return out
 
 
+def head_argmax_fm_wide(x_fm, rows, w):
+    """Each row's first maximal index of the bf16-rounded product x . w^T (the
+    greedy decisions' argmax of an lm_head's logits), without storing the
+    product: (rows,) int32, -1 for a row of NaN (wptv_gemm_fm_wide_argmax).
+    x a flat fm operand of rows x K, w an FmWeight (N, K), N a multiple of 256."""
+    _gpu(x_fm, w.data)
+    N, K = w.shape
+    _fm_output(x_fm, rows, K)
+    blocks = x_fm.numel() // (16 * K)
+    library = _lib.lib()
+    size = _lib.ctypes.c_size_t(0)
+    check(library.wptv_gemm_fm_wide_argmax_workspace(rows, N, _lib.ctypes.byref(size)), "gemm_fm_wide_argmax")
+    workspace = torch.empty(size.value, dtype=torch.uint8, device=x_fm.device)
+    best = torch.empty(rows, dtype=torch.int32, device=x_fm.device)
+    check(library.wptv_gemm_fm_wide_argmax(ptr(x_fm), blocks, ptr(w.data), rows, N, K, ptr(best), ptr(workspace),
+                                           size.value, _lib.stream(x_fm.device)), "gemm_fm_wide_argmax")
+    return best
+
+
 def linear_fm_swiglu(x_fm, rows, w):
     """silu(gate) * up of x (a flat fm operand of rows x K) and the gate/up
     FmWeight packed from interleave_gate_up's order: a flat fm operand of

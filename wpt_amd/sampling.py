@@ -17,7 +17,7 @@ import torch
 from . import _lib
 from ._lib import KernelUnavailable, check, ptr
 
-__all__ = ["accept", "greedy_chain", "greedy_tree", "draws", "written"]
+__all__ = ["accept", "greedy_chain", "greedy_tree", "greedy_tree_from_argmax", "draws", "written"]
 
 
 def _on_gpu(*tensors):
@@ -150,13 +150,7 @@ def greedy_tree(scores, node_tokens, parents):
     scores = _scores(scores)
     B, M, V = scores.shape
     device = scores.device
-    parents = [int(p) for p in parents]
-    if len(parents) != M or parents[0] != -1 or any(not 0 <= p < i for i, p in enumerate(parents) if i > 0):
-        raise ValueError("parents must be (M,) with parents[0] = -1 and 0 <= parents[i] < i")
-    key = (tuple(parents), device)
-    parents_ = _PARENTS.get(key)
-    if parents_ is None:  # made once per tree and device, outside any graph capture
-        parents_ = _PARENTS[key] = torch.tensor(parents, dtype=torch.int32, device=device)
+    parents_ = _parents(parents, M, device)
     node_tokens = node_tokens.to(device=device, dtype=torch.long).contiguous()
     if node_tokens.shape != (B, M):
         raise ValueError(f"node_tokens must be (B={B}, M={M}); got {tuple(node_tokens.shape)}")
@@ -170,6 +164,37 @@ def greedy_tree(scores, node_tokens, parents):
                                       ptr(parents_), B, M, V, ptr(path), ptr(tokens), ptr(counts), ptr(workspace),
                                       size, _lib.stream(device)), "greedy_tree")
     return path, tokens, counts
+
+
+def greedy_tree_from_argmax(best, node_tokens, parents):
+    """greedy_tree from each node's argmax already found: best (B, M) int32
+    (-1 for a node with no maximum, e.g. layers.head_argmax_fm_wide of the
+    nodes' lm_head rows).  Returns (path, tokens, counts) as greedy_tree."""
+    B, M = best.shape
+    device = best.device
+    parents_ = _parents(parents, M, device)
+    node_tokens = node_tokens.to(device=device, dtype=torch.long).contiguous()
+    if node_tokens.shape != (B, M) or best.dtype != torch.int32:
+        raise ValueError(f"best must be (B, M) int32 and node_tokens (B={B}, M={M})")
+    _on_gpu(best, node_tokens)
+    path = torch.empty(B, M + 1, dtype=torch.long, device=device)
+    tokens = torch.empty(B, M + 1, dtype=torch.long, device=device)
+    counts = torch.empty(B, dtype=torch.int32, device=device)
+    check(_lib.lib().wptv_greedy_tree_best(ptr(best.contiguous()), ptr(node_tokens), ptr(parents_), B, M, ptr(path),
+                                           ptr(tokens), ptr(counts), _lib.stream(device)), "greedy_tree_best")
+    return path, tokens, counts
+
+
+def _parents(parents, M, device):
+    """The tree's parents on the device, checked (made once per tree and device)."""
+    parents = [int(p) for p in parents]
+    if len(parents) != M or parents[0] != -1 or any(not 0 <= p < i for i, p in enumerate(parents) if i > 0):
+        raise ValueError("parents must be (M,) with parents[0] = -1 and 0 <= parents[i] < i")
+    key = (tuple(parents), device)
+    found = _PARENTS.get(key)
+    if found is None:  # outside any graph capture
+        found = _PARENTS[key] = torch.tensor(parents, dtype=torch.int32, device=device)
+    return found
 
 
 _PARENTS = {}  # (parents, device) -> the parents on the device
