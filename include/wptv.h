@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define WPTV_ABI_VERSION 8
+#define WPTV_ABI_VERSION 9
 
 enum {
   WPTV_OK = 0,
@@ -481,6 +481,34 @@ int wptv_accept_commit(const void* scores, int64_t scores_stride_b, int64_t scor
                        int32_t* n_tokens, void* workspace, size_t workspace_bytes, int64_t* cache_lengths,
                        const int64_t* cache_before, int64_t* feeds, int64_t feeds_stride, int32_t* failed,
                        int64_t* written, hipStream_t stream);
+
+/* wptv_accept_in_order: wptv_accept (with wptv_accept_commit's moves when
+ *   cache_lengths is not NULL) drawing as the reference's loop draws from a
+ *   torch generator on this device, in its order (Writer._speculate,
+ *   __init__.py:214-229): row by row, one torch.rand(()) per draft it judges,
+ *   then one torch.multinomial(w, 1) over the vocabulary; or, with joint = 1
+ *   and L = 0, one torch.multinomial of every row's distribution at once
+ *   (Writer._sample, :181-182).  No tape: the draws are torch's Philox4x32-10
+ *   stream itself (torch's device generator through hipRAND).
+ *   generator_state  [2] int64 on the device: the generator's seed and
+ *                    offset (its get_state())
+ *   next_offset      int64 on the device out: the offset after these draws
+ *                    (may be generator_state + 1); set it back on the
+ *                    generator to continue its stream
+ *   the rest as wptv_accept (u and e replaced by the two above; greedy is
+ *   not taken: a greedy step draws nothing) and wptv_accept_commit (all of
+ *   cache_lengths, cache_before, feeds, failed, written may be NULL).
+ *   B (L + 1) <= 4096, L <= 64; workspace wptv_accept_workspace(B, L) bytes.
+ *   Three launches: the statistics, the draws (the loop's uniforms replayed
+ *   to find each row's first rejection; the multinomial's exponentials over
+ *   eight slices of the vocabulary a row), the pick. */
+int wptv_accept_in_order(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
+                         const int32_t* firsts, const float* q, int64_t q_stride_b, int64_t q_stride_t,
+                         const int64_t* drafts, int64_t drafts_stride_b, const int32_t* lengths,
+                         const int64_t* generator_state, int64_t* next_offset, int joint, float temperature, int top_k,
+                         int B, int L, int V, int64_t* tokens, int32_t* n_tokens, void* workspace,
+                         size_t workspace_bytes, int64_t* cache_lengths, const int64_t* cache_before, int64_t* feeds,
+                         int64_t feeds_stride, int32_t* failed, int64_t* written, hipStream_t stream);
 
 /* Greedy verification of a draft tree of M nodes per row (node 0 the root,
  * the token already written; parents[i] < i, parents[0] = -1): from the root,

@@ -11,7 +11,10 @@ rejection rule of its speculative-decoding step, restated on the CPU in FP32
                        drawn from p at the position after the last draft
     LazyDraws          the reference's draws from a torch generator, in its
                        order: torch.rand(()) per draft considered (:214), then
-                       torch.multinomial(w, 1) (:219, :222)
+                       torch.multinomial(w, 1) (:219, :222); on the
+                       generator's device (a GPU generator with scores, q and
+                       drafts on that GPU runs the reference's loop as it runs
+                       there)
     TapeDraws          the same draws read from a tape: u[j] for draft j and
                        one row e of Exp(1) values; multinomial(w, 1) is
                        argmax(w / e) (the exponential-race form torch's
@@ -61,7 +64,7 @@ class LazyDraws:
         self.uniforms, self.exponentials = [], []  # what was drawn, for a tape replay
 
     def uniform(self, j):
-        u = torch.rand((), generator=self.generator)
+        u = torch.rand((), generator=self.generator, device=self.generator.device)
         self.uniforms.append(float(u))
         return u
 

@@ -151,6 +151,81 @@ class Uniform:
         return tokens, torch.full((len(histories), count, V), 1.0 / V, device=generator.device), None
 
 
+def reference_rounds(model, prompt, rows, calls, temperature, top_k, generator, drafter, draft):
+    """The reference Writer's speculative rounds (__init__.py:71-233, no
+    features or scheduler), restated with the oracle's rule drawing lazily
+    from `generator` (oracle.sampling.LazyDraws): the tokens of each call."""
+    device = generator.device
+    one = model.new_cache(1)
+    if len(prompt) > 1:
+        model.extend(torch.tensor([prompt[:-1]], device=device), one)
+    cache = one.select([0] * rows)
+    pending, histories = [[prompt[-1]] for _ in range(rows)], [list(prompt) for _ in range(rows)]
+
+    def probabilities(scores):
+        return oracle_sampling.probabilities(scores, temperature, top_k)
+
+    out = []
+    for limits in calls:
+        rs = sorted(limits)
+        drafted, q, _ = drafter.draft(model, [histories[r] for r in rs], None, draft, probabilities, generator)
+        drafted, q = drafted.to(device), q.to(device).float()
+        caps = [min(draft, limits[r] - 1) for r in rs]
+        feeds = [[] for _ in range(rows)]
+        for i, r in enumerate(rs):
+            feeds[r] = pending[r] + drafted[i, :caps[i]].tolist()
+        width = max(len(f) for f in feeds)
+        ids = torch.tensor([f + [0] * (width - len(f)) for f in feeds], device=device)
+        scores = model.extend(ids, cache, [len(f) for f in feeds], True)[0][rs]
+        written, kept = {}, [0] * rows
+        for i, r in enumerate(rs):
+            first = len(pending[r]) - 1
+            p = probabilities(scores[i, first:first + caps[i] + 1])
+            tokens = oracle_sampling.accept_row(p, q[i], drafted[i], caps[i], oracle_sampling.LazyDraws(generator))
+            written[r] = oracle_sampling.cut(tokens, set(), limits[r])
+            kept[r] = first + len(written[r])
+        model.undo(cache, kept)
+        for r, tokens in written.items():
+            histories[r] += tokens
+            pending[r] = [tokens[-1]]
+        out.append(written)
+    return out
+
+
+@pytest.mark.parametrize("top_k", [None, 40])
+def test_a_seeded_writer_writes_the_reference_writer_s_tokens(device, top_k):
+    # the same model, drafter and seed: the Writer (its draws replayed from the
+    # generator's stream on the GPU) and the reference's rounds write the same
+    # tokens, and leave their generators at the same offset
+    gpu, _ = models(PLUMBING, torch.float32, std=0.05)
+    prompt, calls = [0, 5, 7, 9], [{0: 4, 1: 4, 2: 4}, {0: 2, 2: 5}, {0: 4, 1: 1, 2: 4}, {0: 4, 1: 4, 2: 4}]
+    reference = torch.Generator(device=device).manual_seed(21)
+    expected = reference_rounds(gpu, prompt, 3, calls, 1.0, top_k, reference, Uniform(), 3)
+    mine = torch.Generator(device=device).manual_seed(21)
+    writer = Writer(gpu, prompt, 3, temperature=1.0, top_k=top_k, generator=mine, drafter=Uniform(), draft=3)
+    assert [writer.write({}, limits) for limits in calls] == expected
+    assert torch.equal(mine.get_state(), reference.get_state())
+
+
+def test_a_seeded_writer_without_drafts_samples_as_the_reference_does(device):
+    # Writer._sample (__init__.py:181-182): one multinomial over every row's
+    # distribution at its last token
+    gpu, _ = models(PLUMBING, torch.float32, std=0.05)
+    prompt = [1, 2, 3]
+    mine = torch.Generator(device=device).manual_seed(8)
+    writer = Writer(gpu, prompt, 4, temperature=0.7, top_k=40, generator=mine)
+    got = writer.write({}, {0: 1, 1: 1, 3: 1})
+    reference = torch.Generator(device=device).manual_seed(8)
+    one = gpu.new_cache(1)  # the reading the Writer makes: the prompt but its last token, then each row's last
+    gpu.extend(torch.tensor([prompt[:-1]], device=device), one)
+    ids = torch.tensor([[prompt[-1]]] * 4, device=device)
+    scores = gpu.extend(ids, one.select([0] * 4), [1, 1, 0, 1])[0][[0, 1, 3], 0]
+    p = oracle_sampling.probabilities(scores, 0.7, 40)
+    expected = torch.multinomial(p, 1, generator=reference)[:, 0].tolist()
+    assert got == {0: [expected[0]], 1: [expected[1]], 3: [expected[2]]}
+    assert torch.equal(mine.get_state(), reference.get_state())
+
+
 def test_the_writer_keeps_every_draft_of_the_model_itself(device):
     gpu, _ = models(PLUMBING, torch.float32, std=0.05)
     writer = Writer(gpu, [0, 5, 7], 2, temperature=1.0, top_k=None,

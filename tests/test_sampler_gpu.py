@@ -146,6 +146,98 @@ def test_a_lazy_run_is_replayed_through_its_tape(device):
     assert sampling.written(tokens, counts) == expected
 
 
+def offset(generator):
+    return int(generator.get_state().view(torch.int64)[1])
+
+
+def race_gap(w, e):
+    """The relative gap between the two largest w / e (how far a
+    multinomial draw is from another outcome)."""
+    top = torch.topk((w.double() / e.double()).reshape(-1), 2).values
+    return float((top[0] - top[1]) / top[0])
+
+
+@pytest.mark.parametrize("V, top_k, temperature, dtype", [(32768, None, 0.8, torch.float32),
+                                                          (32768, 40, 0.8, torch.bfloat16),
+                                                          (4096, 1024, 1.0, torch.float32),
+                                                          (50, None, 1.3, torch.float32)])
+def test_in_order_draws_write_the_reference_loop_s_tokens_from_a_gpu_generator(device, V, top_k, temperature,
+                                                                               dtype):
+    # the reference's loop run on the GPU with its generator there (torch.rand
+    # per draft judged, then a multinomial, row after row) against the fused
+    # path drawing the same stream from a generator seeded alike: the same
+    # tokens, and the two generators end at the same offset
+    B, L = 32, 4
+    scores, q, drafts, _, _ = step_inputs(B, L, V, seed=100 + V + (top_k or 0))
+    scores = scores.to(dtype).float() if dtype == torch.bfloat16 else scores
+    lengths = [(b * 7) % (L + 1) for b in range(B)]  # 0 .. L drafts a row
+    on = [x.to(device) for x in (scores, q, drafts)]
+    reference = torch.Generator(device=device).manual_seed(11)
+    lazy = [oracle.LazyDraws(reference) for _ in range(B)]
+    expected = [oracle.accept(on[0][b:b + 1], on[1][b:b + 1], on[2][b:b + 1], [lengths[b]], temperature, top_k,
+                              [lazy[b]])[0] for b in range(B)]
+    # no decision or draw of the reference's within 1e-5 of flipping (a flip moves every later row's draws)
+    u = torch.zeros(B, L)
+    for b in range(B):
+        u[b, :len(lazy[b].uniforms)] = torch.tensor(lazy[b].uniforms)
+    assert min(oracle.margins(scores, q, drafts, lengths, temperature, top_k, u)) > NEAR
+    for b in range(B):
+        n = len(expected[b]) - 1
+        p = oracle.probabilities(on[0][b, n], temperature, top_k)
+        w = (p - on[1][b, n]).clamp(min=0) if n < lengths[b] else p
+        assert race_gap(w / w.sum(), lazy[b].exponentials[0]) > NEAR
+    mine = torch.Generator(device=device).manual_seed(11)
+    state = sampling.generator_state(mine, device)
+    given = on[0].to(dtype) if dtype == torch.bfloat16 else on[0]
+    tokens, counts = sampling.accept_in_order(given, on[1], on[2], state, temperature, top_k, lengths=lengths)
+    assert sampling.written(tokens, counts) == expected
+    sampling.set_offset(mine, state)
+    assert offset(mine) == offset(reference) == 4 * sum(min(len(t), lengths[b]) + 1 for b, t in enumerate(expected))
+    # the stream goes on where the reference's does
+    assert torch.equal(torch.rand(3, generator=mine, device=device), torch.rand(3, generator=reference, device=device))
+
+
+@pytest.mark.parametrize("B, V, top_k", [(7, 32768, 40), (65, 32768, None)])
+def test_a_joint_in_order_draw_is_the_reference_s_sample_of_every_row(device, B, V, top_k):
+    # Writer._sample: one torch.multinomial over the (rows, V) distributions;
+    # at 65 x 32768 entries torch's draw takes two words of some threads
+    generator = torch.Generator().manual_seed(B)
+    scores = (3 * torch.randn(B, 1, V, generator=generator)).to(device)
+    reference = torch.Generator(device=device).manual_seed(5)
+    p = oracle.probabilities(scores[:, 0], 0.9, top_k)
+    state_before = reference.get_state()
+    e = torch.empty_like(p).exponential_(generator=reference)
+    reference.set_state(state_before)
+    expected = torch.multinomial(p, 1, generator=reference)[:, 0].tolist()
+    assert min(race_gap(p[b], e[b]) for b in range(B)) > NEAR
+    mine = torch.Generator(device=device).manual_seed(5)
+    state = sampling.generator_state(mine, device)
+    tokens, counts = sampling.accept_in_order(scores, None, None, state, 0.9, top_k, joint=True)
+    assert [t[0] for t in sampling.written(tokens, counts)] == expected
+    sampling.set_offset(mine, state)
+    assert offset(mine) == offset(reference)
+
+
+def test_in_order_draws_with_the_commit_move_the_cache_as_the_tape_path_does(device):
+    # the same tokens with or without the commit, and the commit's lengths,
+    # feeds and counts as wptv_accept_commit's for those tokens
+    B, L, V = 16, 4, 8192
+    scores, q, drafts, _, _ = step_inputs(B, L, V, seed=77)
+    on = [x.to(device) for x in (scores, q, drafts)]
+    state = sampling.generator_state(torch.Generator(device=device).manual_seed(3), device)
+    t1, c1 = sampling.accept_in_order(*on, state.clone(), 0.8, 40)
+    before = torch.arange(B, dtype=torch.long, device=device) * 10
+    lengths = before + L + 1
+    feeds = torch.full((B, 1), -5, dtype=torch.long, device=device)
+    written = torch.zeros(B, dtype=torch.long, device=device)
+    failed = torch.zeros(1, dtype=torch.int32, device=device)
+    t2, c2 = sampling.accept_in_order(*on, state, 0.8, 40, commit=(lengths, before, feeds, failed, written))
+    assert torch.equal(t1, t2) and torch.equal(c1, c2)
+    assert torch.equal(lengths, before + c2.long()) and torch.equal(written, c2.long())
+    last = t2.gather(1, (c2.long() - 1)[:, None])[:, 0]
+    assert torch.equal(feeds[:, 0], last) and int(failed) == 0
+
+
 def test_greedy_chain_matches_the_oracle_and_top_k_one(device):
     B, L, V = 64, 4, 32768
     scores, q, drafts, u, e = step_inputs(B, L, V, seed=8)

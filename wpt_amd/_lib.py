@@ -12,7 +12,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwptv.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 WPTV_F32, WPTV_BF16 = 0, 1
 DTYPES = {torch.float32: WPTV_F32, torch.bfloat16: WPTV_BF16}
@@ -78,6 +78,8 @@ SIGNATURES = {
                     _P, _SZ, _P],
     "wptv_accept_commit": [_P, _I64, _I64, _I, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P,
                            _P, _P, _SZ, _P, _P, _P, _I64, _P, _P, _P],
+    "wptv_accept_in_order": [_P, _I64, _I64, _I, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _I, _F, _I, _I, _I, _I,
+                             _P, _P, _P, _SZ, _P, _P, _P, _I64, _P, _P, _P],
     "wptv_greedy_tree": [_P, _I64, _I64, _I, _P, _P, _I, _I, _I, _P, _P, _P, _P, _SZ, _P],
     "wptv_greedy_tree_best": [_P, _P, _P, _I, _I, _P, _P, _P, _P],
 }

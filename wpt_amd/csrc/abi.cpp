@@ -12,6 +12,7 @@ namespace {
 thread_local char last_error[512] = "";
 constexpr int kMaxDevices = 64;
 int cu_count[kMaxDevices] = {0};
+int draw_cap[kMaxDevices] = {0};
 std::mutex cu_mutex;
 }  // namespace
 
@@ -39,6 +40,21 @@ int compute_units() {
     cu_count[device] = n;
   }
   return cu_count[device];
+}
+
+int draw_workgroups_cap() {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return -1;
+  std::lock_guard<std::mutex> lock(cu_mutex);
+  if (draw_cap[device] == 0) {
+    int cus = 0, threads = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        hipDeviceGetAttribute(&threads, hipDeviceAttributeMaxThreadsPerMultiProcessor, device) != hipSuccess ||
+        cus <= 0 || threads < 256)
+      return -1;
+    draw_cap[device] = cus * (threads / 256);
+  }
+  return draw_cap[device];
 }
 
 }  // namespace wptv

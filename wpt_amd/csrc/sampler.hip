@@ -19,11 +19,20 @@
 //                  row's tokens from the per-position results
 //   tree_walk      greedy verification of a draft tree from the per-node argmax
 //
+// Or with the draws the reference's loop makes from a torch generator on the
+// device, in its order (wptv_accept_in_order): accept_stats leaves each
+// position's p and q of its draft and its residual mass; order_draw replays
+// the loop's uniforms (Philox4x32-10, as torch's device generator draws
+// them) to find each row's first rejection and the generator offset of its
+// multinomial, then draws that multinomial's exponentials over a slice of
+// the vocabulary; accept_pick joins the slices.
+//
 // Each vocabulary row is read once per pass from HBM with coalesced loads and
 // kept in registers (ITEMS values per thread); reductions are wavefront
 // shuffles, then one LDS step across the 16 wavefronts.
 #include "wptv_common.h"
 
+#include <algorithm>
 #include <climits>
 
 namespace wptv {
@@ -40,6 +49,9 @@ struct Stats {  // per (batch row, position); arrays of B * P in the workspace
   int* best;    // first maximal index of the scores
   int* keep;    // 1 if the draft at this position is kept
   int* cand;    // the token drawn if this position is the first rejection (the bonus at the last), -1: none
+  float* pd;    // in-order draws: p of the draft at this position
+  float* qd;    // and its q
+  float* rest;  // the residual's mass max(0, p - q) summed (1 after the last draft)
 };
 
 __device__ __forceinline__ float block_max(float x, float* red) {
@@ -164,12 +176,13 @@ __device__ __forceinline__ float div_by(float x, float d, float y) {
 }
 
 // e^t for t <= 0 (NaN gives 0): 2^(t log2 e) with the product carried in two
-// parts (its rounding error by an FMA, plus t times the low part of log2 e),
-// split at its nearest integer n, the fraction's power on the hardware's
-// exp2 and scaled by 2^n; below ln 2^-149 the result is 0.  The same steps
-// and constants as the device library's expf, whose overflow branch a
-// non-positive argument never takes.  Contraction off: ph - n must subtract
-// the rounded product, whose rounding error pl carries.
+// parts (its rounding error by an FMA, plus t times the low part of log2 e:
+// a Cody-Waite style split of the constant, Cody and Waite, "Software Manual
+// for the Elementary Functions", 1980), split at its nearest integer n, the
+// fraction's power on the hardware's exp2 and scaled by 2^n; below ln 2^-149
+// the result is 0.  A non-positive argument needs no overflow branch.
+// Contraction off: ph - n must subtract the rounded product, whose rounding
+// error pl carries.
 __device__ __forceinline__ float exp_nonpos(float t) {
 #pragma clang fp contract(off)
   const float ph = t * kLog2e;
@@ -285,8 +298,9 @@ __device__ float kth_largest(const float (&s)[ITEMS], int k, int* hist, int* sel
 // need the registers), so that the rows stream in together, and the draft's
 // own p and q come from the thread that holds its score; needs the row in
 // LDS (V <= 32768, a multiple of 4 floats, 16-byte aligned).  CUT: a top-k
-// cut (0 < top_k < V).
-template <int ITEMS, typename S, bool QLDS, bool CUT>
+// cut (0 < top_k < V).  ORDER: no tape; the position's p and q of its draft
+// and its residual mass are left for order_draw, which makes the draws.
+template <int ITEMS, typename S, bool QLDS, bool CUT, bool ORDER>
 __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores, int64_t sb, int64_t st,
                                                    const int32_t* __restrict__ firsts, const float* q,
                                                    int64_t qb, int64_t qt, const int64_t* __restrict__ drafts,
@@ -314,7 +328,7 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
   // read 0, masked after
   const bool draft_pos = j < n;
   const float* qrow = (!greedy && draft_pos) ? q + b * qb + j * qt : nullptr;
-  const float* erow = greedy ? nullptr : e + (int64_t)b * V;
+  const float* erow = (greedy || ORDER) ? nullptr : e + (int64_t)b * V;
   S bits[ITEMS];
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) bits[i] = score_bits<S>(row, V, i);
@@ -345,7 +359,7 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
     // it is before the residual): wave w's instruction c moves floats 4096 c
     // + 256 w .. + 255 to the same entries of qs (16 bytes a lane); the range
     // check covers the row's V * 4 bytes
-    if constexpr (!CUT) {
+    if constexpr (!CUT && !ORDER) {
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i) ev[i] = row_item(erow, V, i);
     }
@@ -376,7 +390,7 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
   float thr = kNegInfS;
   if constexpr (CUT) {
     thr = kth_largest<ITEMS>(x, top_k, hist, sel, redv);
-    if constexpr (QLDS) {
+    if constexpr (QLDS && !ORDER) {
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i) ev[i] = row_item(erow, V, i);
     }
@@ -440,45 +454,258 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
     }
     rest_sum = block_sum(rest, redv);
   }
-  if constexpr (!QLDS) {
+  if constexpr (ORDER) {
+    if (tid == 0) {
+      stats.m[idx] = m;
+      stats.z[idx] = z;
+      stats.thr[idx] = thr;
+      stats.best[idx] = -1;
+      stats.rest[idx] = rest_sum;
+      if constexpr (!QLDS) {
+        float pdg = 0.f, qdg = 0.f;  // an out-of-range draft is rejected: u * 0 < 0 never holds
+        if (d >= 0 && d < V) {
+          const float sd = load_f32(row + d) / temperature;
+          pdg = sd >= thr ? exp_nonpos(sd - m) * zinv : 0.f;
+          qdg = q[b * qb + j * qt + d];
+        }
+        stats.pd[idx] = pdg;
+        stats.qd[idx] = qdg;
+      } else if (!(d >= 0 && d < V)) {
+        stats.pd[idx] = 0.f;
+        stats.qd[idx] = 0.f;
+      }
+    }
+    if (owner) {
+      stats.pd[idx] = pd;
+      stats.qd[idx] = qs[d];
+    }
+    return;
+  } else {
+    if constexpr (!QLDS) {
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) ev[i] = row_item(erow, V, i);
+      for (int i = 0; i < ITEMS; ++i) ev[i] = row_item(erow, V, i);
+    }
+    // each thread's entries in index order: the first of its largest values
+    // wins (a NaN never does), as arg_better's order across threads has it
+    float cv = kNegInfS;
+    int ci = INT_MAX;
+    const float rinv = 1.f / rest_sum;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const float c = (draft_pos ? div_by(x[i], rest_sum, rinv) : x[i]) / ev[i];
+      if (c > cv) {
+        cv = c;
+        ci = tid + i * kT;
+      }
+    }
+    const int drawn = block_argmax(cv, ci, redv, redi);
+    if (tid == 0) {
+      stats.m[idx] = m;
+      stats.z[idx] = z;
+      stats.thr[idx] = thr;
+      stats.best[idx] = -1;  // the raw argmax: greedy decisions only
+      // a residual with no mass has no draw (the reference's multinomial raises)
+      stats.cand[idx] = (!(draft_pos && !(rest_sum > 0.f)) && drawn >= 0 && drawn < V) ? drawn : -1;
+      if constexpr (!QLDS) {
+        int keep = 0;
+        if (d >= 0 && d < V) {
+          const float sd = load_f32(row + d) / temperature;
+          const float pdg = sd >= thr ? exp_nonpos(sd - m) * zinv : 0.f;
+          keep = u[(int64_t)b * L + j] * q[b * qb + j * qt + d] < pdg;
+        }
+        stats.keep[idx] = keep;
+      } else if (!(d >= 0 && d < V)) {
+        stats.keep[idx] = 0;
+      }
+    }
+    // the same p as exp(s_d - m) * (1 / z) of the draft's score: the decision u * q[d] < p[d]
+    if (owner) stats.keep[idx] = u[(int64_t)b * L + j] * qs[d] < pd;
   }
-  // each thread's entries in index order: the first of its largest values
-  // wins (a NaN never does), as arg_better's order across threads has it
+}
+
+// ---- the draws of torch's device generator, in the reference's order --------
+//
+// torch draws on the GPU from Philox4x32-10 (Salmon, Moraes, Dror and Shaw,
+// "Parallel random numbers: as easy as 1, 2, 3", SC 2011) through hipRAND:
+// a call that draws numel floats at the generator's offset o runs S threads
+// (256 a workgroup, min(multiprocessors x max threads a multiprocessor / 256,
+// ceil(numel / 256)) workgroups), and thread t takes block (o / 4 + k) of its
+// subsequence t, word w of it giving entry 4 S k + S w + t; each float is
+// (word + 1) 2^-32 rounded, in (0, 1]; the call then moves the offset on by
+// 4 ceil(numel / 4 S).  The reference's loop draws, row by row, one
+// torch.rand(()) per draft it judges (offset + 4 each; a value of 1 read as
+// 0) and then one torch.multinomial(w, 1) over the vocabulary, which is
+// argmax_v w_v / e_v over numel = V exponentials e_v = -log u_v (u at or
+// above 1 - 2^-24 taken as giving 2^-24) and moves the offset by 4 more.
+
+constexpr int kDT = 256;        // threads of a draw workgroup
+constexpr int kSlices = 8;      // draw workgroups a row's multinomial is shared over
+constexpr int kScanMax = 4096;  // positions B (L + 1) the in-order scan may read
+
+struct Order {
+  const int64_t* state;  // the generator's [seed, offset] on the device
+  int64_t* next;         // where the offset after this call's draws is written
+  uint32_t threads;      // S of the multinomial's draw (of V entries, or of B V when joint)
+  int joint;             // one multinomial over every row's V entries (L = 0: Writer._sample's)
+  int64_t joint_step;    // that draw's offset step
+  int2* rows;            // per row: (first rejected draft, or the count when none is; its draw's block index)
+  float2* parts;         // per row and slice: the slice's race winner (value, index bits)
+};
+
+__device__ __forceinline__ uint32_t philox_word(uint64_t counter, uint64_t subsequence, uint64_t seed, int word) {
+  uint32_t c0 = (uint32_t)counter, c1 = (uint32_t)(counter >> 32);
+  uint32_t c2 = (uint32_t)subsequence, c3 = (uint32_t)(subsequence >> 32);
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+    c1 = (uint32_t)p1;
+    c3 = (uint32_t)p0;
+    c0 = n0;
+    c2 = n2;
+    k0 += 0x9E3779B9u;  // the key schedule's Weyl increments
+    k1 += 0xBB67AE85u;
+  }
+  return word == 0 ? c0 : word == 1 ? c1 : word == 2 ? c2 : c3;
+}
+
+__device__ __forceinline__ float word_uniform(uint32_t w) { return 0x1p-32f + (float)w * 0x1p-32f; }
+
+// Entry li of a draw of S threads at offset o.
+__device__ __forceinline__ float drawn_uniform(uint64_t seed, uint64_t o, uint32_t li, uint32_t S) {
+  const uint32_t block = li / (4u * S), rest = li - block * 4u * S, word = rest / S;
+  return word_uniform(philox_word(o / 4 + block, rest - word * S, seed, (int)word));
+}
+
+__device__ __forceinline__ float drawn_exponential(float u) {
+  return -1.f * (u >= 1.f - 0x1p-24f ? -0x1p-24f : __logf(u));
+}
+
+// The draws of row b's multinomial over vocabulary slice s (blockIdx.x = b
+// kSlices + s).  Each workgroup first replays the loop up to its row: the
+// uniforms u_t = U(o + 4 t) it may read, every row's drafts' p and q, then
+// wavefront 0 takes the rows in turn (lane j judging draft j:
+// u * q < p keeps it), a row of n judged drafts moving t on by n + 1.  Row
+// b's multinomial then draws at offset o + 4 t from position js's
+// distribution: the residual max(0, p - q) over its mass, or p after the
+// last draft; its p from the statistics of that position (the same steps as
+// accept_stats, so the same bits).  Only entries with w > 0 draw an
+// exponential: 0 / e is 0 for every e the draw can give.
+template <int N, typename S, bool CUT>
+__global__ __launch_bounds__(kDT) void order_draw(const S* __restrict__ scores, int64_t sb, int64_t st,
+                                                  const int32_t* __restrict__ firsts, const float* __restrict__ q,
+                                                  int64_t qb, int64_t qt, const int32_t* __restrict__ lengths,
+                                                  float temperature, int B, int L, int V, Stats stats, Order order) {
+  __shared__ float utab[kScanMax];
+  __shared__ float spd[kScanMax], sqd[kScanMax];
+  __shared__ int slen[kScanMax];
+  __shared__ float redv[kDT / 64];
+  __shared__ int redi[kDT / 64];
+  __shared__ int found[2];
+  const int b = blockIdx.x / kSlices, s = blockIdx.x % kSlices, tid = threadIdx.x;
+  if (b >= B) return;
+  const int P = L + 1;
+  const uint64_t seed = (uint64_t)order.state[0], base = (uint64_t)order.state[1];
+  int js = 0, t_draw = 0;
+  if (!order.joint) {
+    const int reach = (b + 1) * P;  // t stays below this up to row b
+    for (int t = tid; t < reach; t += kDT) {
+      const float u = word_uniform(philox_word(base / 4 + (uint64_t)t, 0, seed, 0));
+      utab[t] = u == 1.f ? 0.f : u;
+    }
+    for (int r = tid; r <= b; r += kDT) slen[r] = lengths ? min(max(lengths[r], 0), L) : L;
+    for (int k = tid; k < (b + 1) * L; k += kDT) {
+      const int r = k / L, j = k - r * L;
+      spd[k] = stats.pd[r * P + j];
+      sqd[k] = stats.qd[r * P + j];
+    }
+    __syncthreads();
+    if (tid < 64) {
+      int t = 0;
+      for (int r = 0; r <= b; ++r) {
+        const int len = slen[r];
+        const bool rejected = tid < len && !(utab[t + tid] * sqd[r * L + tid] < spd[r * L + tid]);
+        const uint64_t mask = __builtin_amdgcn_ballot_w64(rejected);
+        const int first = mask ? __builtin_ctzll(mask) : len;
+        const int n = first < len ? first + 1 : len;
+        if (r == b) {
+          js = first;
+          t_draw = t + n;
+        }
+        t += n + 1;
+      }
+      if (tid == 0) {
+        found[0] = js;
+        found[1] = t_draw;
+      }
+    }
+    __syncthreads();
+    js = found[0];
+    t_draw = found[1];
+    if (s == 0 && tid == 0) order.rows[b] = make_int2(js, t_draw);
+  } else if (s == 0 && tid == 0) {
+    order.rows[b] = make_int2(0, 0);
+  }
+  const int len = order.joint ? 0 : (lengths ? min(max(lengths[b], 0), L) : L);
+  const bool draft_pos = js < len;
+  const int idx = b * P + js;
+  const float m = stats.m[idx], z = stats.z[idx], thr = stats.thr[idx], rest = stats.rest[idx];
+  const float zinv = 1.f / z, rinv = 1.f / rest, tinv = 1.f / temperature;
+  const int64_t first = firsts ? firsts[b] : 0;
+  const S* row = scores + b * sb + (first + js) * st;
+  const float* qrow = draft_pos ? q + b * qb + js * qt : nullptr;
+  const uint64_t o = base + 4 * (uint64_t)t_draw;
+  const uint32_t li0 = order.joint ? (uint32_t)b * (uint32_t)V : 0u;
+  const int per = (V + kSlices - 1) / kSlices, v0 = s * per, v1 = min(V, v0 + per);
+  // every load first: the slice's scores and draft entries
+  S bits[N];
+  float qv[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int v = v0 + tid + i * kDT;
+    bits[i] = v < v1 ? row[v] : S(0);
+    qv[i] = (draft_pos && v < v1) ? qrow[v] : 0.f;
+  }
   float cv = kNegInfS;
   int ci = INT_MAX;
-  const float rinv = 1.f / rest_sum;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    const float c = (draft_pos ? div_by(x[i], rest_sum, rinv) : x[i]) / ev[i];
+  for (int i = 0; i < N; ++i) {
+    const int v = v0 + tid + i * kDT;
+    if (v >= v1) continue;
+    const float x = div_by(score_value<S>(bits[i]), temperature, tinv);
+    float w;
+    if constexpr (CUT)
+      w = x >= thr ? exp_nonpos(x - m) : 0.f;
+    else
+      w = exp_nonpos(x - m);
+    w = w * zinv;
+    if (draft_pos) w = div_by(fmaxf(w - qv[i], 0.f), rest, rinv);
+    float c = w;  // 0 (and a NaN) as w / e would give them
+    if (w > 0.f) c = w / drawn_exponential(drawn_uniform(seed, o, li0 + (uint32_t)v, order.threads));
     if (c > cv) {
       cv = c;
-      ci = tid + i * kT;
+      ci = v;
     }
   }
-  const int drawn = block_argmax(cv, ci, redv, redi);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float v2 = __shfl_xor(cv, off, 64);
+    const int i2 = __shfl_xor(ci, off, 64);
+    arg_better(cv, ci, v2, i2);
+  }
+  if ((tid & 63) == 0) {
+    redv[tid >> 6] = cv;
+    redi[tid >> 6] = ci;
+  }
+  __syncthreads();
   if (tid == 0) {
-    stats.m[idx] = m;
-    stats.z[idx] = z;
-    stats.thr[idx] = thr;
-    stats.best[idx] = -1;  // the raw argmax: greedy decisions only
-    // a residual with no mass has no draw (the reference's multinomial raises)
-    stats.cand[idx] = (!(draft_pos && !(rest_sum > 0.f)) && drawn >= 0 && drawn < V) ? drawn : -1;
-    if constexpr (!QLDS) {
-      int keep = 0;
-      if (d >= 0 && d < V) {
-        const float sd = load_f32(row + d) / temperature;
-        const float pdg = sd >= thr ? exp_nonpos(sd - m) * zinv : 0.f;
-        keep = u[(int64_t)b * L + j] * q[b * qb + j * qt + d] < pdg;
-      }
-      stats.keep[idx] = keep;
-    } else if (!(d >= 0 && d < V)) {
-      stats.keep[idx] = 0;
-    }
+    float bv = redv[0];
+    int bi = redi[0];
+#pragma unroll
+    for (int w = 1; w < kDT / 64; ++w) arg_better(bv, bi, redv[w], redi[w]);
+    order.parts[b * kSlices + s] = make_float2(bv, __int_as_float(bi));
   }
-  // the same p as exp(s_d - m) * (1 / z) of the draft's score: the decision u * q[d] < p[d]
-  if (owner) stats.keep[idx] = u[(int64_t)b * L + j] * qs[d] < pd;
 }
 
 // What a verify step does with a row's count once it is known, in the pick's
@@ -510,14 +737,38 @@ __device__ inline void commit_row(const Commit& c, int b, int n, int64_t last) {
 // Each row's tokens from the per-position decisions: the drafts up to the
 // first rejected one, then that position's draw (the argmax in greedy mode),
 // or every draft and the bonus draw (__init__.py:210-229).  One thread per row.
-template <bool COMMIT>
+// ORDER: the first rejection from order_draw's replay and the draw joined
+// from its slices in index order; the row of the last batch row writes the
+// generator's next offset.
+template <bool COMMIT, bool ORDER>
 __global__ __launch_bounds__(64) void accept_pick(const int64_t* __restrict__ drafts, int64_t db,
                                                   const int32_t* __restrict__ lengths, int greedy, int L, int B,
-                                                  Stats stats, int64_t* __restrict__ tokens,
-                                                  int32_t* __restrict__ n_tokens, Commit commit) {
+                                                  int V, Stats stats, int64_t* __restrict__ tokens,
+                                                  int32_t* __restrict__ n_tokens, Commit commit, Order order) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
   const int P = L + 1;
+  if constexpr (ORDER) {
+    const int2 at = order.rows[b];
+    const int js = at.x, len = order.joint ? 0 : (lengths ? min(max(lengths[b], 0), L) : L);
+    float2 parts[kSlices];
+#pragma unroll
+    for (int s = 0; s < kSlices; ++s) parts[s] = order.parts[b * kSlices + s];
+    float bv = kNegInfS;
+    int bi = INT_MAX;
+#pragma unroll
+    for (int s = 0; s < kSlices; ++s) arg_better(bv, bi, parts[s].x, __float_as_int(parts[s].y));
+    int pick = bi >= 0 && bi < V ? bi : -1;
+    // a residual with no mass has no draw (the reference's multinomial raises)
+    if (js < len && !(stats.rest[b * P + js] > 0.f)) pick = -1;
+    for (int t = 0; t < P; ++t)
+      tokens[(int64_t)b * P + t] = t < js ? drafts[b * db + t] : (t == js ? pick : -1);
+    n_tokens[b] = pick >= 0 ? js + 1 : -1;
+    if constexpr (COMMIT) commit_row(commit, b, pick >= 0 ? js + 1 : -1, pick);
+    if (b == B - 1)
+      *order.next = order.state[1] + (order.joint ? order.joint_step : 4 * ((int64_t)at.y + 1));
+    return;
+  }
   const int* drawn_at = greedy ? stats.best : stats.cand;
   constexpr int kMaxP = 16;
   if (P <= kMaxP) {
@@ -603,10 +854,15 @@ Stats carve(void* workspace, int B, int P) {
   s.best = reinterpret_cast<int*>(p + 3 * n);
   s.keep = reinterpret_cast<int*>(p + 4 * n);
   s.cand = reinterpret_cast<int*>(p + 5 * n);
+  s.pd = reinterpret_cast<float*>(p + 6 * n);
+  s.qd = reinterpret_cast<float*>(p + 7 * n);
+  s.rest = reinterpret_cast<float*>(p + 8 * n);
   return s;
 }
 
-size_t stats_bytes(int B, int P) { return 6 * align_up((size_t)B * P * 4, 256); }
+// The per-position arrays, then the in-order draws' per-row and per-slice results.
+size_t stats_bytes(int B, int P) { return 9 * align_up((size_t)B * P * 4, 256); }
+size_t order_bytes(int B) { return align_up((size_t)B * 8, 256) + align_up((size_t)B * kSlices * 8, 256); }
 
 int items_for(int V) {
   const int per = (V + kT - 1) / kT;
@@ -704,7 +960,7 @@ __global__ __launch_bounds__(kGT) void greedy_argmax(const S* __restrict__ score
 
 // One workgroup per (batch row, position): 8 ceil(B / 8) (L + 1) of them,
 // those past B returning at once.
-template <typename S>
+template <typename S, bool ORDER = false>
 void launch_stats(int B, hipStream_t stream, const void* scores, int64_t sb, int64_t st, const int32_t* firsts,
                   const float* q, int64_t qb, int64_t qt, const int64_t* drafts, int64_t db, const int32_t* lengths,
                   const float* u, const float* e, float temperature, int top_k, int greedy, int L, int V, Stats s) {
@@ -720,8 +976,8 @@ void launch_stats(int B, hipStream_t stream, const void* scores, int64_t sb, int
   const bool qlds = !greedy && q && V <= 32 * kT && V % 4 == 0 && aligned(q, 16) && qb % 4 == 0 && qt % 4 == 0;
   const bool cut = !greedy && top_k > 0 && top_k < V;
 #define WPTV_STATS_Q(I, QL, CU)                                                                                  \
-  hipLaunchKernelGGL((accept_stats<I, S, QL, CU>), grid, dim3(kT), 0, stream, rows, sb, st, firsts, q, qb, qt,     \
-                     drafts, db, lengths, u, e, temperature, top_k, greedy, B, L, V, s)
+  hipLaunchKernelGGL((accept_stats<I, S, QL, CU, ORDER>), grid, dim3(kT), 0, stream, rows, sb, st, firsts, q, qb,  \
+                     qt, drafts, db, lengths, u, e, temperature, top_k, greedy, B, L, V, s)
 #define WPTV_STATS_C(I, QL)            \
   if (cut) WPTV_STATS_Q(I, QL, true);  \
   else WPTV_STATS_Q(I, QL, false);
@@ -749,7 +1005,7 @@ using namespace wptv;
 extern "C" int wptv_accept_workspace(int B, int L, size_t* bytes) {
   if (!bytes) return fail(WPTV_E_INVALID, "accept_workspace: null output pointer");
   if (B <= 0 || L < 0) return fail(WPTV_E_INVALID, "accept_workspace: B must be positive and L >= 0 (got %d, %d)", B, L);
-  *bytes = stats_bytes(B, L + 1);
+  *bytes = stats_bytes(B, L + 1) + order_bytes(B);
   return WPTV_OK;
 }
 
@@ -780,11 +1036,11 @@ int accept_impl(const void* scores, int64_t scores_stride_b, int64_t scores_stri
   int st = launched("accept_stats");
   if (st != WPTV_OK) return st;
   if (commit)
-    hipLaunchKernelGGL(accept_pick<true>, dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b, lengths,
-                       greedy, L, B, s, tokens, n_tokens, *commit);
+    hipLaunchKernelGGL((accept_pick<true, false>), dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b,
+                       lengths, greedy, L, B, V, s, tokens, n_tokens, *commit, Order{});
   else
-    hipLaunchKernelGGL(accept_pick<false>, dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b, lengths,
-                       greedy, L, B, s, tokens, n_tokens, Commit{});
+    hipLaunchKernelGGL((accept_pick<false, false>), dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b,
+                       lengths, greedy, L, B, V, s, tokens, n_tokens, Commit{}, Order{});
   return launched("accept_pick");
 }
 
@@ -815,6 +1071,103 @@ extern "C" int wptv_accept_commit(const void* scores, int64_t scores_stride_b, i
   return accept_impl(scores, scores_stride_b, scores_stride_t, scores_dtype, firsts, q, q_stride_b, q_stride_t, drafts,
                      drafts_stride_b, lengths, u, e, temperature, top_k, greedy, B, L, V, tokens, n_tokens, workspace,
                      workspace_bytes, &c, stream);
+}
+
+namespace {
+
+template <typename S>
+void launch_order_draw(int B, hipStream_t stream, const void* scores, int64_t sb, int64_t st, const int32_t* firsts,
+                       const float* q, int64_t qb, int64_t qt, const int32_t* lengths, float temperature, int top_k,
+                       int L, int V, Stats s, Order o) {
+  const int per = (V + kSlices - 1) / kSlices;
+  const int n = (per + kDT - 1) / kDT;
+  const bool cut = top_k > 0 && top_k < V;
+  const S* rows = static_cast<const S*>(scores);
+  const dim3 grid(B * kSlices);
+#define WPTV_DRAW(N)                                                                                                  \
+  do {                                                                                                                \
+    if (cut)                                                                                                          \
+      hipLaunchKernelGGL((order_draw<N, S, true>), grid, dim3(kDT), 0, stream, rows, sb, st, firsts, q, qb, qt,     \
+                         lengths, temperature, B, L, V, s, o);                                                        \
+    else                                                                                                              \
+      hipLaunchKernelGGL((order_draw<N, S, false>), grid, dim3(kDT), 0, stream, rows, sb, st, firsts, q, qb, qt,    \
+                         lengths, temperature, B, L, V, s, o);                                                        \
+  } while (0)
+  if (n <= 1) WPTV_DRAW(1);
+  else if (n <= 2) WPTV_DRAW(2);
+  else if (n <= 4) WPTV_DRAW(4);
+  else if (n <= 8) WPTV_DRAW(8);
+  else if (n <= 16) WPTV_DRAW(16);
+  else WPTV_DRAW(32);
+#undef WPTV_DRAW
+}
+
+}  // namespace
+
+extern "C" int wptv_accept_in_order(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t,
+                                    int scores_dtype, const int32_t* firsts, const float* q, int64_t q_stride_b,
+                                    int64_t q_stride_t, const int64_t* drafts, int64_t drafts_stride_b,
+                                    const int32_t* lengths, const int64_t* generator_state, int64_t* next_offset,
+                                    int joint, float temperature, int top_k, int B, int L, int V, int64_t* tokens,
+                                    int32_t* n_tokens, void* workspace, size_t workspace_bytes,
+                                    int64_t* cache_lengths, const int64_t* cache_before, int64_t* feeds,
+                                    int64_t feeds_stride, int32_t* failed, int64_t* written, hipStream_t stream) {
+  if (!scores || !tokens || !n_tokens || !generator_state || !next_offset || (L > 0 && (!drafts || !q)))
+    return fail(WPTV_E_INVALID,
+                "accept_in_order: scores, tokens, n_tokens, the generator state, next_offset (and drafts and q when "
+                "L > 0) must be given");
+  if (B <= 0 || L < 0 || V <= 0) return fail(WPTV_E_INVALID, "accept_in_order: bad shape B=%d L=%d V=%d", B, L, V);
+  if (!(temperature > 0.f))
+    return fail(WPTV_E_INVALID, "accept_in_order: temperature must be positive (got %g)", (double)temperature);
+  if (joint && L != 0) return fail(WPTV_E_INVALID, "accept_in_order: a joint draw takes no drafts (L = %d)", L);
+  if ((int64_t)B * (L + 1) > kScanMax || L > 64)
+    return fail(WPTV_E_UNSUPPORTED, "accept_in_order: B (L + 1) = %lld above %d or L = %d above 64",
+                (long long)B * (L + 1), kScanMax, L);
+  if (items_for(V) == 0)
+    return fail(WPTV_E_UNSUPPORTED, "accept_in_order: a vocabulary of %d is above %d", V, 64 * kT);
+  if (scores_dtype != WPTV_F32 && scores_dtype != WPTV_BF16)
+    return fail(WPTV_E_UNSUPPORTED, "accept_in_order: scores dtype %d is neither fp32 nor bf16", scores_dtype);
+  const size_t need = stats_bytes(B, L + 1) + order_bytes(B);
+  if (!workspace || workspace_bytes < need)
+    return fail(WPTV_E_INVALID, "accept_in_order: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  if (cache_lengths && (!cache_before || !feeds))
+    return fail(WPTV_E_INVALID, "accept_in_order: a commit needs cache_lengths, cache_before and feeds");
+  const int cap = draw_workgroups_cap();
+  if (cap <= 0) return fail(WPTV_E_HIP, "accept_in_order: the device's multiprocessors cannot be queried");
+  // the multinomial's draw as torch launches it: numel entries over S threads
+  const int64_t numel = joint ? (int64_t)B * V : V;
+  if (numel >= (int64_t)1 << 31)
+    return fail(WPTV_E_UNSUPPORTED, "accept_in_order: a joint draw of %lld entries", (long long)numel);
+  const int64_t threads = 256 * std::min<int64_t>(cap, (numel + 255) / 256);
+  const Stats s = carve(workspace, B, L + 1);
+  char* extra = static_cast<char*>(workspace) + stats_bytes(B, L + 1);
+  Order o{};
+  o.state = generator_state;
+  o.next = next_offset;
+  o.threads = (uint32_t)threads;
+  o.joint = joint ? 1 : 0;
+  o.joint_step = 4 * ((numel - 1) / (4 * threads) + 1);
+  o.rows = reinterpret_cast<int2*>(extra);
+  o.parts = reinterpret_cast<float2*>(extra + align_up((size_t)B * 8, 256));
+  (scores_dtype == WPTV_BF16 ? launch_stats<unsigned short, true> : launch_stats<float, true>)(
+      B, stream, scores, scores_stride_b, scores_stride_t, firsts, q, q_stride_b, q_stride_t, drafts,
+      drafts_stride_b, lengths, nullptr, nullptr, temperature, top_k, 0, L, V, s);
+  int st = launched("accept_stats");
+  if (st != WPTV_OK) return st;
+  (scores_dtype == WPTV_BF16 ? launch_order_draw<unsigned short> : launch_order_draw<float>)(
+      B, stream, scores, scores_stride_b, scores_stride_t, firsts, q, q_stride_b, q_stride_t, lengths, temperature,
+      top_k, L, V, s, o);
+  st = launched("order_draw");
+  if (st != WPTV_OK) return st;
+  if (cache_lengths) {
+    const Commit c{cache_lengths, cache_before, feeds, feeds_stride, failed, written};
+    hipLaunchKernelGGL((accept_pick<true, true>), dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b,
+                       lengths, 0, L, B, V, s, tokens, n_tokens, c, o);
+  } else {
+    hipLaunchKernelGGL((accept_pick<false, true>), dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b,
+                       lengths, 0, L, B, V, s, tokens, n_tokens, Commit{}, o);
+  }
+  return launched("accept_pick");
 }
 
 extern "C" int wptv_greedy_tree(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t,

@@ -21,6 +21,11 @@ int launched(const char* kernel);
 // Compute units of the current device (cached per device).
 int compute_units();
 
+// The most workgroups torch's distribution kernels launch on the current
+// device: multiprocessors x (max threads a multiprocessor / 256); -1 when
+// the device cannot be queried (cached per device).
+int draw_workgroups_cap();
+
 // The wide-tile product (gemm_wide.hip): out[M, N] = x . w^T on 256 x 256
 // tiles, for readings of more rows than the skinny products take.
 bool gemm_wide_fits(int M, int N, int K);

@@ -17,11 +17,11 @@ How a round runs here:
                 cache then keeps what each row wrote, and the features
                 context follows.
 
-The draws come from a tape per round (sampling.draws: the uniforms of the
-drafts, then one row of Exp(1) per row) drawn from `generator`; the reference
-draws lazily in its row loop, so a seeded Writer here writes another stream
-of the same distribution.  A tape recovered from a lazy run replays that run
-exactly (tests/test_writer_golden_gpu.py).
+The draws are the ones the reference's loop makes from `generator` (a torch
+generator on the model's GPU; None: the device's default one), in its order:
+the sampler replays the generator's stream on the device
+(sampling.accept_in_order) and the generator is then moved past what was
+drawn, so a Writer seeded alike writes the reference Writer's tokens.
 """
 
 from dataclasses import dataclass, field
@@ -195,12 +195,13 @@ class Writer:
             pick = torch.tensor(order, dtype=torch.long, device=self.device)
             at = torch.tensor([counts[r] - 1 for r in order], dtype=torch.long, device=self.device)
             last = scores[pick, at]
-        n, V = last.shape
-        u, e = sampling.draws(n, 0, V, self.generator, self.device)
-        tokens, counts = sampling.accept(last[:, None].float(), last.new_empty(n, 0, V, dtype=torch.float32),
-                                         torch.empty(n, 0, dtype=torch.long, device=self.device), u, e,
-                                         self.temperature, self.top_k)
-        return [drawn[0] for drawn in sampling.written(tokens, counts)]
+        # the reference's _sample: one multinomial over every row's distribution
+        scores = last[:, None] if last.dtype in (torch.float32, torch.bfloat16) else last[:, None].float()
+        state = sampling.generator_state(self.generator, self.device)
+        tokens, counts = sampling.accept_in_order(scores, None, None, state, self.temperature, self.top_k, joint=True)
+        drawn = sampling.written(tokens, counts)
+        sampling.set_offset(self.generator, state, self.device)
+        return [d[0] for d in drawn]
 
     # ---- a speculative round ------------------------------------------------
 
@@ -243,10 +244,11 @@ class Writer:
         else:
             read = self.model.extend(ids, self.cache, counts, True, features=self.features)
         scores = read[0] if order == list(range(len(self._rows))) else read[0][pick]
-        u, e = sampling.draws(len(order), L, scores.shape[-1], self.generator, self.device)
-        tokens, ncounts = sampling.accept(scores, q, drafts, u, e, self.temperature, self.top_k,
-                                          lengths=verify, firsts=firsts)
+        state = sampling.generator_state(self.generator, self.device)
+        tokens, ncounts = sampling.accept_in_order(scores, q, drafts, state, self.temperature, self.top_k,
+                                                   lengths=verify, firsts=firsts)
         drawn = sampling.written(tokens, ncounts)  # the round's synchronization
+        sampling.set_offset(self.generator, state, self.device)
         out, keep = {}, [0] * len(self._rows)
         for i, r in enumerate(order):
             self.verified += verify[i]
