@@ -101,10 +101,13 @@ def graphed(fn):
 # the verify step of the 24-layer decoder
 # ---------------------------------------------------------------------------
 
-def decoder_step(B, kv, k, steps, warmup, temperature=0.8, top_k=None, seed=0, keep=False, config=None):
+def decoder_step(B, kv, k, steps, warmup, temperature=0.8, top_k=None, seed=0, keep=False, config=None,
+                 in_order=True):
     """Builds the decoder (the 24-layer one unless config is given), prefills
     kv - 1 tokens per row, captures the step and times it.  Returns a dict of
-    figures (and the pieces, with keep)."""
+    figures (and the pieces, with keep).  in_order: the step draws as the
+    reference's loop does from a seeded generator on the GPU (its stream
+    replayed on the device); otherwise from a tape drawn inside the step."""
     import torch
 
     from wpt_amd.decoder import LARGE, MQADecoder, random_weights
@@ -121,12 +124,13 @@ def decoder_step(B, kv, k, steps, warmup, temperature=0.8, top_k=None, seed=0, k
     prefill(model, cache, prompt[:, :-1], chunk=1024)
     torch.cuda.synchronize()
     log(f"prefill B={B} x {kv - 1} tokens: {time.perf_counter() - started:.1f} s")
-    step = VerifyStep(model, cache, k, temperature=temperature, top_k=top_k)
+    draws = torch.Generator(device=device).manual_seed(seed + 2)
+    step = VerifyStep(model, cache, k, temperature=temperature, top_k=top_k, in_order=in_order, generator=draws)
     step.feeds[:, 0] = prompt[:, -1]
     logits = torch.randn(B, k, config.vocab, generator=generator, device=device)
     step.q.copy_(torch.softmax(logits, -1))
     step.feeds[:, 1:] = torch.multinomial(step.q.reshape(-1, config.vocab), 1, generator=generator).reshape(B, k)
-    torch.cuda.manual_seed(seed + 2)  # the tape's draws come from the device's default generator: seeded
+    torch.cuda.manual_seed(seed + 2)  # a tape's draws come from the device's default generator: seeded
     step.capture(warmup=1)
     for _ in range(warmup):
         step.replay()
@@ -704,6 +708,9 @@ def main():
     parser.add_argument("--writer", action="store_true",
                         help="only the drafted Writer rounds over the 24-layer decoder (batch 32, KV 4096, k 4); "
                              "prints their JSON")
+    parser.add_argument("--tape-draws", action="store_true",
+                        help="the headline step reads a tape drawn inside it instead of drawing in the reference's "
+                             "order")
     parser.add_argument("--pmc-workload", action="store_true",
                         help="for a counter pass: five verify-attention calls of the roofline shape, then five "
                              "plain 64 MiB device copies (the counters' calibration); prints no JSON")
@@ -729,7 +736,7 @@ def main():
 
     B, KV, K = 32, 4096, 4
     log("headline step")
-    head = decoder_step(B, KV, K, args.steps, args.warmup, keep=True)
+    head = decoder_step(B, KV, K, args.steps, args.warmup, keep=True, in_order=not args.tape_draws)
     log(f"headline step: {head['ms_per_step']:.3f} ms, {head['tokens_per_s']:.0f} accepted tok/s")
     attn = attention_c2(args.steps, args.warmup)
     log(f"verify attention: {attn['ms'] * 1e3:.2f} us, {attn['GBps']:.0f} GB/s")
@@ -779,6 +786,8 @@ def main():
         "config": {"workload": "speculative verify step: random-init 24-layer MQA decoder (d_model 2048, 16q/1kv "
                                "heads, head 128, SwiGLU 5632, vocab 32768), batch 32, KV 4096, chain k=4, "
                                "rejection sampling T=0.8, HIP graph", "global_batch": B, "seq_len": KV,
+                   "draws": "tape drawn in the step" if args.tape_draws else
+                            "the reference's order from a seeded GPU generator",
                    "draft": K, "tokens_per_row_step": head["tokens_per_row_step"]},
         "roofline": {"bound": "hbm", "achieved": attn["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": attn["GBps"] / HBM_PEAK_GBS, "traffic": traffic,

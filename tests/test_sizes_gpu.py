@@ -275,3 +275,36 @@ def test_a_captured_stochastic_step_replays_as_eager_steps_on_its_tapes(large):
         step.check()
         eager.check()
     assert int(cache.lengths.min()) > KV - 1  # the steps moved on
+
+
+def test_a_captured_step_drawing_in_the_reference_s_order_replays_as_eager_steps(large):
+    # the headline workload's step drawing as the reference's loop does from a
+    # generator on the GPU (its state on the device, moved on by each replay)
+    # against eager steps on a copy of the cache from a generator seeded alike
+    model, _ = large
+    B, KV, k = 32, 4096, 4
+    cache, step = prepared_step(model, B, KV, k, seed=9)
+    mine = torch.Generator(device=model.device).manual_seed(31)
+    other = torch.Generator(device=model.device).manual_seed(31)
+    captured = VerifyStep(model, cache, k, temperature=0.8, in_order=True, generator=mine)
+    captured.feeds.copy_(step.feeds)
+    captured.q.copy_(step.q)
+    twin = cache.select(list(range(B)))
+    eager = VerifyStep(model, twin, k, temperature=0.8, in_order=True, generator=other)
+    eager.feeds.copy_(step.feeds)
+    eager.q.copy_(step.q)
+    captured.capture(warmup=0)
+    moved = 0
+    for i in range(4):
+        tokens, counts = captured.replay()
+        torch.zeros(1000, device=model.device).sum()  # eager work between replays
+        tokens_e, counts_e = eager.run()
+        torch.cuda.synchronize()
+        assert torch.equal(tokens, tokens_e) and torch.equal(counts, counts_e), f"replay {i}"
+        assert torch.equal(captured.state, eager.state) and torch.equal(cache.lengths, twin.lengths)
+        moved += 4 * int((counts.clamp(max=k) + 1).sum())  # each row: its judged drafts' uniforms, one multinomial
+        assert int(captured.state[1]) == moved, f"replay {i}"
+        captured.check()
+    captured.sync_generator()
+    eager.sync_generator()
+    assert torch.equal(mine.get_state(), other.get_state())

@@ -9,10 +9,14 @@ last one written (firsts = 0, kept = tokens written).
 The inputs live in static device buffers (`feeds`: the pending token then the
 drafts; `q`: the drafts' distributions), so that a captured graph replays on
 new values: after each step the token it drew becomes each row's pending
-token.  The tape (u, e) is drawn inside the step from torch's generator of the
-device, or read from the static buffers `u`, `e` (`given_tape=True`), which
-the caller fills before each step.  After a step, `scores`, `u` and `e` hold
-what it read.  The cache's tables must hold every row the replays will write
+token.  The draws: with `in_order=True` the ones the reference's loop makes
+from `generator` (None: the device's default one), in its order, its Philox
+stream replayed on the device from a device copy of the generator's state
+(`state`, moved on by every step and replay; `sync_generator()` hands the
+offset back to the generator); otherwise a tape (u, e) drawn inside the step
+from torch's generator of the device, or read from the static buffers `u`,
+`e` (`given_tape=True`), which the caller fills before each step.  After a
+step, `scores` (and `u` and `e` for a tape) hold what it read.  The cache's tables must hold every row the replays will write
 (reserve), since a graph cannot grow them.
 
 A row whose residual max(0, p - q) has no mass cannot draw; the reference's
@@ -47,12 +51,17 @@ def next_feeds(tokens, counts, feeds, failed=None, written=None):
 
 
 class VerifyStep:
-    def __init__(self, model, cache, k, temperature=0.8, top_k=None, greedy=False, given_tape=False):
+    def __init__(self, model, cache, k, temperature=0.8, top_k=None, greedy=False, given_tape=False,
+                 in_order=False, generator=None):
         self.model, self.cache, self.k = model, cache, k
         self.temperature, self.top_k, self.greedy = temperature, top_k, greedy
         self.given_tape = given_tape
         B, V = cache.rows, model.config.vocab
         device = model.device
+        if in_order and (greedy or given_tape):
+            raise ValueError("in-order draws replace the tape; a greedy step draws nothing")
+        self.in_order, self.generator = in_order, generator
+        self.state = sampling.generator_state(generator, device) if in_order else None
         self.feeds = torch.zeros(B, k + 1, dtype=torch.long, device=device)
         self.q = torch.full((B, k, V), 1.0 / V, device=device)
         self.u = torch.zeros(B, k, device=device) if given_tape else None
@@ -66,7 +75,7 @@ class VerifyStep:
         """One eager step; returns (tokens (B, k + 1), counts (B,)) on the device."""
         scores, _ = self.model.extend(self.feeds, self.cache, undoable=True, logits=True)  # read as they come
         drafts = self.feeds[:, 1:]
-        if not (self.greedy or self.given_tape):
+        if not (self.greedy or self.given_tape or self.in_order):
             B, V = scores.shape[0], scores.shape[-1]
             self.u, self.e = sampling.draws(B, self.k, V, device=scores.device)
         # the pick's kernel also takes back the rejected drafts (the model's
@@ -77,13 +86,22 @@ class VerifyStep:
             commit = (lengths, before, self.feeds, self.failed, self.written)
         else:
             commit = None
-        tokens, counts = sampling.accept(scores, self.q, drafts, self.u, self.e, self.temperature, self.top_k,
-                                         greedy=self.greedy, commit=commit)
+        if self.in_order:
+            tokens, counts = sampling.accept_in_order(scores, self.q, drafts, self.state, self.temperature,
+                                                      self.top_k, commit=commit)
+        else:
+            tokens, counts = sampling.accept(scores, self.q, drafts, self.u, self.e, self.temperature, self.top_k,
+                                             greedy=self.greedy, commit=commit)
         if commit is None:
             self.model.undo(self.cache, counts)
             next_feeds(tokens, counts, self.feeds, self.failed, self.written)
         self.tokens, self.counts, self.scores = tokens, counts, scores
         return tokens, counts
+
+    def sync_generator(self):
+        """Moves the generator past every draw the in-order steps made (one
+        synchronization)."""
+        sampling.set_offset(self.generator, self.state, self.model.device)
 
     def check(self):
         """Raises if a step since the last check had a row with nothing to
