@@ -498,10 +498,10 @@ int wptv_accept_commit(const void* scores, int64_t scores_stride_b, int64_t scor
  *   the rest as wptv_accept (u and e replaced by the two above; greedy is
  *   not taken: a greedy step draws nothing) and wptv_accept_commit (all of
  *   cache_lengths, cache_before, feeds, failed, written may be NULL).
- *   B (L + 1) <= 4096, L <= 64; workspace wptv_accept_workspace(B, L) bytes.
+ *   B (L + 1) <= 3072, L <= 64; workspace wptv_accept_workspace(B, L) bytes.
  *   Three launches: the statistics, the draws (the loop's uniforms replayed
  *   to find each row's first rejection; the multinomial's exponentials over
- *   eight slices of the vocabulary a row), the pick. */
+ *   32 slices of the vocabulary a row), the pick. */
 int wptv_accept_in_order(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
                          const int32_t* firsts, const float* q, int64_t q_stride_b, int64_t q_stride_t,
                          const int64_t* drafts, int64_t drafts_stride_b, const int32_t* lengths,

@@ -539,8 +539,8 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
 // above 1 - 2^-24 taken as giving 2^-24) and moves the offset by 4 more.
 
 constexpr int kDT = 256;        // threads of a draw workgroup
-constexpr int kSlices = 8;      // draw workgroups a row's multinomial is shared over
-constexpr int kScanMax = 4096;  // positions B (L + 1) the in-order scan may read
+constexpr int kSlices = 32;     // draw workgroups a row's multinomial is shared over
+constexpr int kScanMax = 3072;  // positions B (L + 1) the in-order scan may read (16 B P bytes of LDS)
 
 struct Order {
   const int64_t* state;  // the generator's [seed, offset] on the device
@@ -597,9 +597,12 @@ __global__ __launch_bounds__(kDT) void order_draw(const S* __restrict__ scores, 
                                                   const int32_t* __restrict__ firsts, const float* __restrict__ q,
                                                   int64_t qb, int64_t qt, const int32_t* __restrict__ lengths,
                                                   float temperature, int B, int L, int V, Stats stats, Order order) {
-  __shared__ float utab[kScanMax];
-  __shared__ float spd[kScanMax], sqd[kScanMax];
-  __shared__ int slen[kScanMax];
+  // the replay's tables, sized at launch: uniforms B P, drafts' p and q B L each, lengths B
+  extern __shared__ __attribute__((aligned(16))) float scan_lds[];
+  float* utab = scan_lds;
+  float* spd = utab + B * (L + 1);
+  float* sqd = spd + B * L;
+  int* slen = reinterpret_cast<int*>(sqd + B * L);
   __shared__ float redv[kDT / 64];
   __shared__ int redi[kDT / 64];
   __shared__ int found[2];
@@ -737,38 +740,14 @@ __device__ inline void commit_row(const Commit& c, int b, int n, int64_t last) {
 // Each row's tokens from the per-position decisions: the drafts up to the
 // first rejected one, then that position's draw (the argmax in greedy mode),
 // or every draft and the bonus draw (__init__.py:210-229).  One thread per row.
-// ORDER: the first rejection from order_draw's replay and the draw joined
-// from its slices in index order; the row of the last batch row writes the
-// generator's next offset.
-template <bool COMMIT, bool ORDER>
+template <bool COMMIT>
 __global__ __launch_bounds__(64) void accept_pick(const int64_t* __restrict__ drafts, int64_t db,
                                                   const int32_t* __restrict__ lengths, int greedy, int L, int B,
-                                                  int V, Stats stats, int64_t* __restrict__ tokens,
-                                                  int32_t* __restrict__ n_tokens, Commit commit, Order order) {
+                                                  Stats stats, int64_t* __restrict__ tokens,
+                                                  int32_t* __restrict__ n_tokens, Commit commit) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
   const int P = L + 1;
-  if constexpr (ORDER) {
-    const int2 at = order.rows[b];
-    const int js = at.x, len = order.joint ? 0 : (lengths ? min(max(lengths[b], 0), L) : L);
-    float2 parts[kSlices];
-#pragma unroll
-    for (int s = 0; s < kSlices; ++s) parts[s] = order.parts[b * kSlices + s];
-    float bv = kNegInfS;
-    int bi = INT_MAX;
-#pragma unroll
-    for (int s = 0; s < kSlices; ++s) arg_better(bv, bi, parts[s].x, __float_as_int(parts[s].y));
-    int pick = bi >= 0 && bi < V ? bi : -1;
-    // a residual with no mass has no draw (the reference's multinomial raises)
-    if (js < len && !(stats.rest[b * P + js] > 0.f)) pick = -1;
-    for (int t = 0; t < P; ++t)
-      tokens[(int64_t)b * P + t] = t < js ? drafts[b * db + t] : (t == js ? pick : -1);
-    n_tokens[b] = pick >= 0 ? js + 1 : -1;
-    if constexpr (COMMIT) commit_row(commit, b, pick >= 0 ? js + 1 : -1, pick);
-    if (b == B - 1)
-      *order.next = order.state[1] + (order.joint ? order.joint_step : 4 * ((int64_t)at.y + 1));
-    return;
-  }
   const int* drawn_at = greedy ? stats.best : stats.cand;
   constexpr int kMaxP = 16;
   if (P <= kMaxP) {
@@ -809,6 +788,44 @@ __global__ __launch_bounds__(64) void accept_pick(const int64_t* __restrict__ dr
   tokens[(int64_t)b * P + js] = pick;
   n_tokens[b] = pick >= 0 ? js + 1 : -1;
   if constexpr (COMMIT) commit_row(commit, b, pick >= 0 ? js + 1 : -1, pick);
+}
+
+// The in-order draws' pick (accept_pick's results and moves): one wavefront
+// per row, lane s holding slice s's race winner, the slices joined in index
+// order; the first rejected draft from order_draw's replay.  The last row
+// also writes the generator's next offset.
+template <bool COMMIT>
+__global__ __launch_bounds__(64) void order_pick(const int64_t* __restrict__ drafts, int64_t db,
+                                                 const int32_t* __restrict__ lengths, int L, int B, int V,
+                                                 Stats stats, int64_t* __restrict__ tokens,
+                                                 int32_t* __restrict__ n_tokens, Commit commit, Order order) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  if (b >= B) return;
+  const int P = L + 1;
+  float bv = kNegInfS;
+  int bi = INT_MAX;
+  if (lane < kSlices) {
+    const float2 part = order.parts[b * kSlices + lane];
+    bv = part.x;
+    bi = __float_as_int(part.y);
+  }
+  const int2 at = order.rows[b];
+  const int js = at.x, len = order.joint ? 0 : (lengths ? min(max(lengths[b], 0), L) : L);
+  const float rest = stats.rest[b * P + js];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float v2 = __shfl_xor(bv, off, 64);
+    const int i2 = __shfl_xor(bi, off, 64);
+    arg_better(bv, bi, v2, i2);
+  }
+  int pick = bi >= 0 && bi < V ? bi : -1;
+  // a residual with no mass has no draw (the reference's multinomial raises)
+  if (js < len && !(rest > 0.f)) pick = -1;
+  for (int t = lane; t < P; t += 64) tokens[(int64_t)b * P + t] = t < js ? drafts[b * db + t] : (t == js ? pick : -1);
+  if (lane != 0) return;
+  n_tokens[b] = pick >= 0 ? js + 1 : -1;
+  if constexpr (COMMIT) commit_row(commit, b, pick >= 0 ? js + 1 : -1, pick);
+  if (b == B - 1) *order.next = order.state[1] + (order.joint ? order.joint_step : 4 * ((int64_t)at.y + 1));
 }
 
 // Greedy walk down a draft tree: node i's parent parents[i] < i, the root 0.
@@ -1036,11 +1053,11 @@ int accept_impl(const void* scores, int64_t scores_stride_b, int64_t scores_stri
   int st = launched("accept_stats");
   if (st != WPTV_OK) return st;
   if (commit)
-    hipLaunchKernelGGL((accept_pick<true, false>), dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b,
-                       lengths, greedy, L, B, V, s, tokens, n_tokens, *commit, Order{});
+    hipLaunchKernelGGL(accept_pick<true>, dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b, lengths,
+                       greedy, L, B, s, tokens, n_tokens, *commit);
   else
-    hipLaunchKernelGGL((accept_pick<false, false>), dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b,
-                       lengths, greedy, L, B, V, s, tokens, n_tokens, Commit{}, Order{});
+    hipLaunchKernelGGL(accept_pick<false>, dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b, lengths,
+                       greedy, L, B, s, tokens, n_tokens, Commit{});
   return launched("accept_pick");
 }
 
@@ -1084,13 +1101,14 @@ void launch_order_draw(int B, hipStream_t stream, const void* scores, int64_t sb
   const bool cut = top_k > 0 && top_k < V;
   const S* rows = static_cast<const S*>(scores);
   const dim3 grid(B * kSlices);
+  const size_t lds = 4 * ((size_t)B * (L + 1) + 2 * (size_t)B * L + B);
 #define WPTV_DRAW(N)                                                                                                  \
   do {                                                                                                                \
     if (cut)                                                                                                          \
-      hipLaunchKernelGGL((order_draw<N, S, true>), grid, dim3(kDT), 0, stream, rows, sb, st, firsts, q, qb, qt,     \
+      hipLaunchKernelGGL((order_draw<N, S, true>), grid, dim3(kDT), lds, stream, rows, sb, st, firsts, q, qb, qt,   \
                          lengths, temperature, B, L, V, s, o);                                                        \
     else                                                                                                              \
-      hipLaunchKernelGGL((order_draw<N, S, false>), grid, dim3(kDT), 0, stream, rows, sb, st, firsts, q, qb, qt,    \
+      hipLaunchKernelGGL((order_draw<N, S, false>), grid, dim3(kDT), lds, stream, rows, sb, st, firsts, q, qb, qt,  \
                          lengths, temperature, B, L, V, s, o);                                                        \
   } while (0)
   if (n <= 1) WPTV_DRAW(1);
@@ -1161,13 +1179,13 @@ extern "C" int wptv_accept_in_order(const void* scores, int64_t scores_stride_b,
   if (st != WPTV_OK) return st;
   if (cache_lengths) {
     const Commit c{cache_lengths, cache_before, feeds, feeds_stride, failed, written};
-    hipLaunchKernelGGL((accept_pick<true, true>), dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b,
-                       lengths, 0, L, B, V, s, tokens, n_tokens, c, o);
+    hipLaunchKernelGGL(order_pick<true>, dim3(B), dim3(64), 0, stream, drafts, drafts_stride_b, lengths, L, B, V, s,
+                       tokens, n_tokens, c, o);
   } else {
-    hipLaunchKernelGGL((accept_pick<false, true>), dim3((B + 63) / 64), dim3(64), 0, stream, drafts, drafts_stride_b,
-                       lengths, 0, L, B, V, s, tokens, n_tokens, Commit{}, o);
+    hipLaunchKernelGGL(order_pick<false>, dim3(B), dim3(64), 0, stream, drafts, drafts_stride_b, lengths, L, B, V, s,
+                       tokens, n_tokens, Commit{}, o);
   }
-  return launched("accept_pick");
+  return launched("order_pick");
 }
 
 extern "C" int wptv_greedy_tree(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t,
