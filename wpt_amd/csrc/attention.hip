@@ -220,6 +220,12 @@ __device__ __forceinline__ int tile_sigma(int r) {
   else return 2 * ((r >> 1) & 3) + (r >> 3);
 }
 
+// The 32-row kernel's swizzle of its V halves (head width 128): its
+// transposed reads take, in each half of the wavefront, rows 4 i .. 4 i + 3
+// at chunks 4 cb + a (a < 4), and 4 (r % 4) moves those 16 (row, chunk)
+// pairs onto 16 distinct bank groups.
+__device__ __forceinline__ int v_sigma(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
+
 // A row's softmax reference maximum is its first finite tile maximum and
 // moves only when a later tile's maximum exceeds it by more than this many
 // powers of two (p then stays below 2^32, far inside the fp32 and bf16
@@ -741,7 +747,7 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
       const int ii = mb * kCnt + c;
       const int part = ii / G::kPerHalf, quarter = ii % G::kPerHalf;
       const int row = quarter * (64 / kXC) + lane / kXC;
-      const int x = (lane % kXC) ^ tile_sigma<C>(row);
+      const int x = (lane % kXC) ^ (part < 2 ? tile_sigma<C>(row) : v_sigma(row));
       int n = s_lo + tile * 32 + 16 * (part & 1) + row;
       n = n < s_hi ? n : s_hi;
       const uint32_t phys = (uint32_t)(n - rbase) & rows.mask;
@@ -820,9 +826,9 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
   const int gq = lane >> 4, rr = (lane >> 2) & 3, qq = lane & 3;
   const int va_row = 4 * (gq >> 1) + rr;
   const int va_base = 8 * kXC * va_row + 4 * (qq & 1);
-  const int va_y = ((2 * (gq & 1)) | (qq >> 1)) ^ tile_sigma<C>(va_row);
+  const int va_y = ((2 * (gq & 1)) | (qq >> 1)) ^ v_sigma(va_row);
   const int vb_base = 8 * kXC * (va_row + 8) + 4 * (qq & 1);
-  const int vb_y = ((2 * (gq & 1)) | (qq >> 1)) ^ tile_sigma<C>(va_row + 8);
+  const int vb_y = ((2 * (gq & 1)) | (qq >> 1)) ^ v_sigma(va_row + 8);
 
   auto arrive = [&](int t, int later) {
     if (dma_wave && t < mine) {
