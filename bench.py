@@ -642,6 +642,35 @@ def pmc_workload():
     log("pmc workload done")
 
 
+def pmc_products():
+    """For counter passes over the layer products: the verify step's four
+    fragment-major products at 160 rows (batch 32, k = 4), each called once
+    per layer of the 24-layer decoder's weights (every weight read cold, as in
+    the step), eagerly, twice over."""
+    import torch
+
+    from wpt_amd import layers
+    from wpt_amd.decoder import LARGE, MQADecoder, random_weights
+
+    device = torch.device("cuda", 0)
+    weights = random_weights(LARGE, seed=0, std=0.02, dtype=torch.bfloat16, device=device)
+    model = MQADecoder(LARGE, weights, dtype=torch.bfloat16, device=device)
+    rows = 160
+    generator = torch.Generator(device=device).manual_seed(7)
+    for _ in range(2):
+        for name, K in (("qkv", LARGE.d_model), ("out", LARGE.heads * LARGE.head_dim),
+                        ("gate_up_tiles", LARGE.d_model), ("down", LARGE.ffn)):
+            xf = layers.fm_pack(torch.randn(rows, K, generator=generator, device=device).to(torch.bfloat16))
+            for i in range(LARGE.layers):
+                w = model.fm[f"layers.{i}.{name}"]
+                if name == "gate_up_tiles":
+                    layers.linear_fm_swiglu(xf, rows, w)
+                else:
+                    layers.linear_fm_parts(xf, rows, w)
+            torch.cuda.synchronize()
+    log("pmc products done")
+
+
 COPY_BYTES = 64 * 1024 * 1024  # the plain device copy of --pmc-workload (32 Mi bf16 values), read and written once
 
 
@@ -711,12 +740,18 @@ def main():
     parser.add_argument("--tape-draws", action="store_true",
                         help="the headline step reads a tape drawn inside it instead of drawing in the reference's "
                              "order")
+    parser.add_argument("--pmc-products", action="store_true",
+                        help="for counter passes: the step's four fragment-major layer products at 160 rows, each "
+                             "over the 24 layers' weights, twice; prints no JSON")
     parser.add_argument("--pmc-workload", action="store_true",
                         help="for a counter pass: five verify-attention calls of the roofline shape, then five "
                              "plain 64 MiB device copies (the counters' calibration); prints no JSON")
     args = parser.parse_args()
     if args.pmc_workload:
         pmc_workload()
+        return
+    if args.pmc_products:
+        pmc_products()
         return
     if args.wpt_layers:
         print(json.dumps(wpt_layers(args.steps, args.warmup)), flush=True)
