@@ -101,3 +101,41 @@ def test_the_writer_drafts_with_it(device):
     assert writer.rounds == 4 and writer.verified == 4 * 4 * 3
     assert writer.cache.lengths.tolist() == [len(h) - 1 for h in writer.histories]
     assert writer.context.shape == (3, oracle_drafter.WINDOW, 2 * CONFIG.d_model)
+
+
+def test_captured_writer_rounds_write_what_eager_rounds_write(device):
+    # the drafter's backbone and the Writer's steady rounds from HIP graphs
+    # (capture=True) against both eager, from generators seeded alike: the
+    # same tokens round after round, a round with tool inputs (eager either
+    # way) in between, and the same cache lengths and generator state after
+    model, config, _, _ = setup(device, seed=5)
+    w = gpu_drafter.random_drafter_weights(CONFIG, config, seed=6, std=0.05)
+    runs = []
+    for capture in (False, True):
+        drafter = gpu_drafter.Drafter(model, config, w, capture=capture)
+        generator = torch.Generator(device=device).manual_seed(9)
+        writer = Writer(model, [3, 5, 7, 9], 4, temperature=1.0, top_k=None, draft=4, generator=generator,
+                        drafter=drafter, capture=capture)
+        out = [writer.write(inputs, {row: 5 for row in range(4)})
+               for inputs in ({}, {}, {2: [11, 12]}, {}, {}, {})]
+        runs.append((out, writer.cache.lengths.tolist(), generator.get_state(), writer.context.clone()))
+        if capture:
+            assert writer._reads and drafter._graphs  # the graphs were captured and replayed
+    (eager, lengths_e, state_e, context_e), (captured, lengths_c, state_c, context_c) = runs
+    assert captured == eager
+    assert lengths_c == lengths_e and torch.equal(state_c, state_e) and torch.equal(context_c, context_e)
+
+
+def test_a_captured_backbone_replays_the_eager_one(device):
+    model, config, gpu, _ = setup(device, seed=3)
+    captured = gpu_drafter.Drafter(model, config, {k: v for k, v in gpu.w.items()}, capture=True)
+    R, count = len(LENGTHS), 4
+    generator = torch.Generator(device=device).manual_seed(1)
+    for call in range(3):  # the first call runs eagerly and captures; the others replay
+        features = torch.randn(R, gpu_drafter.WINDOW, len(config.features) * CONFIG.d_model, generator=generator,
+                               device=device)
+        lengths = torch.tensor(LENGTHS, device=device) + call
+        anchors = torch.randint(CONFIG.vocab, (R,), generator=generator, device=device)
+        h, U = gpu.backbone(features, lengths, anchors, count)
+        h2, U2 = captured._replayed(features, lengths, anchors, count)
+        assert torch.equal(h, h2) and torch.equal(U, U2), f"call {call}"

@@ -33,7 +33,9 @@ product) up to 512 rows, the context fuse (R x WINDOW rows) on torch's; the
 attention on wptv_verify_attention's row-block kernel, with the table laid
 out as [context ; block] and each place's position chosen so that the
 kernel's window is exactly what the reference's mask shows it; norms, rotary
-encoding and sampling in torch (small tensors).
+encoding and sampling in torch (small tensors).  With capture=True the
+backbone of each (rows, count) shape is captured once in a HIP graph and
+replayed on copies of its inputs (the same kernels, so the same results).
 """
 
 from dataclasses import dataclass
@@ -132,8 +134,10 @@ class Drafter:
     """features, window: what the Writer reads (the drafter protocol,
     wpt_inference/__init__.py:17-33); draft() proposes tokens."""
 
-    def __init__(self, model, config, weights):
+    def __init__(self, model, config, weights, capture=False):
         self.model, self.config = model, config
+        self.capture = capture
+        self._graphs = {}  # (rows, count) -> (graph, its inputs, its outputs)
         self.features, self.window, self.block = config.features, WINDOW, config.block
         mc = model.config
         self.heads, self.head_dim = mc.heads, mc.head_dim
@@ -210,6 +214,28 @@ class Drafter:
         h = self._norm(h, self.w["final_norm"])
         return h.float(), self._linear(h, self.model.w["head"]).float()
 
+    def _replayed(self, features, lengths, anchors, count):
+        """backbone() from its HIP graph for this shape; the first call of a
+        shape runs eagerly (which also readies the libraries it calls) and then
+        captures the graph (which runs nothing).  A replay's outputs are the
+        graph's own tensors, valid until the next replay."""
+        key = (anchors.shape[0], count)
+        if key not in self._graphs:
+            eager = self.backbone(features, lengths, anchors, count)
+            inputs = (torch.zeros_like(features, dtype=torch.float32), torch.zeros_like(lengths, dtype=torch.long),
+                      torch.zeros_like(anchors))
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                outputs = self.backbone(*inputs, count)
+            self._graphs[key] = (graph, inputs, outputs)
+            return eager
+        graph, (f_in, l_in, a_in), outputs = self._graphs[key]
+        f_in.copy_(features)
+        l_in.copy_(lengths)
+        a_in.copy_(anchors)
+        graph.replay()
+        return outputs
+
     def _markov(self, previous):
         embedded = self.w["markov_in"][previous]
         return embedded @ self.w["markov_out"].T, embedded
@@ -221,7 +247,10 @@ class Drafter:
         distribution with the writer's generator."""
         features, lengths = context
         anchors = torch.tensor([history[-1] for history in histories], dtype=torch.long, device=self.model.device)
-        h, U = self.backbone(features, lengths, anchors, count)
+        if self.capture:
+            h, U = self._replayed(features, lengths, anchors, count)
+        else:
+            h, U = self.backbone(features, lengths, anchors, count)
         tokens, distributions, confidences = [], [], []
         previous = anchors
         for k in range(count):

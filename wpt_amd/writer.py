@@ -22,6 +22,13 @@ generator on the model's GPU; None: the device's default one), in its order:
 the sampler replays the generator's stream on the device
 (sampling.accept_in_order) and the generator is then moved past what was
 drawn, so a Writer seeded alike writes the reference Writer's tokens.
+
+capture=True (an MQADecoder): a round in which every row verifies the same
+number of drafts after its anchor alone (no inputs, no scheduler cut) runs
+the verify reading and the acceptance from a HIP graph captured for that
+shape, on static copies of the feed and the drafts; the cache's tables are
+reserved ahead for the replays.  The same kernels run, so the tokens are the
+eager round's.
 """
 
 from dataclasses import dataclass, field
@@ -73,7 +80,7 @@ class Writer:
     model's cache)."""
 
     def __init__(self, model, prompt, rows=1, *, temperature=0.8, top_k=40, generator=None, stops=(), drafter=None,
-                 draft=DRAFT, costs=None, outcomes=None, routes=False):
+                 draft=DRAFT, costs=None, outcomes=None, routes=False, capture=False):
         if not prompt:
             raise ValueError("a prompt holds at least one token")
         if costs is not None and len(costs) < draft + 1:
@@ -89,6 +96,8 @@ class Writer:
         self.features = tuple(getattr(drafter, "features", ())) if drafter is not None else ()
         self.cache = None
         self.context = None  # a feature-reading drafter's context: (rows, window, features x d_model) FP32
+        self.capture = bool(capture) and isinstance(model, MQADecoder)
+        self._reads = {}  # drafts a row -> _CapturedRead
         if not cached:
             return
         # the prompt but its last token is read once, into a one-row cache copied to every row
@@ -226,6 +235,11 @@ class Writer:
         feeds = [[] for _ in self._rows]
         for i, r in enumerate(order):
             feeds[r] = self._rows[r].unread + [0] * verify[i]
+        steady = (self.capture and L > 0 and order == list(range(len(self._rows))) and not any(firsts)
+                  and all(v == L for v in verify))
+        if steady:
+            read, scores, tokens, ncounts = self._captured_round(drafts, q, L)
+            return self._finish_round(order, limits, verify, firsts, confidence, read, tokens, ncounts)
         ids, counts = self._ids(feeds, spare=1)
         width = ids.shape[1] - 1
         pick = torch.tensor(order, dtype=torch.long, device=self.device)
@@ -247,8 +261,15 @@ class Writer:
         state = sampling.generator_state(self.generator, self.device)
         tokens, ncounts = sampling.accept_in_order(scores, q, drafts, state, self.temperature, self.top_k,
                                                    lengths=verify, firsts=firsts)
+        return self._finish_round(order, limits, verify, firsts, confidence, read, tokens, ncounts, state)
+
+    def _finish_round(self, order, limits, verify, firsts, confidence, read, tokens, ncounts, state=None):
+        """The round's one synchronization and the host's part: each row's
+        written tokens cut at its stops and limit, the counters, the undo of
+        what the rows did not keep, the features context."""
         drawn = sampling.written(tokens, ncounts)  # the round's synchronization
-        sampling.set_offset(self.generator, state, self.device)
+        if state is not None:
+            sampling.set_offset(self.generator, state, self.device)
         out, keep = {}, [0] * len(self._rows)
         for i, r in enumerate(order):
             self.verified += verify[i]
@@ -262,3 +283,50 @@ class Writer:
         self.model.undo(self.cache, keep)
         self._follow(read, keep)
         return out
+
+    def _captured_round(self, drafts, q, L):
+        """The verify reading and the acceptance of a steady round from the
+        graph of its shape: (read, scores, tokens, counts), the graph's
+        tensors.  The generator hands its state over and takes it back."""
+        cap = self._reads.get(L)
+        width = L + 1
+        if cap is None or self.cache.bound + width > cap.limit:
+            cap = self._reads[L] = _CapturedRead(self, L)
+        anchors = torch.tensor([row.unread[0] for row in self._rows], dtype=torch.long)
+        cap.ids[:, 0].copy_(anchors, non_blocking=True)
+        cap.ids[:, 1:].copy_(drafts)
+        cap.q.copy_(q)
+        cap.drafts.copy_(drafts)
+        cap.state.copy_(sampling.generator_state(self.generator, self.device))
+        cap.graph.replay()
+        # what the reading's host side would have recorded (a replay runs no Python)
+        self.cache.pending = True
+        self.cache.bound += width
+        sampling.set_offset(self.generator, cap.state, self.device)  # the round's synchronization
+        return cap.read, cap.read[0], cap.tokens, cap.counts
+
+
+class _CapturedRead:
+    """A steady round's verify reading (every row: its anchor, then L drafts)
+    and its acceptance, captured in a HIP graph over static inputs; the
+    cache's tables are reserved for ROUNDS more such readings first (a
+    graph cannot grow them: past that a new one is captured)."""
+
+    ROUNDS = 64
+
+    def __init__(self, writer, L):
+        model, cache, device = writer.model, writer.cache, writer.device
+        rows, V, width = cache.rows, model.config.vocab, L + 1
+        self.ids = torch.zeros(rows, width, dtype=torch.long, device=device)
+        self.q = torch.zeros(rows, L, V, device=device)
+        self.drafts = torch.zeros(rows, L, dtype=torch.long, device=device)
+        self.state = sampling.generator_state(writer.generator, device).clone()
+        cache.reserve(cache.bound + width * self.ROUNDS)
+        self.limit = cache.capacity
+        pending, bound = cache.pending, cache.bound
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):  # records the kernels; runs none
+            self.read = model.extend(self.ids, cache, None, True, features=writer.features, logits=True)
+            self.tokens, self.counts = sampling.accept_in_order(self.read[0], self.q, self.drafts, self.state,
+                                                                writer.temperature, writer.top_k)
+        cache.pending, cache.bound = pending, bound
