@@ -151,10 +151,12 @@ class Uniform:
         return tokens, torch.full((len(histories), count, V), 1.0 / V, device=generator.device), None
 
 
-def reference_rounds(model, prompt, rows, calls, temperature, top_k, generator, drafter, draft):
+def reference_rounds(model, prompt, rows, calls, temperature, top_k, generator, drafter, draft, inputs=None,
+                     stops=()):
     """The reference Writer's speculative rounds (__init__.py:71-233, no
     features or scheduler), restated with the oracle's rule drawing lazily
-    from `generator` (oracle.sampling.LazyDraws): the tokens of each call."""
+    from `generator` (oracle.sampling.LazyDraws): the tokens of each call.
+    inputs: per call, {row: tokens read before writing} (None: none)."""
     device = generator.device
     one = model.new_cache(1)
     if len(prompt) > 1:
@@ -166,8 +168,11 @@ def reference_rounds(model, prompt, rows, calls, temperature, top_k, generator, 
         return oracle_sampling.probabilities(scores, temperature, top_k)
 
     out = []
-    for limits in calls:
+    for call, limits in enumerate(calls):
         rs = sorted(limits)
+        for r, tokens in (inputs[call] if inputs else {}).items():
+            pending[r] = pending[r] + list(tokens)
+            histories[r] = histories[r] + list(tokens)
         drafted, q, _ = drafter.draft(model, [histories[r] for r in rs], None, draft, probabilities, generator)
         drafted, q = drafted.to(device), q.to(device).float()
         caps = [min(draft, limits[r] - 1) for r in rs]
@@ -182,7 +187,7 @@ def reference_rounds(model, prompt, rows, calls, temperature, top_k, generator, 
             first = len(pending[r]) - 1
             p = probabilities(scores[i, first:first + caps[i] + 1])
             tokens = oracle_sampling.accept_row(p, q[i], drafted[i], caps[i], oracle_sampling.LazyDraws(generator))
-            written[r] = oracle_sampling.cut(tokens, set(), limits[r])
+            written[r] = oracle_sampling.cut(tokens, set(stops), limits[r])
             kept[r] = first + len(written[r])
         model.undo(cache, kept)
         for r, tokens in written.items():
@@ -204,6 +209,24 @@ def test_a_seeded_writer_writes_the_reference_writer_s_tokens(device, top_k):
     mine = torch.Generator(device=device).manual_seed(21)
     writer = Writer(gpu, prompt, 3, temperature=1.0, top_k=top_k, generator=mine, drafter=Uniform(), draft=3)
     assert [writer.write({}, limits) for limits in calls] == expected
+    assert torch.equal(mine.get_state(), reference.get_state())
+
+
+def test_a_seeded_writer_with_inputs_limits_and_stops_writes_the_reference_writer_s_tokens(device):
+    # rows that read tool inputs first (their first new token scored after
+    # them), limits below a full round (fewer drafts verified), a stop token,
+    # and a call that leaves a row out: still the reference's tokens and
+    # generator state
+    gpu, _ = models(PLUMBING, torch.float32, std=0.05)
+    prompt = [0, 5, 7, 9]
+    calls = [{0: 4, 1: 4, 2: 4}, {0: 2, 2: 5}, {0: 4, 1: 1, 2: 3}, {1: 4, 2: 4}, {0: 4, 1: 4, 2: 4}]
+    inputs = [{}, {2: [11, 12, 13]}, {0: [4]}, {1: [21, 22], 2: [8]}, {}]
+    reference = torch.Generator(device=device).manual_seed(33)
+    expected = reference_rounds(gpu, prompt, 3, calls, 0.9, 40, reference, Uniform(), 3, inputs, stops=(17,))
+    mine = torch.Generator(device=device).manual_seed(33)
+    writer = Writer(gpu, prompt, 3, temperature=0.9, top_k=40, generator=mine, drafter=Uniform(), draft=3,
+                    stops=(17,))
+    assert [writer.write(given, limits) for given, limits in zip(inputs, calls)] == expected
     assert torch.equal(mine.get_state(), reference.get_state())
 
 
