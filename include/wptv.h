@@ -408,8 +408,8 @@ int wptv_gemm_fm_wide(const void* x_fm, int x_blocks, const void* w_fm, int M, i
  *   product without storing it: best[m] = the first index of the largest
  *   bf16-rounded value of row m of x . w^T (torch.argmax of the reference's
  *   bf16 logits, model.py:471, as its greedy verification reads them:
- *   packages/wpt-worker/src/wpt_worker/evaluation.py:74-81), -1 for a row
- *   whose values are all NaN.  The 256 x 256 tiles' epilogue keeps each
+ *   packages/wpt-worker/src/wpt_worker/evaluation.py:74-81: a NaN counts
+ *   as the largest value, the first of several).  The 256 x 256 tiles' epilogue keeps each
  *   row's (maximum, index) over its columns in the workspace
  *   (wptv_gemm_fm_wide_argmax_workspace bytes: 8 (N / 256) M), a second
  *   kernel reduces them in column order.  Shapes as wptv_gemm_fm_wide. */
@@ -445,7 +445,8 @@ int wptv_gemm_fm_wide_argmax(const void* x_fm, int x_blocks, const void* w_fm, i
  *   temperature, top_k  the reference's (top_k <= 0 or >= V: no cut)
  *   greedy   1: greedy verification instead (q, u, e unused and may be
  *            NULL): a draft is kept iff it is the first maximal index of its
- *            position's scores, and the replacement or bonus is that index
+ *            position's scores (torch.argmax's: a NaN counts as the largest
+ *            value), and the replacement or bonus is that index
  *   tokens   [B, L + 1] int64 out: the kept drafts, then the drawn token;
  *            entries past n_tokens[b] are -1
  *   n_tokens [B] int32 out: kept drafts + 1; -1 for a row whose residual
@@ -522,8 +523,8 @@ int wptv_accept_in_order(const void* scores, int64_t scores_stride_b, int64_t sc
  *            (the root included), -1 after
  *   tokens   [B, M + 1] int64 out: the accepted nodes' tokens after the
  *            root, then the argmax; -1 after
- *   n_tokens [B] int32 out: accepted nodes after the root + 1 (-1: a node
- *            on the walk had no maximum, every score NaN)
+ *   n_tokens [B] int32 out: accepted nodes after the root + 1 (each
+ *            node's argmax in torch.argmax's order, a NaN the largest)
  *   workspace  wptv_accept_workspace(B, M - 1) bytes */
 int wptv_greedy_tree(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
                      const int64_t* node_tokens, const int32_t* parents, int B, int M, int V, int64_t* path,
@@ -531,8 +532,9 @@ int wptv_greedy_tree(const void* scores, int64_t scores_stride_b, int64_t scores
                      hipStream_t stream);
 
 /* wptv_greedy_tree_best: the same walk from each node's argmax already
- *   found (best [B, M] int32, -1 for a node with no maximum: for instance
- *   wptv_gemm_fm_wide_argmax of the nodes' lm_head rows). */
+ *   found (best [B, M] int32: for instance wptv_gemm_fm_wide_argmax of the
+ *   nodes' lm_head rows; a node whose best is -1 ends the walk writing
+ *   nothing, n_tokens -1). */
 int wptv_greedy_tree_best(const int32_t* best, const int64_t* node_tokens, const int32_t* parents, int B, int M,
                           int64_t* path, int64_t* tokens, int32_t* n_tokens, hipStream_t stream);
 

@@ -198,7 +198,8 @@ def test_the_wide_fm_product_refuses_bad_shapes(device):
 def test_the_fused_head_argmax_is_the_argmax_of_the_bf16_logits(device, M, N, K):
     # the first maximal index of each row's bf16 logits, without storing them:
     # ties planted within a column tile (5, 6) and across tiles (N - 100), a
-    # row of NaN (no maximum: -1)
+    # row of NaN and a row of infinities and NaN (torch.argmax takes a NaN as
+    # the largest value, the first of several)
     generator = torch.Generator().manual_seed(M + N)
     x = torch.randn(M, K, generator=generator).to(torch.bfloat16)
     w = (torch.randn(N, K, generator=generator) * 0.02).to(torch.bfloat16)
@@ -206,13 +207,15 @@ def test_the_fused_head_argmax_is_the_argmax_of_the_bf16_logits(device, M, N, K)
     favourite = torch.full((K,), 0.05).to(torch.bfloat16)
     w[[5, 6, N - 100]] = favourite  # the same column three times (the last in another column tile)
     x[1] = float("nan")
+    x[2, 0] = float("inf")  # +inf or -inf by the sign of column 0 of w, NaN where inf meets -inf
+    x[2, 1] = float("-inf")
     x, w = x.to(device), w.to(device)
     x[rows_tied] = x[rows_tied].abs() + 0.5  # these rows prefer the planted columns
     x_fm, w_fm = layers.fm_pack(x), layers.FmWeight(w)
     best = layers.head_argmax_fm_wide(x_fm, M, w_fm)
     logits = layers.linear_fm_wide(x_fm, M, w_fm).float()
     expected = logits.argmax(-1).to(torch.int32)
-    expected[1] = -1  # torch takes the NaN as the maximum; a greedy row of NaN has none
     assert best.dtype == torch.int32 and best.shape == (M,)
     assert torch.equal(best, expected)
-    assert (best[rows_tied[rows_tied != 1]] == 5).all()
+    assert best[1] == 0 and torch.isnan(logits[2]).any()
+    assert (best[rows_tied[(rows_tied != 1) & (rows_tied != 2)]] == 5).all()

@@ -332,24 +332,34 @@ def test_a_residual_with_no_mass_raises(device):
         sampling.written(tokens, counts)
 
 
-def test_a_greedy_row_of_nan_scores_writes_nothing(device):
-    # no maximum to take: the row writes no token (the failed-row path), the
-    # other rows decide as usual, in the chain and in the tree
+def test_greedy_decisions_take_nan_as_torch_argmax_does(device):
+    # torch.argmax (the reference's greedy, evaluation.py:74-81) takes a NaN
+    # above every number, the first one among several: a row of NaN decides
+    # index 0, a row with a NaN its first NaN, in the chain and in the tree
     B, L, V = 3, 2, 64
     generator = torch.Generator().manual_seed(13)
     scores = torch.randn(B, L + 1, V, generator=generator)
     scores[1] = float("nan")
-    drafts = scores.argmax(-1)[:, :L].clone()
+    scores[2, 1, 40] = scores[2, 1, 9] = float("nan")
+    best = scores.to(device).argmax(-1).cpu()
+    assert best[1].tolist() == [0, 0, 0] and best[2, 1] == 9
+    drafts = best[:, :L].clone()
+    drafts[0, 1] = (drafts[0, 1] + 1) % V  # row 0 rejects its second draft
     tokens, counts = sampling.greedy_chain(scores.to(device), drafts.to(device))
-    assert counts.tolist() == [L + 1, -1, L + 1]
-    with pytest.raises(RuntimeError, match="no maximum"):
-        sampling.written(tokens, counts)
+    assert counts.tolist() == [2, L + 1, L + 1]
+    assert sampling.written(tokens, counts) == [[best[0, 0].item(), best[0, 1].item()], best[1].tolist(),
+                                                best[2].tolist()]
     parents = [-1, 0, 0]
     tree_scores = torch.randn(B, 3, V, generator=generator)
     tree_scores[2, 0] = float("nan")
-    _, _, tree_counts = sampling.greedy_tree(tree_scores.to(device), torch.zeros(B, 3, dtype=torch.long).to(device),
-                                             parents)
-    assert tree_counts[2] == -1 and (tree_counts[:2] >= 1).all()
+    tree_scores[0, 0, 17] = float("nan")
+    node_tokens = torch.tensor([[0, 5, 17], [0, 1, 2], [0, 0, 0]])
+    want = sampling.greedy_tree_from_argmax(tree_scores.to(device).argmax(-1).to(torch.int32), node_tokens.to(device),
+                                            parents)
+    got = sampling.greedy_tree(tree_scores.to(device), node_tokens.to(device), parents)
+    for a, b in zip(want, got):
+        assert torch.equal(a, b)
+    assert got[1][0, 0] == 17 and got[1][2, 0] == 0  # both walks go through a NaN node
 
 
 def test_bad_shapes_raise_value_error(device):

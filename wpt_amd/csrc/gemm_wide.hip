@@ -89,10 +89,11 @@ __device__ __forceinline__ void wait_lgkm0() {
 // reduced over the column tiles by wide_argmax_reduce).
 enum WideOut { kWideBf16 = 0, kWideF32 = 1, kWideArgmax = 2 };
 
-// The larger value, the lower index on a tie; a NaN never wins (the first
-// maximal index torch.argmax gives, over the non-NaN values).
+// torch.argmax's order: a NaN above every number, then the larger value;
+// the lower index among equals (NaNs included).
 __device__ __forceinline__ void wide_better(float& v, int& i, float v2, int i2) {
-  if (v2 > v || (v2 == v && i2 < i)) {
+  const bool nan = v != v, nan2 = v2 != v2;
+  if (nan2 ? (!nan || i2 < i) : (!nan && (v2 > v || (v2 == v && i2 < i)))) {
     v = v2;
     i = i2;
   }
@@ -328,8 +329,8 @@ __global__ __launch_bounds__(kWideWaves * 64, 1) void gemm_wide(const unsigned s
   }
 }
 
-// Each row's first maximal index over the column tiles' (value, index) pairs,
-// -1 for a row with no maximum (every value NaN): one wavefront per row.
+// Each row's first maximal index over the column tiles' (value, index) pairs
+// (torch.argmax's order): one wavefront per row.
 __global__ __launch_bounds__(256) void wide_argmax_reduce(const float2* __restrict__ parts, int col_tiles, int M,
                                                           int32_t* __restrict__ best) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;

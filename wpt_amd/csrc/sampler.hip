@@ -79,7 +79,9 @@ __device__ __forceinline__ float block_sum(float x, float* red) {
   return r;
 }
 
-// The larger value, the lower index on a tie (torch.argmax's first maximum).
+// The draws' race: the larger value, the lower index on a tie; a NaN never
+// wins (a distribution of NaN has nothing to draw, as torch.multinomial
+// refuses it).
 __device__ __forceinline__ void arg_better(float& v, int& i, float v2, int i2) {
   if (v2 > v || (v2 == v && i2 < i) || (v != v && v2 == v2)) {
     v = v2;
@@ -87,12 +89,31 @@ __device__ __forceinline__ void arg_better(float& v, int& i, float v2, int i2) {
   }
 }
 
+// Greedy decisions, torch.argmax's order: a NaN above every number, then the
+// larger value; the lower index among equals (NaNs included).
+__device__ __forceinline__ void argmax_better(float& v, int& i, float v2, int i2) {
+  const bool nan = v != v, nan2 = v2 != v2;
+  if (nan2 ? (!nan || i2 < i) : (!nan && (v2 > v || (v2 == v && i2 < i)))) {
+    v = v2;
+    i = i2;
+  }
+}
+
+template <bool GREEDY = false>
+__device__ __forceinline__ void better(float& v, int& i, float v2, int i2) {
+  if constexpr (GREEDY)
+    argmax_better(v, i, v2, i2);
+  else
+    arg_better(v, i, v2, i2);
+}
+
+template <bool GREEDY = false>
 __device__ __forceinline__ int block_argmax(float v, int i, float* redv, int* redi) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float v2 = __shfl_xor(v, o, 64);
     const int i2 = __shfl_xor(i, o, 64);
-    arg_better(v, i, v2, i2);
+    better<GREEDY>(v, i, v2, i2);
   }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   __syncthreads();
@@ -103,7 +124,7 @@ __device__ __forceinline__ int block_argmax(float v, int i, float* redv, int* re
   __syncthreads();
   float bv = redv[0];
   int bi = redi[0];
-  for (int w = 1; w < kW; ++w) arg_better(bv, bi, redv[w], redi[w]);
+  for (int w = 1; w < kW; ++w) better<GREEDY>(bv, bi, redv[w], redi[w]);
   return bi;
 }
 
@@ -342,9 +363,8 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
     int bi = INT_MAX;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i)
-      if (tid + i * kT < V) arg_better(bv, bi, x[i], tid + i * kT);
-    // a row of NaN has no maximum: no index (the pick then writes nothing and flags the row)
-    const int found = block_argmax(bv, bi, redv, redi);
+      if (tid + i * kT < V) argmax_better(bv, bi, x[i], tid + i * kT);
+    const int found = block_argmax<true>(bv, bi, redv, redi);
     const int best = found >= 0 && found < V ? found : -1;
     if (tid == 0) {
       stats.best[idx] = best;
@@ -857,7 +877,7 @@ __global__ void tree_walk(const int64_t* __restrict__ node_tokens, const int32_t
     ++depth;
     pa[depth] = node;
   }
-  // a node whose scores are all NaN has no maximum: the row writes nothing (-1)
+  // a given best of -1 ends the walk with nothing written
   n_tokens[b] = tk[depth] >= 0 ? depth + 1 : -1;
 }
 
@@ -903,9 +923,10 @@ int items_for(int V) {
 // Greedy decisions alone (no drafts' distributions to form): each (batch
 // row, position)'s first maximal index of the raw scores, by one workgroup of
 // kGT threads reading the row 16 bytes a lane, every load of a thread issued
-// before the first comparison; the same order as arg_better's (larger value,
-// then lower index; a NaN never wins), so the index does not depend on how the
-// row is shared out.  Rows 16-byte aligned, V a multiple of 16 / sizeof(S).
+// before the first comparison; torch.argmax's order (argmax_better: a NaN
+// the largest, then the larger value, then the lower index), so the index does
+// not depend on how the row is shared out.  Rows 16-byte aligned, V a
+// multiple of 16 / sizeof(S).
 constexpr int kGT = 256;
 constexpr int kGLoads = 16;  // 16-byte loads a thread has in flight
 
@@ -947,7 +968,7 @@ __global__ __launch_bounds__(kGT) void greedy_argmax(const S* __restrict__ score
           x = __uint_as_float(e & 1 ? (w[u][e >> 1] & 0xffff0000u) : (w[u][e >> 1] << 16));
         else
           x = __uint_as_float(w[u][e]);
-        arg_better(bv, bi, x, c * kPer + e);
+        argmax_better(bv, bi, x, c * kPer + e);
       }
     }
   }
@@ -955,7 +976,7 @@ __global__ __launch_bounds__(kGT) void greedy_argmax(const S* __restrict__ score
   for (int o = 32; o > 0; o >>= 1) {
     const float v2 = __shfl_xor(bv, o, 64);
     const int i2 = __shfl_xor(bi, o, 64);
-    arg_better(bv, bi, v2, i2);
+    argmax_better(bv, bi, v2, i2);
   }
   const int wave = tid >> 6, lane = tid & 63;
   if (lane == 0) {
@@ -967,9 +988,9 @@ __global__ __launch_bounds__(kGT) void greedy_argmax(const S* __restrict__ score
     float v = redv[0];
     int i = redi[0];
 #pragma unroll
-    for (int w = 1; w < kGT / 64; ++w) arg_better(v, i, redv[w], redi[w]);
+    for (int w = 1; w < kGT / 64; ++w) argmax_better(v, i, redv[w], redi[w]);
     const int idx = b * P + j;
-    const int best = i >= 0 && i < V ? i : -1;  // a row of NaN has no maximum
+    const int best = i >= 0 && i < V ? i : -1;
     stats.best[idx] = best;
     stats.keep[idx] = (j < n && drafts && best >= 0) ? (drafts[b * db + j] == best) : 0;
   }

@@ -381,7 +381,8 @@ def linear_fm_wide(x_fm, rows, w, out_dtype=torch.bfloat16):
 def head_argmax_fm_wide(x_fm, rows, w):
     """Each row's first maximal index of the bf16-rounded product x . w^T (the
     greedy decisions' argmax of an lm_head's logits), without storing the
-    product: (rows,) int32, -1 for a row of NaN (wptv_gemm_fm_wide_argmax).
+    product: (rows,) int32, in torch.argmax's order (a NaN the largest value)
+    (wptv_gemm_fm_wide_argmax).
     x a flat fm operand of rows x K, w an FmWeight (N, K), N a multiple of 256."""
     _gpu(x_fm, w.data)
     N, K = w.shape

@@ -252,8 +252,8 @@ def greedy_tree(scores, node_tokens, parents):
 
 def greedy_tree_from_argmax(best, node_tokens, parents):
     """greedy_tree from each node's argmax already found: best (B, M) int32
-    (-1 for a node with no maximum, e.g. layers.head_argmax_fm_wide of the
-    nodes' lm_head rows).  Returns (path, tokens, counts) as greedy_tree."""
+    (e.g. layers.head_argmax_fm_wide of the nodes' lm_head rows; a -1 ends
+    the walk writing nothing).  Returns (path, tokens, counts) as greedy_tree."""
     B, M = best.shape
     device = best.device
     parents_ = _parents(parents, M, device)
@@ -293,6 +293,6 @@ def written(tokens, counts):
     for b, n in enumerate(counts):
         if n < 0:
             raise RuntimeError(f"row {b}: no token to write: the residual distribution max(0, p - q) has no mass to "
-                               f"draw from, or the scores have no maximum (all NaN)")
+                               f"draw from")
         out.append(rows[b][:n])
     return out
