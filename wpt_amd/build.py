@@ -21,9 +21,12 @@ LIBRARY = PACKAGE / "lib" / "libwptv.so"
 ARCH = "gfx950"
 
 # Every HIP source is compiled with packed FP32 arithmetic off (the packed
-# forms are left to no code in this library).
+# forms are left to no code in this library), and with the first 16 dwords
+# of each kernel's arguments preloaded into SGPRs at wave launch (gfx950's
+# kernarg preload; the code keeps the loads as a fallback prologue).
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
-             "-packed-fp32-ops", "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-but-set-variable"]
+             "-packed-fp32-ops", "-mllvm", "-amdgpu-kernarg-preload-count=16", "-Wall", "-Wno-unused-function",
+             "-Wno-unused-variable", "-Wno-unused-but-set-variable"]
 
 
 def hipcc():

@@ -97,7 +97,7 @@ __global__ __launch_bounds__(64) void add_rms_norm(T* __restrict__ h, const T* _
     for (int e = 0; e < 8; ++e) part += x[k][e] * x[k][e];
     ss += in ? part : 0.f;
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   const float inv = rsqrtf(ss / (float)D + eps);
   T* yrow = y + (int64_t)row * D;
 #pragma unroll
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(64) void embed_rms_norm(const int64_t* __restrict__
     for (int e = 0; e < 8; ++e) part += x[k][e] * x[k][e];
     ss += (k * 64 + lane) * 8 < D ? part : 0.f;
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   const float inv = rsqrtf(ss / (float)D + eps);
   T* hrow = h + (int64_t)row * D;
   T* yrow = y + (int64_t)row * D;
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(1024) void add_rms_norm_parts(T* __restrict__ h, co
     x[e] = rounded<T>(x[e] + rounded<T>(delta));
     ss += x[e] * x[e];
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   if (lane == 0) wsum[wv] = ss;
   __syncthreads();
   float total = 0.f;
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(256) void qkv_post(const T* __restrict__ qkv, int64
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) ss += v[e] * v[e];
-    ss = wave_sum(ss);
+    ss = wave_sum_dpp(ss);
     const float inv = rsqrtf(ss / (float)C + eps);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) v[e] = v[e] * inv * wt[e];
@@ -355,7 +355,7 @@ __global__ __launch_bounds__(256) void heads_rms_norm(const T* __restrict__ x, i
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) ss += v[e] * v[e];
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   const float inv = rsqrtf(ss / (float)C + eps);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) v[e] = v[e] * inv * weight[EPL * lane + e];

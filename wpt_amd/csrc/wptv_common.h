@@ -123,6 +123,24 @@ __device__ __forceinline__ float row16_max(float x) {
   return fmaxf(x, __int_as_float(dpp_move<kDppMirror>(__float_as_int(x))));
 }
 
+// The sum over the 64 lanes of a wavefront, in every lane, without LDS
+// traffic (wave_sum's shuffles are six dependent ds_bpermute round trips):
+// pairs, quads, 8 and 16 lanes by DPP, then the rows by permlane swaps.  Each
+// step adds two equal-count partial sums, so every lane ends with the same bits.
+// The DPP and permlane moves read inactive lanes' registers as they stand, so
+// a wavefront with lanes off (a row narrower than 64 lanes) takes wave_sum.
+__device__ __forceinline__ float wave_sum_dpp(float x) {
+  if (__builtin_amdgcn_read_exec() != ~0ull) return wave_sum(x);
+  x += __int_as_float(dpp_move<kDppXor1>(__float_as_int(x)));
+  x += __int_as_float(dpp_move<kDppXor2>(__float_as_int(x)));
+  x += __int_as_float(dpp_move<kDppHalfMirror>(__float_as_int(x)));
+  x += __int_as_float(dpp_move<kDppMirror>(__float_as_int(x)));
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // The sum over the 64 lanes of a wavefront, in every lane: the rows by DPP,
 // then across the four rows by permlane swaps.
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t x) {
