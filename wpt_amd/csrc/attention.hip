@@ -265,15 +265,18 @@ __device__ __forceinline__ float group_sum(float x) {
 // wavefronts; wavefront (s, mb) holds m-block mb (16 query rows) and takes the
 // 32-row key tiles s, s + 2, ... of the split.  The tiles of a key set are
 // DMA'd into its LDS ring by its first DMAW wavefronts and read by all MB of
-// them; a workgroup barrier per iteration hands them over.
+// them; a workgroup barrier per iteration hands them over.  The parameters
+// the first key range depends on come first: gfx950 preloads a kernel's first
+// 14 argument dwords into SGPRs, so the positions load is issued at once and
+// the rest of the arguments arrive meanwhile.
 template <int C, int MB, bool TREE>
 __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
-    const unsigned short* __restrict__ q, const unsigned short* __restrict__ k, int64_t ksb, int64_t ksn,
-    const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn, const int64_t* __restrict__ positions,
-    int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
-    const float* __restrict__ sink, int T, int H, int N, float scale_log2, int groups, int splits,
-    int range_from_positions, int xcd_map, RowMap rows, OutGate gate, unsigned short* __restrict__ out,
-    int out_fm, float* __restrict__ lse_out, unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
+    const int64_t* __restrict__ positions, const int64_t* __restrict__ tree_base, int xcd_map, int groups,
+    int splits, int T, int H, int N, int window, int range_from_positions, const unsigned short* __restrict__ k,
+    int64_t ksb, int64_t ksn, const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn,
+    const unsigned short* __restrict__ q, const uint64_t* __restrict__ ancestors, const float* __restrict__ sink,
+    float scale_log2, RowMap rows, OutGate gate, unsigned short* __restrict__ out, int out_fm,
+    float* __restrict__ lse_out, unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
   using G = Tile<C>;
   constexpr int kRows = 16 * MB;
   constexpr int kXC = C / 8;  // 16-byte chunks per key or value row
@@ -661,12 +664,12 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
 //                               keys, two transposed 4-row reads
 template <int C, int MB, bool TREE>
 __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
-    const unsigned short* __restrict__ q, const unsigned short* __restrict__ k, int64_t ksb, int64_t ksn,
-    const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn, const int64_t* __restrict__ positions,
-    int window, const int64_t* __restrict__ tree_base, const uint64_t* __restrict__ ancestors,
-    const float* __restrict__ sink, int T, int H, int N, float scale_log2, int groups, int splits,
-    int range_from_positions, int xcd_map, RowMap rows, OutGate gate, unsigned short* __restrict__ out,
-    int out_fm, float* __restrict__ lse_out, unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
+    const int64_t* __restrict__ positions, const int64_t* __restrict__ tree_base, int xcd_map, int groups,
+    int splits, int T, int H, int N, int window, int range_from_positions, const unsigned short* __restrict__ k,
+    int64_t ksb, int64_t ksn, const unsigned short* __restrict__ v, int64_t vsb, int64_t vsn,
+    const unsigned short* __restrict__ q, const uint64_t* __restrict__ ancestors, const float* __restrict__ sink,
+    float scale_log2, RowMap rows, OutGate gate, unsigned short* __restrict__ out, int out_fm,
+    float* __restrict__ lse_out, unsigned short* __restrict__ part_o, float* __restrict__ part_lse) {
   static_assert(C == 128, "the 32-row kernel is built for head width 128");
   using G = Tile<C>;
   typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -1978,9 +1981,9 @@ void launch_mfma(dim3 grid, hipStream_t stream, const unsigned short* q, const u
                  int N, float scale_log2, int groups, int splits, int range_from_positions, int xcd_map,
                  RowMap rows, OutGate gate, unsigned short* out, int out_fm, float* lse, unsigned short* part_o,
                  float* part_lse) {
-  hipLaunchKernelGGL((verify_attention_mfma<C, MBW, TREE>), grid, dim3(kKeySets * MBW * 64), 0, stream, q, k, ksb,
-                     ksn, v, vsb, vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, groups,
-                     splits, range_from_positions, xcd_map, rows, gate, out, out_fm, lse, part_o, part_lse);
+  hipLaunchKernelGGL((verify_attention_mfma<C, MBW, TREE>), grid, dim3(kKeySets * MBW * 64), 0, stream, positions,
+                     tree_base, xcd_map, groups, splits, T, H, N, window, range_from_positions, k, ksb, ksn, v, vsb,
+                     vsn, q, ancestors, sink, scale_log2, rows, gate, out, out_fm, lse, part_o, part_lse);
 }
 
 template <int MB, bool TREE>
@@ -1989,9 +1992,9 @@ void launch_m32(dim3 grid, hipStream_t stream, const unsigned short* q, const un
                 const int64_t* tree_base, const uint64_t* ancestors, const float* sink, int T, int H, int N,
                 float scale_log2, int groups, int splits, int range_from_positions, int xcd_map, RowMap rows,
                 OutGate gate, unsigned short* out, int out_fm, float* lse, unsigned short* part_o, float* part_lse) {
-  hipLaunchKernelGGL((verify_attention_m32<128, MB, TREE>), grid, dim3(kKeySets * MB * 64), 0, stream, q, k, ksb,
-                     ksn, v, vsb, vsn, positions, window, tree_base, ancestors, sink, T, H, N, scale_log2, groups,
-                     splits, range_from_positions, xcd_map, rows, gate, out, out_fm, lse, part_o, part_lse);
+  hipLaunchKernelGGL((verify_attention_m32<128, MB, TREE>), grid, dim3(kKeySets * MB * 64), 0, stream, positions,
+                     tree_base, xcd_map, groups, splits, T, H, N, window, range_from_positions, k, ksb, ksn, v, vsb,
+                     vsn, q, ancestors, sink, scale_log2, rows, gate, out, out_fm, lse, part_o, part_lse);
 }
 
 }  // namespace

@@ -257,14 +257,17 @@ struct Rope {
   uint32_t ring_mask;  // 0: the entry at row start[b] + t (no ring)
 };
 
+// The arguments the first loads depend on come first (gfx950 preloads a
+// kernel's first 14 argument dwords into SGPRs; the others arrive by a
+// scalar load meanwhile).
 template <typename T, int EPL, int S>
-__global__ __launch_bounds__(256) void qkv_post(const T* __restrict__ qkv, int64_t qkv_row,
-                                                const float* __restrict__ qkv_parts,
+__global__ __launch_bounds__(256) void qkv_post(int rows, int T_, int H, const float* __restrict__ qkv_parts,
                                                 const float* __restrict__ q_norm, const float* __restrict__ k_norm,
-                                                T* __restrict__ q_out, T* __restrict__ table, int64_t tsb,
-                                                int64_t tsn, int64_t capacity, const int64_t* __restrict__ start,
-                                                const int64_t* __restrict__ counts, int rows, int T_, int H,
-                                                float eps, Rope rope) {
+                                                const int64_t* __restrict__ start,
+                                                const int64_t* __restrict__ counts, float eps,
+                                                const T* __restrict__ qkv, int64_t qkv_row, T* __restrict__ q_out,
+                                                T* __restrict__ table, int64_t tsb, int64_t tsn, int64_t capacity,
+                                                Rope rope) {
   constexpr int C = 64 * EPL;
   const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -531,9 +534,9 @@ extern "C" int wptv_qkv_post(const void* qkv, int64_t qkv_row_stride, const floa
   const int rows = B * T;
   dim3 grid((unsigned)(((int64_t)rows * (H + 2) + 3) / 4));
 #define WPTV_QKV(TT, EE)                                                                                          \
-  hipLaunchKernelGGL((qkv_post<TT, EE, 0>), grid, dim3(256), 0, stream, static_cast<const TT*>(qkv),             \
-                     qkv_row_stride, nullptr, q_norm, k_norm, static_cast<TT*>(q_out), static_cast<TT*>(table),  \
-                     table_stride_b, table_stride_n, capacity, start, counts, rows, T, H, eps, rope)
+  hipLaunchKernelGGL((qkv_post<TT, EE, 0>), grid, dim3(256), 0, stream, rows, T, H, nullptr, q_norm, k_norm,     \
+                     start, counts, eps, static_cast<const TT*>(qkv), qkv_row_stride, static_cast<TT*>(q_out),    \
+                     static_cast<TT*>(table), table_stride_b, table_stride_n, capacity, rope)
   const Rope rope{0, nullptr, 0u};
   if (dtype == WPTV_BF16) {
     if (epl == 1) WPTV_QKV(unsigned short, 1);
@@ -577,9 +580,9 @@ extern "C" int wptv_window_qkv_post(const void* qkv, int64_t qkv_row_stride, con
   const Rope rope{rope_dims, rope_div, (uint32_t)(ring_rows - 1)};
   dim3 grid((unsigned)(((int64_t)rows * (H + 2) + 3) / 4));
 #define WPTV_WQKV(TT, EE)                                                                                         \
-  hipLaunchKernelGGL((qkv_post<TT, EE, 0>), grid, dim3(256), 0, stream, static_cast<const TT*>(qkv),             \
-                     qkv_row_stride, nullptr, q_norm, k_norm, static_cast<TT*>(q_out), static_cast<TT*>(ring),   \
-                     ring_stride_b, ring_stride_n, (int64_t)ring_rows, start, counts, rows, T, H, eps, rope)
+  hipLaunchKernelGGL((qkv_post<TT, EE, 0>), grid, dim3(256), 0, stream, rows, T, H, nullptr, q_norm, k_norm,     \
+                     start, counts, eps, static_cast<const TT*>(qkv), qkv_row_stride, static_cast<TT*>(q_out),    \
+                     static_cast<TT*>(ring), ring_stride_b, ring_stride_n, (int64_t)ring_rows, rope)
   if (dtype == WPTV_BF16) {
     if (epl == 1) WPTV_WQKV(unsigned short, 1);
     else if (epl == 2) WPTV_WQKV(unsigned short, 2);
@@ -616,9 +619,9 @@ extern "C" int wptv_qkv_post_parts(const float* parts, int splits, const float* 
   const int rows = B * T;
   dim3 grid((unsigned)(((int64_t)rows * (H + 2) + 3) / 4));
 #define WPTV_QKVP(TT, EE, SS)                                                                                     \
-  hipLaunchKernelGGL((qkv_post<TT, EE, SS>), grid, dim3(256), 0, stream, nullptr, 0, parts, q_norm, k_norm,       \
-                     static_cast<TT*>(q_out), static_cast<TT*>(table), table_stride_b, table_stride_n, capacity, \
-                     start, counts, rows, T, H, eps, Rope{0, nullptr, 0u})
+  hipLaunchKernelGGL((qkv_post<TT, EE, SS>), grid, dim3(256), 0, stream, rows, T, H, parts, q_norm, k_norm, start, \
+                     counts, eps, nullptr, 0, static_cast<TT*>(q_out), static_cast<TT*>(table), table_stride_b,   \
+                     table_stride_n, capacity, Rope{0, nullptr, 0u})
 #define WPTV_QKVP_S(TT, EE)               \
   switch (splits) {                       \
     case 1: WPTV_QKVP(TT, EE, 1); break;  \
