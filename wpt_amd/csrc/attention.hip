@@ -72,6 +72,26 @@ __device__ __forceinline__ Bounds query_bounds(const QueryPos& pos_b, int t, int
   return r;
 }
 
+// The union [u_lo, u_hi] of the key rows that positions t_first .. t_last
+// see (u_hi < u_lo: none), uniform.  A lane per position, so the positions
+// come in by one vector load instead of one dependent scalar load each; every
+// lane of the wavefront must be active.
+__device__ __forceinline__ void union_bounds(const QueryPos& pos_b, int t_first, int t_last, int window, int N,
+                                             int lane, int& u_lo, int& u_hi) {
+  int lo_l = INT_MAX, hi_l = -1;
+  for (int t0 = t_first; t0 <= t_last; t0 += 64) {
+    if (t0 + lane <= t_last) {
+      const Bounds bt = query_bounds(pos_b, t0 + lane, window, N);
+      if (bt.hi >= bt.lo) {
+        lo_l = min(lo_l, bt.lo);
+        hi_l = max(hi_l, bt.hi);
+      }
+    }
+  }
+  u_lo = __builtin_amdgcn_readfirstlane(wave_min_i32(lo_l));
+  u_hi = __builtin_amdgcn_readfirstlane(wave_max_i32(hi_l));
+}
+
 __device__ __forceinline__ bool tree_visible(int n, int64_t tbase, uint64_t anc) {
   if ((int64_t)n < tbase) return true;
   const int64_t node = (int64_t)n - tbase;
@@ -319,18 +339,8 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
 
   // The key rows this workgroup's queries can see.
   int u_lo = 0, u_hi = N - 1;
-  if (range_from_positions) {
-    u_lo = INT_MAX;
-    u_hi = -1;
-    const int t_first = r_base / H, t_last = (min(r_base + kRows, R) - 1) / H;
-    for (int t = t_first; t <= t_last; ++t) {
-      const Bounds bt = query_bounds(pos_b, t, window, N);
-      if (bt.hi >= bt.lo) {
-        u_lo = min(u_lo, bt.lo);
-        u_hi = max(u_hi, bt.hi);
-      }
-    }
-  }
+  if (range_from_positions)
+    union_bounds(pos_b, r_base / H, (min(r_base + kRows, R) - 1) / H, window, N, lane, u_lo, u_hi);
   int s_lo = 0, s_hi = -1;
   if (u_hi >= u_lo) split_range(u_lo, u_hi, splits, split, s_lo, s_hi);
   const int ntiles = s_hi >= s_lo ? (s_hi - s_lo + 1 + 31) / 32 : 0;
@@ -388,7 +398,9 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   const int r = r_base + 16 * mb + j;
   const bool real = r < R;
   if (kset == 0) {
-    const i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
+    i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qrs[e] = __builtin_amdgcn_readfirstlane(qrs[e]);
     const uint32_t qoff = (uint32_t)(real ? r : R - 1) * (uint32_t)(C * 2) + 16u * g;  // a padding row reads row R-1
     const uint32_t qdst = __builtin_amdgcn_readfirstlane(lds_address(qlds + mb * 16 * C));
 #pragma unroll
@@ -409,21 +421,20 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   {
     const int w_first = r_base + 16 * mb;
     if (w_first < R) {
-      const int t_first = w_first / H, t_last = (min(w_first + 16, R) - 1) / H;
-      const int my_t = real ? r / H : -1;
-      for (int t = t_first; t <= t_last; ++t) {
-        const Bounds bt = query_bounds(pos_b, t, window, N);
-        f_lo = max(f_lo, bt.lo);
-        f_hi = min(f_hi, bt.hi);
-        if (my_t == t) {
-          lo = bt.lo;
-          hi = min(bt.hi, s_hi);
-        }
-        if constexpr (TREE) {
-          const uint64_t a = ancestors[t];
-          if (my_t == t) anc = a;
-        }
+      // each lane its own row's position (a vector load), the wavefront's
+      // common range by DPP reductions over its real rows
+      int blo = 0, bhi = INT_MAX;
+      if (real) {
+        const int my_t = r / H;
+        const Bounds bt = query_bounds(pos_b, my_t, window, N);
+        blo = bt.lo;
+        bhi = bt.hi;
+        lo = bt.lo;
+        hi = min(bt.hi, s_hi);
+        if constexpr (TREE) anc = ancestors[my_t];
       }
+      f_lo = max(f_lo, __builtin_amdgcn_readfirstlane(wave_max_i32(blo)));
+      f_hi = min(f_hi, __builtin_amdgcn_readfirstlane(wave_min_i32(bhi)));
     } else {
       f_hi = -1;
     }
@@ -715,18 +726,8 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
   const QueryPos pos_b = query_pos(positions, tree_base, b, T);
 
   int u_lo = 0, u_hi = N - 1;
-  if (range_from_positions) {
-    u_lo = INT_MAX;
-    u_hi = -1;
-    const int t_first = r_base / H, t_last = (min(r_base + kRows, R) - 1) / H;
-    for (int t = t_first; t <= t_last; ++t) {
-      const Bounds bt = query_bounds(pos_b, t, window, N);
-      if (bt.hi >= bt.lo) {
-        u_lo = min(u_lo, bt.lo);
-        u_hi = max(u_hi, bt.hi);
-      }
-    }
-  }
+  if (range_from_positions)
+    union_bounds(pos_b, r_base / H, (min(r_base + kRows, R) - 1) / H, window, N, lane, u_lo, u_hi);
   int s_lo = 0, s_hi = -1;
   if (u_hi >= u_lo) split_range(u_lo, u_hi, splits, split, s_lo, s_hi);
   const int ntiles = s_hi >= s_lo ? (s_hi - s_lo + 1 + 31) / 32 : 0;
@@ -773,7 +774,9 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
   const int r = r_base + 32 * mb + j;
   const bool real = r < R;
   if (kset == 0) {
-    const i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
+    i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qrs[e] = __builtin_amdgcn_readfirstlane(qrs[e]);
     const uint32_t qoff = (uint32_t)(real ? r : R - 1) * (uint32_t)(C * 2) + 16u * h;
     const uint32_t qdst = __builtin_amdgcn_readfirstlane(lds_address(qlds + mb * 32 * C));
 #pragma unroll
@@ -791,21 +794,20 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
   {
     const int w_first = r_base + 32 * mb;
     if (w_first < R) {
-      const int t_first = w_first / H, t_last = (min(w_first + 32, R) - 1) / H;
-      const int my_t = real ? r / H : -1;
-      for (int t = t_first; t <= t_last; ++t) {
-        const Bounds bt = query_bounds(pos_b, t, window, N);
-        f_lo = max(f_lo, bt.lo);
-        f_hi = min(f_hi, bt.hi);
-        if (my_t == t) {
-          lo = bt.lo;
-          hi = min(bt.hi, s_hi);
-        }
-        if constexpr (TREE) {
-          const uint64_t a = ancestors[t];
-          if (my_t == t) anc = a;
-        }
+      // each lane its own row's position (a vector load), the wavefront's
+      // common range by DPP reductions over its real rows
+      int blo = 0, bhi = INT_MAX;
+      if (real) {
+        const int my_t = r / H;
+        const Bounds bt = query_bounds(pos_b, my_t, window, N);
+        blo = bt.lo;
+        bhi = bt.hi;
+        lo = bt.lo;
+        hi = min(bt.hi, s_hi);
+        if constexpr (TREE) anc = ancestors[my_t];
       }
+      f_lo = max(f_lo, __builtin_amdgcn_readfirstlane(wave_max_i32(blo)));
+      f_hi = min(f_hi, __builtin_amdgcn_readfirstlane(wave_min_i32(bhi)));
     } else {
       f_hi = -1;
     }
@@ -1374,7 +1376,9 @@ __global__ __launch_bounds__(kKeyWaves * 64, 1) void verify_attention_keys(
   // Queries first: wavefront w DMAs the 1 KiB pieces w, w + 4, ... of the
   // R rows (padding rows repeat row R - 1).
   {
-    const i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
+    i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qrs[e] = __builtin_amdgcn_readfirstlane(qrs[e]);
     const uint32_t qdst = __builtin_amdgcn_readfirstlane(lds_address(qlds));
 #pragma unroll
     for (int ii = 0; ii < kQLoads; ++ii) {

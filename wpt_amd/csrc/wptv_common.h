@@ -141,6 +141,30 @@ __device__ __forceinline__ float wave_sum_dpp(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// The minimum and the maximum over the 64 lanes of a wavefront, in every lane
+// (DPP within rows, permlane swaps across them); every lane must be active.
+__device__ __forceinline__ int wave_min_i32(int x) {
+  x = min(x, dpp_move<kDppXor1>(x));
+  x = min(x, dpp_move<kDppXor2>(x));
+  x = min(x, dpp_move<kDppHalfMirror>(x));
+  x = min(x, dpp_move<kDppMirror>(x));
+  const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = min((int)a[0], (int)a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return min((int)b[0], (int)b[1]);
+}
+
+__device__ __forceinline__ int wave_max_i32(int x) {
+  x = max(x, dpp_move<kDppXor1>(x));
+  x = max(x, dpp_move<kDppXor2>(x));
+  x = max(x, dpp_move<kDppHalfMirror>(x));
+  x = max(x, dpp_move<kDppMirror>(x));
+  const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = max((int)a[0], (int)a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return max((int)b[0], (int)b[1]);
+}
+
 // The sum over the 64 lanes of a wavefront, in every lane: the rows by DPP,
 // then across the four rows by permlane swaps.
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t x) {
