@@ -51,10 +51,19 @@ struct Bounds {
 // The key rows query position t of batch row b sees, before the tree mask.
 // A batch row's query positions: p[t], or (a draft tree given without
 // positions) node t at base + t.
+// p[i] of an input that no kernel of the launch writes, read as constant
+// memory: a scalar load where i is uniform (on the scalar counter, apart from
+// the vector-memory counter the kernels' DMA runs on, which the compiler's own
+// waits cannot count), a vector load where it is not.
+template <typename T>
+__device__ __forceinline__ T const_load(const T* p, int64_t i) {
+  return ((const __attribute__((address_space(4))) T*)(uintptr_t)p)[i];
+}
+
 struct QueryPos {
   const int64_t* p;
   int64_t base;
-  __device__ __forceinline__ int64_t at(int t) const { return p ? p[t] : base + t; }
+  __device__ __forceinline__ int64_t at(int t) const { return p ? const_load(p, t) : base + t; }
 };
 
 __device__ __forceinline__ QueryPos query_pos(const int64_t* positions, const int64_t* tree_base, int b, int T) {
@@ -108,7 +117,8 @@ struct RowMap {
   uint32_t mask;
 };
 
-__device__ __forceinline__ int row_base(const RowMap& m, int b) { return m.base ? (int)m.base[b] : 0; }
+// The table row of batch row b's first ring slot (a scalar load).
+__device__ __forceinline__ int row_base(const RowMap& m, int b) { return m.base ? (int)const_load(m.base, b) : 0; }
 
 // A window or sparse layer's output gate (attention.py:128-130): the output
 // o (rounded to bf16, the attention's dtype) times sigmoid(gate) (rounded to
@@ -337,7 +347,12 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   const int r_base = grp * kRows;
   const QueryPos pos_b = query_pos(positions, tree_base, b, T);
 
-  // The key rows this workgroup's queries can see.
+  // The key rows this workgroup's queries can see: the positions come in by
+  // one vector load (a lane each), waited for here, before any DMA (the
+  // compiler's waits on vector memory cannot count the DMA, so a vector load
+  // waited for among the DMA would drain the DMA with it).
+  const int r = r_base + 16 * mb + j;
+  const bool real = r < R;
   int u_lo = 0, u_hi = N - 1;
   if (range_from_positions)
     union_bounds(pos_b, r_base / H, (min(r_base + kRows, R) - 1) / H, window, N, lane, u_lo, u_hi);
@@ -392,11 +407,9 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   // key half, so that the Q^T operand of k-step s is unit 64s + lane; the
   // first key set loads them, the second reads them after the first
   // barrier), then the first tiles.  Waiting for tile 0 then implies the
-  // queries.  The bounds come through scalar loads, on their own counter, so
-  // the compiler needs no vector-memory wait of its own inside the loop (it
-  // cannot count the DMA).
-  const int r = r_base + 16 * mb + j;
-  const bool real = r < R;
+  // queries.  Every other load of the kernel was waited for before this
+  // point, so the compiler needs no vector-memory wait of its own from here
+  // on (it cannot count the DMA).
   if (kset == 0) {
     i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
 #pragma unroll
@@ -412,8 +425,9 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
       if (it < mine) issue(it);
   }
   // Per-row bounds: the wavefront's 16 rows span positions t_first..t_last;
-  // each position is read with a uniform (scalar) load and the lanes of that
-  // position take it.  f_lo, f_hi: the rows every query of the wavefront sees.
+  // each position is read with a uniform (scalar) load, on the scalar counter,
+  // and the lanes of that position take it.  f_lo, f_hi: the rows every query
+  // of the wavefront sees.
   int lo = 0, hi = -1;
   uint64_t anc = 0;
   int f_lo = 0, f_hi = INT_MAX;
@@ -421,20 +435,21 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_mfma(
   {
     const int w_first = r_base + 16 * mb;
     if (w_first < R) {
-      // each lane its own row's position (a vector load), the wavefront's
-      // common range by DPP reductions over its real rows
-      int blo = 0, bhi = INT_MAX;
-      if (real) {
-        const int my_t = r / H;
-        const Bounds bt = query_bounds(pos_b, my_t, window, N);
-        blo = bt.lo;
-        bhi = bt.hi;
-        lo = bt.lo;
-        hi = min(bt.hi, s_hi);
-        if constexpr (TREE) anc = ancestors[my_t];
+      const int t_first = w_first / H, t_last = (min(w_first + 16, R) - 1) / H;
+      const int my_t = real ? r / H : -1;
+      for (int t = t_first; t <= t_last; ++t) {
+        const Bounds bt = query_bounds(pos_b, t, window, N);
+        f_lo = max(f_lo, bt.lo);
+        f_hi = min(f_hi, bt.hi);
+        if (my_t == t) {
+          lo = bt.lo;
+          hi = min(bt.hi, s_hi);
+        }
+        if constexpr (TREE) {
+          const uint64_t a = const_load(ancestors, t);
+          if (my_t == t) anc = a;
+        }
       }
-      f_lo = max(f_lo, __builtin_amdgcn_readfirstlane(wave_max_i32(blo)));
-      f_hi = min(f_hi, __builtin_amdgcn_readfirstlane(wave_min_i32(bhi)));
     } else {
       f_hi = -1;
     }
@@ -725,6 +740,12 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
   const int r_base = grp * kRows;
   const QueryPos pos_b = query_pos(positions, tree_base, b, T);
 
+  // The key rows this workgroup's queries can see: the positions come in by
+  // one vector load (a lane each), waited for here, before any DMA (the
+  // compiler's waits on vector memory cannot count the DMA, so a vector load
+  // waited for among the DMA would drain the DMA with it).
+  const int r = r_base + 32 * mb + j;
+  const bool real = r < R;
   int u_lo = 0, u_hi = N - 1;
   if (range_from_positions)
     union_bounds(pos_b, r_base / H, (min(r_base + kRows, R) - 1) / H, window, N, lane, u_lo, u_hi);
@@ -771,8 +792,6 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
   // The queries first (each m-block's Q^T operand of k-step s at units
   // 64 s + lane: query row l % 32, columns 16 s + 8 (l / 32) .. + 7), by
   // the first key set; then the first tiles.
-  const int r = r_base + 32 * mb + j;
-  const bool real = r < R;
   if (kset == 0) {
     i32x4 qrs = buffer_resource(q + (int64_t)b * R * C);
 #pragma unroll
@@ -787,6 +806,10 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
     for (int it = 0; it < G::kSlots - 1; ++it)
       if (it < mine) issue(it);
   }
+  // Per-row bounds: the wavefront's 32 rows span positions t_first..t_last;
+  // each position is read with a uniform (scalar) load, on the scalar counter,
+  // and the lanes of that position take it.  f_lo, f_hi: the rows every query
+  // of the wavefront sees.
   int lo = 0, hi = -1;
   uint64_t anc = 0;
   int f_lo = 0, f_hi = INT_MAX;
@@ -794,20 +817,21 @@ __global__ __launch_bounds__(kKeySets * MB * 64, 1) void verify_attention_m32(
   {
     const int w_first = r_base + 32 * mb;
     if (w_first < R) {
-      // each lane its own row's position (a vector load), the wavefront's
-      // common range by DPP reductions over its real rows
-      int blo = 0, bhi = INT_MAX;
-      if (real) {
-        const int my_t = r / H;
-        const Bounds bt = query_bounds(pos_b, my_t, window, N);
-        blo = bt.lo;
-        bhi = bt.hi;
-        lo = bt.lo;
-        hi = min(bt.hi, s_hi);
-        if constexpr (TREE) anc = ancestors[my_t];
+      const int t_first = w_first / H, t_last = (min(w_first + 32, R) - 1) / H;
+      const int my_t = real ? r / H : -1;
+      for (int t = t_first; t <= t_last; ++t) {
+        const Bounds bt = query_bounds(pos_b, t, window, N);
+        f_lo = max(f_lo, bt.lo);
+        f_hi = min(f_hi, bt.hi);
+        if (my_t == t) {
+          lo = bt.lo;
+          hi = min(bt.hi, s_hi);
+        }
+        if constexpr (TREE) {
+          const uint64_t a = const_load(ancestors, t);
+          if (my_t == t) anc = a;
+        }
       }
-      f_lo = max(f_lo, __builtin_amdgcn_readfirstlane(wave_max_i32(blo)));
-      f_hi = min(f_hi, __builtin_amdgcn_readfirstlane(wave_min_i32(bhi)));
     } else {
       f_hi = -1;
     }
