@@ -1118,6 +1118,16 @@ __global__ __launch_bounds__(kSparseWaves * 64, 1) void sparse_attention_mfma(
   const int nwin = hi >= lo ? hi - lo + 1 : 0;
   const int e0 = split * per_split;
   const int cnt = max(0, min(K + nwin, e0 + per_split) - e0);
+  // Q^T operand: head j of the query (a padding head repeats head H - 1),
+  // loaded with the row list and waited for before the first DMA (the
+  // compiler's waits on vector memory cannot count the DMA, so a load waited
+  // for among the DMA would drain the DMA with it)
+  bf16x8 qf[G::kSteps];
+  {
+    const unsigned short* qrow = q + ((int64_t)unit * H + min(j, H - 1)) * C;
+#pragma unroll
+    for (int s = 0; s < G::kSteps; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g);
+  }
   for (int i = threadIdx.x; i < per_split; i += kSparseWaves * 64) {
     const int e = e0 + i;
     int n = -1;
@@ -1132,6 +1142,8 @@ __global__ __launch_bounds__(kSparseWaves * 64, 1) void sparse_attention_mfma(
     rows_lds[i] = n;
   }
   __syncthreads();
+#pragma unroll
+  for (int s = 0; s < G::kSteps; ++s) asm volatile("" ::"v"(qf[s]));
   const int ntiles = (cnt + 31) / 32;
   const int mine = ntiles > w ? (ntiles - w + kSparseWaves - 1) / kSparseWaves : 0;  // tiles w, w + 4, ...
   const int fallback = nwin > 0 ? lo : 0;  // a valid row for a missing entry's DMA
@@ -1157,11 +1169,6 @@ __global__ __launch_bounds__(kSparseWaves * 64, 1) void sparse_attention_mfma(
   for (int i = 0; i < kSparseSlots; ++i)
     if (i < mine) issue(i);
 
-  // Q^T operand: head j of the query (a padding head repeats head H - 1)
-  bf16x8 qf[G::kSteps];
-  const unsigned short* qrow = q + ((int64_t)unit * H + min(j, H - 1)) * C;
-#pragma unroll
-  for (int s = 0; s < G::kSteps; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g);
   const int tr_off =
       128 * ((lane & 3) >> 1) + 8 * ((4 * g + ((lane >> 2) & 3)) ^ (12 * ((lane >> 1) & 1))) + 4 * (lane & 1);
   const int k_off = 128 * g + 8 * (j ^ (12 * (g & 1)));
