@@ -1972,8 +1972,11 @@ int plan(int B, int T, int H, int c, int N, int window, int dtype, int flags, in
   long long span = N;
   if (window > 0 && (long long)window + T - 1 < span) span = (long long)window + T - 1;
   // The smallest useful part: one 32-row tile per wavefront (key-parallel
-  // kernel) or per key set (row-block kernel).
-  const long long quantum = p.kind == kKeySplit ? 32 * kKeyWaves : 32 * kKeySets;
+  // kernel) or two per key set (row-block kernels: with one, the key sets'
+  // merge and the part write outweigh the shorter stream; measured on the
+  // MI355X at batch 8, a 1024-row window: 13.15 us a call at 8 or 12 splits
+  // against 13.75 at 17).
+  const long long quantum = p.kind == kKeySplit ? 32 * kKeyWaves : 64 * kKeySets;
   int splits = requested;
   if (splits <= 0) {
     const long long cus = compute_units();
@@ -2192,8 +2195,9 @@ int attend(const void* q, const void* k, int64_t k_stride_b, int64_t k_stride_n,
     st = launched("verify_attention_mfma");
   }
   if (st != WPTV_OK || p.splits == 1) return st;
-  const int threads = 256;
+  // 64-thread workgroups when 256-thread ones would leave compute units idle
   const long long items = (long long)B * R * (c / 8);
+  const int threads = items >= 256LL * 256 ? 256 : 64;
   dim3 cgrid((unsigned)((items + threads - 1) / threads));
   hipLaunchKernelGGL(combine_splits, cgrid, dim3(threads), 0, stream,
                      static_cast<const unsigned short*>(part_o), part_lse, sink, B, T, H, c, rows_per_group, p.groups,
