@@ -168,7 +168,19 @@ class Drafter:
 
     @staticmethod
     def _norm(x, weight):
+        """RMSNorm of x's rows times weight (FP32 math, one rounding to x's
+        dtype, as torch's rms_norm of a bf16 x and an FP32 weight): the
+        library's one-launch kernel for contiguous bf16 rows, torch otherwise."""
+        if x.dtype == torch.bfloat16 and x.is_contiguous() and x.shape[-1] % 8 == 0 and x.shape[-1] <= 4096:
+            return layers.add_rms_norm(x, None, weight, torch.empty_like(x), EPS)
         return F.rms_norm(x, (x.shape[-1],), weight, EPS)
+
+    def _heads_norm(self, x, weight, heads):
+        """RMSNorm of each of the first heads * c columns' heads of x (R, T,
+        width), times weight (c,): (R, T, heads, c), one launch."""
+        if x.dtype == torch.bfloat16 and weight.shape[0] in (64, 128, 256):
+            return layers.heads_rms_norm(x, weight, heads, EPS)
+        return self._norm(x[..., :heads * weight.shape[0]].unflatten(-1, (heads, weight.shape[0])), weight)
 
     def _layer(self, i, h, fused, positions, context_positions, places, span):
         w = lambda name: self.w[f"layers.{i}.{name}"]  # noqa: E731
@@ -176,13 +188,13 @@ class Drafter:
         H, c = self.heads, self.head_dim
         x = self._norm(h, w("attn_norm"))
         proj = self._linear(x, w("qkvg"))  # (R, count, (2H + 2) c): q, k, v, gate
-        q = self._rotate(self._norm(proj[..., :H * c].unflatten(-1, (H, c)), w("q_norm")), positions)
-        block = torch.cat([self._rotate(self._norm(proj[..., H * c:H * c + c], w("k_norm")), positions),
+        q = self._rotate(self._heads_norm(proj, w("q_norm"), H), positions)
+        block = torch.cat([self._rotate(self._heads_norm(proj[..., H * c:], w("k_norm"), 1)[..., 0, :], positions),
                            proj[..., H * c + c:H * c + 2 * c]], -1)
         kv = w("qkvg")[H * c:H * c + 2 * c]  # the layer's own key/value projection injects the context
         ctx = self._linear(fused, kv)  # (R, WINDOW, 2c)
-        injected = torch.cat([self._rotate(self._norm(ctx[..., :c], w("k_norm")), context_positions), ctx[..., c:]],
-                             -1)
+        injected = torch.cat([self._rotate(self._heads_norm(ctx, w("k_norm"), 1)[..., 0, :], context_positions),
+                              ctx[..., c:]], -1)
         table = torch.cat([injected, block], 1).contiguous()  # [context ; block]
         o = kernels.verify_attention(q.contiguous(), table[..., :c], table[..., c:], places, c ** -0.5, window=span,
                                      sink=w("sink"))

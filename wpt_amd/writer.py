@@ -95,7 +95,7 @@ class Writer:
         self._rows = [_Row(list(prompt), [prompt[-1]]) for _ in range(rows)]
         self.features = tuple(getattr(drafter, "features", ())) if drafter is not None else ()
         self.cache = None
-        self.context = None  # a feature-reading drafter's context: (rows, window, features x d_model) FP32
+        self.context = None  # a feature-reading drafter's context: (rows, window, features x d_model)
         self.capture = bool(capture) and isinstance(model, MQADecoder)
         self._reads = {}  # drafts a row -> _CapturedRead
         if not cached:
@@ -110,7 +110,7 @@ class Writer:
         if self.features:
             if self.context is None:  # nothing read: the window holds zeros before the text
                 self.context = torch.zeros(1, drafter.window, len(self.features) * model.config.d_model,
-                                           device=self.device)
+                                           dtype=getattr(model, "dtype", torch.float32), device=self.device)
             self.context = self.context.expand(rows, -1, -1).clone()
 
     @property
@@ -171,7 +171,7 @@ class Writer:
         each row keeps the features of its last `window` read tokens."""
         if not self.features:
             return
-        fresh = read[2].float()
+        fresh = read[2]  # the features in the model's dtype, as the reference keeps them
         window = self.drafter.window
         held = self.context if self.context is not None else fresh.new_zeros(fresh.shape[0], window, fresh.shape[-1])
         both = torch.cat([held, fresh], 1)
@@ -217,7 +217,11 @@ class Writer:
     def _round(self, order, limits):
         if self.features:
             self._read_up_to_anchor(order)
-        context = (self.context[order], self.cache.lengths[order]) if self.features else None
+        if self.features:  # every row in order (a steady round) takes the context as it stands: no copy
+            whole = list(order) == list(range(len(self._rows)))
+            context = (self.context, self.cache.lengths) if whole else (self.context[order], self.cache.lengths[order])
+        else:
+            context = None
         drafts, q, confidence = self.drafter.draft(self.model, [self._rows[r].text for r in order], context,
                                                    self.draft, self._probabilities, self.generator)
         drafts = drafts.to(self.device, torch.long)
