@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define WPTV_ABI_VERSION 9
+#define WPTV_ABI_VERSION 10
 
 enum {
   WPTV_OK = 0,
@@ -309,6 +309,17 @@ int wptv_window_qkv_post(const void* qkv, int64_t qkv_row_stride, const float* q
  *   (row r at x + r*row_stride) times weight [c], in FP32. */
 int wptv_heads_rms_norm(const void* x, int64_t row_stride, const float* weight, void* out, int rows, int H, int c,
                         int dtype, float eps, hipStream_t stream);
+
+/* wptv_heads_rms_norm_rope: a window attention's query and key
+ *   (packages/wpt-model/src/wpt_model/attention.py:130-136:
+ *   rotate(q_norm(q(x)), positions), rotate(k_norm(k(x)), positions)):
+ *   wptv_heads_rms_norm, then the last rope_dims (even, <= c) values of each
+ *   head of row r turned by positions[r] (rotate, attention.py:59-71: pairs
+ *   (2i, 2i + 1) by the angle positions[r] / rope_div[i], in FP32 from the
+ *   normed values rounded to the dtype).  rope_div [rope_dims / 2] FP32. */
+int wptv_heads_rms_norm_rope(const void* x, int64_t row_stride, const float* weight, void* out, int rows, int H,
+                             int c, int dtype, float eps, const int64_t* positions, int rope_dims,
+                             const float* rope_div, hipStream_t stream);
 
 int wptv_swiglu(const void* gate_up, void* out, int M, int F, int dtype, hipStream_t stream);
 

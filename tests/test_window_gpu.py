@@ -110,6 +110,28 @@ def test_window_qkv_post_rotates_and_appends_to_the_ring(device, dtype, c, start
                 assert (ring[b, slot] == 7.0).all()  # past counts[b]: untouched
 
 
+@pytest.mark.parametrize("dtype, c, heads, rope_dims, share", [
+    (torch.float32, 64, 4, 32, 1e-5), (torch.bfloat16, 128, 16, 64, 2e-2), (torch.bfloat16, 128, 1, 64, 2e-2),
+    (torch.bfloat16, 256, 2, 256, 2e-2)])
+def test_head_norms_with_the_rotation_match_the_reference_rotate(device, dtype, c, heads, rope_dims, share):
+    # the drafter's q and k: rotate(norm(x), positions) per head of a strided
+    # projection, positions per row (clamped at 0 as a window before the text)
+    B, T = 3, 7
+    proj = draw(B, T, heads * c + 96, seed=11, dtype=dtype)  # wider rows: the heads are a strided view
+    weight = 1 + 0.1 * draw(c, seed=12, dtype=torch.float32)
+    positions = (torch.tensor([[5], [900], [40000]]) - 3 + torch.arange(T)).clamp(min=0)
+    norm = lambda x: torch.nn.functional.rms_norm(x.float(), (c,), weight, 1e-6).to(dtype)  # noqa: E731
+    want = oracle.rotate(norm(proj[..., :heads * c].reshape(B, T, heads, c)), positions, dims=rope_dims)
+    divisors = layers.rope_divisors(rope_dims, device=device)
+    got = layers.heads_rms_norm(proj.to(device), weight.to(device), heads, positions=positions.to(device),
+                                divisors=divisors)
+    assert got.shape == (B, T, heads, c) and got.dtype == dtype
+    assert relative_error(got.cpu(), want) < share
+    # without positions: the norm alone
+    plain = layers.heads_rms_norm(proj.to(device), weight.to(device), heads)
+    assert relative_error(plain.cpu(), norm(proj[..., :heads * c].reshape(B, T, heads, c))) < share
+
+
 # FP32 on the generic kernels; bf16 with 16 heads of width 128 on the
 # matrix-core kernels (two layers and small weights, as the exact decoder's
 # bf16 tests, so that bf16 rounding stays inside 2e-2)

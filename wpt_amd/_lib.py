@@ -12,7 +12,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwptv.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 WPTV_F32, WPTV_BF16 = 0, 1
 DTYPES = {torch.float32: WPTV_F32, torch.bfloat16: WPTV_BF16}
@@ -55,6 +55,7 @@ SIGNATURES = {
     "wptv_qkv_post": [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I, _I, _F, _P],
     "wptv_window_qkv_post": [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I, _P, _P, _I, _I, _I, _I, _I, _P, _I, _F, _P],
     "wptv_heads_rms_norm": [_P, _I64, _P, _P, _I, _I, _I, _I, _F, _P],
+    "wptv_heads_rms_norm_rope": [_P, _I64, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P, _P],
     "wptv_embed_rms_norm": [_P, _P, _I64, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _I, _P],
     "wptv_cache_lengths": [_P, _P, _P, _I, _I, _I, _P],
     "wptv_next_feeds": [_P, _I64, _P, _P, _I64, _I, _I, _P, _P, _P],

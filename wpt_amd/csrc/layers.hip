@@ -257,6 +257,37 @@ struct Rope {
   uint32_t ring_mask;  // 0: the entry at row start[b] + t (no ring)
 };
 
+// The rotation of one head's last `dims` of its C = 64 EPL values, lane l
+// holding elements EPL l .. EPL l + EPL - 1: adjacent pairs (2i, 2i + 1) of
+// the rotated part turned by the angle pos / div[i], from the values rounded
+// to T, in FP32 (attention.py:59-71).  Every lane of the wavefront takes part.
+template <typename T, int EPL>
+__device__ __forceinline__ void rotate_lane(float (&v)[EPL], int lane, int64_t pos, int dims, const float* div) {
+  constexpr int C = 64 * EPL;
+  // element d = EPL lane + e; rotated when d >= C - dims, pair i = (d - first) / 2
+  const int first = C - dims;
+  float mine[EPL], other[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) mine[e] = rounded<T>(v[e]);
+  if constexpr (EPL == 1) {
+    other[0] = __shfl_xor(mine[0], 1, 64);  // the pair's other element sits on the next lane
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) other[e] = mine[e ^ 1];
+  }
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int d = EPL * lane + e;
+    if (d < first) continue;
+    const int i = (d - first) >> 1;
+    const float angle = (float)pos / div[i];
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
+    // (even, odd) -> (even cos - odd sin, even sin + odd cos)
+    v[e] = (d & 1) == 0 ? mine[e] * cs - other[e] * sn : other[e] * sn + mine[e] * cs;
+  }
+}
+
 // The arguments the first loads depend on come first (gfx950 preloads a
 // kernel's first 14 argument dwords into SGPRs; the others arrive by a
 // scalar load meanwhile).
@@ -314,40 +345,20 @@ __global__ __launch_bounds__(256) void qkv_post(int rows, int T_, int H, const f
     const float inv = rsqrtf(ss / (float)C + eps);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) v[e] = v[e] * inv * wt[e];
-    if (rope.dims > 0) {
-      // element d = EPL lane + e; rotated when d >= C - dims, pair i = (d - first) / 2
-      const int first = C - rope.dims;
-      float mine[EPL], other[EPL];
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) mine[e] = rounded<T>(v[e]);
-      if constexpr (EPL == 1) {
-        other[0] = __shfl_xor(mine[0], 1, 64);  // the pair's other element sits on the next lane
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) other[e] = mine[e ^ 1];
-      }
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const int d = EPL * lane + e;
-        if (d < first) continue;
-        const int i = (d - first) >> 1;
-        const float angle = (float)pos / rope.div[i];
-        float sn, cs;
-        sincosf(angle, &sn, &cs);
-        // (even, odd) -> (even cos - odd sin, even sin + odd cos)
-        v[e] = (d & 1) == 0 ? mine[e] * cs - other[e] * sn : other[e] * sn + mine[e] * cs;
-      }
-    }
+    if (rope.dims > 0) rotate_lane<T, EPL>(v, lane, pos, rope.dims, rope.div);
   }
   Lane<T, EPL>::store(dst + EPL * lane, v);
 }
 
 // RMSNorm of each head of each row: x row r at x + r*row_stride, H heads of
-// C = 64 EPL values; out [rows, H, C].  One wavefront per (row, head).
-template <typename T, int EPL>
+// C = 64 EPL values; out [rows, H, C].  One wavefront per (row, head).  ROPE:
+// then each head's last rope_dims values turned by row r's position
+// positions[r] (rotate_lane).
+template <typename T, int EPL, bool ROPE>
 __global__ __launch_bounds__(256) void heads_rms_norm(const T* __restrict__ x, int64_t row_stride,
                                                       const float* __restrict__ weight, T* __restrict__ out, int rows,
-                                                      int H, float eps) {
+                                                      int H, float eps, const int64_t* __restrict__ positions,
+                                                      int rope_dims, const float* __restrict__ rope_div) {
   constexpr int C = 64 * EPL;
   const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -362,6 +373,7 @@ __global__ __launch_bounds__(256) void heads_rms_norm(const T* __restrict__ x, i
   const float inv = rsqrtf(ss / (float)C + eps);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) v[e] = v[e] * inv * weight[EPL * lane + e];
+  if constexpr (ROPE) rotate_lane<T, EPL>(v, lane, positions[row], rope_dims, rope_div);
   Lane<T, EPL>::store(out + ((int64_t)row * H + head) * C + EPL * lane, v);
 }
 
@@ -649,22 +661,29 @@ extern "C" int wptv_qkv_post_parts(const float* parts, int splits, const float* 
   return launched("qkv_post_parts");
 }
 
-extern "C" int wptv_heads_rms_norm(const void* x, int64_t row_stride, const float* weight, void* out, int rows, int H,
-                                   int c, int dtype, float eps, hipStream_t stream) {
-  if (!x || !weight || !out) return fail(WPTV_E_INVALID, "heads_rms_norm: every pointer must be given");
-  if (rows < 0 || H <= 0) return fail(WPTV_E_INVALID, "heads_rms_norm: bad shape rows=%d H=%d", rows, H);
+namespace {
+int heads_norm(const char* what, const void* x, int64_t row_stride, const float* weight, void* out, int rows, int H,
+               int c, int dtype, float eps, const int64_t* positions, int rope_dims, const float* rope_div,
+               hipStream_t stream) {
+  if (!x || !weight || !out) return fail(WPTV_E_INVALID, "%s: every pointer must be given", what);
+  if (rows < 0 || H <= 0) return fail(WPTV_E_INVALID, "%s: bad shape rows=%d H=%d", what, rows, H);
   if (c != 64 && c != 128 && c != 256)
-    return fail(WPTV_E_UNSUPPORTED, "heads_rms_norm: head width %d is not 64, 128 or 256", c);
-  if (row_stride < (int64_t)H * c) return fail(WPTV_E_INVALID, "heads_rms_norm: a row stride below H*c");
+    return fail(WPTV_E_UNSUPPORTED, "%s: head width %d is not 64, 128 or 256", what, c);
+  if (row_stride < (int64_t)H * c) return fail(WPTV_E_INVALID, "%s: a row stride below H*c", what);
+  const bool rope = rope_dims > 0;
+  if (rope && (!positions || !rope_div || rope_dims % 2 || rope_dims > c))
+    return fail(WPTV_E_INVALID, "%s: the rotation needs positions, divisors and an even width up to %d (got %d)", what,
+                c, rope_dims);
   const int epl = c / 64;
   const int esize = dtype == WPTV_F32 ? 4 : 2;
   if (row_stride % epl || !aligned(x, epl * esize) || !aligned(out, epl * esize))
-    return fail(WPTV_E_INVALID, "heads_rms_norm: rows must be aligned to %d elements", epl);
+    return fail(WPTV_E_INVALID, "%s: rows must be aligned to %d elements", what, epl);
   if (rows == 0) return WPTV_OK;
   dim3 grid((unsigned)(((int64_t)rows * H + 3) / 4));
-#define WPTV_HN(TT, EE)                                                                                          \
-  hipLaunchKernelGGL((heads_rms_norm<TT, EE>), grid, dim3(256), 0, stream, static_cast<const TT*>(x), row_stride, \
-                     weight, static_cast<TT*>(out), rows, H, eps)
+#define WPTV_HN(TT, EE)                                                                                             \
+  hipLaunchKernelGGL((rope ? heads_rms_norm<TT, EE, true> : heads_rms_norm<TT, EE, false>), grid, dim3(256), 0,     \
+                     stream, static_cast<const TT*>(x), row_stride, weight, static_cast<TT*>(out), rows, H, eps,     \
+                     positions, rope_dims, rope_div)
   if (dtype == WPTV_BF16) {
     if (epl == 1) WPTV_HN(unsigned short, 1);
     else if (epl == 2) WPTV_HN(unsigned short, 2);
@@ -674,10 +693,23 @@ extern "C" int wptv_heads_rms_norm(const void* x, int64_t row_stride, const floa
     else if (epl == 2) WPTV_HN(float, 2);
     else WPTV_HN(float, 4);
   } else {
-    return fail(WPTV_E_UNSUPPORTED, "heads_rms_norm: dtype %d is neither fp32 nor bf16", dtype);
+    return fail(WPTV_E_UNSUPPORTED, "%s: dtype %d is neither fp32 nor bf16", what, dtype);
   }
 #undef WPTV_HN
-  return launched("heads_rms_norm");
+  return launched(what);
+}
+}  // namespace
+
+extern "C" int wptv_heads_rms_norm(const void* x, int64_t row_stride, const float* weight, void* out, int rows, int H,
+                                   int c, int dtype, float eps, hipStream_t stream) {
+  return heads_norm("heads_rms_norm", x, row_stride, weight, out, rows, H, c, dtype, eps, nullptr, 0, nullptr, stream);
+}
+
+extern "C" int wptv_heads_rms_norm_rope(const void* x, int64_t row_stride, const float* weight, void* out, int rows,
+                                        int H, int c, int dtype, float eps, const int64_t* positions, int rope_dims,
+                                        const float* rope_div, hipStream_t stream) {
+  return heads_norm("heads_rms_norm_rope", x, row_stride, weight, out, rows, H, c, dtype, eps, positions, rope_dims,
+                    rope_div, stream);
 }
 
 extern "C" int wptv_swiglu(const void* gate_up, void* out, int M, int F, int dtype, hipStream_t stream) {

@@ -175,12 +175,14 @@ class Drafter:
             return layers.add_rms_norm(x, None, weight, torch.empty_like(x), EPS)
         return F.rms_norm(x, (x.shape[-1],), weight, EPS)
 
-    def _heads_norm(self, x, weight, heads):
+    def _heads_norm(self, x, weight, heads, positions):
         """RMSNorm of each of the first heads * c columns' heads of x (R, T,
-        width), times weight (c,): (R, T, heads, c), one launch."""
+        width), times weight (c,), then the rotary encoding at positions (R,
+        T): (R, T, heads, c), one launch."""
         if x.dtype == torch.bfloat16 and weight.shape[0] in (64, 128, 256):
-            return layers.heads_rms_norm(x, weight, heads, EPS)
-        return self._norm(x[..., :heads * weight.shape[0]].unflatten(-1, (heads, weight.shape[0])), weight)
+            return layers.heads_rms_norm(x, weight, heads, EPS, positions=positions, divisors=self.divisors)
+        normed = self._norm(x[..., :heads * weight.shape[0]].unflatten(-1, (heads, weight.shape[0])), weight)
+        return self._rotate(normed, positions)
 
     def _layer(self, i, h, fused, positions, context_positions, places, span):
         w = lambda name: self.w[f"layers.{i}.{name}"]  # noqa: E731
@@ -188,13 +190,12 @@ class Drafter:
         H, c = self.heads, self.head_dim
         x = self._norm(h, w("attn_norm"))
         proj = self._linear(x, w("qkvg"))  # (R, count, (2H + 2) c): q, k, v, gate
-        q = self._rotate(self._heads_norm(proj, w("q_norm"), H), positions)
-        block = torch.cat([self._rotate(self._heads_norm(proj[..., H * c:], w("k_norm"), 1)[..., 0, :], positions),
+        q = self._heads_norm(proj, w("q_norm"), H, positions)
+        block = torch.cat([self._heads_norm(proj[..., H * c:], w("k_norm"), 1, positions)[..., 0, :],
                            proj[..., H * c + c:H * c + 2 * c]], -1)
         kv = w("qkvg")[H * c:H * c + 2 * c]  # the layer's own key/value projection injects the context
         ctx = self._linear(fused, kv)  # (R, WINDOW, 2c)
-        injected = torch.cat([self._rotate(self._heads_norm(ctx, w("k_norm"), 1)[..., 0, :], context_positions),
-                              ctx[..., c:]], -1)
+        injected = torch.cat([self._heads_norm(ctx, w("k_norm"), 1, context_positions)[..., 0, :], ctx[..., c:]], -1)
         table = torch.cat([injected, block], 1).contiguous()  # [context ; block]
         o = kernels.verify_attention(q.contiguous(), table[..., :c], table[..., c:], places, c ** -0.5, window=span,
                                      sink=w("sink"))

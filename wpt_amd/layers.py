@@ -139,17 +139,32 @@ def window_qkv_post(proj, q_norm, k_norm, ring, start, counts, heads, rope_dims=
     return q
 
 
-def heads_rms_norm(x, weight, heads, eps=EPS):
+def heads_rms_norm(x, weight, heads, eps=EPS, positions=None, divisors=None):
     """x (B, T, >= H*c) (rows one after another) -> (B, T, H, c): RMSNorm of
-    each head of the first H*c columns, times weight (c,) FP32."""
+    each head of the first H*c columns, times weight (c,) FP32.  With
+    positions (B, T) int64 and divisors (rope_dims / 2,) FP32 (rope_divisors),
+    each head's last rope_dims values then turned by the row's position, as
+    the reference's rotate (attention.py:59-71, 130-136)."""
     _gpu(x, weight)
     B, T, width = x.shape
     c = weight.shape[0]
     if width < heads * c or x.stride(-1) != 1 or x.stride(0) != T * x.stride(1):
         raise ValueError(f"x must be (B, T, >= H*c) with rows one after another; got {tuple(x.shape)}")
     out = torch.empty(B, T, heads, c, dtype=x.dtype, device=x.device)
-    check(_lib.lib().wptv_heads_rms_norm(ptr(x), x.stride(1), ptr(weight), ptr(out), B * T, heads, c,
-                                         _lib.dtype_code(x.dtype), float(eps), _lib.stream(x.device)), "heads_rms_norm")
+    if positions is None:
+        check(_lib.lib().wptv_heads_rms_norm(ptr(x), x.stride(1), ptr(weight), ptr(out), B * T, heads, c,
+                                             _lib.dtype_code(x.dtype), float(eps), _lib.stream(x.device)),
+              "heads_rms_norm")
+        return out
+    _gpu(positions, divisors)
+    if positions.shape != (B, T) or positions.dtype != torch.int64 or divisors.dtype != torch.float32:
+        raise ValueError(f"positions must be int64 ({B}, {T}) and divisors FP32; got {tuple(positions.shape)} "
+                         f"{positions.dtype}, {divisors.dtype}")
+    positions = positions.contiguous()
+    check(_lib.lib().wptv_heads_rms_norm_rope(ptr(x), x.stride(1), ptr(weight), ptr(out), B * T, heads, c,
+                                              _lib.dtype_code(x.dtype), float(eps), ptr(positions),
+                                              2 * divisors.shape[0], ptr(divisors), _lib.stream(x.device)),
+          "heads_rms_norm_rope")
     return out
 
 
