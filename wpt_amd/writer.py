@@ -171,7 +171,10 @@ class Writer:
         each row keeps the features of its last `window` read tokens."""
         if not self.features:
             return
-        fresh = read[2]  # the features in the model's dtype, as the reference keeps them
+        # the features come as FP32 (the reference's dtype for them); they are the
+        # model's residual stream, so its dtype (bf16) holds them exactly and
+        # halves the window's traffic
+        fresh = read[2].to(getattr(self.model, "dtype", read[2].dtype))
         window = self.drafter.window
         held = self.context if self.context is not None else fresh.new_zeros(fresh.shape[0], window, fresh.shape[-1])
         both = torch.cat([held, fresh], 1)
