@@ -52,6 +52,7 @@ struct Stats {  // per (batch row, position); arrays of B * P in the workspace
   float* pd;    // in-order draws: p of the draft at this position
   float* qd;    // and its q
   float* rest;  // the residual's mass max(0, p - q) summed (1 after the last draft)
+  int* arrivals;  // in-order draws: per row, the vocabulary slices whose draws are done (zeroed by accept_stats)
 };
 
 __device__ __forceinline__ float block_max(float x, float* red) {
@@ -339,6 +340,10 @@ __global__ __launch_bounds__(kT) void accept_stats(const S* __restrict__ scores,
   // is read from HBM once and found in that XCD's L2 by the others.
   const int P = L + 1, slot = blockIdx.x >> 3;
   const int b = 8 * (slot / P) + (blockIdx.x & 7), j = slot % P;
+  if constexpr (ORDER) {  // order_draw, the next launch, counts each row's slices from zero
+    if (blockIdx.x == 0)
+      for (int i = threadIdx.x; i < B; i += kT) stats.arrivals[i] = 0;
+  }
   if (b >= B) return;
   const int n = lengths ? min(max(lengths[b], 0), L) : L;
   if (j > n) return;
@@ -568,7 +573,6 @@ struct Order {
   uint32_t threads;      // S of the multinomial's draw (of V entries, or of B V when joint)
   int joint;             // one multinomial over every row's V entries (L = 0: Writer._sample's)
   int64_t joint_step;    // that draw's offset step
-  int2* rows;            // per row: (first rejected draft, or the count when none is; its draw's block index)
   float2* parts;         // per row and slice: the slice's race winner (value, index bits)
 };
 
@@ -602,6 +606,32 @@ __device__ __forceinline__ float drawn_exponential(float u) {
   return -1.f * (u >= 1.f - 0x1p-24f ? -0x1p-24f : __logf(u));
 }
 
+// What a verify step does with a row's count once it is known, in the pick's
+// own thread (COMMIT): the cache takes back the rejected drafts (the
+// reference's Rows.undo, cache.py:69-77: lengths = before + kept, kept outside
+// 0 .. the tokens read taken as the nearest end) and the last written token
+// becomes the row's pending token; a row that wrote nothing keeps its pending
+// token and raises *failed.
+struct Commit {
+  int64_t* lengths;
+  const int64_t* before;
+  int64_t* feeds;
+  int64_t feeds_stride;
+  int* failed;
+  int64_t* written;
+};
+
+__device__ inline void commit_row(const Commit& c, int b, int n, int64_t last) {
+  const int64_t start = c.before[b], read = c.lengths[b] - start;
+  c.lengths[b] = start + min(max((int64_t)n, (int64_t)0), read);
+  if (n < 1) {
+    if (c.failed) *c.failed = 1;
+    return;
+  }
+  c.feeds[(int64_t)b * c.feeds_stride] = last;
+  if (c.written) c.written[b] += n;
+}
+
 // The draws of row b's multinomial over vocabulary slice s (blockIdx.x = b
 // kSlices + s).  Each workgroup first replays the loop up to its row: the
 // uniforms u_t = U(o + 4 t) it may read, every row's drafts' p and q, then
@@ -612,11 +642,25 @@ __device__ __forceinline__ float drawn_exponential(float u) {
 // last draft; its p from the statistics of that position (the same steps as
 // accept_stats, so the same bits).  Only entries with w > 0 draw an
 // exponential: 0 / e is 0 for every e the draw can give.
-template <int N, typename S, bool CUT>
+//
+// The row's pick runs in the last of its slices to finish: each slice stores
+// its race winner with a device-scope store, waits for it to complete, then
+// counts itself in stats.arrivals[b] (a device-scope atomic, zeroed by
+// accept_stats); the slice that counts the row's last reads the kSlices
+// winners back with device-scope loads (they see every XCD's stores), joins
+// them in index order and writes the row's tokens (the drafts up to the
+// first rejected one, then the draw: __init__.py:210-229), its count, and
+// with COMMIT its cache length, pending token and running count; the last
+// row's pick also writes the generator's next offset.  No workgroup waits
+// for another.
+template <int N, typename S, bool CUT, bool COMMIT>
 __global__ __launch_bounds__(kDT) void order_draw(const S* __restrict__ scores, int64_t sb, int64_t st,
                                                   const int32_t* __restrict__ firsts, const float* __restrict__ q,
                                                   int64_t qb, int64_t qt, const int32_t* __restrict__ lengths,
-                                                  float temperature, int B, int L, int V, Stats stats, Order order) {
+                                                  float temperature, int B, int L, int V, Stats stats, Order order,
+                                                  const int64_t* __restrict__ drafts, int64_t db,
+                                                  int64_t* __restrict__ tokens, int32_t* __restrict__ n_tokens,
+                                                  Commit commit) {
   // the replay's tables, sized at launch: uniforms B P, drafts' p and q B L each, lengths B
   extern __shared__ __attribute__((aligned(16))) float scan_lds[];
   float* utab = scan_lds;
@@ -626,6 +670,7 @@ __global__ __launch_bounds__(kDT) void order_draw(const S* __restrict__ scores, 
   __shared__ float redv[kDT / 64];
   __shared__ int redi[kDT / 64];
   __shared__ int found[2];
+  __shared__ int last;
   const int b = blockIdx.x / kSlices, s = blockIdx.x % kSlices, tid = threadIdx.x;
   if (b >= B) return;
   const int P = L + 1;
@@ -666,9 +711,6 @@ __global__ __launch_bounds__(kDT) void order_draw(const S* __restrict__ scores, 
     __syncthreads();
     js = found[0];
     t_draw = found[1];
-    if (s == 0 && tid == 0) order.rows[b] = make_int2(js, t_draw);
-  } else if (s == 0 && tid == 0) {
-    order.rows[b] = make_int2(0, 0);
   }
   const int len = order.joint ? 0 : (lengths ? min(max(lengths[b], 0), L) : L);
   const bool draft_pos = js < len;
@@ -727,35 +769,43 @@ __global__ __launch_bounds__(kDT) void order_draw(const S* __restrict__ scores, 
     int bi = redi[0];
 #pragma unroll
     for (int w = 1; w < kDT / 64; ++w) arg_better(bv, bi, redv[w], redi[w]);
-    order.parts[b * kSlices + s] = make_float2(bv, __int_as_float(bi));
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(order.parts + b * kSlices + s),
+                       __builtin_bit_cast(uint64_t, make_float2(bv, __int_as_float(bi))), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::: "memory");
+    wait_vmcnt<0>();
+    last = __hip_atomic_fetch_add(stats.arrivals + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kSlices - 1;
   }
+  __syncthreads();
+  if (!last || tid >= 64) return;
+
+  // the row's pick: lane l < kSlices holds slice l's winner
+  const int lane = tid;
+  float bv = kNegInfS;
+  int bi = INT_MAX;
+  if (lane < kSlices) {
+    const float2 part = __builtin_bit_cast(
+        float2, __hip_atomic_load(reinterpret_cast<uint64_t*>(order.parts + b * kSlices + lane), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT));
+    bv = part.x;
+    bi = __float_as_int(part.y);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float v2 = __shfl_xor(bv, off, 64);
+    const int i2 = __shfl_xor(bi, off, 64);
+    arg_better(bv, bi, v2, i2);
+  }
+  int pick = bi >= 0 && bi < V ? bi : -1;
+  // a residual with no mass has no draw (the reference's multinomial raises)
+  if (draft_pos && !(rest > 0.f)) pick = -1;
+  for (int t = lane; t < P; t += 64) tokens[(int64_t)b * P + t] = t < js ? drafts[b * db + t] : (t == js ? pick : -1);
+  if (lane != 0) return;
+  n_tokens[b] = pick >= 0 ? js + 1 : -1;
+  if constexpr (COMMIT) commit_row(commit, b, pick >= 0 ? js + 1 : -1, pick);
+  if (b == B - 1) *order.next = order.state[1] + (order.joint ? order.joint_step : 4 * ((int64_t)t_draw + 1));
 }
 
-// What a verify step does with a row's count once it is known, in the pick's
-// own thread (COMMIT): the cache takes back the rejected drafts (the
-// reference's Rows.undo, cache.py:69-77: lengths = before + kept, kept outside
-// 0 .. the tokens read taken as the nearest end) and the last written token
-// becomes the row's pending token; a row that wrote nothing keeps its pending
-// token and raises *failed.
-struct Commit {
-  int64_t* lengths;
-  const int64_t* before;
-  int64_t* feeds;
-  int64_t feeds_stride;
-  int* failed;
-  int64_t* written;
-};
-
-__device__ inline void commit_row(const Commit& c, int b, int n, int64_t last) {
-  const int64_t start = c.before[b], read = c.lengths[b] - start;
-  c.lengths[b] = start + min(max((int64_t)n, (int64_t)0), read);
-  if (n < 1) {
-    if (c.failed) *c.failed = 1;
-    return;
-  }
-  c.feeds[(int64_t)b * c.feeds_stride] = last;
-  if (c.written) c.written[b] += n;
-}
 
 // Each row's tokens from the per-position decisions: the drafts up to the
 // first rejected one, then that position's draw (the argmax in greedy mode),
@@ -810,44 +860,6 @@ __global__ __launch_bounds__(64) void accept_pick(const int64_t* __restrict__ dr
   if constexpr (COMMIT) commit_row(commit, b, pick >= 0 ? js + 1 : -1, pick);
 }
 
-// The in-order draws' pick (accept_pick's results and moves): one wavefront
-// per row, lane s holding slice s's race winner, the slices joined in index
-// order; the first rejected draft from order_draw's replay.  The last row
-// also writes the generator's next offset.
-template <bool COMMIT>
-__global__ __launch_bounds__(64) void order_pick(const int64_t* __restrict__ drafts, int64_t db,
-                                                 const int32_t* __restrict__ lengths, int L, int B, int V,
-                                                 Stats stats, int64_t* __restrict__ tokens,
-                                                 int32_t* __restrict__ n_tokens, Commit commit, Order order) {
-  const int b = blockIdx.x, lane = threadIdx.x;
-  if (b >= B) return;
-  const int P = L + 1;
-  float bv = kNegInfS;
-  int bi = INT_MAX;
-  if (lane < kSlices) {
-    const float2 part = order.parts[b * kSlices + lane];
-    bv = part.x;
-    bi = __float_as_int(part.y);
-  }
-  const int2 at = order.rows[b];
-  const int js = at.x, len = order.joint ? 0 : (lengths ? min(max(lengths[b], 0), L) : L);
-  const float rest = stats.rest[b * P + js];
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float v2 = __shfl_xor(bv, off, 64);
-    const int i2 = __shfl_xor(bi, off, 64);
-    arg_better(bv, bi, v2, i2);
-  }
-  int pick = bi >= 0 && bi < V ? bi : -1;
-  // a residual with no mass has no draw (the reference's multinomial raises)
-  if (js < len && !(rest > 0.f)) pick = -1;
-  for (int t = lane; t < P; t += 64) tokens[(int64_t)b * P + t] = t < js ? drafts[b * db + t] : (t == js ? pick : -1);
-  if (lane != 0) return;
-  n_tokens[b] = pick >= 0 ? js + 1 : -1;
-  if constexpr (COMMIT) commit_row(commit, b, pick >= 0 ? js + 1 : -1, pick);
-  if (b == B - 1) *order.next = order.state[1] + (order.joint ? order.joint_step : 4 * ((int64_t)at.y + 1));
-}
-
 // Greedy walk down a draft tree: node i's parent parents[i] < i, the root 0.
 __global__ void tree_walk(const int64_t* __restrict__ node_tokens, const int32_t* __restrict__ parents, int B, int M,
                           Stats stats, int64_t* __restrict__ path, int64_t* __restrict__ tokens,
@@ -894,10 +906,11 @@ Stats carve(void* workspace, int B, int P) {
   s.pd = reinterpret_cast<float*>(p + 6 * n);
   s.qd = reinterpret_cast<float*>(p + 7 * n);
   s.rest = reinterpret_cast<float*>(p + 8 * n);
+  s.arrivals = nullptr;
   return s;
 }
 
-// The per-position arrays, then the in-order draws' per-row and per-slice results.
+// The per-position arrays, then the in-order draws' per-row arrival counts and per-slice results.
 size_t stats_bytes(int B, int P) { return 9 * align_up((size_t)B * P * 4, 256); }
 size_t order_bytes(int B) { return align_up((size_t)B * 8, 256) + align_up((size_t)B * kSlices * 8, 256); }
 
@@ -1116,21 +1129,28 @@ namespace {
 template <typename S>
 void launch_order_draw(int B, hipStream_t stream, const void* scores, int64_t sb, int64_t st, const int32_t* firsts,
                        const float* q, int64_t qb, int64_t qt, const int32_t* lengths, float temperature, int top_k,
-                       int L, int V, Stats s, Order o) {
+                       int L, int V, Stats s, Order o, const int64_t* drafts, int64_t db, int64_t* tokens,
+                       int32_t* n_tokens, const Commit* commit) {
   const int per = (V + kSlices - 1) / kSlices;
   const int n = (per + kDT - 1) / kDT;
   const bool cut = top_k > 0 && top_k < V;
   const S* rows = static_cast<const S*>(scores);
   const dim3 grid(B * kSlices);
   const size_t lds = 4 * ((size_t)B * (L + 1) + 2 * (size_t)B * L + B);
+  const Commit c = commit ? *commit : Commit{};
+#define WPTV_DRAW_C(N, CU, CM)                                                                                        \
+  hipLaunchKernelGGL((order_draw<N, S, CU, CM>), grid, dim3(kDT), lds, stream, rows, sb, st, firsts, q, qb, qt,     \
+                     lengths, temperature, B, L, V, s, o, drafts, db, tokens, n_tokens, c)
 #define WPTV_DRAW(N)                                                                                                  \
   do {                                                                                                                \
-    if (cut)                                                                                                          \
-      hipLaunchKernelGGL((order_draw<N, S, true>), grid, dim3(kDT), lds, stream, rows, sb, st, firsts, q, qb, qt,   \
-                         lengths, temperature, B, L, V, s, o);                                                        \
+    if (cut && commit)                                                                                                \
+      WPTV_DRAW_C(N, true, true);                                                                                     \
+    else if (cut)                                                                                                     \
+      WPTV_DRAW_C(N, true, false);                                                                                    \
+    else if (commit)                                                                                                  \
+      WPTV_DRAW_C(N, false, true);                                                                                    \
     else                                                                                                              \
-      hipLaunchKernelGGL((order_draw<N, S, false>), grid, dim3(kDT), lds, stream, rows, sb, st, firsts, q, qb, qt,  \
-                         lengths, temperature, B, L, V, s, o);                                                        \
+      WPTV_DRAW_C(N, false, false);                                                                                   \
   } while (0)
   if (n <= 1) WPTV_DRAW(1);
   else if (n <= 2) WPTV_DRAW(2);
@@ -1139,6 +1159,7 @@ void launch_order_draw(int B, hipStream_t stream, const void* scores, int64_t sb
   else if (n <= 16) WPTV_DRAW(16);
   else WPTV_DRAW(32);
 #undef WPTV_DRAW
+#undef WPTV_DRAW_C
 }
 
 }  // namespace
@@ -1178,35 +1199,26 @@ extern "C" int wptv_accept_in_order(const void* scores, int64_t scores_stride_b,
   if (numel >= (int64_t)1 << 31)
     return fail(WPTV_E_UNSUPPORTED, "accept_in_order: a joint draw of %lld entries", (long long)numel);
   const int64_t threads = 256 * std::min<int64_t>(cap, (numel + 255) / 256);
-  const Stats s = carve(workspace, B, L + 1);
+  Stats s = carve(workspace, B, L + 1);
   char* extra = static_cast<char*>(workspace) + stats_bytes(B, L + 1);
+  s.arrivals = reinterpret_cast<int*>(extra);
   Order o{};
   o.state = generator_state;
   o.next = next_offset;
   o.threads = (uint32_t)threads;
   o.joint = joint ? 1 : 0;
   o.joint_step = 4 * ((numel - 1) / (4 * threads) + 1);
-  o.rows = reinterpret_cast<int2*>(extra);
   o.parts = reinterpret_cast<float2*>(extra + align_up((size_t)B * 8, 256));
   (scores_dtype == WPTV_BF16 ? launch_stats<unsigned short, true> : launch_stats<float, true>)(
       B, stream, scores, scores_stride_b, scores_stride_t, firsts, q, q_stride_b, q_stride_t, drafts,
       drafts_stride_b, lengths, nullptr, nullptr, temperature, top_k, 0, L, V, s);
   int st = launched("accept_stats");
   if (st != WPTV_OK) return st;
+  const Commit c{cache_lengths, cache_before, feeds, feeds_stride, failed, written};
   (scores_dtype == WPTV_BF16 ? launch_order_draw<unsigned short> : launch_order_draw<float>)(
       B, stream, scores, scores_stride_b, scores_stride_t, firsts, q, q_stride_b, q_stride_t, lengths, temperature,
-      top_k, L, V, s, o);
-  st = launched("order_draw");
-  if (st != WPTV_OK) return st;
-  if (cache_lengths) {
-    const Commit c{cache_lengths, cache_before, feeds, feeds_stride, failed, written};
-    hipLaunchKernelGGL(order_pick<true>, dim3(B), dim3(64), 0, stream, drafts, drafts_stride_b, lengths, L, B, V, s,
-                       tokens, n_tokens, c, o);
-  } else {
-    hipLaunchKernelGGL(order_pick<false>, dim3(B), dim3(64), 0, stream, drafts, drafts_stride_b, lengths, L, B, V, s,
-                       tokens, n_tokens, Commit{}, o);
-  }
-  return launched("order_pick");
+      top_k, L, V, s, o, drafts, drafts_stride_b, tokens, n_tokens, cache_lengths ? &c : nullptr);
+  return launched("order_draw");
 }
 
 extern "C" int wptv_greedy_tree(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t,
