@@ -511,9 +511,11 @@ int wptv_accept_commit(const void* scores, int64_t scores_stride_b, int64_t scor
  *   not taken: a greedy step draws nothing) and wptv_accept_commit (all of
  *   cache_lengths, cache_before, feeds, failed, written may be NULL).
  *   B (L + 1) <= 3072, L <= 64; workspace wptv_accept_workspace(B, L) bytes.
- *   Three launches: the statistics, the draws (the loop's uniforms replayed
- *   to find each row's first rejection; the multinomial's exponentials over
- *   32 slices of the vocabulary a row), the pick. */
+ *   Two launches: the statistics, then the draws (the loop's uniforms
+ *   replayed to find each row's first rejection; the multinomial's
+ *   exponentials over 32 slices of the vocabulary a row), whose last slice
+ *   of a row to finish makes that row's pick.  Calls that share a workspace
+ *   must not overlap. */
 int wptv_accept_in_order(const void* scores, int64_t scores_stride_b, int64_t scores_stride_t, int scores_dtype,
                          const int32_t* firsts, const float* q, int64_t q_stride_b, int64_t q_stride_t,
                          const int64_t* drafts, int64_t drafts_stride_b, const int32_t* lengths,
