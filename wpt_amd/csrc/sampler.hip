@@ -25,7 +25,8 @@
 // the loop's uniforms (Philox4x32-10, as torch's device generator draws
 // them) to find each row's first rejection and the generator offset of its
 // multinomial, then draws that multinomial's exponentials over a slice of
-// the vocabulary; accept_pick joins the slices.
+// the vocabulary; the last slice of a row to finish joins the row's slices
+// and makes its pick.
 //
 // Each vocabulary row is read once per pass from HBM with coalesced loads and
 // kept in registers (ITEMS values per thread); reductions are wavefront
