@@ -40,8 +40,6 @@
 namespace wptv {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
 constexpr float kNegInf = -__builtin_inff();
 
 struct Bounds {
